@@ -1,0 +1,82 @@
+"""Wrapper for oracle/_ref/libmgref.so — TEST INFRASTRUCTURE ONLY.
+
+libmgref.so is the reference's own F32 CPU executor (mg-tensor.cpp + mg-cpu.cpp +
+mg-model.cpp + mg-transformer.cpp, compiled from the reference tree by
+``make -C oracle ref`` with oracle/ref_harness.cpp as the C entry layer). It exists only
+where that build ran; ``available()`` says whether it did.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_ref", "libmgref.so")
+_lib = None
+
+
+def available() -> bool:
+    return os.path.exists(_LIB_PATH)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        I64 = ctypes.c_int64
+        L.mgref_last_error.restype = ctypes.c_char_p
+        L.mgref_mul_mat.argtypes = [P, I64, I64, P, I64, P, ctypes.c_int, P, P]
+        L.mgref_norm_affine.argtypes = [P, I64, I64, P, P, ctypes.c_float, P]
+        L.mgref_attention.argtypes = [P, P, P, I64, I64, I64, I64, ctypes.c_float, P]
+        L.mgref_transformer_forward.argtypes = [ctypes.c_char_p, P, I64, I64, P, I64]
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _check(rc):
+    if rc != 0:
+        raise RuntimeError("libmgref: " + lib().mgref_last_error().decode())
+
+
+def mul_mat(w, x, bias=None, act=0, resid=None):
+    w = np.ascontiguousarray(w, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    N, K = w.shape
+    M = x.shape[0]
+    bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    resid = None if resid is None else np.ascontiguousarray(resid, np.float32)
+    y = np.empty((M, N), np.float32)
+    _check(lib().mgref_mul_mat(_p(w), N, K, _p(x), M, _p(bias), act, _p(resid), _p(y)))
+    return y
+
+
+def norm_affine(x, gamma, beta, eps):
+    x = np.ascontiguousarray(x, np.float32)
+    D = x.shape[-1]
+    y = np.empty_like(x)
+    _check(lib().mgref_norm_affine(_p(x), x.size // D, D, _p(np.ascontiguousarray(gamma, np.float32)),
+                                   _p(np.ascontiguousarray(beta, np.float32)), eps, _p(y)))
+    return y
+
+
+def attention(q, k, v, D, S, H, B, scale):
+    """q/k/v are [B][S][H*D] linear outputs; returns contiguous {D,S,H,B}."""
+    q, k, v = (np.ascontiguousarray(a, np.float32) for a in (q, k, v))
+    o = np.empty(D * S * H * B, np.float32)
+    _check(lib().mgref_attention(_p(q), _p(k), _p(v), D, S, H, B, scale, _p(o)))
+    return o
+
+
+def transformer_forward(gguf_path: str, tokens, vocab: int):
+    tokens = np.ascontiguousarray(tokens, np.int32)
+    B, S = tokens.shape
+    out = np.empty((B, S, vocab), np.float32)
+    _check(lib().mgref_transformer_forward(gguf_path.encode(), _p(tokens), S, B, _p(out), out.size))
+    return out

@@ -1,0 +1,103 @@
+// ref_harness.cpp — C entry points over the reference's own CPU executor (TEST INFRASTRUCTURE).
+//
+// Linked against the reference sources where they lie (mg-tensor.cpp, mg-cpu/mg-cpu.cpp,
+// mg-model.cpp, mg-transformer.cpp) by oracle/Makefile into oracle/_ref/libmgref.so. Only
+// tests and bench.py's cpu_baseline leg load it. Each function builds the same graph the
+// reference builds and runs the reference's mg::compute (src/mg-cpu/mg-cpu.cpp:296-298),
+// so its results are the reference's F32 CPU semantics, not a restatement.
+#include "mg-model.hpp"
+#include "mg-tensor.hpp"
+#include "mg-transformer.hpp"
+
+#include <cstdint>
+#include <cstring>
+#include <exception>
+#include <memory>
+#include <string>
+
+using namespace mg;
+
+namespace {
+std::string g_err;
+
+Tensor* ext2(Context& c, const float* p, int64_t ne0, int64_t ne1) {
+    int64_t ne[4] = {ne0, ne1, 1, 1};
+    return c.external(Type::F32, 2, ne, const_cast<float*>(p));
+}
+}  // namespace
+
+extern "C" {
+
+const char* mgref_last_error() { return g_err.c_str(); }
+
+// y[M][N] = act(w[N][K] . x[M][K] + bias) + resid via mul_mat_ex (mg-tensor.cpp:117-123)
+int mgref_mul_mat(const float* w, int64_t N, int64_t K, const float* x, int64_t M,
+                  const float* bias, int act, const float* resid, float* y) {
+    try {
+        Context c(64 << 20);
+        Tensor* tw = ext2(c, w, K, N);
+        Tensor* tx = ext2(c, x, K, M);
+        Tensor* tb = nullptr;
+        if (bias) { int64_t ne[4] = {N, 1, 1, 1}; tb = c.external(Type::F32, 1, ne, const_cast<float*>(bias)); }
+        Tensor* tr = resid ? ext2(c, resid, N, M) : nullptr;
+        Tensor* out = mul_mat_ex(c, tw, tx, tb, act, tr);
+        Graph g; g.build_forward(out); compute(c, g);
+        std::memcpy(y, out->data, (size_t)(M * N) * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) { g_err = e.what(); return -1; }
+}
+
+// LayerNorm + affine via norm_affine (mg-tensor.cpp:141-147)
+int mgref_norm_affine(const float* x, int64_t rows, int64_t D, const float* gamma,
+                      const float* beta, float eps, float* y) {
+    try {
+        Context c(16 << 20);
+        Tensor* tx = ext2(c, x, D, rows);
+        int64_t ne[4] = {D, 1, 1, 1};
+        Tensor* tg = c.external(Type::F32, 1, ne, const_cast<float*>(gamma));
+        Tensor* tb = c.external(Type::F32, 1, ne, const_cast<float*>(beta));
+        Tensor* out = norm_affine(c, tx, tg, tb, eps);
+        Graph g; g.build_forward(out); compute(c, g);
+        std::memcpy(y, out->data, (size_t)(rows * D) * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) { g_err = e.what(); return -1; }
+}
+
+// Attention on q/k/v laid out as the transformer's linear outputs [B][S][H*D]: the same
+// reshape({D,H,S,B}) + permute(0,2,1,3) views as mg-transformer.cpp:65-67 feed
+// flash_attention (mg-tensor.cpp:186-198). Output is contiguous {D,S,H,B}.
+int mgref_attention(const float* q, const float* k, const float* v, int64_t D, int64_t S,
+                    int64_t H, int64_t B, float scale, float* o) {
+    try {
+        Context c(64 << 20);
+        int64_t ne[4] = {D * H, S, B, 1};
+        auto view = [&](const float* p) {
+            Tensor* t = c.external(Type::F32, 3, ne, const_cast<float*>(p));
+            return permute(c, reshape(c, t, {D, H, S, B}), 0, 2, 1, 3);
+        };
+        Tensor* out = flash_attention(c, view(q), view(k), view(v), scale);
+        Graph g; g.build_forward(out); compute(c, g);
+        std::memcpy(o, out->data, (size_t)(D * S * H * B) * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) { g_err = e.what(); return -1; }
+}
+
+// Full transformer forward on an F32 GGUF: Model::load + build_transformer + compute
+// (the path of tools/verify-transformer.cpp:40-55). tokens [B][S] -> logits [B][S][vocab].
+int mgref_transformer_forward(const char* gguf_path, const int32_t* tokens, int64_t S,
+                              int64_t B, float* logits, int64_t logits_len) {
+    try {
+        Context wctx(64 << 20);
+        auto model = Model::load(gguf_path, wctx);
+        Context ctx((size_t)1 << 30);
+        Tensor* tok = ctx.tensor2d(Type::I32, S, B);
+        std::memcpy(tok->data, tokens, (size_t)(S * B) * sizeof(int32_t));
+        Tensor* out = build_transformer(ctx, *model, tok);
+        if (out->nelements() != logits_len) { g_err = "logits size mismatch"; return -2; }
+        Graph g; g.build_forward(out); compute(ctx, g);
+        std::memcpy(logits, out->data, (size_t)logits_len * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) { g_err = e.what(); return -1; }
+}
+
+}  // extern "C"
