@@ -1,0 +1,195 @@
+"""edge_maskgit_amd — MI355X (gfx950) backend for the edge_maskgit Q8_0/Q4_K FC hot path.
+
+The product is the native code: ``lib/libmgh.so`` (HIP kernels + the C ABI declared in
+``include/mgh.h``) and ``lib/libmg_hip.so`` (the C++ mg tensor/graph API and HipRuntime).
+This module is a thin ctypes binding used by tests and bench.py. It never falls back to
+a CPU implementation: if the native library is missing or no gfx950 device is present,
+calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(PKG, "lib")
+LIBMGH = os.path.join(LIB_DIR, "libmgh.so")
+
+WTYPE_F32 = 0
+WTYPE_Q8_0 = 8
+WTYPE_Q4_K = 12
+ACT_NONE, ACT_GELU, ACT_SILU = 0, 1, 2
+ALGO_AUTO, ALGO_INT8, ALGO_DEQ_F16 = 0, 1, 2
+
+# every entry point include/mgh.h declares (checked by tests/test_abi.py)
+MGH_SYMBOLS = [
+    "mgh_create", "mgh_destroy", "mgh_last_error", "mgh_device_name", "mgh_version",
+    "mgh_alloc", "mgh_free", "mgh_h2d", "mgh_d2h", "mgh_fill_u32", "mgh_sync",
+    "mgh_timer_start", "mgh_timer_stop",
+    "mgh_quantize_act_q8", "mgh_gemm_q", "mgh_gemm_q_f32in", "mgh_debug_block_dots",
+]
+
+_lib = None
+
+
+class MghError(RuntimeError):
+    pass
+
+
+def build(verbose: bool = False) -> None:
+    from . import build as _b
+    _b.build(verbose=verbose, force=True)
+
+
+def lib():
+    """Load libmgh.so (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIBMGH):
+            raise MghError(f"native library missing: {LIBMGH} — run __graft_entry__.build()")
+        L = ctypes.CDLL(LIBMGH)
+        P, I, SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+        L.mgh_create.argtypes = [I, ctypes.POINTER(P)]
+        L.mgh_destroy.argtypes = [P]
+        L.mgh_destroy.restype = None
+        L.mgh_last_error.argtypes = [P]
+        L.mgh_last_error.restype = ctypes.c_char_p
+        L.mgh_device_name.argtypes = [P]
+        L.mgh_device_name.restype = ctypes.c_char_p
+        L.mgh_alloc.argtypes = [P, SZ, ctypes.POINTER(P)]
+        L.mgh_free.argtypes = [P, P]
+        L.mgh_h2d.argtypes = [P, P, P, SZ]
+        L.mgh_d2h.argtypes = [P, P, P, SZ]
+        L.mgh_fill_u32.argtypes = [P, P, ctypes.c_uint32, SZ]
+        L.mgh_sync.argtypes = [P]
+        L.mgh_timer_start.argtypes = [P]
+        L.mgh_timer_stop.argtypes = [P, ctypes.POINTER(ctypes.c_float)]
+        L.mgh_quantize_act_q8.argtypes = [P, P, I, I, P, P, P]
+        L.mgh_gemm_q.argtypes = [P, I, P, I, I, P, P, P, I, P, I, P, P]
+        L.mgh_gemm_q_f32in.argtypes = [P, I, I, P, I, I, P, I, P, I, P, P]
+        L.mgh_debug_block_dots.argtypes = [P, I, P, I, I, P, I, P]
+        _lib = L
+    return _lib
+
+
+class DeviceBuffer:
+    """Owned device allocation (freed with the context)."""
+
+    def __init__(self, ctx: "Context", nbytes: int):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        p = ctypes.c_void_p()
+        ctx._check(lib().mgh_alloc(ctx.h, self.nbytes, ctypes.byref(p)))
+        self.ptr = p.value
+
+    def free(self):
+        if self.ptr:
+            lib().mgh_free(self.ctx.h, ctypes.c_void_p(self.ptr))
+            self.ptr = None
+
+    @property
+    def p(self):
+        return ctypes.c_void_p(self.ptr)
+
+
+class Context:
+    """One mgh_ctx (device + stream). Not thread-safe, like the reference runtime."""
+
+    def __init__(self, device: int = 0):
+        h = ctypes.c_void_p()
+        rc = lib().mgh_create(device, ctypes.byref(h))
+        if rc != 0:
+            raise MghError(f"mgh_create({device}) failed with {rc} (no gfx950 device?)")
+        self.h = h
+        self._bufs: list[DeviceBuffer] = []
+
+    def close(self):
+        if self.h:
+            for b in self._bufs:
+                b.free()
+            self._bufs.clear()
+            lib().mgh_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _check(self, rc):
+        if rc != 0:
+            raise MghError(f"mgh error {rc}: {lib().mgh_last_error(self.h).decode()}")
+
+    @property
+    def device_name(self) -> str:
+        return lib().mgh_device_name(self.h).decode()
+
+    # ---- memory ----
+    def alloc(self, nbytes: int) -> DeviceBuffer:
+        b = DeviceBuffer(self, nbytes)
+        self._bufs.append(b)
+        return b
+
+    def upload(self, arr: np.ndarray) -> DeviceBuffer:
+        arr = np.ascontiguousarray(arr)
+        b = self.alloc(max(arr.nbytes, 1))
+        self._check(lib().mgh_h2d(self.h, b.p, arr.ctypes.data_as(ctypes.c_void_p), arr.nbytes))
+        return b
+
+    def download(self, buf: DeviceBuffer, shape, dtype) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        self._check(lib().mgh_d2h(self.h, out.ctypes.data_as(ctypes.c_void_p), buf.p, out.nbytes))
+        return out
+
+    def free(self, buf: DeviceBuffer):
+        buf.free()
+        if buf in self._bufs:
+            self._bufs.remove(buf)
+
+    def sync(self):
+        self._check(lib().mgh_sync(self.h))
+
+    def timer_start(self):
+        self._check(lib().mgh_timer_start(self.h))
+
+    def timer_stop(self) -> float:
+        ms = ctypes.c_float()
+        self._check(lib().mgh_timer_stop(self.h, ctypes.byref(ms)))
+        return ms.value
+
+    # ---- kernels (device pointers in, device pointers out; stream-ordered) ----
+    @staticmethod
+    def _ptr(b):
+        if b is None:
+            return None
+        return b.p if isinstance(b, DeviceBuffer) else ctypes.c_void_p(int(b))
+
+    def quantize_act_q8(self, x, M, K, qx, dx, sx=None):
+        P = self._ptr
+        self._check(lib().mgh_quantize_act_q8(self.h, P(x), M, K, P(qx), P(dx), P(sx)))
+
+    def gemm_q(self, wtype, w, N, K, qx, dx, sx, M, bias, act, resid, y):
+        P = self._ptr
+        self._check(lib().mgh_gemm_q(self.h, wtype, P(w), N, K, P(qx), P(dx), P(sx), M,
+                                     P(bias), act, P(resid), P(y)))
+
+    def gemm_q_f32in(self, algo, wtype, w, N, K, x, M, bias, act, resid, y):
+        P = self._ptr
+        self._check(lib().mgh_gemm_q_f32in(self.h, algo, wtype, P(w), N, K, P(x), M,
+                                           P(bias), act, P(resid), P(y)))
+
+    def debug_block_dots(self, wtype, w, N, K, qx, M, out):
+        P = self._ptr
+        self._check(lib().mgh_debug_block_dots(self.h, wtype, P(w), N, K, P(qx), M, P(out)))
+
+
+def gpu_available() -> bool:
+    """True if libmgh.so loads and a gfx950 device can be opened."""
+    try:
+        with Context(0):
+            return True
+    except Exception:
+        return False

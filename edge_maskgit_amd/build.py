@@ -1,0 +1,102 @@
+"""Build the gfx950 libraries in-tree with hipcc (no JIT, no site-packages install).
+
+  libmgh.so      HIP kernels + the C ABI of include/mgh.h
+  libmg_hip.so   C++ host side: the mg tensor/graph API, GGUF loader, transformer graph
+                 builder and HipRuntime (include/mg-tensor.hpp, include/mg-hip.hpp)
+
+Objects go to edge_maskgit_amd/_build/, libraries to edge_maskgit_amd/lib/.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+HOST = os.path.join(PKG, "host")
+OBJ = os.path.join(PKG, "_build")
+LIB = os.path.join(PKG, "lib")
+
+ARCH = "gfx950"
+# Packed fp32 VALU ops are disabled for all device code; see DESIGN.md ("build flags").
+HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             "-Wno-unused-command-line-argument"]
+
+KERNEL_SOURCES = ["k_quant_act.hip", "k_gemm_i8.hip", "mgh_api.cpp"]
+HOST_SOURCES = []
+
+
+def hipcc() -> str:
+    for c in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if c and os.path.exists(c):
+            return c
+    raise RuntimeError("hipcc not found (ROCm install expected at /opt/rocm)")
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    out = "\n".join(l for l in (r.stdout + r.stderr).splitlines()
+                    if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"build failed: {' '.join(cmd)}\n{out}")
+    if out.strip() and verbose:
+        print(out)
+
+
+def _stale(target, deps):
+    if not os.path.exists(target):
+        return True
+    t = os.path.getmtime(target)
+    return any(os.path.getmtime(d) > t for d in deps)
+
+
+def _headers():
+    hs = []
+    for d in (CSRC, HOST, os.path.join(ROOT, "include")):
+        if os.path.isdir(d):
+            hs += [os.path.join(d, f) for f in os.listdir(d) if f.endswith((".h", ".hpp"))]
+    return hs
+
+
+def build(verbose: bool = False, force: bool = True) -> None:
+    """Compile every source (force=True rebuilds everything, as __graft_entry__.build()
+    requires); force=False only rebuilds stale objects."""
+    os.makedirs(OBJ, exist_ok=True)
+    os.makedirs(LIB, exist_ok=True)
+    cc = hipcc()
+    hdrs = _headers()
+    inc = ["-I" + os.path.join(ROOT, "include"), "-I" + CSRC, "-I" + HOST]
+    objs = []
+    for src in KERNEL_SOURCES:
+        s = os.path.join(CSRC, src)
+        o = os.path.join(OBJ, src + ".o")
+        if force or _stale(o, [s] + hdrs):
+            _run([cc, *HIP_FLAGS, *inc, "-c", s, "-o", o], verbose)
+        objs.append(o)
+    libmgh = os.path.join(LIB, "libmgh.so")
+    tmp = libmgh + ".tmp"
+    _run([cc, *HIP_FLAGS, "-shared", "-o", tmp, *objs], verbose)
+    os.replace(tmp, libmgh)
+    if HOST_SOURCES:
+        hobjs = []
+        for src in HOST_SOURCES:
+            s = os.path.join(HOST, src)
+            o = os.path.join(OBJ, src + ".o")
+            if force or _stale(o, [s] + hdrs):
+                _run([cc, *HIP_FLAGS, *inc, "-c", s, "-o", o], verbose)
+            hobjs.append(o)
+        libmg = os.path.join(LIB, "libmg_hip.so")
+        tmp = libmg + ".tmp"
+        _run([cc, *HIP_FLAGS, "-shared", "-o", tmp, *hobjs, "-L" + LIB, "-lmgh",
+              "-Wl,-rpath,$ORIGIN"], verbose)
+        os.replace(tmp, libmg)
+
+
+if __name__ == "__main__":
+    build(verbose="-v" in sys.argv, force="--force" in sys.argv or "-f" in sys.argv)

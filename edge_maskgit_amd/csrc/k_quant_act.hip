@@ -1,0 +1,79 @@
+// k_quant_act.hip — per-32-block int8 activation quantizer (gfx950).
+//
+// Semantics of the reference's k_quantize_q8 (src/mg-opencl/mg-opencl.cpp:424-434):
+//   amax = max|x| over the block; d = amax/127; id = d > 0 ? 1/d : 0;
+//   dx[block] = d (fp32); qx[i] = round(x[i]*id) with round half away from zero.
+// Additionally emits sx[block] = sum of the block's qx (used by the Q4_K min term,
+// mg-opencl.cpp:559-563), so the GEMM does not re-sum the activations.
+//
+// Layout: x [M][K] fp32 row-major, blocks run along K, so the flat block index
+// b = m*(K/32) + t addresses x + 32*b, dx[b], sx[b]. Eight lanes own one block, each lane
+// one float4 (16-byte coalesced loads); the block max and sum are xor-shuffle reductions
+// inside the 8-lane group. HBM-bound: 4 B read and 1.25 B written per element.
+#include "mgh_common.h"
+#include "mgh_kernels.h"
+
+namespace mgh {
+
+__global__ __launch_bounds__(256) void k_quantize_act_q8(const float* __restrict__ x,
+                                                         int8_t* __restrict__ qx,
+                                                         float* __restrict__ dx,
+                                                         int32_t* __restrict__ sx,
+                                                         int64_t nblocks) {
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t blk = gid >> 3;
+    const int sub = (int)(gid & 7);
+    const bool valid = blk < nblocks;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (valid) v = *(const f32x4*)(x + blk * 32 + sub * 4);
+    float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    a = fmaxf(a, __shfl_xor(a, 1));
+    a = fmaxf(a, __shfl_xor(a, 2));
+    a = fmaxf(a, __shfl_xor(a, 4));
+    const float d = a / 127.0f;
+    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+    const int q0 = (int)roundf(v.x * id);
+    const int q1 = (int)roundf(v.y * id);
+    const int q2 = (int)roundf(v.z * id);
+    const int q3 = (int)roundf(v.w * id);
+    int s = q0 + q1 + q2 + q3;
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    if (valid) {
+        const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
+                                ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+        *(uint32_t*)(qx + blk * 32 + sub * 4) = packed;
+        if (sub == 0) {
+            dx[blk] = d;
+            if (sx) sx[blk] = s;
+        }
+    }
+}
+
+hipError_t launch_quantize_act_q8(const float* x, int8_t* qx, float* dx, int32_t* sx,
+                                  int64_t M, int64_t K, hipStream_t s) {
+    const int64_t nblocks = M * (K / 32);
+    const int64_t threads = nblocks * 8;
+    const int64_t grid = (threads + 255) / 256;
+    hipLaunchKernelGGL(k_quantize_act_q8, dim3((unsigned)grid), dim3(256), 0, s, x, qx, dx, sx,
+                       nblocks);
+    return hipGetLastError();
+}
+
+// Graph-capture-safe fill (used instead of hipMemsetAsync).
+__global__ __launch_bounds__(256) void k_fill_u32(uint32_t* __restrict__ p, uint32_t v, size_t n) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * 256;
+    for (; i < n; i += stride) p[i] = v;
+}
+
+hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    size_t grid = (n + 255) / 256;
+    if (grid > 65536) grid = 65536;
+    hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)grid), dim3(256), 0, s, p, v, n);
+    return hipGetLastError();
+}
+
+}  // namespace mgh

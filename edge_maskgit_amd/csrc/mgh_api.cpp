@@ -1,0 +1,243 @@
+// mgh_api.cpp — the C ABI (include/mgh.h): argument validation, contexts, dispatch.
+#include "../../include/mgh.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "mgh_kernels.h"
+
+struct mgh_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    std::string err;
+    std::string name;
+    // grow-on-demand activation scratch for mgh_gemm_q_f32in (qx | dx | sx)
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
+};
+
+namespace {
+
+int fail(mgh_ctx* c, int code, const std::string& msg) {
+    if (c) c->err = msg;
+    return code;
+}
+
+int hip_fail(mgh_ctx* c, hipError_t e, const char* what) {
+    return fail(c, MGH_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define MGH_HIP(ctx, expr, what)                                  \
+    do {                                                          \
+        hipError_t e_ = (expr);                                   \
+        if (e_ != hipSuccess) return hip_fail((ctx), e_, (what)); \
+    } while (0)
+
+int set_dev(mgh_ctx* c) {
+    MGH_HIP(c, hipSetDevice(c->device), "hipSetDevice");
+    return MGH_OK;
+}
+
+int check_quant_shape(mgh_ctx* c, int wtype, int N, int K, int M) {
+    if (wtype != MGH_WTYPE_Q8_0 && wtype != MGH_WTYPE_Q4_K)
+        return fail(c, MGH_ERR_ARG, "wtype must be MGH_WTYPE_Q8_0 (8) or MGH_WTYPE_Q4_K (12)");
+    if (N <= 0 || K <= 0 || M < 0) return fail(c, MGH_ERR_ARG, "shape must have N>0, K>0, M>=0");
+    if (K % 32) return fail(c, MGH_ERR_ARG, "K must be a multiple of 32 (ggml block size)");
+    if (wtype == MGH_WTYPE_Q8_0 && K % 64)
+        return fail(c, MGH_ERR_UNSUPPORTED, "Q8_0 GEMM needs K % 64 == 0 (dword-aligned block pairs)");
+    if (wtype == MGH_WTYPE_Q4_K && K % 256)
+        return fail(c, MGH_ERR_ARG, "Q4_K needs K % 256 == 0 (super-block size)");
+    return MGH_OK;
+}
+
+// Pick the workgroup tile: the largest tile that still gives about one workgroup per CU
+// (256 CUs); small problems fall back to 64x64 tiles.
+mgh::TileCfg pick_tile(int M, int N) {
+    auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+    if (tiles(128, 128) >= 256) return {2, 2};
+    if (tiles(64, 128) >= 256) return {1, 2};
+    return {1, 1};
+}
+
+}  // namespace
+
+extern "C" {
+
+int mgh_version(void) { return 1; }
+
+int mgh_create(int device_ordinal, mgh_ctx** out) {
+    if (!out) return MGH_ERR_ARG;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device_ordinal < 0 || device_ordinal >= n)
+        return MGH_ERR_NO_DEVICE;
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, device_ordinal) != hipSuccess) return MGH_ERR_NO_DEVICE;
+    if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0) return MGH_ERR_NO_DEVICE;
+    mgh_ctx* c = new mgh_ctx();
+    c->device = device_ordinal;
+    c->name = p.name;
+    c->name += " (";
+    c->name += p.gcnArchName;
+    c->name += ")";
+    if (hipSetDevice(device_ordinal) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreate(&c->ev0) != hipSuccess || hipEventCreate(&c->ev1) != hipSuccess) {
+        mgh_destroy(c);
+        return MGH_ERR_HIP;
+    }
+    *out = c;
+    return MGH_OK;
+}
+
+void mgh_destroy(mgh_ctx* c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    if (c->scratch) (void)hipFree(c->scratch);
+    if (c->ev0) (void)hipEventDestroy(c->ev0);
+    if (c->ev1) (void)hipEventDestroy(c->ev1);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+const char* mgh_last_error(const mgh_ctx* c) { return c ? c->err.c_str() : "null context"; }
+const char* mgh_device_name(const mgh_ctx* c) { return c ? c->name.c_str() : ""; }
+
+int mgh_alloc(mgh_ctx* c, size_t bytes, void** out) {
+    if (!c || !out) return fail(c, MGH_ERR_ARG, "mgh_alloc: null argument");
+    if (int r = set_dev(c)) return r;
+    *out = nullptr;
+    if (bytes == 0) bytes = 256;
+    MGH_HIP(c, hipMalloc(out, bytes), "hipMalloc");
+    return MGH_OK;
+}
+
+int mgh_free(mgh_ctx* c, void* p) {
+    if (!c) return MGH_ERR_ARG;
+    if (!p) return MGH_OK;
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    MGH_HIP(c, hipFree(p), "hipFree");
+    return MGH_OK;
+}
+
+int mgh_h2d(mgh_ctx* c, void* d, const void* h, size_t n) {
+    if (!c || (n && (!d || !h))) return fail(c, MGH_ERR_ARG, "mgh_h2d: null argument");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, hipMemcpyAsync(d, h, n, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(H2D)");
+    MGH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return MGH_OK;
+}
+
+int mgh_d2h(mgh_ctx* c, void* h, const void* d, size_t n) {
+    if (!c || (n && (!d || !h))) return fail(c, MGH_ERR_ARG, "mgh_d2h: null argument");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, hipMemcpyAsync(h, d, n, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync(D2H)");
+    MGH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return MGH_OK;
+}
+
+int mgh_fill_u32(mgh_ctx* c, void* d, uint32_t v, size_t n) {
+    if (!c || (n && !d)) return fail(c, MGH_ERR_ARG, "mgh_fill_u32: null argument");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_fill_u32((uint32_t*)d, v, n, c->stream), "k_fill_u32");
+    return MGH_OK;
+}
+
+int mgh_sync(mgh_ctx* c) {
+    if (!c) return MGH_ERR_ARG;
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return MGH_OK;
+}
+
+int mgh_timer_start(mgh_ctx* c) {
+    if (!c) return MGH_ERR_ARG;
+    MGH_HIP(c, hipEventRecord(c->ev0, c->stream), "hipEventRecord");
+    return MGH_OK;
+}
+
+int mgh_timer_stop(mgh_ctx* c, float* ms) {
+    if (!c || !ms) return fail(c, MGH_ERR_ARG, "mgh_timer_stop: null argument");
+    MGH_HIP(c, hipEventRecord(c->ev1, c->stream), "hipEventRecord");
+    MGH_HIP(c, hipEventSynchronize(c->ev1), "hipEventSynchronize");
+    MGH_HIP(c, hipEventElapsedTime(ms, c->ev0, c->ev1), "hipEventElapsedTime");
+    return MGH_OK;
+}
+
+int mgh_quantize_act_q8(mgh_ctx* c, const float* x, int M, int K, int8_t* qx, float* dx, int32_t* sx) {
+    if (!c) return MGH_ERR_ARG;
+    if (M < 0 || K <= 0 || K % 32) return fail(c, MGH_ERR_ARG, "quantize_act_q8: need M>=0, K>0, K%32==0");
+    if (M == 0) return MGH_OK;
+    if (!x || !qx || !dx) return fail(c, MGH_ERR_ARG, "quantize_act_q8: null pointer");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_quantize_act_q8(x, qx, dx, sx, M, K, c->stream), "k_quantize_act_q8");
+    return MGH_OK;
+}
+
+int mgh_gemm_q(mgh_ctx* c, int wtype, const void* w, int N, int K, const int8_t* qx,
+               const float* dx, const int32_t* sx, int M, const float* bias, int act,
+               const float* resid, float* y) {
+    if (!c) return MGH_ERR_ARG;
+    if (int r = check_quant_shape(c, wtype, N, K, M)) return r;
+    if (act < 0 || act > 2) return fail(c, MGH_ERR_ARG, "act must be 0 (none), 1 (gelu) or 2 (silu)");
+    if (M == 0) return MGH_OK;
+    if (!w || !qx || !dx || !y) return fail(c, MGH_ERR_ARG, "gemm_q: null pointer");
+    if (wtype == MGH_WTYPE_Q4_K && !sx) return fail(c, MGH_ERR_ARG, "gemm_q: Q4_K needs block sums sx");
+    if (int r = set_dev(c)) return r;
+    mgh::GemmArgs a{};
+    a.w = (const uint8_t*)w; a.qx = qx; a.dx = dx; a.sx = sx;
+    a.bias = bias; a.resid = resid; a.y = y;
+    a.M = M; a.N = N; a.K = K; a.act = act;
+    MGH_HIP(c, mgh::launch_gemm_q_i8(wtype, a, pick_tile(M, N), false, c->stream), "k_gemm_q_i8");
+    return MGH_OK;
+}
+
+int mgh_gemm_q_f32in(mgh_ctx* c, int algo, int wtype, const void* w, int N, int K, const float* x,
+                     int M, const float* bias, int act, const float* resid, float* y) {
+    if (!c) return MGH_ERR_ARG;
+    if (int r = check_quant_shape(c, wtype, N, K, M)) return r;
+    if (algo != MGH_ALGO_AUTO && algo != MGH_ALGO_INT8 && algo != MGH_ALGO_DEQ_F16)
+        return fail(c, MGH_ERR_ARG, "algo must be MGH_ALGO_AUTO, _INT8 or _DEQ_F16");
+    if (algo == MGH_ALGO_DEQ_F16) return fail(c, MGH_ERR_UNSUPPORTED, "dequant-fp16 GEMM not built yet");
+    if (M == 0) return MGH_OK;
+    if (!x) return fail(c, MGH_ERR_ARG, "gemm_q_f32in: null x");
+    if (int r = set_dev(c)) return r;
+    const size_t nb = (size_t)K / 32;
+    const size_t qx_b = ((size_t)M * K + 255) & ~(size_t)255;
+    const size_t dx_b = ((size_t)M * nb * 4 + 255) & ~(size_t)255;
+    const size_t need = qx_b + 2 * dx_b;
+    if (c->scratch_bytes < need) {
+        MGH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        if (c->scratch) MGH_HIP(c, hipFree(c->scratch), "hipFree(scratch)");
+        c->scratch = nullptr;
+        c->scratch_bytes = 0;
+        MGH_HIP(c, hipMalloc(&c->scratch, need), "hipMalloc(scratch)");
+        c->scratch_bytes = need;
+    }
+    int8_t* qx = (int8_t*)c->scratch;
+    float* dx = (float*)((char*)c->scratch + qx_b);
+    int32_t* sx = (int32_t*)((char*)c->scratch + qx_b + dx_b);
+    if (int r = mgh_quantize_act_q8(c, x, M, K, qx, dx, sx)) return r;
+    return mgh_gemm_q(c, wtype, w, N, K, qx, dx, sx, M, bias, act, resid, y);
+}
+
+int mgh_debug_block_dots(mgh_ctx* c, int wtype, const void* w, int N, int K, const int8_t* qx,
+                         int M, int32_t* out) {
+    if (!c) return MGH_ERR_ARG;
+    if (int r = check_quant_shape(c, wtype, N, K, M)) return r;
+    if (M == 0) return MGH_OK;
+    if (!w || !qx || !out) return fail(c, MGH_ERR_ARG, "debug_block_dots: null pointer");
+    if (int r = set_dev(c)) return r;
+    mgh::GemmArgs a{};
+    a.w = (const uint8_t*)w; a.qx = qx; a.dots = out;
+    a.M = M; a.N = N; a.K = K;
+    MGH_HIP(c, mgh::launch_gemm_q_i8(wtype, a, pick_tile(M, N), true, c->stream), "k_gemm_q_i8(debug)");
+    return MGH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,106 @@
+/* mgh.h — C ABI of the MI355X (gfx950) kernel layer for the edge_maskgit FC hot path.
+ *
+ * This is the boundary the C++ backend (HipRuntime, include/mg-hip.hpp) and any FFI
+ * (ctypes, cgo, ...) bind. It replaces the OpenCL kernel dispatches inside
+ * OpenCLRuntime::compute (reference src/mg-opencl/mg-opencl.cpp:1354-1656).
+ *
+ * Conventions
+ *  - Status: every call returns 0 (MGH_OK) or a negative MGH_ERR_*; no exception or
+ *    abort crosses the ABI. mgh_last_error() gives the message of the last failure.
+ *  - Memory: pointers named d_* are device pointers the caller owns (mgh_alloc/mgh_free
+ *    or any hipMalloc'd memory); h_* are host pointers.
+ *  - Ordering: compute calls are enqueued on the context's stream and return without
+ *    waiting (stream-ordered, like the reference's in-order cl queue). mgh_sync waits.
+ *  - Threading: one context per host thread; a context is not thread-safe (the reference
+ *    OpenCLRuntime is single-threaded too, mg-opencl.cpp:1108-1212).
+ *  - Shapes follow the reference (include/mg-tensor.hpp:3-13): a weight has N rows of K
+ *    values (GGUF ne={K,N}) stored as raw ggml blocks, activations are [M][K] row-major,
+ *    outputs are [M][N] row-major.
+ */
+#ifndef MGH_H
+#define MGH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mgh_ctx mgh_ctx;
+
+enum {
+    MGH_OK = 0,
+    MGH_ERR_ARG = -1,          /* invalid argument (null pointer, bad shape, bad enum) */
+    MGH_ERR_UNSUPPORTED = -2,  /* valid but not implemented (e.g. K not a multiple of 64) */
+    MGH_ERR_HIP = -3,          /* HIP runtime error (message has the HIP error string) */
+    MGH_ERR_NO_DEVICE = -4     /* no gfx950 device at that ordinal */
+};
+
+/* weight types: the GGUF tensor type codes (reference src/mg-model.cpp:22) */
+enum { MGH_WTYPE_F32 = 0, MGH_WTYPE_Q8_0 = 8, MGH_WTYPE_Q4_K = 12 };
+
+/* fused epilogue activations (reference mg-opencl.cpp:36-40) */
+enum { MGH_ACT_NONE = 0, MGH_ACT_GELU = 1, MGH_ACT_SILU = 2 };
+
+/* GEMM algorithm for quantized weights. INT8 = per-32 int8 activations on int8 MFMA
+ * (the reference's int8-dot path, mg-opencl.cpp:1381-1398); DEQ_F16 = dequantize weights
+ * to fp16 on load and run fp16 MFMA on fp16-rounded activations (the reference's
+ * dequant-fused 2D path, mg-opencl.cpp:1400-1423). AUTO = INT8. */
+enum { MGH_ALGO_AUTO = 0, MGH_ALGO_INT8 = 1, MGH_ALGO_DEQ_F16 = 2 };
+
+/* ---- context: replaces OpenCLRuntime::OpenCLRuntime / ~OpenCLRuntime / device_name
+ *      (reference include/mg-opencl.hpp:25-31, src/mg-opencl/mg-opencl.cpp:1214-1280) ---- */
+int         mgh_create(int device_ordinal, mgh_ctx** out);
+void        mgh_destroy(mgh_ctx* ctx);
+const char* mgh_last_error(const mgh_ctx* ctx);      /* never NULL; "" after success */
+const char* mgh_device_name(const mgh_ctx* ctx);
+int         mgh_version(void);
+
+/* ---- device memory: replaces the clCreateBuffer / clEnqueueWriteBuffer /
+ *      clEnqueueReadBuffer traffic of OpenCLRuntime::Impl::buf() and the final readback
+ *      (mg-opencl.cpp:1172-1206, 1622-1626) ---- */
+int mgh_alloc(mgh_ctx* ctx, size_t bytes, void** d_out);
+int mgh_free(mgh_ctx* ctx, void* d_ptr);
+int mgh_h2d(mgh_ctx* ctx, void* d_dst, const void* h_src, size_t bytes);   /* synchronous */
+int mgh_d2h(mgh_ctx* ctx, void* h_dst, const void* d_src, size_t bytes);   /* synchronous */
+int mgh_fill_u32(mgh_ctx* ctx, void* d_dst, uint32_t value, size_t n_words); /* kernel fill */
+int mgh_sync(mgh_ctx* ctx);                                                  /* clFinish */
+
+/* ---- timing on the context stream (HIP events), for benchmarks ---- */
+int mgh_timer_start(mgh_ctx* ctx);
+int mgh_timer_stop(mgh_ctx* ctx, float* ms_out);   /* waits for the stop event */
+
+/* ---- activation quantizer: replaces k_quantize_q8 and its dispatch
+ *      (mg-opencl.cpp:424-434, 1381-1389). x [M][K] -> qx [M][K] int8,
+ *      dx [M][K/32] fp32 scales, sx [M][K/32] int32 block sums (nullable). K % 32 == 0. */
+int mgh_quantize_act_q8(mgh_ctx* ctx, const float* d_x, int M, int K,
+                        int8_t* d_qx, float* d_dx, int32_t* d_sx);
+
+/* ---- quantized FC GEMM on pre-quantized activations: replaces k_mul_mat_q8_i8 /
+ *      k_mul_mat_q4k_i8 and their dispatch (mg-opencl.cpp:440-590, 1390-1398).
+ *      y[M][N] = act(w . x + bias) + resid; bias [N] and resid [M][N] nullable.
+ *      Q8_0 needs K % 64 == 0, Q4_K needs K % 256 == 0 and d_sx. ---- */
+int mgh_gemm_q(mgh_ctx* ctx, int wtype, const void* d_w, int N, int K,
+               const int8_t* d_qx, const float* d_dx, const int32_t* d_sx, int M,
+               const float* d_bias, int act, const float* d_resid, float* d_y);
+
+/* ---- quantized FC GEMM on fp32 activations: replaces the whole MulMat(q) node
+ *      dispatch (mg-opencl.cpp:1367-1428): quantize + GEMM for ALGO_INT8 (activation
+ *      scratch owned by the context and grown on demand, like the reference's
+ *      qx_buf/dx_buf, mg-opencl.cpp:1125-1134), or one dequant-fp16 GEMM for
+ *      ALGO_DEQ_F16. Output semantics as mgh_gemm_q. ---- */
+int mgh_gemm_q_f32in(mgh_ctx* ctx, int algo, int wtype, const void* d_w, int N, int K,
+                     const float* d_x, int M, const float* d_bias, int act,
+                     const float* d_resid, float* d_y);
+
+/* ---- debug: the int32 per-block dot products exactly as the production GEMM's MFMA
+ *      computes them, out[m][n][t] (t = K/32 blocks). The reference has no counterpart;
+ *      it exposes the quantity mg-opencl.cpp:472-478 / :571-576 accumulates. ---- */
+int mgh_debug_block_dots(mgh_ctx* ctx, int wtype, const void* d_w, int N, int K,
+                         const int8_t* d_qx, int M, int32_t* d_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MGH_H */

@@ -1,0 +1,50 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point the public
+headers declare, and rejects bad arguments without touching a device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import edge_maskgit_amd as ema
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared(header):
+    text = open(os.path.join(ROOT, "include", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mgh_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ema.lib()
+    declared = _declared("mgh.h")
+    assert declared, "no declarations parsed"
+    missing = [s for s in declared if not hasattr(lib, s)]
+    assert not missing, missing
+    assert sorted(ema.MGH_SYMBOLS) == declared
+
+
+def test_version():
+    assert ema.lib().mgh_version() == 1
+
+
+def test_null_context_errors_without_device():
+    L = ema.lib()
+    assert L.mgh_last_error(None) == b"null context"
+    assert L.mgh_gemm_q(None, 8, None, 1, 64, None, None, None, 1, None, 0, None, None) == -1
+    assert L.mgh_quantize_act_q8(None, None, 1, 32, None, None, None) == -1
+    assert L.mgh_sync(None) == -1
+    L.mgh_destroy(None)      # no-op
+
+
+def test_package_has_no_cpu_fallback():
+    # The shipped package must not import the oracle or any CPU compute path.
+    src_dir = os.path.join(ROOT, "edge_maskgit_amd")
+    for dirpath, _, files in os.walk(src_dir):
+        for f in files:
+            if f.endswith((".py", ".cpp", ".hip", ".h", ".hpp")):
+                txt = open(os.path.join(dirpath, f)).read()
+                assert "import oracle" not in txt and "from oracle" not in txt, f
+                assert "mg_oracle" not in txt, f
