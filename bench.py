@@ -1,0 +1,294 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X Q8_0 / Q4_K FC hot path (one JSON line on stdout).
+
+Workload (the metric's configuration): one MaskGIT transformer
+layer's four Q8_0 FC GEMMs at M = 1025 tokens (32x32 grid + class token), fp32 activations:
+    QKV   768 -> 2304  (+bias)            (q/k/v stacked: Q8_0 blocks are row-local)
+    out   768 -> 768   (+bias +residual)
+    up    768 -> 3072  (+bias, GELU)
+    down 3072 -> 768   (+bias +residual)
+A step runs each FC as the int8-dot path does it: per-32 activation quantization
+(k_quantize_act_q8) then the int8-MFMA GEMM (k_gemm_q_i8), all inputs already resident in
+HBM. Buffers rotate over >= --rotate-gb of distinct sets so the 256 MB MALL and the L2s do
+not serve the timed reads. Synthetic data: x ~ N(0,1), W ~ N(0,0.02) quantized to Q8_0,
+biases ~ N(0,0.01), residuals ~ N(0,1), seeded.
+
+value = 2*M*K*N summed over the four GEMMs / step time, in TOPS (int8 ops).
+roofline = the dominant kernel k_gemm_q_i8, HBM-bound: algorithmic bytes of its launches
+(Q8_0 weights once + int8 activations + fp32 block scales + fp32 output + bias + residual)
+divided by its average launch duration, timed with HIP events on the stream it runs on.
+cpu_baseline = the reference's own CPU executor (mg-cpu k_mul_mat, single thread, built
+from the reference sources into oracle/_ref) on the dequantized weights, timed on this
+host over the same four GEMMs; if that library is absent, the C oracle's int8 path.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import edge_maskgit_amd as ema  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, published
+INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA, published
+
+LAYER = [  # name, N, K, act, residual
+    ("qkv", 2304, 768, ema.ACT_NONE, False),
+    ("out", 768, 768, ema.ACT_NONE, True),
+    ("up", 3072, 768, ema.ACT_GELU, False),
+    ("down", 768, 3072, ema.ACT_NONE, True),
+]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def row_bytes(wtype, K):
+    return (K // 32) * 34 if wtype == ema.WTYPE_Q8_0 else (K // 256) * 144
+
+
+class LayerSet:
+    """One set of device buffers for the four FC GEMMs of a layer."""
+
+    def __init__(self, ctx, host, M, wtype):
+        self.ctx = ctx
+        self.M = M
+        self.wtype = wtype
+        self.g = []
+        for (name, N, K, act, res), h in zip(LAYER, host):
+            nb = K // 32
+            d = dict(name=name, N=N, K=K, act=act,
+                     w=ctx.upload(h["wq"]), x=ctx.upload(h["x"]), b=ctx.upload(h["bias"]),
+                     r=ctx.upload(h["resid"]) if res else None, y=ctx.alloc(M * N * 4),
+                     qx=ctx.alloc(M * K), dx=ctx.alloc(M * nb * 4), sx=ctx.alloc(M * nb * 4))
+            self.g.append(d)
+
+    def step(self):
+        c = self.ctx
+        for d in self.g:
+            c.quantize_act_q8(d["x"], self.M, d["K"], d["qx"], d["dx"], d["sx"])
+            c.gemm_q(self.wtype, d["w"], d["N"], d["K"], d["qx"], d["dx"], d["sx"], self.M,
+                     d["b"], d["act"], d["r"], d["y"])
+
+    def gemms_only(self):
+        c = self.ctx
+        for d in self.g:
+            c.gemm_q(self.wtype, d["w"], d["N"], d["K"], d["qx"], d["dx"], d["sx"], self.M,
+                     d["b"], d["act"], d["r"], d["y"])
+
+
+def synth_q8_0(w):
+    """Synthetic-data encoder: ggml Q8_0 blocks (fp16 d = amax/127, int8 q = rint(w/d))."""
+    N, K = w.shape
+    b = w.reshape(N, K // 32, 32)
+    d = (np.abs(b).max(-1) / np.float32(127)).astype(np.float32)
+    q = np.clip(np.rint(b / np.where(d > 0, d, 1)[..., None]), -127, 127).astype(np.int8)
+    out = np.empty((N, K // 32, 34), np.uint8)
+    out[..., 0:2] = d.astype(np.float16)[..., None].view(np.uint8)
+    out[..., 2:] = q.view(np.uint8)
+    return out.reshape(N, -1)
+
+
+def synth_q4_k(w):
+    """Synthetic-data encoder: ggml Q4_K super-blocks (min/max sub-block scales)."""
+    N, K = w.shape
+    x = w.reshape(-1, 8, 32)
+    mn = np.minimum(x.min(-1), 0)
+    sc = (x.max(-1) - mn) / 15.0
+    d = sc.max(-1) / 63.0
+    dm = (-mn).max(-1) / 63.0
+    scq = np.clip(np.rint(sc / np.where(d > 0, d, 1)[:, None]), 0, 63).astype(np.uint8)
+    mq = np.clip(np.rint(-mn / np.where(dm > 0, dm, 1)[:, None]), 0, 63).astype(np.uint8)
+    step = np.where(d[:, None] * scq > 0, d[:, None] * scq, 1.0)
+    q = np.clip(np.rint((x + (dm[:, None] * mq)[..., None]) / step[..., None]), 0, 15).astype(np.uint8)
+    out = np.zeros((x.shape[0], 144), np.uint8)
+    out[:, 0:2] = d.astype(np.float16)[:, None].view(np.uint8)
+    out[:, 2:4] = dm.astype(np.float16)[:, None].view(np.uint8)
+    out[:, 4:8] = (scq[:, :4] & 63) | ((scq[:, 4:] >> 4) << 6)
+    out[:, 8:12] = (mq[:, :4] & 63) | ((mq[:, 4:] >> 4) << 6)
+    out[:, 12:16] = (scq[:, 4:] & 0xF) | ((mq[:, 4:] & 0xF) << 4)
+    for g in range(4):
+        out[:, 16 + 32 * g:48 + 32 * g] = q[:, 2 * g] | (q[:, 2 * g + 1] << 4)
+    return out.reshape(N, -1)
+
+
+def host_layer(M, wtype, seed=0):
+    rng = np.random.default_rng(seed)
+    out = []
+    enc = synth_q8_0 if wtype == ema.WTYPE_Q8_0 else synth_q4_k
+    for name, N, K, act, res in LAYER:
+        w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        out.append(dict(w=w, wq=enc(w),
+                        x=rng.standard_normal((M, K)).astype(np.float32),
+                        bias=(rng.standard_normal(N) * 0.01).astype(np.float32),
+                        resid=rng.standard_normal((M, N)).astype(np.float32) if res else None))
+    return out
+
+
+def layer_ops(M):
+    return sum(2.0 * M * N * K for _, N, K, _, _ in LAYER)
+
+
+def gemm_alg_bytes(M, wtype):
+    """Algorithmic HBM bytes of the four k_gemm_q_i8 launches of one step."""
+    tot = 0
+    for _, N, K, act, res in LAYER:
+        nb = K // 32
+        tot += N * row_bytes(wtype, K) + M * K + M * nb * 4 + M * N * 4 + N * 4
+        if wtype == ema.WTYPE_Q4_K:
+            tot += M * nb * 4
+        if res:
+            tot += M * N * 4
+    return tot
+
+
+def step_alg_bytes(M, wtype):
+    """Algorithmic bytes of the whole FC op: weights once, fp32 x once, fp32 y once, bias,
+    residual once."""
+    tot = 0
+    for _, N, K, act, res in LAYER:
+        tot += N * row_bytes(wtype, K) + M * K * 4 + M * N * 4 + N * 4 + (M * N * 4 if res else 0)
+    return tot
+
+
+def measure(ctx, M, wtype, steps, warmup, rotate_gb):
+    host = host_layer(M, wtype)
+    set_bytes = sum(h["wq"].nbytes + h["x"].nbytes + h["bias"].nbytes + M * len(h["bias"]) * 4 * 2
+                    + (h["resid"].nbytes if h["resid"] is not None else 0) + h["x"].nbytes // 2
+                    for h in host)
+    nsets = max(2, int(np.ceil(rotate_gb * 1e9 / set_bytes)))
+    log(f"[bench] M={M} wtype={wtype}: {nsets} buffer sets x {set_bytes/1e6:.1f} MB")
+    sets = [LayerSet(ctx, host, M, wtype) for _ in range(nsets)]
+    for i in range(warmup):
+        sets[i % nsets].step()
+    ctx.sync()
+    ctx.timer_start()
+    for i in range(steps):
+        sets[i % nsets].step()
+    ms_step = ctx.timer_stop() / steps
+    # dominant kernel alone: the four GEMM launches per step, same rotation
+    for s in sets:
+        s.step()
+    ctx.sync()
+    ctx.timer_start()
+    for i in range(steps):
+        sets[i % nsets].gemms_only()
+    ms_gemms = ctx.timer_stop() / steps
+    for s in sets:
+        for d in s.g:
+            for k in ("w", "x", "b", "r", "y", "qx", "dx", "sx"):
+                if d[k] is not None:
+                    ctx.free(d[k])
+    return ms_step, ms_gemms, host
+
+
+def cpu_baseline(host, M, wtype, budget_s=15.0):
+    """The reference CPU executor (libmgref) on dequantized weights, single thread, over the
+    same four GEMMs; rows are processed in chunks until the budget is spent."""
+    import oracle
+    from oracle import ref
+    if ref.available():
+        ops = 0.0
+        t0 = time.perf_counter()
+        rows_done = 0
+        chunk = 64
+        wdeq = [oracle.dequant(wtype, h["wq"], h["wq"].shape[0], h["x"].shape[1]) for h in host]
+        while rows_done < M and time.perf_counter() - t0 < budget_s:
+            r0, r1 = rows_done, min(M, rows_done + chunk)
+            for (name, N, K, act, res), h, w in zip(LAYER, host, wdeq):
+                ref.mul_mat(w, h["x"][r0:r1], bias=h["bias"], act=act,
+                            resid=None if h["resid"] is None else h["resid"][r0:r1])
+                ops += 2.0 * (r1 - r0) * N * K
+            rows_done = r1
+        dt = time.perf_counter() - t0
+        return {"value": round(ops / dt / 1e12, 6), "unit": "TOPS", "cores": 1, "kind": "reference",
+                "sample": f"reference mg-cpu k_mul_mat (F32, dequantized Q8_0 weights), the same four "
+                          f"GEMMs on rows 0..{rows_done - 1} of M={M} ({ops/1e9:.2f} Gop in {dt:.1f} s)"}
+    nth = os.cpu_count() or 1
+    ops = 0.0
+    t0 = time.perf_counter()
+    for (name, N, K, act, res), h in zip(LAYER, host):
+        qx, dx, _ = oracle.quantize_act_q8(h["x"][:256])
+        oracle.gemm_q_i8(wtype, h["wq"], N, K, qx, dx, bias=h["bias"], act=act)
+        ops += 2.0 * 256 * N * K
+    dt = time.perf_counter() - t0
+    return {"value": round(ops / dt / 1e12, 6), "unit": "TOPS", "cores": nth, "kind": "port",
+            "sample": f"C oracle int8 path (OpenMP), four GEMMs on 256 of {M} rows"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--rotate-gb", type=float, default=3.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--extra", action="store_true",
+                    help="also measure Q8_0 M=4097 and Q4_K M=1025/4097 layers")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
+              "the path shards by data parallelism over images with no per-layer exchange, "
+              "but multi-GPU runs are not part of this build.", file=sys.stderr)
+        sys.exit(2)
+
+    ctx = ema.Context(0)
+    log(f"[bench] device: {ctx.device_name}")
+    M, wtype = 1025, ema.WTYPE_Q8_0
+    ms_step, ms_gemms, host = measure(ctx, M, wtype, a.steps, a.warmup, a.rotate_gb)
+    ops = layer_ops(M)
+    value = ops / (ms_step * 1e-3) / 1e12
+    gb = gemm_alg_bytes(M, wtype)
+    achieved = gb / (ms_gemms * 1e-3) / 1e9
+    extra = {"gemm_only_ms_per_step": round(ms_gemms, 5),
+             "gemm_tops": round(ops / (ms_gemms * 1e-3) / 1e12, 2),
+             "step_alg_bytes": step_alg_bytes(M, wtype),
+             "step_hbm_roofline_us": round(step_alg_bytes(M, wtype) / (HBM_PEAK_GBS * 1e9) * 1e6, 2),
+             "step_frac_of_hbm_roofline": round(step_alg_bytes(M, wtype) / (HBM_PEAK_GBS * 1e9)
+                                                / (ms_step * 1e-3), 4)}
+    if a.extra:
+        for (mm, wt) in ((4097, ema.WTYPE_Q8_0), (1025, ema.WTYPE_Q4_K), (4097, ema.WTYPE_Q4_K)):
+            s, g, _ = measure(ctx, mm, wt, max(10, a.steps // 2), a.warmup, a.rotate_gb)
+            key = f"{'q8_0' if wt == ema.WTYPE_Q8_0 else 'q4_k'}_m{mm}"
+            extra[key] = {"ms_per_step": round(s, 5), "tops": round(layer_ops(mm) / (s * 1e-3) / 1e12, 2),
+                          "gemm_tops": round(layer_ops(mm) / (g * 1e-3) / 1e12, 2),
+                          "frac_of_hbm_roofline": round(step_alg_bytes(mm, wt) / (HBM_PEAK_GBS * 1e9)
+                                                        / (s * 1e-3), 4)}
+    cpu = None if a.no_cpu else cpu_baseline(host, M, wtype)
+    line = {
+        "metric": "Q8_0/Q4_K GEMM TOPS + % roofline at M=1025/4097; transformer fwd ms",
+        "value": round(value, 3),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "cfg2: one MaskGIT layer's four Q8_0 FC GEMMs (QKV 768->2304, "
+                               "out 768->768 +resid, up 768->3072 +GELU, down 3072->768 +resid), "
+                               "M=1025, fp32 activations, int8-dot path (quantize + GEMM)",
+                   "M": M, "weights": "Q8_0", "rotate_gb": a.rotate_gb},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_gemm_q_i8", "bytes_per_step": gb},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    ctx.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

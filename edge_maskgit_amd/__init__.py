@@ -38,9 +38,10 @@ class MghError(RuntimeError):
     pass
 
 
-def build(verbose: bool = False) -> None:
-    from . import build as _b
-    _b.build(verbose=verbose, force=True)
+def build_native(verbose: bool = False) -> None:
+    """Compile the native libraries in-tree (see edge_maskgit_amd/build.py)."""
+    import importlib
+    importlib.import_module(__name__ + ".build").build(verbose=verbose, force=True)
 
 
 def lib():

@@ -27,6 +27,9 @@ HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC",
              "-Wno-unused-command-line-argument"]
 
 KERNEL_SOURCES = ["k_quant_act.hip", "k_gemm_i8.hip", "mgh_api.cpp"]
+# Per-source extra flags. The int8 GEMM keeps MFMA results in VGPRs so the per-block
+# scale FMAs read them without v_accvgpr_read copies.
+EXTRA_FLAGS = {"k_gemm_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HOST_SOURCES = []
 
 
@@ -77,7 +80,7 @@ def build(verbose: bool = False, force: bool = True) -> None:
         s = os.path.join(CSRC, src)
         o = os.path.join(OBJ, src + ".o")
         if force or _stale(o, [s] + hdrs):
-            _run([cc, *HIP_FLAGS, *inc, "-c", s, "-o", o], verbose)
+            _run([cc, *HIP_FLAGS, *EXTRA_FLAGS.get(src, []), *inc, "-c", s, "-o", o], verbose)
         objs.append(o)
     libmgh = os.path.join(LIB, "libmgh.so")
     tmp = libmgh + ".tmp"

@@ -54,12 +54,13 @@ int check_quant_shape(mgh_ctx* c, int wtype, int N, int K, int M) {
     return MGH_OK;
 }
 
-// Pick the workgroup tile: the largest tile that still gives about one workgroup per CU
-// (256 CUs); small problems fall back to 64x64 tiles.
+// Pick the workgroup tile: the larger 128x64 / 64x128 tiles when they still yield >= 2
+// workgroups per CU (256 CUs); otherwise 64x64, which maximizes the number of busy SIMDs.
+// (128x128 tiles exceed the register file with the scale outer products in flight.)
 mgh::TileCfg pick_tile(int M, int N) {
     auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-    if (tiles(128, 128) >= 256) return {2, 2};
-    if (tiles(64, 128) >= 256) return {1, 2};
+    if (tiles(128, 64) >= 512) return {2, 1};
+    if (tiles(64, 128) >= 512) return {1, 2};
     return {1, 1};
 }
 

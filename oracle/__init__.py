@@ -40,9 +40,9 @@ _lib = None
 def build() -> None:
     """Compile the C restatement (and, where the reference tree exists, libmgref)."""
     import subprocess
-    subprocess.check_call(["make", "-s", "-C", _HERE, "all"])
+    subprocess.check_call(["make", "-s", "-B", "-C", _HERE, "all"])
     if os.path.isdir("/root/reference/src"):
-        subprocess.check_call(["make", "-s", "-C", _HERE, "ref"])
+        subprocess.check_call(["make", "-s", "-B", "-C", _HERE, "ref"])
 
 
 def lib():
