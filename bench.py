@@ -8,14 +8,16 @@ layer's four Q8_0 FC GEMMs at M = 1025 tokens (32x32 grid + class token), fp32 a
     up    768 -> 3072  (+bias, GELU)
     down 3072 -> 768   (+bias +residual)
 A step runs each FC as the int8-dot path does it: per-32 activation quantization
-(k_quantize_act_q8) then the int8-MFMA GEMM (k_gemm_q_i8), all inputs already resident in
-HBM. Buffers rotate over >= --rotate-gb of distinct sets so the 256 MB MALL and the L2s do
+(k_quantize_act_q8, codes written as fp16) then the GEMM (k_gemm_q_f16x: block dots on fp16
+MFMA, exact), i.e. exactly what mgh_gemm_q_f32in runs, all inputs already resident in HBM. Each buffer set's step is captured once as a HIP graph and replayed (--no-graphs
+enqueues the kernels one by one instead). Buffers rotate over >= --rotate-gb of distinct sets so the 256 MB MALL and the L2s do
 not serve the timed reads. Synthetic data: x ~ N(0,1), W ~ N(0,0.02) quantized to Q8_0,
 biases ~ N(0,0.01), residuals ~ N(0,1), seeded.
 
 value = 2*M*K*N summed over the four GEMMs / step time, in TOPS (int8 ops).
-roofline = the dominant kernel k_gemm_q_i8, HBM-bound: algorithmic bytes of its launches
-(Q8_0 weights once + int8 activations + fp32 block scales + fp32 output + bias + residual)
+roofline = the dominant kernel k_gemm_q_f16x, HBM-bound: algorithmic bytes of its launches
+(quantized weights once + fp16 activation codes + fp32 block scales (+ block sums for Q4_K)
++ fp32 output + bias + residual)
 divided by its average launch duration, timed with HIP events on the stream it runs on.
 cpu_baseline = the reference's own CPU executor (mg-cpu k_mul_mat, single thread, built
 from the reference sources into oracle/_ref) on the dequantized weights, timed on this
@@ -68,21 +70,21 @@ class LayerSet:
             d = dict(name=name, N=N, K=K, act=act,
                      w=ctx.upload(h["wq"]), x=ctx.upload(h["x"]), b=ctx.upload(h["bias"]),
                      r=ctx.upload(h["resid"]) if res else None, y=ctx.alloc(M * N * 4),
-                     qx=ctx.alloc(M * K), dx=ctx.alloc(M * nb * 4), sx=ctx.alloc(M * nb * 4))
+                     qx=ctx.alloc(M * K * 2), dx=ctx.alloc(M * nb * 4), sx=ctx.alloc(M * nb * 4))
             self.g.append(d)
 
     def step(self):
         c = self.ctx
         for d in self.g:
-            c.quantize_act_q8(d["x"], self.M, d["K"], d["qx"], d["dx"], d["sx"])
-            c.gemm_q(self.wtype, d["w"], d["N"], d["K"], d["qx"], d["dx"], d["sx"], self.M,
-                     d["b"], d["act"], d["r"], d["y"])
+            c.quantize_act_q8_codes16(d["x"], self.M, d["K"], d["qx"], d["dx"], d["sx"])
+            c.gemm_q_codes16(self.wtype, d["w"], d["N"], d["K"], d["qx"], d["dx"], d["sx"], self.M,
+                             d["b"], d["act"], d["r"], d["y"])
 
     def gemms_only(self):
         c = self.ctx
         for d in self.g:
-            c.gemm_q(self.wtype, d["w"], d["N"], d["K"], d["qx"], d["dx"], d["sx"], self.M,
-                     d["b"], d["act"], d["r"], d["y"])
+            c.gemm_q_codes16(self.wtype, d["w"], d["N"], d["K"], d["qx"], d["dx"], d["sx"], self.M,
+                             d["b"], d["act"], d["r"], d["y"])
 
 
 def synth_q8_0(w):
@@ -142,7 +144,7 @@ def gemm_alg_bytes(M, wtype):
     tot = 0
     for _, N, K, act, res in LAYER:
         nb = K // 32
-        tot += N * row_bytes(wtype, K) + M * K + M * nb * 4 + M * N * 4 + N * 4
+        tot += N * row_bytes(wtype, K) + M * K * 2 + M * nb * 4 + M * N * 4 + N * 4
         if wtype == ema.WTYPE_Q4_K:
             tot += M * nb * 4
         if res:
@@ -159,7 +161,16 @@ def step_alg_bytes(M, wtype):
     return tot
 
 
-def measure(ctx, M, wtype, steps, warmup, rotate_gb):
+def _capture(ctx, fn):
+    ctx.graph_begin()
+    try:
+        fn()
+    finally:
+        g = ctx.graph_end()
+    return g
+
+
+def measure(ctx, M, wtype, steps, warmup, rotate_gb, use_graphs=True):
     host = host_layer(M, wtype)
     set_bytes = sum(h["wq"].nbytes + h["x"].nbytes + h["bias"].nbytes + M * len(h["bias"]) * 4 * 2
                     + (h["resid"].nbytes if h["resid"] is not None else 0) + h["x"].nbytes // 2
@@ -167,21 +178,35 @@ def measure(ctx, M, wtype, steps, warmup, rotate_gb):
     nsets = max(2, int(np.ceil(rotate_gb * 1e9 / set_bytes)))
     log(f"[bench] M={M} wtype={wtype}: {nsets} buffer sets x {set_bytes/1e6:.1f} MB")
     sets = [LayerSet(ctx, host, M, wtype) for _ in range(nsets)]
-    for i in range(warmup):
-        sets[i % nsets].step()
-    ctx.sync()
-    ctx.timer_start()
-    for i in range(steps):
-        sets[i % nsets].step()
-    ms_step = ctx.timer_stop() / steps
-    # dominant kernel alone: the four GEMM launches per step, same rotation
-    for s in sets:
+    for s in sets:                      # first run outside any graph
         s.step()
     ctx.sync()
+    if use_graphs:                      # one graph per buffer set: the step, and the GEMMs alone
+        g_step = [_capture(ctx, s.step) for s in sets]
+        g_gemm = [_capture(ctx, s.gemms_only) for s in sets]
+        run_step = [g.launch for g in g_step]
+        run_gemm = [g.launch for g in g_gemm]
+    else:
+        run_step = [s.step for s in sets]
+        run_gemm = [s.gemms_only for s in sets]
+    for i in range(warmup):
+        run_step[i % nsets]()
+    ctx.sync()
     ctx.timer_start()
     for i in range(steps):
-        sets[i % nsets].gemms_only()
+        run_step[i % nsets]()
+    ms_step = ctx.timer_stop() / steps
+    # dominant kernel alone: the four GEMM launches per step, same rotation
+    for i in range(min(warmup, nsets)):
+        run_gemm[i]()
+    ctx.sync()
+    ctx.timer_start()
+    for i in range(steps):
+        run_gemm[i % nsets]()
     ms_gemms = ctx.timer_stop() / steps
+    if use_graphs:
+        for g in g_step + g_gemm:
+            g.destroy()
     for s in sets:
         for d in s.g:
             for k in ("w", "x", "b", "r", "y", "qx", "dx", "sx"):
@@ -231,6 +256,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--rotate-gb", type=float, default=3.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="enqueue kernels one by one instead of replaying a captured HIP graph")
     ap.add_argument("--extra", action="store_true",
                     help="also measure Q8_0 M=4097 and Q4_K M=1025/4097 layers")
     a = ap.parse_args()
@@ -243,7 +270,8 @@ def main():
     ctx = ema.Context(0)
     log(f"[bench] device: {ctx.device_name}")
     M, wtype = 1025, ema.WTYPE_Q8_0
-    ms_step, ms_gemms, host = measure(ctx, M, wtype, a.steps, a.warmup, a.rotate_gb)
+    ms_step, ms_gemms, host = measure(ctx, M, wtype, a.steps, a.warmup, a.rotate_gb,
+                                      use_graphs=not a.no_graphs)
     ops = layer_ops(M)
     value = ops / (ms_step * 1e-3) / 1e12
     gb = gemm_alg_bytes(M, wtype)
@@ -256,7 +284,8 @@ def main():
                                                 / (ms_step * 1e-3), 4)}
     if a.extra:
         for (mm, wt) in ((4097, ema.WTYPE_Q8_0), (1025, ema.WTYPE_Q4_K), (4097, ema.WTYPE_Q4_K)):
-            s, g, _ = measure(ctx, mm, wt, max(10, a.steps // 2), a.warmup, a.rotate_gb)
+            s, g, _ = measure(ctx, mm, wt, max(10, a.steps // 2), a.warmup, a.rotate_gb,
+                              use_graphs=not a.no_graphs)
             key = f"{'q8_0' if wt == ema.WTYPE_Q8_0 else 'q4_k'}_m{mm}"
             extra[key] = {"ms_per_step": round(s, 5), "tops": round(layer_ops(mm) / (s * 1e-3) / 1e12, 2),
                           "gemm_tops": round(layer_ops(mm) / (g * 1e-3) / 1e12, 2),
@@ -279,10 +308,11 @@ def main():
         "config": {"workload": "cfg2: one MaskGIT layer's four Q8_0 FC GEMMs (QKV 768->2304, "
                                "out 768->768 +resid, up 768->3072 +GELU, down 3072->768 +resid), "
                                "M=1025, fp32 activations, int8-dot path (quantize + GEMM)",
-                   "M": M, "weights": "Q8_0", "rotate_gb": a.rotate_gb},
+                   "M": M, "weights": "Q8_0", "rotate_gb": a.rotate_gb,
+                   "launch": "stream" if a.no_graphs else "hip_graph_per_step"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_gemm_q_i8", "bytes_per_step": gb},
+                     "kernel": "k_gemm_q_f16x", "bytes_per_step": gb},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -29,6 +29,8 @@ MGH_SYMBOLS = [
     "mgh_alloc", "mgh_free", "mgh_h2d", "mgh_d2h", "mgh_fill_u32", "mgh_sync",
     "mgh_timer_start", "mgh_timer_stop",
     "mgh_quantize_act_q8", "mgh_gemm_q", "mgh_gemm_q_f32in", "mgh_debug_block_dots",
+    "mgh_graph_begin", "mgh_graph_end", "mgh_graph_launch", "mgh_graph_destroy",
+    "mgh_quantize_act_q8_codes16", "mgh_gemm_q_codes16",
 ]
 
 _lib = None
@@ -71,6 +73,13 @@ def lib():
         L.mgh_gemm_q.argtypes = [P, I, P, I, I, P, P, P, I, P, I, P, P]
         L.mgh_gemm_q_f32in.argtypes = [P, I, I, P, I, I, P, I, P, I, P, P]
         L.mgh_debug_block_dots.argtypes = [P, I, P, I, I, P, I, P]
+        L.mgh_quantize_act_q8_codes16.argtypes = [P, P, I, I, P, P, P]
+        L.mgh_gemm_q_codes16.argtypes = [P, I, P, I, I, P, P, P, I, P, I, P, P]
+        L.mgh_graph_begin.argtypes = [P]
+        L.mgh_graph_end.argtypes = [P, ctypes.POINTER(P)]
+        L.mgh_graph_launch.argtypes = [P, P]
+        L.mgh_graph_destroy.argtypes = [P]
+        L.mgh_graph_destroy.restype = None
         _lib = L
     return _lib
 
@@ -177,14 +186,48 @@ class Context:
         self._check(lib().mgh_gemm_q(self.h, wtype, P(w), N, K, P(qx), P(dx), P(sx), M,
                                      P(bias), act, P(resid), P(y)))
 
+    def quantize_act_q8_codes16(self, x, M, K, qx16, dx, sx=None):
+        P = self._ptr
+        self._check(lib().mgh_quantize_act_q8_codes16(self.h, P(x), M, K, P(qx16), P(dx), P(sx)))
+
+    def gemm_q_codes16(self, wtype, w, N, K, qx16, dx, sx, M, bias, act, resid, y):
+        P = self._ptr
+        self._check(lib().mgh_gemm_q_codes16(self.h, wtype, P(w), N, K, P(qx16), P(dx), P(sx), M,
+                                             P(bias), act, P(resid), P(y)))
+
     def gemm_q_f32in(self, algo, wtype, w, N, K, x, M, bias, act, resid, y):
         P = self._ptr
         self._check(lib().mgh_gemm_q_f32in(self.h, algo, wtype, P(w), N, K, P(x), M,
                                            P(bias), act, P(resid), P(y)))
 
+    # ---- graphs ----
+    def graph_begin(self):
+        self._check(lib().mgh_graph_begin(self.h))
+
+    def graph_end(self) -> "Graph":
+        g = ctypes.c_void_p()
+        self._check(lib().mgh_graph_end(self.h, ctypes.byref(g)))
+        return Graph(self, g)
+
     def debug_block_dots(self, wtype, w, N, K, qx, M, out):
         P = self._ptr
         self._check(lib().mgh_debug_block_dots(self.h, wtype, P(w), N, K, P(qx), M, P(out)))
+
+
+class Graph:
+    """A captured, instantiated sequence of calls (mgh_graph)."""
+
+    def __init__(self, ctx: Context, h):
+        self.ctx = ctx
+        self.h = h
+
+    def launch(self):
+        self.ctx._check(lib().mgh_graph_launch(self.ctx.h, self.h))
+
+    def destroy(self):
+        if self.h:
+            lib().mgh_graph_destroy(self.h)
+            self.h = None
 
 
 def gpu_available() -> bool:

@@ -26,10 +26,13 @@ HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wno-unused-command-line-argument"]
 
-KERNEL_SOURCES = ["k_quant_act.hip", "k_gemm_i8.hip", "mgh_api.cpp"]
+KERNEL_SOURCES = ["k_quant_act.hip", "k_gemm_i8.hip", "k_gemm_i8_stream.hip", "k_gemm_q_f16x.hip",
+                  "mgh_api.cpp"]
 # Per-source extra flags. The int8 GEMM keeps MFMA results in VGPRs so the per-block
 # scale FMAs read them without v_accvgpr_read copies.
-EXTRA_FLAGS = {"k_gemm_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+EXTRA_FLAGS = {"k_gemm_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+               "k_gemm_i8_stream.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+               "k_gemm_q_f16x.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HOST_SOURCES = []
 
 

@@ -15,8 +15,11 @@
 
 namespace mgh {
 
+// F16 = false: qx is int8 (the reference layout). F16 = true: the same codes are written as
+// fp16 values (exact for |q| <= 127), the operand format of k_gemm_q_f16x.
+template <bool F16>
 __global__ __launch_bounds__(256) void k_quantize_act_q8(const float* __restrict__ x,
-                                                         int8_t* __restrict__ qx,
+                                                         void* __restrict__ qx,
                                                          float* __restrict__ dx,
                                                          int32_t* __restrict__ sx,
                                                          int64_t nblocks) {
@@ -41,9 +44,15 @@ __global__ __launch_bounds__(256) void k_quantize_act_q8(const float* __restrict
     s += __shfl_xor(s, 2);
     s += __shfl_xor(s, 4);
     if (valid) {
-        const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
-                                ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
-        *(uint32_t*)(qx + blk * 32 + sub * 4) = packed;
+        if (F16) {
+            typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+            *(f16x4*)((_Float16*)qx + blk * 32 + sub * 4) =
+                f16x4{(_Float16)q0, (_Float16)q1, (_Float16)q2, (_Float16)q3};
+        } else {
+            const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
+                                    ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+            *(uint32_t*)((int8_t*)qx + blk * 32 + sub * 4) = packed;
+        }
         if (sub == 0) {
             dx[blk] = d;
             if (sx) sx[blk] = s;
@@ -56,8 +65,34 @@ hipError_t launch_quantize_act_q8(const float* x, int8_t* qx, float* dx, int32_t
     const int64_t nblocks = M * (K / 32);
     const int64_t threads = nblocks * 8;
     const int64_t grid = (threads + 255) / 256;
-    hipLaunchKernelGGL(k_quantize_act_q8, dim3((unsigned)grid), dim3(256), 0, s, x, qx, dx, sx,
-                       nblocks);
+    hipLaunchKernelGGL(k_quantize_act_q8<false>, dim3((unsigned)grid), dim3(256), 0, s, x,
+                       (void*)qx, dx, sx, nblocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_act_q8_f16(const float* x, _Float16* qx16, float* dx, int32_t* sx,
+                                      int64_t M, int64_t K, hipStream_t s) {
+    const int64_t nblocks = M * (K / 32);
+    const int64_t grid = (nblocks * 8 + 255) / 256;
+    hipLaunchKernelGGL(k_quantize_act_q8<true>, dim3((unsigned)grid), dim3(256), 0, s, x,
+                       (void*)qx16, dx, sx, nblocks);
+    return hipGetLastError();
+}
+
+// int8 codes -> fp16 codes (exact); lets the debug entry point feed given int8 activations
+// to the fp16-operand GEMM.
+__global__ __launch_bounds__(256) void k_i8_to_f16(const int8_t* __restrict__ q,
+                                                   _Float16* __restrict__ h, size_t n) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * 256;
+    for (; i < n; i += stride) h[i] = (_Float16)q[i];
+}
+
+hipError_t launch_i8_to_f16(const int8_t* q, _Float16* h, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    size_t grid = (n + 255) / 256;
+    if (grid > 65536) grid = 65536;
+    hipLaunchKernelGGL(k_i8_to_f16, dim3((unsigned)grid), dim3(256), 0, s, q, h, n);
     return hipGetLastError();
 }
 

@@ -3,14 +3,21 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <string>
 
 #include "mgh_kernels.h"
 
+struct mgh_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
 struct mgh_ctx {
     int device = 0;
+    bool capturing = false;
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     std::string err;
@@ -62,6 +69,41 @@ mgh::TileCfg pick_tile(int M, int N) {
     if (tiles(128, 64) >= 512) return {2, 1};
     if (tiles(64, 128) >= 512) return {1, 2};
     return {1, 1};
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// fp16-code production kernel: K % 256 == 0, N % 4 == 0, 16-byte aligned w/bias/resid/y.
+bool f16x_ok(int K, int N, const void* w, const void* bias, const void* resid, const void* y) {
+    return K % 256 == 0 && N % 4 == 0 && aligned16(w) && aligned16(bias) && aligned16(resid) &&
+           aligned16(y);
+}
+
+size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Grow-on-demand activation scratch (like the reference's qx_buf/dx_buf,
+// mg-opencl.cpp:1125-1134). Not allowed while a graph is being captured.
+int ensure_scratch(mgh_ctx* c, size_t need) {
+    if (c->scratch_bytes >= need) return MGH_OK;
+    if (c->capturing)
+        return fail(c, MGH_ERR_ARG, "activation scratch must grow, which is not allowed during "
+                                    "graph capture (run the call once before capturing)");
+    MGH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    if (c->scratch) MGH_HIP(c, hipFree(c->scratch), "hipFree(scratch)");
+    c->scratch = nullptr;
+    c->scratch_bytes = 0;
+    MGH_HIP(c, hipMalloc(&c->scratch, need), "hipMalloc(scratch)");
+    c->scratch_bytes = need;
+    return MGH_OK;
+}
+
+// Streamed kernel when K is a multiple of 256 and every streamed operand is 16-byte aligned
+// (its 16-byte direct-to-LDS loads and vector scale loads need both); general kernel otherwise.
+hipError_t launch_gemm(int wtype, const mgh::GemmArgs& a, bool dbg, hipStream_t s) {
+    if (a.K % 256 == 0 && aligned16(a.w) && aligned16(a.qx) && (dbg || aligned16(a.dx)) &&
+        (dbg || wtype != MGH_WTYPE_Q4_K || aligned16(a.sx)))
+        return mgh::launch_gemm_q_i8_s256(wtype, a, dbg, s);
+    return mgh::launch_gemm_q_i8(wtype, a, pick_tile(a.M, a.N), dbg, s);
 }
 
 }  // namespace
@@ -170,6 +212,43 @@ int mgh_timer_stop(mgh_ctx* c, float* ms) {
     return MGH_OK;
 }
 
+int mgh_graph_begin(mgh_ctx* c) {
+    if (!c) return MGH_ERR_ARG;
+    if (c->capturing) return fail(c, MGH_ERR_ARG, "mgh_graph_begin: already capturing");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    c->capturing = true;
+    return MGH_OK;
+}
+
+int mgh_graph_end(mgh_ctx* c, mgh_graph** out) {
+    if (!c || !out) return fail(c, MGH_ERR_ARG, "mgh_graph_end: null argument");
+    if (!c->capturing) return fail(c, MGH_ERR_ARG, "mgh_graph_end: not capturing");
+    c->capturing = false;
+    mgh_graph* g = new mgh_graph();
+    hipError_t e = hipStreamEndCapture(c->stream, &g->graph);
+    if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        mgh_graph_destroy(g);
+        return hip_fail(c, e, "graph capture/instantiate");
+    }
+    *out = g;
+    return MGH_OK;
+}
+
+int mgh_graph_launch(mgh_ctx* c, mgh_graph* g) {
+    if (!c || !g || !g->exec) return fail(c, MGH_ERR_ARG, "mgh_graph_launch: null argument");
+    MGH_HIP(c, hipGraphLaunch(g->exec, c->stream), "hipGraphLaunch");
+    return MGH_OK;
+}
+
+void mgh_graph_destroy(mgh_graph* g) {
+    if (!g) return;
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
+}
+
 int mgh_quantize_act_q8(mgh_ctx* c, const float* x, int M, int K, int8_t* qx, float* dx, int32_t* sx) {
     if (!c) return MGH_ERR_ARG;
     if (M < 0 || K <= 0 || K % 32) return fail(c, MGH_ERR_ARG, "quantize_act_q8: need M>=0, K>0, K%32==0");
@@ -194,7 +273,40 @@ int mgh_gemm_q(mgh_ctx* c, int wtype, const void* w, int N, int K, const int8_t*
     a.w = (const uint8_t*)w; a.qx = qx; a.dx = dx; a.sx = sx;
     a.bias = bias; a.resid = resid; a.y = y;
     a.M = M; a.N = N; a.K = K; a.act = act;
-    MGH_HIP(c, mgh::launch_gemm_q_i8(wtype, a, pick_tile(M, N), false, c->stream), "k_gemm_q_i8");
+    MGH_HIP(c, launch_gemm(wtype, a, false, c->stream), "k_gemm_q_i8");
+    return MGH_OK;
+}
+
+int mgh_quantize_act_q8_codes16(mgh_ctx* c, const float* x, int M, int K, uint16_t* qx16,
+                                float* dx, int32_t* sx) {
+    if (!c) return MGH_ERR_ARG;
+    if (M < 0 || K <= 0 || K % 32) return fail(c, MGH_ERR_ARG, "quantize_act_q8_codes16: need M>=0, K>0, K%32==0");
+    if (M == 0) return MGH_OK;
+    if (!x || !qx16 || !dx) return fail(c, MGH_ERR_ARG, "quantize_act_q8_codes16: null pointer");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_quantize_act_q8_f16(x, (_Float16*)qx16, dx, sx, M, K, c->stream),
+            "k_quantize_act_q8<f16>");
+    return MGH_OK;
+}
+
+int mgh_gemm_q_codes16(mgh_ctx* c, int wtype, const void* w, int N, int K, const uint16_t* qx16,
+                       const float* dx, const int32_t* sx, int M, const float* bias, int act,
+                       const float* resid, float* y) {
+    if (!c) return MGH_ERR_ARG;
+    if (int r = check_quant_shape(c, wtype, N, K, M)) return r;
+    if (act < 0 || act > 2) return fail(c, MGH_ERR_ARG, "act must be 0 (none), 1 (gelu) or 2 (silu)");
+    if (M == 0) return MGH_OK;
+    if (!w || !qx16 || !dx || !y) return fail(c, MGH_ERR_ARG, "gemm_q_codes16: null pointer");
+    if (wtype == MGH_WTYPE_Q4_K && !sx) return fail(c, MGH_ERR_ARG, "gemm_q_codes16: Q4_K needs block sums sx");
+    if (!f16x_ok(K, N, w, bias, resid, y) || !aligned16(qx16) || !aligned16(dx) || !aligned16(sx))
+        return fail(c, MGH_ERR_UNSUPPORTED, "gemm_q_codes16 needs K % 256 == 0, N % 4 == 0 and "
+                                            "16-byte aligned operands");
+    if (int r = set_dev(c)) return r;
+    mgh::GemmArgs a{};
+    a.w = (const uint8_t*)w; a.qx16 = qx16; a.dx = dx; a.sx = sx;
+    a.bias = bias; a.resid = resid; a.y = y;
+    a.M = M; a.N = N; a.K = K; a.act = act;
+    MGH_HIP(c, mgh::launch_gemm_q_f16x(wtype, a, false, c->stream), "k_gemm_q_f16x");
     return MGH_OK;
 }
 
@@ -205,26 +317,30 @@ int mgh_gemm_q_f32in(mgh_ctx* c, int algo, int wtype, const void* w, int N, int 
     if (algo != MGH_ALGO_AUTO && algo != MGH_ALGO_INT8 && algo != MGH_ALGO_DEQ_F16)
         return fail(c, MGH_ERR_ARG, "algo must be MGH_ALGO_AUTO, _INT8 or _DEQ_F16");
     if (algo == MGH_ALGO_DEQ_F16) return fail(c, MGH_ERR_UNSUPPORTED, "dequant-fp16 GEMM not built yet");
+    if (act < 0 || act > 2) return fail(c, MGH_ERR_ARG, "act must be 0 (none), 1 (gelu) or 2 (silu)");
     if (M == 0) return MGH_OK;
-    if (!x) return fail(c, MGH_ERR_ARG, "gemm_q_f32in: null x");
+    if (!x || !w || !y) return fail(c, MGH_ERR_ARG, "gemm_q_f32in: null pointer");
     if (int r = set_dev(c)) return r;
     const size_t nb = (size_t)K / 32;
-    const size_t qx_b = ((size_t)M * K + 255) & ~(size_t)255;
-    const size_t dx_b = ((size_t)M * nb * 4 + 255) & ~(size_t)255;
-    const size_t need = qx_b + 2 * dx_b;
-    if (c->scratch_bytes < need) {
-        MGH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-        if (c->scratch) MGH_HIP(c, hipFree(c->scratch), "hipFree(scratch)");
-        c->scratch = nullptr;
-        c->scratch_bytes = 0;
-        MGH_HIP(c, hipMalloc(&c->scratch, need), "hipMalloc(scratch)");
-        c->scratch_bytes = need;
+    const bool fast = f16x_ok(K, N, w, bias, resid, y);
+    const size_t q_b = round256((size_t)M * K * (fast ? 2 : 1));
+    const size_t d_b = round256((size_t)M * nb * 4);
+    if (int r = ensure_scratch(c, q_b + 2 * d_b)) return r;
+    void* q = c->scratch;
+    float* dx = (float*)((char*)c->scratch + q_b);
+    int32_t* sx = (int32_t*)((char*)c->scratch + q_b + d_b);
+    if (!fast) {
+        if (int r = mgh_quantize_act_q8(c, x, M, K, (int8_t*)q, dx, sx)) return r;
+        return mgh_gemm_q(c, wtype, w, N, K, (const int8_t*)q, dx, sx, M, bias, act, resid, y);
     }
-    int8_t* qx = (int8_t*)c->scratch;
-    float* dx = (float*)((char*)c->scratch + qx_b);
-    int32_t* sx = (int32_t*)((char*)c->scratch + qx_b + dx_b);
-    if (int r = mgh_quantize_act_q8(c, x, M, K, qx, dx, sx)) return r;
-    return mgh_gemm_q(c, wtype, w, N, K, qx, dx, sx, M, bias, act, resid, y);
+    MGH_HIP(c, mgh::launch_quantize_act_q8_f16(x, (_Float16*)q, dx, sx, M, K, c->stream),
+            "k_quantize_act_q8<f16>");
+    mgh::GemmArgs a{};
+    a.w = (const uint8_t*)w; a.qx16 = q; a.dx = dx; a.sx = sx;
+    a.bias = bias; a.resid = resid; a.y = y;
+    a.M = M; a.N = N; a.K = K; a.act = act;
+    MGH_HIP(c, mgh::launch_gemm_q_f16x(wtype, a, false, c->stream), "k_gemm_q_f16x");
+    return MGH_OK;
 }
 
 int mgh_debug_block_dots(mgh_ctx* c, int wtype, const void* w, int N, int K, const int8_t* qx,
@@ -237,7 +353,16 @@ int mgh_debug_block_dots(mgh_ctx* c, int wtype, const void* w, int N, int K, con
     mgh::GemmArgs a{};
     a.w = (const uint8_t*)w; a.qx = qx; a.dots = out;
     a.M = M; a.N = N; a.K = K;
-    MGH_HIP(c, mgh::launch_gemm_q_i8(wtype, a, pick_tile(M, N), true, c->stream), "k_gemm_q_i8(debug)");
+    if (f16x_ok(K, N, w, nullptr, nullptr, nullptr)) {
+        // the kernel mgh_gemm_q_f32in runs for this shape: feed it the codes as fp16
+        const size_t n = (size_t)M * K;
+        if (int r = ensure_scratch(c, round256(n * 2))) return r;
+        MGH_HIP(c, mgh::launch_i8_to_f16(qx, (_Float16*)c->scratch, n, c->stream), "k_i8_to_f16");
+        a.qx16 = c->scratch;
+        MGH_HIP(c, mgh::launch_gemm_q_f16x(wtype, a, true, c->stream), "k_gemm_q_f16x(debug)");
+        return MGH_OK;
+    }
+    MGH_HIP(c, launch_gemm(wtype, a, true, c->stream), "k_gemm_q_i8(debug)");
     return MGH_OK;
 }
 

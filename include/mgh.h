@@ -71,6 +71,16 @@ int mgh_sync(mgh_ctx* ctx);                                                  /* 
 int mgh_timer_start(mgh_ctx* ctx);
 int mgh_timer_stop(mgh_ctx* ctx, float* ms_out);   /* waits for the stop event */
 
+/* ---- HIP graphs: capture a sequence of calls on the context stream and replay it as one
+ *      submission (the reference re-enqueues every node each step, mg-opencl.cpp:1362).
+ *      Between mgh_graph_begin and mgh_graph_end only stream-ordered compute calls may be
+ *      made (no mgh_alloc/mgh_free/mgh_h2d/mgh_d2h/mgh_sync, no scratch growth). ---- */
+typedef struct mgh_graph mgh_graph;
+int  mgh_graph_begin(mgh_ctx* ctx);
+int  mgh_graph_end(mgh_ctx* ctx, mgh_graph** out);
+int  mgh_graph_launch(mgh_ctx* ctx, mgh_graph* graph);
+void mgh_graph_destroy(mgh_graph* graph);
+
 /* ---- activation quantizer: replaces k_quantize_q8 and its dispatch
  *      (mg-opencl.cpp:424-434, 1381-1389). x [M][K] -> qx [M][K] int8,
  *      dx [M][K/32] fp32 scales, sx [M][K/32] int32 block sums (nullable). K % 32 == 0. */
@@ -84,6 +94,18 @@ int mgh_quantize_act_q8(mgh_ctx* ctx, const float* d_x, int M, int K,
 int mgh_gemm_q(mgh_ctx* ctx, int wtype, const void* d_w, int N, int K,
                const int8_t* d_qx, const float* d_dx, const int32_t* d_sx, int M,
                const float* d_bias, int act, const float* d_resid, float* d_y);
+
+/* ---- the two kernels mgh_gemm_q_f32in runs when K % 256 == 0, N % 4 == 0 and d_w,
+ *      d_bias, d_resid, d_y are 16-byte aligned: the quantizer of mgh_quantize_act_q8
+ *      writing its int8 codes as fp16 values (uint16 bit patterns, exact for |q| <= 127),
+ *      and the GEMM consuming them (fp16 MFMA block dots, exact). Same semantics as
+ *      mgh_quantize_act_q8 + mgh_gemm_q; mgh_gemm_q_codes16 returns MGH_ERR_UNSUPPORTED
+ *      outside those shape/alignment conditions. ---- */
+int mgh_quantize_act_q8_codes16(mgh_ctx* ctx, const float* d_x, int M, int K,
+                                uint16_t* d_qx16, float* d_dx, int32_t* d_sx);
+int mgh_gemm_q_codes16(mgh_ctx* ctx, int wtype, const void* d_w, int N, int K,
+                       const uint16_t* d_qx16, const float* d_dx, const int32_t* d_sx, int M,
+                       const float* d_bias, int act, const float* d_resid, float* d_y);
 
 /* ---- quantized FC GEMM on fp32 activations: replaces the whole MulMat(q) node
  *      dispatch (mg-opencl.cpp:1367-1428): quantize + GEMM for ALGO_INT8 (activation

@@ -173,3 +173,71 @@ def test_gemm_rejects_bad_shapes(ctx):
         ctx.gemm_q_f32in(ema.ALGO_INT8, ema.WTYPE_Q8_0, 1, 8, 96, 1, 4, None, 0, None, 1)
     # M == 0 is a no-op
     ctx.gemm_q_f32in(ema.ALGO_INT8, ema.WTYPE_Q8_0, 1, 8, 128, 1, 0, None, 0, None, 1)
+
+
+def test_graph_replay_matches_eager(ctx):
+    """A captured quantize+GEMM graph replayed several times, with eager work and syncs
+    between replays, reproduces the eager result every time."""
+    rng = np.random.default_rng(5)
+    M, N, K = 300, 768, 768
+    for wtype in (ema.WTYPE_Q8_0, ema.WTYPE_Q4_K):
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        _, wq = _weights(rng, wtype, N, K)
+        dW, dX, dY = ctx.upload(wq), ctx.upload(x), ctx.alloc(M * N * 4)
+        dq, dd, ds = ctx.alloc(M * K), ctx.alloc(M * K // 32 * 4), ctx.alloc(M * K // 32 * 4)
+        def step():
+            ctx.quantize_act_q8(dX, M, K, dq, dd, ds)
+            ctx.gemm_q(wtype, dW, N, K, dq, dd, ds, M, None, ema.ACT_GELU, None, dY)
+        step()
+        eager = ctx.download(dY, (M, N), np.float32)
+        ctx.graph_begin()
+        step()
+        g = ctx.graph_end()
+        junk = ctx.upload(np.zeros((M, N), np.float32))
+        for rep in range(4):
+            ctx.gemm_q(wtype, dW, N, K, dq, dd, ds, M, None, 0, None, junk)   # eager work between
+            ctx.sync()
+            g.launch()
+            got = ctx.download(dY, (M, N), np.float32)
+            assert np.array_equal(got, eager), f"replay {rep} differs"
+        g.destroy()
+        for b in (dW, dX, dY, dq, dd, ds, junk):
+            ctx.free(b)
+
+
+@pytest.mark.parametrize("wtype", [ema.WTYPE_Q8_0, ema.WTYPE_Q4_K])
+@pytest.mark.parametrize("M,N,K", [(5, 96, 512), (257, 768, 768), (70, 130, 768), (33, 64, 3072)])
+def test_gemm_q_int8_input_vs_oracle(ctx, wtype, M, N, K):
+    """mgh_gemm_q on int8 codes given by the caller (the reference's qx/dx/sx layout)."""
+    print(f"gemm_q int8-input wtype={wtype} M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M + 3 * N + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    _, wq = _weights(rng, wtype, N, K)
+    bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+    qx, dx, sx = oracle.quantize_act_q8(x)
+    dW, dQ, dD, dS, dB = (ctx.upload(a) for a in (wq, qx, dx, sx, bias))
+    dY = ctx.alloc(M * N * 4)
+    ctx.gemm_q(wtype, dW, N, K, dQ, dD, dS, M, dB, ema.ACT_SILU, None, dY)
+    y = ctx.download(dY, (M, N), np.float32)
+    ref = oracle.gemm_q_i8(wtype, wq, N, K, qx, dx, bias=bias, act=ema.ACT_SILU)
+    for b in (dW, dQ, dD, dS, dB, dY):
+        ctx.free(b)
+    assert _rel_err(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("M,K", [(3, 256), (1025, 768)])
+def test_quantize_codes16_bitexact(ctx, M, K):
+    rng = np.random.default_rng(K + M)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[0, 0] = 127.0
+    x[0, 1:4] = [2.5, -2.5, 0.5]
+    qx_r, dx_r, sx_r = oracle.quantize_act_q8(x)
+    dX = ctx.upload(x)
+    dq, dd, ds = ctx.alloc(M * K * 2), ctx.alloc(M * K // 32 * 4), ctx.alloc(M * K // 32 * 4)
+    ctx.quantize_act_q8_codes16(dX, M, K, dq, dd, ds)
+    codes = ctx.download(dq, (M, K), np.float16)
+    assert np.array_equal(codes.astype(np.int32), qx_r.astype(np.int32))
+    assert np.array_equal(ctx.download(dd, (M, K // 32), np.float32), dx_r)
+    assert np.array_equal(ctx.download(ds, (M, K // 32), np.int32), sx_r)
+    for b in (dX, dq, dd, ds):
+        ctx.free(b)
