@@ -49,6 +49,9 @@ LAYER = [  # name, N, K, act, residual
 ]
 
 
+KERNEL = {"packed": "k_gemm_qp", "raw": "k_gemm_q_f16x"}
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -58,33 +61,49 @@ def row_bytes(wtype, K):
 
 
 class LayerSet:
-    """One set of device buffers for the four FC GEMMs of a layer."""
+    """One set of device buffers for the four FC GEMMs of a layer.
 
-    def __init__(self, ctx, host, M, wtype):
+    path "packed" (production): weights rewritten once at upload into the device-native layout
+    (mgh_pack_weights, outside the timed region, as the reference uploads each weight once),
+    then per FC: quantizer (fp16 codes) + mgh_gemm_q_packed.
+    path "raw": GGUF blocks as stored, per FC: quantizer + mgh_gemm_q_codes16."""
+
+    def __init__(self, ctx, host, M, wtype, path="packed"):
         self.ctx = ctx
         self.M = M
         self.wtype = wtype
+        self.path = path
         self.g = []
         for (name, N, K, act, res), h in zip(LAYER, host):
             nb = K // 32
+            w = ctx.upload(h["wq"])
+            if path == "packed":
+                wp = ctx.alloc(ema.packed_weight_bytes(wtype, N, K))
+                ctx.pack_weights(wtype, w, N, K, wp)
+                ctx.sync()
+                ctx.free(w)
+                w = wp
             d = dict(name=name, N=N, K=K, act=act,
-                     w=ctx.upload(h["wq"]), x=ctx.upload(h["x"]), b=ctx.upload(h["bias"]),
+                     w=w, x=ctx.upload(h["x"]), b=ctx.upload(h["bias"]),
                      r=ctx.upload(h["resid"]) if res else None, y=ctx.alloc(M * N * 4),
                      qx=ctx.alloc(M * K * 2), dx=ctx.alloc(M * nb * 4), sx=ctx.alloc(M * nb * 4))
             self.g.append(d)
+
+    def _gemm(self, d):
+        c = self.ctx
+        f = c.gemm_q_packed if self.path == "packed" else c.gemm_q_codes16
+        f(self.wtype, d["w"], d["N"], d["K"], d["qx"], d["dx"], d["sx"], self.M,
+          d["b"], d["act"], d["r"], d["y"])
 
     def step(self):
         c = self.ctx
         for d in self.g:
             c.quantize_act_q8_codes16(d["x"], self.M, d["K"], d["qx"], d["dx"], d["sx"])
-            c.gemm_q_codes16(self.wtype, d["w"], d["N"], d["K"], d["qx"], d["dx"], d["sx"], self.M,
-                             d["b"], d["act"], d["r"], d["y"])
+            self._gemm(d)
 
     def gemms_only(self):
-        c = self.ctx
         for d in self.g:
-            c.gemm_q_codes16(self.wtype, d["w"], d["N"], d["K"], d["qx"], d["dx"], d["sx"], self.M,
-                             d["b"], d["act"], d["r"], d["y"])
+            self._gemm(d)
 
 
 def synth_q8_0(w):
@@ -170,14 +189,14 @@ def _capture(ctx, fn):
     return g
 
 
-def measure(ctx, M, wtype, steps, warmup, rotate_gb, use_graphs=True):
+def measure(ctx, M, wtype, steps, warmup, rotate_gb, use_graphs=True, path="packed"):
     host = host_layer(M, wtype)
     set_bytes = sum(h["wq"].nbytes + h["x"].nbytes + h["bias"].nbytes + M * len(h["bias"]) * 4 * 2
                     + (h["resid"].nbytes if h["resid"] is not None else 0) + h["x"].nbytes // 2
                     for h in host)
     nsets = max(2, int(np.ceil(rotate_gb * 1e9 / set_bytes)))
     log(f"[bench] M={M} wtype={wtype}: {nsets} buffer sets x {set_bytes/1e6:.1f} MB")
-    sets = [LayerSet(ctx, host, M, wtype) for _ in range(nsets)]
+    sets = [LayerSet(ctx, host, M, wtype, path) for _ in range(nsets)]
     for s in sets:                      # first run outside any graph
         s.step()
     ctx.sync()
@@ -258,6 +277,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-graphs", action="store_true",
                     help="enqueue kernels one by one instead of replaying a captured HIP graph")
+    ap.add_argument("--path", choices=["packed", "raw"], default="packed",
+                    help="packed: device-native weight layout (production); raw: GGUF blocks as stored")
     ap.add_argument("--extra", action="store_true",
                     help="also measure Q8_0 M=4097 and Q4_K M=1025/4097 layers")
     a = ap.parse_args()
@@ -271,7 +292,7 @@ def main():
     log(f"[bench] device: {ctx.device_name}")
     M, wtype = 1025, ema.WTYPE_Q8_0
     ms_step, ms_gemms, host = measure(ctx, M, wtype, a.steps, a.warmup, a.rotate_gb,
-                                      use_graphs=not a.no_graphs)
+                                      use_graphs=not a.no_graphs, path=a.path)
     ops = layer_ops(M)
     value = ops / (ms_step * 1e-3) / 1e12
     gb = gemm_alg_bytes(M, wtype)
@@ -285,7 +306,7 @@ def main():
     if a.extra:
         for (mm, wt) in ((4097, ema.WTYPE_Q8_0), (1025, ema.WTYPE_Q4_K), (4097, ema.WTYPE_Q4_K)):
             s, g, _ = measure(ctx, mm, wt, max(10, a.steps // 2), a.warmup, a.rotate_gb,
-                              use_graphs=not a.no_graphs)
+                              use_graphs=not a.no_graphs, path=a.path)
             key = f"{'q8_0' if wt == ema.WTYPE_Q8_0 else 'q4_k'}_m{mm}"
             extra[key] = {"ms_per_step": round(s, 5), "tops": round(layer_ops(mm) / (s * 1e-3) / 1e12, 2),
                           "gemm_tops": round(layer_ops(mm) / (g * 1e-3) / 1e12, 2),
@@ -312,7 +333,7 @@ def main():
                    "launch": "stream" if a.no_graphs else "hip_graph_per_step"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_gemm_q_f16x", "bytes_per_step": gb},
+                     "kernel": KERNEL[a.path], "bytes_per_step": gb},
         "cpu_baseline": cpu,
         "extra": extra,
     }

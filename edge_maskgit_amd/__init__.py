@@ -31,6 +31,8 @@ MGH_SYMBOLS = [
     "mgh_quantize_act_q8", "mgh_gemm_q", "mgh_gemm_q_f32in", "mgh_debug_block_dots",
     "mgh_graph_begin", "mgh_graph_end", "mgh_graph_launch", "mgh_graph_destroy",
     "mgh_quantize_act_q8_codes16", "mgh_gemm_q_codes16",
+    "mgh_packed_weight_bytes", "mgh_pack_weights", "mgh_gemm_q_packed", "mgh_debug_block_dots_packed",
+    "mgh_gemm_q_packed_f32in",
 ]
 
 _lib = None
@@ -75,6 +77,12 @@ def lib():
         L.mgh_debug_block_dots.argtypes = [P, I, P, I, I, P, I, P]
         L.mgh_quantize_act_q8_codes16.argtypes = [P, P, I, I, P, P, P]
         L.mgh_gemm_q_codes16.argtypes = [P, I, P, I, I, P, P, P, I, P, I, P, P]
+        L.mgh_packed_weight_bytes.argtypes = [I, I, I]
+        L.mgh_packed_weight_bytes.restype = SZ
+        L.mgh_pack_weights.argtypes = [P, I, P, I, I, P]
+        L.mgh_gemm_q_packed.argtypes = [P, I, P, I, I, P, P, P, I, P, I, P, P]
+        L.mgh_debug_block_dots_packed.argtypes = [P, I, P, I, I, P, I, P]
+        L.mgh_gemm_q_packed_f32in.argtypes = [P, I, I, P, I, I, P, I, P, I, P, P]
         L.mgh_graph_begin.argtypes = [P]
         L.mgh_graph_end.argtypes = [P, ctypes.POINTER(P)]
         L.mgh_graph_launch.argtypes = [P, P]
@@ -82,6 +90,11 @@ def lib():
         L.mgh_graph_destroy.restype = None
         _lib = L
     return _lib
+
+
+def packed_weight_bytes(wtype: int, N: int, K: int) -> int:
+    """Size of mgh_pack_weights' output (0 for an invalid type/shape)."""
+    return int(lib().mgh_packed_weight_bytes(wtype, N, K))
 
 
 class DeviceBuffer:
@@ -177,6 +190,9 @@ class Context:
             return None
         return b.p if isinstance(b, DeviceBuffer) else ctypes.c_void_p(int(b))
 
+    def fill_u32(self, buf, value, n_words):
+        self._check(lib().mgh_fill_u32(self.h, self._ptr(buf), value, n_words))
+
     def quantize_act_q8(self, x, M, K, qx, dx, sx=None):
         P = self._ptr
         self._check(lib().mgh_quantize_act_q8(self.h, P(x), M, K, P(qx), P(dx), P(sx)))
@@ -194,6 +210,24 @@ class Context:
         P = self._ptr
         self._check(lib().mgh_gemm_q_codes16(self.h, wtype, P(w), N, K, P(qx16), P(dx), P(sx), M,
                                              P(bias), act, P(resid), P(y)))
+
+    def pack_weights(self, wtype, w, N, K, wp):
+        P = self._ptr
+        self._check(lib().mgh_pack_weights(self.h, wtype, P(w), N, K, P(wp)))
+
+    def gemm_q_packed(self, wtype, wp, N, K, qx16, dx, sx, M, bias, act, resid, y):
+        P = self._ptr
+        self._check(lib().mgh_gemm_q_packed(self.h, wtype, P(wp), N, K, P(qx16), P(dx), P(sx), M,
+                                            P(bias), act, P(resid), P(y)))
+
+    def gemm_q_packed_f32in(self, algo, wtype, wp, N, K, x, M, bias, act, resid, y):
+        P = self._ptr
+        self._check(lib().mgh_gemm_q_packed_f32in(self.h, algo, wtype, P(wp), N, K, P(x), M,
+                                                  P(bias), act, P(resid), P(y)))
+
+    def debug_block_dots_packed(self, wtype, wp, N, K, qx16, M, out):
+        P = self._ptr
+        self._check(lib().mgh_debug_block_dots_packed(self.h, wtype, P(wp), N, K, P(qx16), M, P(out)))
 
     def gemm_q_f32in(self, algo, wtype, w, N, K, x, M, bias, act, resid, y):
         P = self._ptr

@@ -79,6 +79,45 @@ hipError_t launch_quantize_act_q8_f16(const float* x, _Float16* qx16, float* dx,
     return hipGetLastError();
 }
 
+// Activation operand of the dequantize-weights algorithm (MGH_ALGO_DEQ_F16, the reference's
+// fp16-slab path k_mul_mat_*_t2_h, mg-opencl.cpp:320-411): x rounded to fp16 (round to
+// nearest even, as vstore_half_rte), unit block scales so the packed GEMM's per-block scale
+// reduces to the weight scale, and ux[block] = fp32 sum of the rounded values for Q4_K's
+// min term (sum_i (d*sc*q_i - dmin*m) * x_i = d*sc*sum_i q_i*x_i - dmin*m*ux).
+__global__ __launch_bounds__(256) void k_round_act_f16(const float* __restrict__ x,
+                                                       _Float16* __restrict__ x16,
+                                                       float* __restrict__ ones,
+                                                       float* __restrict__ ux, int64_t nblocks) {
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t blk = gid >> 3;
+    const int sub = (int)(gid & 7);
+    const bool valid = blk < nblocks;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (valid) v = *(const f32x4*)(x + blk * 32 + sub * 4);
+    const f16x4 h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+    float s = ((float)h.x + (float)h.y) + ((float)h.z + (float)h.w);
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    if (valid) {
+        *(f16x4*)(x16 + blk * 32 + sub * 4) = h;
+        if (sub == 0) {
+            ones[blk] = 1.0f;
+            if (ux) ux[blk] = s;
+        }
+    }
+}
+
+hipError_t launch_round_act_f16(const float* x, _Float16* x16, float* ones, float* ux,
+                                int64_t M, int64_t K, hipStream_t s) {
+    const int64_t nblocks = M * (K / 32);
+    const int64_t grid = (nblocks * 8 + 255) / 256;
+    hipLaunchKernelGGL(k_round_act_f16, dim3((unsigned)grid), dim3(256), 0, s, x, x16, ones, ux,
+                       nblocks);
+    return hipGetLastError();
+}
+
 // int8 codes -> fp16 codes (exact); lets the debug entry point feed given int8 activations
 // to the fp16-operand GEMM.
 __global__ __launch_bounds__(256) void k_i8_to_f16(const int8_t* __restrict__ q,

@@ -3,10 +3,12 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "mgh_kernels.h"
 
@@ -25,6 +27,12 @@ struct mgh_ctx {
     // grow-on-demand activation scratch for mgh_gemm_q_f32in (qx | dx | sx)
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
+    // grow-on-demand split-K workspace of the packed GEMM
+    void* qp_ws = nullptr;
+    size_t qp_ws_bytes = 0;
+    // buffers replaced by a larger one: a captured graph may still reference them, so they
+    // are released only with the context
+    std::vector<void*> retired;
 };
 
 namespace {
@@ -82,18 +90,48 @@ bool f16x_ok(int K, int N, const void* w, const void* bias, const void* resid, c
 size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 // Grow-on-demand activation scratch (like the reference's qx_buf/dx_buf,
-// mg-opencl.cpp:1125-1134). Not allowed while a graph is being captured.
+// mg-opencl.cpp:1125-1134). Not allowed while a graph is being captured. The replaced
+// buffer is retired, not freed (stream order keeps it valid for queued work and graphs).
 int ensure_scratch(mgh_ctx* c, size_t need) {
     if (c->scratch_bytes >= need) return MGH_OK;
     if (c->capturing)
         return fail(c, MGH_ERR_ARG, "activation scratch must grow, which is not allowed during "
                                     "graph capture (run the call once before capturing)");
-    MGH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-    if (c->scratch) MGH_HIP(c, hipFree(c->scratch), "hipFree(scratch)");
+    need = std::max(need, 2 * c->scratch_bytes);
+    if (c->scratch) c->retired.push_back(c->scratch);
     c->scratch = nullptr;
     c->scratch_bytes = 0;
     MGH_HIP(c, hipMalloc(&c->scratch, need), "hipMalloc(scratch)");
     c->scratch_bytes = need;
+    return MGH_OK;
+}
+
+// Split-K workspace of the packed GEMM (partial tiles).
+int ensure_qp_ws(mgh_ctx* c, size_t need) {
+    if (c->qp_ws_bytes >= need) return MGH_OK;
+    if (c->capturing)
+        return fail(c, MGH_ERR_ARG, "split-K workspace must grow, which is not allowed during graph "
+                                    "capture (run the call once before capturing)");
+    need = std::max(need, 2 * c->qp_ws_bytes);
+    if (c->qp_ws) c->retired.push_back(c->qp_ws);
+    c->qp_ws = nullptr;
+    c->qp_ws_bytes = 0;
+    MGH_HIP(c, hipMalloc(&c->qp_ws, need), "hipMalloc(qp_ws)");
+    c->qp_ws_bytes = need;
+    return MGH_OK;
+}
+
+// The packed GEMM with its split-K plan (workspace from the context).
+int run_gemm_qp(mgh_ctx* c, int wtype, mgh::GemmArgs a, bool dbg) {
+    if (!dbg) {
+        const mgh::QpPlan p = mgh::gemm_qp_plan(a.M, a.N, a.K);
+        a.splits = p.splits;
+        if (p.splits > 1) {
+            if (int r = ensure_qp_ws(c, p.ws_bytes)) return r;
+            a.ws = (float*)c->qp_ws;
+        }
+    }
+    MGH_HIP(c, mgh::launch_gemm_qp(wtype, a, dbg, c->stream), dbg ? "k_gemm_qp(debug)" : "k_gemm_qp");
     return MGH_OK;
 }
 
@@ -104,6 +142,36 @@ hipError_t launch_gemm(int wtype, const mgh::GemmArgs& a, bool dbg, hipStream_t 
         (dbg || wtype != MGH_WTYPE_Q4_K || aligned16(a.sx)))
         return mgh::launch_gemm_q_i8_s256(wtype, a, dbg, s);
     return mgh::launch_gemm_q_i8(wtype, a, pick_tile(a.M, a.N), dbg, s);
+}
+
+// Activation operands + packed GEMM on fp32 input, activation scratch at `base`
+// (x16/codes [M][K] fp16 | dx [M][T] | sx or ux [M][T]).
+int packed_f32in(mgh_ctx* c, int algo, int wtype, const void* wp, int N, int K, const float* x,
+                 int M, const float* bias, int act, const float* resid, float* y, char* base) {
+    const size_t T = (size_t)K / 32;
+    const size_t q_b = round256((size_t)M * K * 2), d_b = round256((size_t)M * T * 4);
+    void* q = base;
+    float* dx = (float*)(base + q_b);
+    void* s4 = base + q_b + d_b;
+    mgh::GemmArgs a{};
+    a.w = (const uint8_t*)wp; a.qx16 = q; a.dx = dx;
+    a.bias = bias; a.resid = resid; a.y = y;
+    a.M = M; a.N = N; a.K = K; a.act = act;
+    if (algo == MGH_ALGO_DEQ_F16) {
+        MGH_HIP(c, mgh::launch_round_act_f16(x, (_Float16*)q, dx, (float*)s4, M, K, c->stream),
+                "k_round_act_f16");
+        a.ux = (const float*)s4;
+    } else {
+        MGH_HIP(c, mgh::launch_quantize_act_q8_f16(x, (_Float16*)q, dx, (int32_t*)s4, M, K, c->stream),
+                "k_quantize_act_q8<f16>");
+        a.sx = (const int32_t*)s4;
+    }
+    return run_gemm_qp(c, wtype, a, false);
+}
+
+size_t packed_f32in_scratch(int M, int K) {
+    const size_t T = (size_t)K / 32;
+    return round256((size_t)M * K * 2) + 2 * round256((size_t)M * T * 4);
 }
 
 }  // namespace
@@ -141,6 +209,8 @@ void mgh_destroy(mgh_ctx* c) {
     (void)hipSetDevice(c->device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     if (c->scratch) (void)hipFree(c->scratch);
+    if (c->qp_ws) (void)hipFree(c->qp_ws);
+    for (void* p : c->retired) (void)hipFree(p);
     if (c->ev0) (void)hipEventDestroy(c->ev0);
     if (c->ev1) (void)hipEventDestroy(c->ev1);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -310,17 +380,118 @@ int mgh_gemm_q_codes16(mgh_ctx* c, int wtype, const void* w, int N, int K, const
     return MGH_OK;
 }
 
+size_t mgh_packed_weight_bytes(int wtype, int N, int K) {
+    if ((wtype != MGH_WTYPE_Q8_0 && wtype != MGH_WTYPE_Q4_K) || N <= 0 || K <= 0 || K % 32) return 0;
+    if (wtype == MGH_WTYPE_Q4_K && K % 256) return 0;
+    return mgh::packed_weight_bytes(wtype, N, K);
+}
+
+int mgh_pack_weights(mgh_ctx* c, int wtype, const void* w, int N, int K, void* wp) {
+    if (!c) return MGH_ERR_ARG;
+    if (int r = check_quant_shape(c, wtype, N, K, 0)) return r;
+    if (!w || !wp) return fail(c, MGH_ERR_ARG, "pack_weights: null pointer");
+    if (!aligned16(wp)) return fail(c, MGH_ERR_ARG, "pack_weights: d_packed must be 16-byte aligned");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_pack_weights(wtype, w, wp, N, K, c->stream), "k_pack_w");
+    return MGH_OK;
+}
+
+namespace {
+// Packed weights and outputs: shape rules, N % 4 == 0, 16-byte aligned wp/bias/resid/y.
+int check_packed_w(mgh_ctx* c, const std::string& f, int wtype, const void* wp, int N, int K, int M,
+                   const float* bias, const float* resid, const float* y, bool need_y) {
+    if (int r = check_quant_shape(c, wtype, N, K, M)) return r;
+    if (M == 0) return MGH_OK;
+    if (!wp || (need_y && !y)) return fail(c, MGH_ERR_ARG, f + ": null pointer");
+    if (N % 4) return fail(c, MGH_ERR_UNSUPPORTED, f + ": needs N % 4 == 0");
+    if (!aligned16(wp) || !aligned16(bias) || !aligned16(resid) || !aligned16(y))
+        return fail(c, MGH_ERR_ARG, f + ": d_wp, d_bias, d_resid and d_y must be 16-byte aligned");
+    return MGH_OK;
+}
+
+// fp16-code activation operands: qx16 16-byte aligned; dx 4-byte aligned (16-byte, with sx,
+// for Q4_K, whose min term reads them as float4).
+int check_act16(mgh_ctx* c, const std::string& f, int wtype, const uint16_t* qx16, const float* dx,
+                const int32_t* sx, bool need_scales) {
+    if (!qx16 || (need_scales && !dx)) return fail(c, MGH_ERR_ARG, f + ": null pointer");
+    if (need_scales && wtype == MGH_WTYPE_Q4_K && !sx)
+        return fail(c, MGH_ERR_ARG, f + ": Q4_K needs block sums sx");
+    if (!aligned16(qx16)) return fail(c, MGH_ERR_ARG, f + ": d_qx16 must be 16-byte aligned");
+    if (need_scales && (((uintptr_t)dx & 3u) || (wtype == MGH_WTYPE_Q4_K && (!aligned16(dx) || !aligned16(sx)))))
+        return fail(c, MGH_ERR_ARG, f + ": d_dx must be 4-byte aligned (16-byte, with d_sx, for Q4_K)");
+    return MGH_OK;
+}
+}  // namespace
+
+int mgh_gemm_q_packed(mgh_ctx* c, int wtype, const void* wp, int N, int K, const uint16_t* qx16,
+                      const float* dx, const int32_t* sx, int M, const float* bias, int act,
+                      const float* resid, float* y) {
+    if (!c) return MGH_ERR_ARG;
+    if (act < 0 || act > 2) return fail(c, MGH_ERR_ARG, "act must be 0 (none), 1 (gelu) or 2 (silu)");
+    if (int r = check_packed_w(c, "gemm_q_packed", wtype, wp, N, K, M, bias, resid, y, true)) return r;
+    if (M == 0) return MGH_OK;
+    if (int r = check_act16(c, "gemm_q_packed", wtype, qx16, dx, sx, true)) return r;
+    if (int r = set_dev(c)) return r;
+    mgh::GemmArgs a{};
+    a.w = (const uint8_t*)wp; a.qx16 = qx16; a.dx = dx; a.sx = sx;
+    a.bias = bias; a.resid = resid; a.y = y;
+    a.M = M; a.N = N; a.K = K; a.act = act;
+    return run_gemm_qp(c, wtype, a, false);
+}
+
+int mgh_debug_block_dots_packed(mgh_ctx* c, int wtype, const void* wp, int N, int K,
+                                const uint16_t* qx16, int M, int32_t* out) {
+    if (!c) return MGH_ERR_ARG;
+    if (int r = check_packed_w(c, "debug_block_dots_packed", wtype, wp, N, K, M, nullptr, nullptr,
+                               nullptr, false)) return r;
+    if (M == 0) return MGH_OK;
+    if (int r = check_act16(c, "debug_block_dots_packed", wtype, qx16, nullptr, nullptr, false)) return r;
+    if (!out) return fail(c, MGH_ERR_ARG, "debug_block_dots_packed: null pointer");
+    if (int r = set_dev(c)) return r;
+    mgh::GemmArgs a{};
+    a.w = (const uint8_t*)wp; a.qx16 = qx16; a.dots = out;
+    a.M = M; a.N = N; a.K = K;
+    return run_gemm_qp(c, wtype, a, true);
+}
+
+int mgh_gemm_q_packed_f32in(mgh_ctx* c, int algo, int wtype, const void* wp, int N, int K,
+                            const float* x, int M, const float* bias, int act, const float* resid,
+                            float* y) {
+    if (!c) return MGH_ERR_ARG;
+    if (algo != MGH_ALGO_AUTO && algo != MGH_ALGO_INT8 && algo != MGH_ALGO_DEQ_F16)
+        return fail(c, MGH_ERR_ARG, "algo must be MGH_ALGO_AUTO, _INT8 or _DEQ_F16");
+    if (act < 0 || act > 2) return fail(c, MGH_ERR_ARG, "act must be 0 (none), 1 (gelu) or 2 (silu)");
+    // the activation operands are built in aligned context scratch
+    if (int r = check_packed_w(c, "gemm_q_packed_f32in", wtype, wp, N, K, M, bias, resid, y, true)) return r;
+    if (M == 0) return MGH_OK;
+    if (!x) return fail(c, MGH_ERR_ARG, "gemm_q_packed_f32in: null pointer");
+    if ((uintptr_t)x & 15u) return fail(c, MGH_ERR_ARG, "gemm_q_packed_f32in: d_x must be 16-byte aligned");
+    if (int r = set_dev(c)) return r;
+    if (int r = ensure_scratch(c, packed_f32in_scratch(M, K))) return r;
+    return packed_f32in(c, algo, wtype, wp, N, K, x, M, bias, act, resid, y, (char*)c->scratch);
+}
+
 int mgh_gemm_q_f32in(mgh_ctx* c, int algo, int wtype, const void* w, int N, int K, const float* x,
                      int M, const float* bias, int act, const float* resid, float* y) {
     if (!c) return MGH_ERR_ARG;
     if (int r = check_quant_shape(c, wtype, N, K, M)) return r;
     if (algo != MGH_ALGO_AUTO && algo != MGH_ALGO_INT8 && algo != MGH_ALGO_DEQ_F16)
         return fail(c, MGH_ERR_ARG, "algo must be MGH_ALGO_AUTO, _INT8 or _DEQ_F16");
-    if (algo == MGH_ALGO_DEQ_F16) return fail(c, MGH_ERR_UNSUPPORTED, "dequant-fp16 GEMM not built yet");
     if (act < 0 || act > 2) return fail(c, MGH_ERR_ARG, "act must be 0 (none), 1 (gelu) or 2 (silu)");
     if (M == 0) return MGH_OK;
     if (!x || !w || !y) return fail(c, MGH_ERR_ARG, "gemm_q_f32in: null pointer");
     if (int r = set_dev(c)) return r;
+    if (algo == MGH_ALGO_DEQ_F16) {
+        // weights packed into scratch for this call, then the packed kernel
+        if (N % 4 || ((uintptr_t)x & 15u) || !aligned16(bias) || !aligned16(resid) || !aligned16(y))
+            return fail(c, MGH_ERR_UNSUPPORTED, "gemm_q_f32in(DEQ_F16) needs N % 4 == 0 and 16-byte "
+                                                "aligned x/bias/resid/y");
+        const size_t wb = round256(mgh::packed_weight_bytes(wtype, N, K));
+        if (int r = ensure_scratch(c, wb + packed_f32in_scratch(M, K))) return r;
+        MGH_HIP(c, mgh::launch_pack_weights(wtype, w, c->scratch, N, K, c->stream), "k_pack_w");
+        return packed_f32in(c, algo, wtype, c->scratch, N, K, x, M, bias, act, resid, y,
+                            (char*)c->scratch + wb);
+    }
     const size_t nb = (size_t)K / 32;
     const bool fast = f16x_ok(K, N, w, bias, resid, y);
     const size_t q_b = round256((size_t)M * K * (fast ? 2 : 1));

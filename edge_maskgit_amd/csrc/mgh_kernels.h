@@ -17,12 +17,16 @@ struct GemmArgs {
     const int32_t* sx;
     const void* qx16;      // activation codes as fp16 [M][K] (k_gemm_q_f16x operand)
     const float* x;        // fp32 activations (dequant-f16 path)
+    const float* ux;       // Q4_K min-term activation factor [M][K/32] in fp32 (dequant-f16
+                           // path: block sums of the fp16 activations); null: dx * sx
     const float* bias;
     const float* resid;
     float* y;
     int32_t* dots;         // debug: [M][N][K/32] int32 block dot products
+    float* ws;             // split-K partial tiles (k_gemm_qp, splits > 1)
     int M, N, K;
     int act;
+    int splits;            // K splits of k_gemm_qp (0 or 1: none)
 };
 
 // Tile configuration chosen by the dispatcher (see mgh_api.cpp: pick_tile()).
@@ -34,6 +38,8 @@ hipError_t launch_quantize_act_q8(const float* x, int8_t* qx, float* dx, int32_t
                                   int64_t M, int64_t K, hipStream_t s);
 hipError_t launch_quantize_act_q8_f16(const float* x, _Float16* qx16, float* dx, int32_t* sx,
                                       int64_t M, int64_t K, hipStream_t s);
+hipError_t launch_round_act_f16(const float* x, _Float16* x16, float* ones, float* ux,
+                                int64_t M, int64_t K, hipStream_t s);
 hipError_t launch_i8_to_f16(const int8_t* q, _Float16* h, size_t n, hipStream_t s);
 hipError_t launch_gemm_q_i8(int wtype, const GemmArgs& a, TileCfg t, bool debug_dots,
                             hipStream_t s);
@@ -43,5 +49,19 @@ hipError_t launch_gemm_q_f16x(int wtype, const GemmArgs& a, bool debug_dots, hip
 // Streamed variant for K % 256 == 0 with 16-byte aligned qx/dx/sx/w (64x64 tiles).
 hipError_t launch_gemm_q_i8_s256(int wtype, const GemmArgs& a, bool debug_dots, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t s);
+// Weight repack (k_pack_w.hip): raw Q8_0/Q4_K -> fp16 codes [N][K] | fp32 scale [K/32][N]
+// (| fp32 min [N][K/32] for Q4_K).
+size_t packed_weight_bytes(int wtype, int64_t N, int64_t K);
+hipError_t launch_pack_weights(int wtype, const void* w, void* out, int N, int K, hipStream_t s);
+// GEMM on packed weights (a.w) and fp16-code activations (a.qx16): K % 64 == 0, N % 4 == 0,
+// 16-byte aligned w/qx16/bias/resid/y.
+hipError_t launch_gemm_qp(int wtype, const GemmArgs& a, bool debug_dots, hipStream_t s);
+// Split-K plan of k_gemm_qp for a shape: activation tile rows, number of K splits and the
+// bytes of partial tiles the splits write (then reduced by a second, stream-ordered kernel).
+struct QpPlan {
+    int bm, splits;
+    size_t ws_bytes;
+};
+QpPlan gemm_qp_plan(int M, int N, int K);
 
 }  // namespace mgh

@@ -43,10 +43,10 @@ enum { MGH_WTYPE_F32 = 0, MGH_WTYPE_Q8_0 = 8, MGH_WTYPE_Q4_K = 12 };
 /* fused epilogue activations (reference mg-opencl.cpp:36-40) */
 enum { MGH_ACT_NONE = 0, MGH_ACT_GELU = 1, MGH_ACT_SILU = 2 };
 
-/* GEMM algorithm for quantized weights. INT8 = per-32 int8 activations on int8 MFMA
- * (the reference's int8-dot path, mg-opencl.cpp:1381-1398); DEQ_F16 = dequantize weights
- * to fp16 on load and run fp16 MFMA on fp16-rounded activations (the reference's
- * dequant-fused 2D path, mg-opencl.cpp:1400-1423). AUTO = INT8. */
+/* GEMM algorithm for quantized weights. INT8 = per-32 int8 activation codes, exact block
+ * dots (the reference's int8-dot path, mg-opencl.cpp:1381-1398); DEQ_F16 = fp16-rounded
+ * activations against the dequantized weights, fp32 accumulation (the reference's
+ * dequant-fused fp16-slab path, mg-opencl.cpp:1400-1423). AUTO = INT8. */
 enum { MGH_ALGO_AUTO = 0, MGH_ALGO_INT8 = 1, MGH_ALGO_DEQ_F16 = 2 };
 
 /* ---- context: replaces OpenCLRuntime::OpenCLRuntime / ~OpenCLRuntime / device_name
@@ -107,6 +107,35 @@ int mgh_gemm_q_codes16(mgh_ctx* ctx, int wtype, const void* d_w, int N, int K,
                        const uint16_t* d_qx16, const float* d_dx, const int32_t* d_sx, int M,
                        const float* d_bias, int act, const float* d_resid, float* d_y);
 
+/* ---- device-native weight layout. The reference's OpenCL runtime uploads each weight
+ *      tensor once into a device buffer it caches for the model's lifetime
+ *      (mg-opencl.cpp:1172-1206); this backend rewrites the tensor once at that point into
+ *      fp16 codes [N][K] | fp32 block scales [K/32][N] (| fp32 block mins [N][K/32] for
+ *      Q4_K: dmin*m_j), so the hot GEMM streams whole aligned lines with no block
+ *      decoding. mgh_packed_weight_bytes returns the size (0 for an invalid type/shape);
+ *      d_packed must be 16-byte aligned. ---- */
+size_t mgh_packed_weight_bytes(int wtype, int N, int K);
+int    mgh_pack_weights(mgh_ctx* ctx, int wtype, const void* d_w, int N, int K, void* d_packed);
+
+/* ---- quantized FC GEMM on packed weights and fp16-code activations (the production
+ *      kernel; replaces k_mul_mat_q8_i8 / k_mul_mat_q4k_i8 and their dispatch,
+ *      mg-opencl.cpp:440-590, 1390-1398). Semantics of mgh_gemm_q. Needs Q8_0 K % 64 == 0
+ *      or Q4_K K % 256 == 0, N % 4 == 0, 16-byte aligned d_wp/d_qx16/d_bias/d_resid/d_y,
+ *      4-byte aligned d_dx (16-byte d_dx and d_sx for Q4_K). ---- */
+int mgh_gemm_q_packed(mgh_ctx* ctx, int wtype, const void* d_wp, int N, int K,
+                      const uint16_t* d_qx16, const float* d_dx, const int32_t* d_sx, int M,
+                      const float* d_bias, int act, const float* d_resid, float* d_y);
+
+/* ---- the whole MulMat(q) node on packed weights and fp32 activations (replaces the node
+ *      dispatch mg-opencl.cpp:1367-1428): ALGO_AUTO/INT8 = per-32 int8 activation codes +
+ *      mgh_gemm_q_packed; ALGO_DEQ_F16 = activations rounded to fp16 against the dequantized
+ *      weights (the reference's fp16-slab path k_mul_mat_*_t2_h, mg-opencl.cpp:320-411),
+ *      same kernel. Activation operands live in context scratch (grown on demand, not during
+ *      graph capture). Shape/alignment rules of mgh_gemm_q_packed; d_x 16-byte aligned. ---- */
+int mgh_gemm_q_packed_f32in(mgh_ctx* ctx, int algo, int wtype, const void* d_wp, int N, int K,
+                            const float* d_x, int M, const float* d_bias, int act,
+                            const float* d_resid, float* d_y);
+
 /* ---- quantized FC GEMM on fp32 activations: replaces the whole MulMat(q) node
  *      dispatch (mg-opencl.cpp:1367-1428): quantize + GEMM for ALGO_INT8 (activation
  *      scratch owned by the context and grown on demand, like the reference's
@@ -121,6 +150,11 @@ int mgh_gemm_q_f32in(mgh_ctx* ctx, int algo, int wtype, const void* d_w, int N, 
  *      it exposes the quantity mg-opencl.cpp:472-478 / :571-576 accumulates. ---- */
 int mgh_debug_block_dots(mgh_ctx* ctx, int wtype, const void* d_w, int N, int K,
                          const int8_t* d_qx, int M, int32_t* d_out);
+
+/* ---- debug: the block dot products of mgh_gemm_q_packed's MFMA, out[m][n][t] (no
+ *      reference counterpart, as mgh_debug_block_dots). ---- */
+int mgh_debug_block_dots_packed(mgh_ctx* ctx, int wtype, const void* d_wp, int N, int K,
+                                const uint16_t* d_qx16, int M, int32_t* d_out);
 
 #ifdef __cplusplus
 }
