@@ -21,6 +21,7 @@ WTYPE_F32 = 0
 WTYPE_Q8_0 = 8
 WTYPE_Q4_K = 12
 ACT_NONE, ACT_GELU, ACT_SILU = 0, 1, 2
+EMIT_NONE, EMIT_INT8, EMIT_DEQ_F16 = 0, 1, 2
 ALGO_AUTO, ALGO_INT8, ALGO_DEQ_F16 = 0, 1, 2
 
 # every entry point include/mgh.h declares (checked by tests/test_abi.py)
@@ -33,6 +34,8 @@ MGH_SYMBOLS = [
     "mgh_quantize_act_q8_codes16", "mgh_gemm_q_codes16",
     "mgh_packed_weight_bytes", "mgh_pack_weights", "mgh_gemm_q_packed", "mgh_debug_block_dots_packed",
     "mgh_gemm_q_packed_f32in",
+    "mgh_layernorm_affine", "mgh_flash_attn_f16kv", "mgh_gemm_f32", "mgh_get_rows", "mgh_add",
+    "mgh_copy_strided",
 ]
 
 _lib = None
@@ -83,6 +86,13 @@ def lib():
         L.mgh_gemm_q_packed.argtypes = [P, I, P, I, I, P, P, P, I, P, I, P, P]
         L.mgh_debug_block_dots_packed.argtypes = [P, I, P, I, I, P, I, P]
         L.mgh_gemm_q_packed_f32in.argtypes = [P, I, I, P, I, I, P, I, P, I, P, P]
+        I64 = ctypes.c_int64
+        L.mgh_layernorm_affine.argtypes = [P, P, P, P, I, I, ctypes.c_float, P, I, P, P, P]
+        L.mgh_flash_attn_f16kv.argtypes = [P, P, P, P, P, I, I, I, I, ctypes.c_float, P, P]
+        L.mgh_gemm_f32.argtypes = [P, P, I, I, P, I, P, I, P, P]
+        L.mgh_get_rows.argtypes = [P, P, I64, I64, P, I64, P]
+        L.mgh_add.argtypes = [P, P, P, I64, P, I64]
+        L.mgh_copy_strided.argtypes = [P, P, P, P, P]
         L.mgh_graph_begin.argtypes = [P]
         L.mgh_graph_end.argtypes = [P, ctypes.POINTER(P)]
         L.mgh_graph_launch.argtypes = [P, P]
@@ -219,6 +229,35 @@ class Context:
         P = self._ptr
         self._check(lib().mgh_gemm_q_packed(self.h, wtype, P(wp), N, K, P(qx16), P(dx), P(sx), M,
                                             P(bias), act, P(resid), P(y)))
+
+    def layernorm_affine(self, x, gamma, beta, rows, D, eps, y, emit=0, codes=None, dx=None, s4=None):
+        P = self._ptr
+        self._check(lib().mgh_layernorm_affine(self.h, P(x), P(gamma), P(beta), rows, D, eps, P(y),
+                                               emit, P(codes), P(dx), P(s4)))
+
+    def flash_attn_f16kv(self, q, k, v, strides, D, S, H, B, scale, o, o_strides=None):
+        P = self._ptr
+        st = (ctypes.c_int64 * 4)(*strides)
+        ost = (ctypes.c_int64 * 4)(*o_strides) if o_strides is not None else None
+        self._check(lib().mgh_flash_attn_f16kv(self.h, P(q), P(k), P(v), st, D, S, H, B, scale,
+                                               P(o), ost))
+
+    def gemm_f32(self, w, N, K, x, M, bias, act, resid, y):
+        P = self._ptr
+        self._check(lib().mgh_gemm_f32(self.h, P(w), N, K, P(x), M, P(bias), act, P(resid), P(y)))
+
+    def get_rows(self, a, E, R, ids, n, out):
+        P = self._ptr
+        self._check(lib().mgh_get_rows(self.h, P(a), E, R, P(ids), n, P(out)))
+
+    def add(self, a, b, nb, out, n):
+        P = self._ptr
+        self._check(lib().mgh_add(self.h, P(a), P(b), nb, P(out), n))
+
+    def copy_strided(self, a, ne, strides, out):
+        P = self._ptr
+        self._check(lib().mgh_copy_strided(self.h, P(a), (ctypes.c_int64 * 4)(*ne),
+                                           (ctypes.c_int64 * 4)(*strides), P(out)))
 
     def gemm_q_packed_f32in(self, algo, wtype, wp, N, K, x, M, bias, act, resid, y):
         P = self._ptr

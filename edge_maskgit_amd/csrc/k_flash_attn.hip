@@ -1,0 +1,173 @@
+// k_flash_attn.hip — fused self-attention with fp16 K/V (gfx950).
+//
+// Semantics: the reference's k_flash_attention_h (src/mg-opencl/mg-opencl.cpp:859-937) with
+// the CPU oracle k_flash_attention (src/mg-cpu/mg-cpu.cpp:211-239) for the math:
+//   per (batch b, head h, query s): q, k, v rounded to fp16; score_t = (q . k_t) * scale in
+//   fp32; softmax over keys in fp32 (online, max-subtracted); o = sum_t p_t v_t / sum_t p_t.
+// Inputs are strided {D, S, H, B} views (element strides st[0..3]); the reference passes
+// the q/k/v FC outputs [S*B][H*D] with st = {1, H*D, D, H*D*S} (mg-opencl.cpp:1493-1496).
+// The output strides are a parameter too, so the head merge that follows in the reference
+// graph (permute + cont, mg-transformer.cpp:84-85) is written directly.
+//
+// gfx950 mapping (one workgroup = 4 waves = 64 queries of one (b, h); keys in chunks of 64
+// staged once per workgroup in LDS as fp16):
+//  * Scores as S^T = K . Q^T on v_mfma_f32_16x16x16_f16: fp16 products are exact in fp32, so
+//    only the summation order differs from the reference. The S^T accumulator layout (lane
+//    = query, registers = 4 consecutive keys) is exactly the A-operand layout of the next
+//    product, so P . V needs no data exchange between lanes.
+//  * Softmax statistics per query in fp32 (max, running sum), cross-lane over the 4 lane
+//    groups; exp is the fp32 expf.
+//  * P . V on the same MFMA with P split into fp16 hi + lo parts (two instructions), so the
+//    fp32 probabilities are applied to ~2^-22 — the reference multiplies them in fp32.
+// LDS rows are padded (K: D+8 halves, V^T: 72 halves) so the fragment reads are
+// bank-conflict free.
+#include "mgh_common.h"
+#include "mgh_kernels.h"
+
+namespace mgh {
+
+namespace {
+
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int KT = 64;             // keys per LDS chunk
+constexpr int VLD = KT + 8;        // V^T row stride (halves)
+
+template <int DC>
+__global__ __launch_bounds__(256) void k_flash_attn_f16kv(FaArgs a) {
+    constexpr int D = 16 * DC;
+    constexpr int KLD = D + 8;     // K row stride (halves)
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[KT * KLD];
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[D * VLD];
+
+    const int S = a.S;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int q0w = blockIdx.x * 64 + wave * 16;
+    const bool active = q0w < S;
+    const int64_t base = (int64_t)b * a.st[3] + (int64_t)h * a.st[2];
+
+    // Q as the B operand: lane = query q0w + l16, k = d = 16c + 4lg + j
+    f16x4 qf[DC];
+    {
+        const int qi = min(q0w + l16, S - 1);
+#pragma unroll
+        for (int c = 0; c < DC; c++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                qf[c][j] = (_Float16)a.q[base + (int64_t)qi * a.st[1] + (int64_t)(16 * c + 4 * lg + j) * a.st[0]];
+    }
+
+    f32x4 O[DC];
+#pragma unroll
+    for (int c = 0; c < DC; c++) O[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;          // statistics of query q0w + l16
+
+    for (int k0 = 0; k0 < S; k0 += KT) {
+        __syncthreads();                   // the previous chunk is consumed
+        for (int idx = tid; idx < KT * D; idx += 256) {
+            const int key = idx / D, d = idx - key * D, t = k0 + key;
+            float kv = 0.f, vv = 0.f;
+            if (t < S) {
+                const int64_t off = base + (int64_t)t * a.st[1] + (int64_t)d * a.st[0];
+                kv = a.k[off];
+                vv = a.v[off];
+            }
+            Ks[key * KLD + d] = (_Float16)kv;
+            Vt[d * VLD + key] = (_Float16)vv;
+        }
+        __syncthreads();
+        if (!active) continue;
+
+        // scores: register r of subtile t holds key k0 + 16t + 4lg + r for query l16
+        f32x4 sc[KT / 16];
+#pragma unroll
+        for (int t = 0; t < KT / 16; t++) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < DC; c++) {
+                const f16x4 kf = *(const f16x4*)&Ks[(16 * t + l16) * KLD + 16 * c + 4 * lg];
+                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kf, qf[c], acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int key = k0 + 16 * t + 4 * lg + r;
+                sc[t][r] = key < S ? acc[r] * a.scale : -INFINITY;
+            }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < KT / 16; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) mx = fmaxf(mx, sc[t][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);
+        const float alpha = expf(m - mn);
+        float ps = 0.f;
+#pragma unroll
+        for (int t = 0; t < KT / 16; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float p = sc[t][r] == -INFINITY ? 0.f : expf(sc[t][r] - mn);
+                sc[t][r] = p;
+                ps += p;
+            }
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        l = alpha * l + ps;
+        m = mn;
+
+        // O rows are queries 4lg + r: rescale by that query's alpha (held by lane 4lg + r)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float ar = __shfl(alpha, 4 * lg + r);
+#pragma unroll
+            for (int c = 0; c < DC; c++) O[c][r] *= ar;
+        }
+        // O += P . V with P = hi + lo in fp16 (A operand: query l16, keys 16t + 4lg + j)
+#pragma unroll
+        for (int t = 0; t < KT / 16; t++) {
+            f16x4 ph, pl;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                ph[j] = (_Float16)sc[t][j];
+                pl[j] = (_Float16)(sc[t][j] - (float)ph[j]);
+            }
+#pragma unroll
+            for (int c = 0; c < DC; c++) {
+                const f16x4 vf = *(const f16x4*)&Vt[(16 * c + l16) * VLD + 16 * t + 4 * lg];
+                O[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vf, O[c], 0, 0, 0);
+                O[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vf, O[c], 0, 0, 0);
+            }
+        }
+    }
+    if (!active) return;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const float inv = 1.f / __shfl(l, 4 * lg + r);
+        const int qi = q0w + 4 * lg + r;
+        if (qi >= S) continue;
+        float* orow = a.o + (int64_t)b * a.os[3] + (int64_t)h * a.os[2] + (int64_t)qi * a.os[1];
+#pragma unroll
+        for (int c = 0; c < DC; c++) orow[(int64_t)(16 * c + l16) * a.os[0]] = O[c][r] * inv;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_flash_attn_f16kv(const FaArgs& a, int D, hipStream_t s) {
+    if (a.S <= 0 || a.H <= 0 || a.B <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((a.S + 63) / 64), (unsigned)a.H, (unsigned)a.B), block(256);
+    switch (D) {
+        case 16: hipLaunchKernelGGL(k_flash_attn_f16kv<1>, grid, block, 0, s, a); break;
+        case 32: hipLaunchKernelGGL(k_flash_attn_f16kv<2>, grid, block, 0, s, a); break;
+        case 48: hipLaunchKernelGGL(k_flash_attn_f16kv<3>, grid, block, 0, s, a); break;
+        case 64: hipLaunchKernelGGL(k_flash_attn_f16kv<4>, grid, block, 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace mgh

@@ -514,6 +514,102 @@ int mgh_gemm_q_f32in(mgh_ctx* c, int algo, int wtype, const void* w, int N, int 
     return MGH_OK;
 }
 
+int mgh_layernorm_affine(mgh_ctx* c, const float* x, const float* g, const float* b, int rows, int D,
+                         float eps, float* y, int emit, void* codes, float* dx, void* s4) {
+    if (!c) return MGH_ERR_ARG;
+    if (rows < 0 || D <= 0) return fail(c, MGH_ERR_ARG, "layernorm_affine: need rows >= 0, D > 0");
+    if (D % 256 || D > 2048) return fail(c, MGH_ERR_UNSUPPORTED, "layernorm_affine: needs D % 256 == 0 and D <= 2048");
+    if (emit < 0 || emit > 2) return fail(c, MGH_ERR_ARG, "layernorm_affine: emit must be 0, 1 or 2");
+    if (rows == 0) return MGH_OK;
+    if (!x || !g || !b || !y) return fail(c, MGH_ERR_ARG, "layernorm_affine: null pointer");
+    if (emit && (!codes || !dx || (emit == 1 && !s4)))
+        return fail(c, MGH_ERR_ARG, "layernorm_affine: emit needs d_codes, d_dx (and d_s4 for INT8)");
+    if (!aligned16(x) || !aligned16(y) || !aligned16(g) || !aligned16(b) || !aligned16(codes) ||
+        ((uintptr_t)dx & 3u) || ((uintptr_t)s4 & 3u))
+        return fail(c, MGH_ERR_ARG, "layernorm_affine: x/y/gamma/beta/codes must be 16-byte aligned");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_layernorm_affine(x, g, b, y, rows, D, eps, emit, codes, dx, s4, c->stream),
+            "k_layernorm_affine");
+    return MGH_OK;
+}
+
+int mgh_flash_attn_f16kv(mgh_ctx* c, const float* q, const float* k, const float* v,
+                         const int64_t st[4], int D, int S, int H, int B, float scale, float* o,
+                         const int64_t ost[4]) {
+    if (!c) return MGH_ERR_ARG;
+    if (S < 0 || H < 0 || B < 0) return fail(c, MGH_ERR_ARG, "flash_attn: negative shape");
+    if (D != 16 && D != 32 && D != 48 && D != 64)
+        return fail(c, MGH_ERR_UNSUPPORTED, "flash_attn: D must be 16, 32, 48 or 64");
+    if (S == 0 || H == 0 || B == 0) return MGH_OK;
+    if (!q || !k || !v || !o || !st) return fail(c, MGH_ERR_ARG, "flash_attn: null pointer");
+    if (H > 65535 || B > 65535) return fail(c, MGH_ERR_UNSUPPORTED, "flash_attn: H and B must be <= 65535");
+    if (int r = set_dev(c)) return r;
+    mgh::FaArgs a{};
+    a.q = q; a.k = k; a.v = v; a.o = o;
+    for (int i = 0; i < 4; i++) a.st[i] = st[i];
+    if (ost) {
+        for (int i = 0; i < 4; i++) a.os[i] = ost[i];
+    } else {
+        a.os[0] = 1; a.os[1] = D; a.os[2] = (int64_t)D * S; a.os[3] = (int64_t)D * S * H;
+    }
+    a.S = S; a.H = H; a.B = B; a.scale = scale;
+    MGH_HIP(c, mgh::launch_flash_attn_f16kv(a, D, c->stream), "k_flash_attn_f16kv");
+    return MGH_OK;
+}
+
+int mgh_gemm_f32(mgh_ctx* c, const float* w, int N, int K, const float* x, int M, const float* bias,
+                 int act, const float* resid, float* y) {
+    if (!c) return MGH_ERR_ARG;
+    if (N <= 0 || K <= 0 || M < 0) return fail(c, MGH_ERR_ARG, "gemm_f32: shape must have N>0, K>0, M>=0");
+    if (act < 0 || act > 2) return fail(c, MGH_ERR_ARG, "act must be 0 (none), 1 (gelu) or 2 (silu)");
+    if (K % 32) return fail(c, MGH_ERR_UNSUPPORTED, "gemm_f32: needs K % 32 == 0");
+    if (M == 0) return MGH_OK;
+    if (!w || !x || !y) return fail(c, MGH_ERR_ARG, "gemm_f32: null pointer");
+    if (!aligned16(w) || !aligned16(x)) return fail(c, MGH_ERR_ARG, "gemm_f32: w and x must be 16-byte aligned");
+    if (int r = set_dev(c)) return r;
+    mgh::GemmF32Args a{};
+    a.w = w; a.x = x; a.bias = bias; a.resid = resid; a.y = y;
+    a.M = M; a.N = N; a.K = K; a.act = act;
+    MGH_HIP(c, mgh::launch_gemm_f32(a, c->stream), "k_gemm_f32");
+    return MGH_OK;
+}
+
+int mgh_get_rows(mgh_ctx* c, const float* a, int64_t E, int64_t R, const int32_t* ids, int64_t n, float* out) {
+    if (!c) return MGH_ERR_ARG;
+    if (E < 0 || R <= 0 || n < 0) return fail(c, MGH_ERR_ARG, "get_rows: need E >= 0, R > 0, n >= 0");
+    if (n == 0 || E == 0) return MGH_OK;
+    if (n > 65535) return fail(c, MGH_ERR_UNSUPPORTED, "get_rows: at most 65535 rows per call");
+    if (!a || !ids || !out) return fail(c, MGH_ERR_ARG, "get_rows: null pointer");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_get_rows(a, E, R, ids, n, out, c->stream), "k_get_rows");
+    return MGH_OK;
+}
+
+int mgh_add(mgh_ctx* c, const float* a, const float* b, int64_t nb, float* out, int64_t n) {
+    if (!c) return MGH_ERR_ARG;
+    if (n < 0 || nb <= 0 || (n % nb)) return fail(c, MGH_ERR_ARG, "add: need nb > 0 dividing n");
+    if (n == 0) return MGH_OK;
+    if (!a || !b || !out) return fail(c, MGH_ERR_ARG, "add: null pointer");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_add_bcast(a, b, nb, out, n, c->stream), "k_add_bcast");
+    return MGH_OK;
+}
+
+int mgh_copy_strided(mgh_ctx* c, const float* a, const int64_t ne[4], const int64_t st[4], float* out) {
+    if (!c) return MGH_ERR_ARG;
+    if (!ne || !st) return fail(c, MGH_ERR_ARG, "copy_strided: null shape");
+    mgh::CopyArgs ca{};
+    for (int i = 0; i < 4; i++) {
+        if (ne[i] <= 0) return fail(c, MGH_ERR_ARG, "copy_strided: shape must be positive");
+        ca.ne[i] = ne[i];
+        ca.st[i] = st[i];
+    }
+    if (!a || !out) return fail(c, MGH_ERR_ARG, "copy_strided: null pointer");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_copy4d(a, ca, out, c->stream), "k_copy4d");
+    return MGH_OK;
+}
+
 int mgh_debug_block_dots(mgh_ctx* c, int wtype, const void* w, int N, int K, const int8_t* qx,
                          int M, int32_t* out) {
     if (!c) return MGH_ERR_ARG;

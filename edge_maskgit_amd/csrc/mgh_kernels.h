@@ -49,6 +49,49 @@ hipError_t launch_gemm_q_f16x(int wtype, const GemmArgs& a, bool debug_dots, hip
 // Streamed variant for K % 256 == 0 with 16-byte aligned qx/dx/sx/w (64x64 tiles).
 hipError_t launch_gemm_q_i8_s256(int wtype, const GemmArgs& a, bool debug_dots, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t s);
+
+// LayerNorm + affine over rows of D (D % 256 == 0, D <= 2048); emit 0: y only, 1: also the
+// int8-dot operand (fp16 codes, dx, int32 sx) of y, 2: also the dequant-fp16 operand
+// (fp16 y, unit dx, fp32 ux).
+hipError_t launch_layernorm_affine(const float* x, const float* gamma, const float* beta, float* y,
+                                   int rows, int D, float eps, int emit, void* codes, float* dx,
+                                   void* s4, hipStream_t s);
+
+// Flash attention with fp16 K/V over strided {D,S,H,B} views (element strides).
+struct FaArgs {
+    const float* q;
+    const float* k;
+    const float* v;
+    float* o;
+    int64_t st[4];         // q/k/v element strides for d, s, h, b
+    int64_t os[4];         // output element strides for d, s, h, b
+    int S, H, B;
+    float scale;
+};
+hipError_t launch_flash_attn_f16kv(const FaArgs& a, int D, hipStream_t s);
+
+// fp32 GEMM with the fused epilogue: y[M][N] = act(x[M][K] . w[N][K]^T + bias) + resid.
+struct GemmF32Args {
+    const float* w;
+    const float* x;
+    const float* bias;
+    const float* resid;
+    float* y;
+    int M, N, K;
+    int act;
+};
+hipError_t launch_gemm_f32(const GemmF32Args& a, hipStream_t s);
+
+// Graph glue: row gather, broadcast add, strided 4-D copy into a contiguous buffer.
+struct CopyArgs {
+    int64_t ne[4];         // output shape (contiguous)
+    int64_t st[4];         // source element strides
+};
+hipError_t launch_get_rows(const float* a, int64_t E, int64_t R, const int32_t* ids, int64_t n,
+                           float* out, hipStream_t s);
+hipError_t launch_add_bcast(const float* a, const float* b, int64_t nb, float* out, int64_t n,
+                            hipStream_t s);
+hipError_t launch_copy4d(const float* a, const CopyArgs& c, float* out, hipStream_t s);
 // Weight repack (k_pack_w.hip): raw Q8_0/Q4_K -> fp16 codes [N][K] | fp32 scale [K/32][N]
 // (| fp32 min [N][K/32] for Q4_K).
 size_t packed_weight_bytes(int wtype, int64_t N, int64_t K);

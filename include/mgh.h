@@ -145,6 +145,47 @@ int mgh_gemm_q_f32in(mgh_ctx* ctx, int algo, int wtype, const void* d_w, int N, 
                      const float* d_x, int M, const float* d_bias, int act,
                      const float* d_resid, float* d_y);
 
+/* LayerNorm-affine output modes: what else mgh_layernorm_affine writes besides y */
+enum { MGH_EMIT_NONE = 0, MGH_EMIT_INT8 = 1, MGH_EMIT_DEQ_F16 = 2 };
+
+/* ---- LayerNorm + affine over rows: replaces the Norm(affine) node and its dispatch
+ *      (k_norm_affine mg-opencl.cpp:705-727, 1450-1465; CPU mg-cpu.cpp:105-121, 249-261).
+ *      x, y [rows][D] fp32 (may alias), gamma/beta [D]; D % 256 == 0, D <= 2048; 16-byte
+ *      aligned x/y/gamma/beta/codes. Statistics in double, as the reference CPU executor.
+ *      emit = MGH_EMIT_INT8 also writes the next GEMM's operand for y (as
+ *      mgh_quantize_act_q8_codes16): d_codes fp16 codes [rows][D], d_dx fp32 and d_s4 int32
+ *      [rows][D/32]; MGH_EMIT_DEQ_F16 writes fp16-rounded y, unit d_dx and fp32 block sums
+ *      in d_s4 (nullable). No reference counterpart for the fused operand (the reference
+ *      quantizes in a separate k_quantize_q8 dispatch, mg-opencl.cpp:1381-1389). ---- */
+int mgh_layernorm_affine(mgh_ctx* ctx, const float* d_x, const float* d_gamma, const float* d_beta,
+                         int rows, int D, float eps, float* d_y, int emit, void* d_codes,
+                         float* d_dx, void* d_s4);
+
+/* ---- flash attention with fp16 K/V: replaces k_flash_attention_h and its dispatch
+ *      (mg-opencl.cpp:859-937, 1483-1511). q/k/v are {D,S,H,B} views with element strides
+ *      strides[4] (d, s, h, b); the output has element strides o_strides[4], or is the
+ *      contiguous {D,S,H,B} tensor when o_strides is NULL. D in {16, 32, 48, 64}. ---- */
+int mgh_flash_attn_f16kv(mgh_ctx* ctx, const float* d_q, const float* d_k, const float* d_v,
+                         const int64_t strides[4], int D, int S, int H, int B, float scale,
+                         float* d_o, const int64_t o_strides[4]);
+
+/* ---- fp32 GEMM with the fused epilogue (tied MLM head, F32 FC weights): replaces
+ *      k_mul_mat_t and its dispatch (mg-opencl.cpp:60-94, 1429-1440).
+ *      y[M][N] = act(x . w^T + bias) + resid; w [N][K], x [M][K]; K % 32 == 0, 16-byte
+ *      aligned w and x. ---- */
+int mgh_gemm_f32(mgh_ctx* ctx, const float* d_w, int N, int K, const float* d_x, int M,
+                 const float* d_bias, int act, const float* d_resid, float* d_y);
+
+/* ---- graph glue: GetRows (k_get_rows mg-opencl.cpp:667-672; negative ids count from the end,
+ *      out-of-range ids are clamped), Add with a repeating second operand (out[i] = a[i] +
+ *      b[i % nb]), and the Cont of a strided view into a contiguous {ne0..ne3} buffer
+ *      (k_cont mg-opencl.cpp:940-945). ---- */
+int mgh_get_rows(mgh_ctx* ctx, const float* d_a, int64_t E, int64_t R, const int32_t* d_ids,
+                 int64_t n, float* d_out);
+int mgh_add(mgh_ctx* ctx, const float* d_a, const float* d_b, int64_t nb, float* d_out, int64_t n);
+int mgh_copy_strided(mgh_ctx* ctx, const float* d_a, const int64_t ne[4], const int64_t strides[4],
+                     float* d_out);
+
 /* ---- debug: the int32 per-block dot products exactly as the production GEMM's MFMA
  *      computes them, out[m][n][t] (t = K/32 blocks). The reference has no counterpart;
  *      it exposes the quantity mg-opencl.cpp:472-478 / :571-576 accumulates. ---- */
