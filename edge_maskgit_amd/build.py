@@ -8,6 +8,7 @@ Objects go to edge_maskgit_amd/_build/, libraries to edge_maskgit_amd/lib/.
 """
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
@@ -35,7 +36,10 @@ EXTRA_FLAGS = {"k_gemm_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
                "k_gemm_i8_stream.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
                "k_gemm_q_f16x.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
                "k_gemm_qp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
-HOST_SOURCES = []
+# C++ host runtime (graph API mirror, GGUF loader, transformer builder, HipRuntime, mgr C ABI):
+# plain host code over the libmgh C ABI, compiled with g++ into lib/libmg_hip.so.
+HOST_SOURCES = ["mg-tensor.cpp", "mg-model.cpp", "mg-transformer.cpp", "mg-hip.cpp", "mgr_api.cpp"]
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-parameter"]
 
 
 def hipcc() -> str:
@@ -80,28 +84,32 @@ def build(verbose: bool = False, force: bool = True) -> None:
     cc = hipcc()
     hdrs = _headers()
     inc = ["-I" + os.path.join(ROOT, "include"), "-I" + CSRC, "-I" + HOST]
+    jobs = []
     objs = []
     for src in KERNEL_SOURCES:
         s = os.path.join(CSRC, src)
         o = os.path.join(OBJ, src + ".o")
         if force or _stale(o, [s] + hdrs):
-            _run([cc, *HIP_FLAGS, *EXTRA_FLAGS.get(src, []), *inc, "-c", s, "-o", o], verbose)
+            jobs.append([cc, *HIP_FLAGS, *EXTRA_FLAGS.get(src, []), *inc, "-c", s, "-o", o])
         objs.append(o)
+    hobjs = []
+    for src in HOST_SOURCES:
+        s = os.path.join(HOST, src)
+        o = os.path.join(OBJ, src + ".o")
+        if force or _stale(o, [s] + hdrs):
+            jobs.append([shutil.which("g++") or "g++", *HOST_FLAGS, *inc, "-c", s, "-o", o])
+        hobjs.append(o)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as ex:
+        for f in [ex.submit(_run, j, verbose) for j in jobs]:
+            f.result()
     libmgh = os.path.join(LIB, "libmgh.so")
     tmp = libmgh + ".tmp"
     _run([cc, *HIP_FLAGS, "-shared", "-o", tmp, *objs], verbose)
     os.replace(tmp, libmgh)
     if HOST_SOURCES:
-        hobjs = []
-        for src in HOST_SOURCES:
-            s = os.path.join(HOST, src)
-            o = os.path.join(OBJ, src + ".o")
-            if force or _stale(o, [s] + hdrs):
-                _run([cc, *HIP_FLAGS, *inc, "-c", s, "-o", o], verbose)
-            hobjs.append(o)
         libmg = os.path.join(LIB, "libmg_hip.so")
         tmp = libmg + ".tmp"
-        _run([cc, *HIP_FLAGS, "-shared", "-o", tmp, *hobjs, "-L" + LIB, "-lmgh",
+        _run([shutil.which("g++") or "g++", "-shared", "-o", tmp, *hobjs, "-L" + LIB, "-lmgh",
               "-Wl,-rpath,$ORIGIN"], verbose)
         os.replace(tmp, libmg)
 

@@ -1,0 +1,415 @@
+// mg-hip.cpp — HipRuntime: the graph walker of the MI355X backend (the role of the
+// reference's OpenCLRuntime::compute, src/mg-opencl/mg-opencl.cpp:1354-1656), built on the
+// libmgh C ABI (include/mgh.h).
+//
+// Per compute():
+//  1. Plan: every node's storage root (views alias their source), each root's last consumer,
+//     the LayerNorm nodes whose output feeds int8-dot FC layers (fused operand), and the
+//     flash-attention -> permute -> cont chains (attention writes the merged layout).
+//  2. Run the nodes in order; device buffers of computed roots come from a size-bucketed
+//     pool and return to it after their last consumer.
+//  3. Copy the final node to its host data and wait (the reference's readback, :1622-1642).
+// Leaves are uploaded once per (host address, byte size) and kept; quantized weights are
+// packed on upload (mgh_pack_weights). Supported ops: MulMat (Q8_0, Q4_K, F32 weights),
+// Norm (plain or affine), FlashAttention, GetRows, Add, Cont, Reshape, View, Permute.
+#include "mg-hip.hpp"
+
+#include <algorithm>
+#include <cstring>
+#include <map>
+#include <stdexcept>
+#include <tuple>
+#include <unordered_map>
+
+#include "mgh.h"
+
+namespace mg {
+
+namespace {
+
+bool is_view_op(Op op) { return op == Op::Reshape || op == Op::View || op == Op::Permute; }
+
+const char* op_name(const Tensor* t) {
+    switch (t->op) {
+        case Op::MulMat:
+            return (t->src[0]->type == Type::Q8_0 || t->src[0]->type == Type::Q4_K) ? "MulMat(q)" : "MulMat(f32)";
+        case Op::Norm: return "Norm";
+        case Op::FlashAttention: return "FlashAttention";
+        case Op::GetRows: return "GetRows";
+        case Op::Add: return "Add";
+        case Op::Cont: return "Cont";
+        default: return "Other";
+    }
+}
+
+}  // namespace
+
+struct HipRuntime::Impl {
+    mgh_ctx* ctx = nullptr;
+    std::string name;
+    int algo = MGH_ALGO_INT8;
+    bool profiling = false;
+    std::map<std::string, std::pair<int, double>> prof;
+
+    // leaf uploads: (host address, bytes, packed?) -> device pointer
+    std::map<std::tuple<const void*, size_t, int>, void*> leaves;
+    // free device buffers by size
+    std::multimap<size_t, void*> pool;
+    // unit gamma / zero beta per D for plain Norm nodes
+    std::map<int64_t, std::pair<void*, void*>> unit_affine;
+
+    // per-compute state
+    std::unordered_map<const Tensor*, void*> addr;            // device address of a tensor
+    struct Codes { void* q = nullptr; void* dx = nullptr; void* sx = nullptr; size_t bytes = 0; };
+    std::unordered_map<const Tensor*, Codes> codes;           // fused int8-dot operand of a Norm node
+
+    void check(int rc) {
+        if (rc != MGH_OK) throw std::runtime_error(std::string("HipRuntime: ") + mgh_last_error(ctx));
+    }
+
+    void* take(size_t bytes) {
+        bytes = (bytes + 255) & ~(size_t)255;
+        auto it = pool.lower_bound(bytes);
+        if (it != pool.end() && it->first <= bytes + bytes / 4) {  // reuse a buffer up to 25% larger
+            void* p = it->second;
+            pool.erase(it);
+            return p;
+        }
+        void* p = nullptr;
+        check(mgh_alloc(ctx, bytes, &p));
+        alloc_size[p] = bytes;
+        return p;
+    }
+    void give(void* p) { pool.emplace(alloc_size.at(p), p); }
+    std::unordered_map<void*, size_t> alloc_size;
+
+    void* upload_leaf(const Tensor* t, bool packed) {
+        const size_t n = t->nbytes();
+        const auto key = std::make_tuple((const void*)t->data, n, packed ? (int)t->type : -1);
+        const auto it = leaves.find(key);
+        if (it != leaves.end()) return it->second;
+        if (!t->data) throw std::runtime_error("HipRuntime: leaf '" + t->name + "' has no host data");
+        void* raw = nullptr;
+        check(mgh_alloc(ctx, n, &raw));
+        check(mgh_h2d(ctx, raw, t->data, n));
+        void* d = raw;
+        if (packed) {
+            const int wt = t->type == Type::Q8_0 ? MGH_WTYPE_Q8_0 : MGH_WTYPE_Q4_K;
+            const int K = (int)t->ne[0], N = (int)(t->nelements() / t->ne[0]);
+            const size_t pb = mgh_packed_weight_bytes(wt, N, K);
+            if (!pb) throw std::runtime_error("HipRuntime: unsupported quantized weight shape for '" + t->name + "'");
+            check(mgh_alloc(ctx, pb, &d));
+            check(mgh_pack_weights(ctx, wt, raw, N, K, d));
+            check(mgh_free(ctx, raw));
+        }
+        leaves[key] = d;
+        return d;
+    }
+
+    const Tensor* root(const Tensor* t) const {
+        while (is_view_op(t->op)) t = t->src[0];
+        return t;
+    }
+
+    void* dev(const Tensor* t) {
+        if (!t) return nullptr;
+        const Tensor* r = root(t);
+        if (r->op == Op::None) {
+            const auto it = addr.find(r);
+            if (it != addr.end()) return it->second;
+            void* d = upload_leaf(r, false);
+            addr[r] = d;
+            return d;
+        }
+        const auto it = addr.find(r);
+        if (it == addr.end()) throw std::runtime_error("HipRuntime: node used before it was computed");
+        return it->second;
+    }
+
+    static void elem_strides(const Tensor* t, int64_t st[4]) {
+        const size_t es = type_size(t->type);
+        for (int i = 0; i < 4; i++) st[i] = (int64_t)(t->nb[i] / es);
+    }
+
+    std::pair<void*, void*> unit(int64_t D) {
+        auto it = unit_affine.find(D);
+        if (it != unit_affine.end()) return it->second;
+        std::vector<float> one((size_t)D, 1.0f), zero((size_t)D, 0.0f);
+        void *g = nullptr, *b = nullptr;
+        check(mgh_alloc(ctx, (size_t)D * 4, &g));
+        check(mgh_alloc(ctx, (size_t)D * 4, &b));
+        check(mgh_h2d(ctx, g, one.data(), (size_t)D * 4));
+        check(mgh_h2d(ctx, b, zero.data(), (size_t)D * 4));
+        return unit_affine[D] = {g, b};
+    }
+};
+
+HipRuntime::HipRuntime() : HipRuntime(0) {}
+
+HipRuntime::HipRuntime(int device) : p_(new Impl()) {
+    if (mgh_create(device, &p_->ctx) != MGH_OK)
+        throw std::runtime_error("HipRuntime: no gfx950 device at ordinal " + std::to_string(device));
+    p_->name = mgh_device_name(p_->ctx);
+}
+
+HipRuntime::~HipRuntime() {
+    if (!p_ || !p_->ctx) return;
+    mgh_sync(p_->ctx);
+    for (auto& kv : p_->leaves) mgh_free(p_->ctx, kv.second);
+    for (auto& kv : p_->pool) mgh_free(p_->ctx, kv.second);
+    for (auto& kv : p_->unit_affine) {
+        mgh_free(p_->ctx, kv.second.first);
+        mgh_free(p_->ctx, kv.second.second);
+    }
+    mgh_destroy(p_->ctx);
+}
+
+const std::string& HipRuntime::device_name() const { return p_->name; }
+
+void HipRuntime::invalidate(Tensor* t) {
+    if (!t) return;
+    for (auto it = p_->leaves.begin(); it != p_->leaves.end();) {
+        if (std::get<0>(it->first) == t->data) {
+            mgh_free(p_->ctx, it->second);
+            it = p_->leaves.erase(it);
+        } else {
+            ++it;
+        }
+    }
+}
+
+bool HipRuntime::import_host_region(void*, size_t) { return false; }
+
+void HipRuntime::profile_enable(bool on) { p_->profiling = on; }
+void HipRuntime::profile_reset() { p_->prof.clear(); }
+std::vector<OpProfile> HipRuntime::profile_report() const {
+    std::vector<OpProfile> r;
+    for (auto& kv : p_->prof) r.push_back({kv.first, kv.second.first, kv.second.second});
+    std::sort(r.begin(), r.end(), [](const OpProfile& a, const OpProfile& b) { return a.ms > b.ms; });
+    return r;
+}
+
+void HipRuntime::set_quant_algo(int algo) {
+    if (algo != MGH_ALGO_INT8 && algo != MGH_ALGO_DEQ_F16)
+        throw std::runtime_error("HipRuntime: quant algo must be 1 (int8) or 2 (dequant-fp16)");
+    p_->algo = algo;
+}
+
+void HipRuntime::compute(Graph& g) {
+    Impl& I = *p_;
+    if (g.nodes.empty()) return;
+    I.addr.clear();
+    I.codes.clear();
+    const int n = (int)g.nodes.size();
+    auto quant = [](const Tensor* w) { return w->type == Type::Q8_0 || w->type == Type::Q4_K; };
+
+    // ---- plan ----
+    std::unordered_map<const Tensor*, int> last;               // root -> last consumer index
+    std::unordered_map<const Tensor*, int> fc_uses, other_uses;  // Norm root -> consumer kinds
+    for (int i = 0; i < n; i++) {
+        const Tensor* t = g.nodes[i];
+        for (const Tensor* s : t->src) {
+            if (!s) continue;
+            const Tensor* r = I.root(s);
+            last[r] = i;
+            if (r->op == Op::Norm && !is_view_op(t->op)) {
+                if (t->op == Op::MulMat && s == t->src[1] && quant(t->src[0])) fc_uses[r]++;
+                else other_uses[r]++;
+            }
+        }
+    }
+    // flash attention -> permute(0,2,1,3) -> cont: the attention writes the cont's buffer
+    std::unordered_map<const Tensor*, const Tensor*> fa_into;  // cont -> its FA source
+    {
+        std::unordered_map<const Tensor*, int> uses;
+        for (const Tensor* t : g.nodes)
+            for (const Tensor* s : t->src)
+                if (s) uses[s]++;
+        for (const Tensor* t : g.nodes) {
+            if (t->op != Op::Cont) continue;
+            const Tensor* p = t->src[0];
+            if (p->op != Op::Permute || !p->src[0] || p->src[0]->op != Op::FlashAttention) continue;
+            const Tensor* fa = p->src[0];
+            if (uses[fa] == 1 && uses[p] == 1 && fa->type == Type::F32) fa_into[t] = fa;
+        }
+    }
+    std::unordered_map<const Tensor*, const Tensor*> fa_target;  // FA -> cont it writes
+    for (auto& kv : fa_into) fa_target[kv.second] = kv.first;
+
+    // ---- run ----
+    for (int i = 0; i < n; i++) {
+        Tensor* t = g.nodes[i];
+        if (is_view_op(t->op)) continue;
+        if (t->type != Type::F32 && t->op != Op::GetRows)
+            throw std::runtime_error("HipRuntime: only F32 results are supported");
+        if (I.profiling) I.check(mgh_timer_start(I.ctx));
+
+        void* out = nullptr;
+        if (t->op == Op::Cont && fa_into.count(t)) {
+            out = I.dev(fa_into.at(t));                         // written by the attention
+            I.addr[t] = out;
+        } else if (t->op == Op::FlashAttention && fa_target.count(t)) {
+            out = I.take(fa_target.at(t)->nbytes());
+            I.addr[fa_target.at(t)] = out;
+            I.addr[t] = out;
+        } else {
+            out = I.take(t->nbytes());
+            I.addr[t] = out;
+        }
+
+        switch (t->op) {
+            case Op::MulMat: {
+                const Tensor* w = t->src[0];
+                const Tensor* x = t->src[1];
+                if (x->type != Type::F32 || !x->is_contiguous())
+                    throw std::runtime_error("HipRuntime: MulMat needs a contiguous F32 input");
+                const int K = (int)w->ne[0], N = (int)w->ne[1];
+                const int M = (int)(x->nelements() / K);     // batch flattened into M
+                const float* bias = (const float*)I.dev(t->src[2]);
+                const float* resid = (const float*)I.dev(t->src[3]);
+                const int act = t->iparam[0];
+                if (quant(w)) {
+                    void* wp = I.upload_leaf(w, true);
+                    const auto c = I.codes.find(I.root(x));
+                    if (c != I.codes.end())
+                        I.check(mgh_gemm_q_packed(I.ctx, w->type == Type::Q8_0 ? MGH_WTYPE_Q8_0 : MGH_WTYPE_Q4_K,
+                                                  wp, N, K, (const uint16_t*)c->second.q, (const float*)c->second.dx,
+                                                  (const int32_t*)c->second.sx, M, bias, act, resid, (float*)out));
+                    else
+                        I.check(mgh_gemm_q_packed_f32in(I.ctx, I.algo,
+                                                        w->type == Type::Q8_0 ? MGH_WTYPE_Q8_0 : MGH_WTYPE_Q4_K, wp,
+                                                        N, K, (const float*)I.dev(x), M, bias, act, resid,
+                                                        (float*)out));
+                } else if (w->type == Type::F32) {
+                    I.check(mgh_gemm_f32(I.ctx, (const float*)I.dev(w), N, K, (const float*)I.dev(x), M, bias,
+                                         act, resid, (float*)out));
+                } else {
+                    throw std::runtime_error("HipRuntime: unsupported MulMat weight type");
+                }
+                break;
+            }
+            case Op::Norm: {
+                const Tensor* x = t->src[0];
+                const int D = (int)t->ne[0];
+                const int rows = (int)(t->nelements() / D);
+                const float* gm = (const float*)I.dev(t->src[1]);
+                const float* bt = (const float*)I.dev(t->src[2]);
+                if (!t->src[1] || !t->src[2]) {
+                    const auto u = I.unit(D);
+                    gm = (const float*)u.first;
+                    bt = (const float*)u.second;
+                }
+                int emit = MGH_EMIT_NONE;
+                Impl::Codes cd;
+                // one int8-dot operand for every quantized FC that reads this LN (flat 32-blocks,
+                // so any FC row length that is a multiple of 32 reads the same codes)
+                if (I.algo == MGH_ALGO_INT8 && fc_uses.count(t)) {
+                    emit = MGH_EMIT_INT8;
+                    const size_t T = (size_t)D / 32;
+                    cd.q = I.take((size_t)rows * D * 2);
+                    cd.dx = I.take((size_t)rows * T * 4);
+                    cd.sx = I.take((size_t)rows * T * 4);
+                }
+                I.check(mgh_layernorm_affine(I.ctx, (const float*)I.dev(x), gm, bt, rows, D, t->fparam[0],
+                                             (float*)out, emit, cd.q, (float*)cd.dx, cd.sx));
+                if (emit) I.codes[t] = cd;
+                break;
+            }
+            case Op::FlashAttention: {
+                const Tensor* q = t->src[0];
+                int64_t st[4], sk[4], sv[4];
+                Impl::elem_strides(q, st);
+                Impl::elem_strides(t->src[1], sk);
+                Impl::elem_strides(t->src[2], sv);
+                if (!std::equal(st, st + 4, sk) || !std::equal(st, st + 4, sv))
+                    throw std::runtime_error("HipRuntime: FlashAttention needs q, k, v with equal strides");
+                const int D = (int)q->ne[0], S = (int)q->ne[1], H = (int)q->ne[2], B = (int)q->ne[3];
+                int64_t ost[4];
+                const int64_t* po = nullptr;
+                if (fa_target.count(t)) {
+                    // output element (d, s, h, b) at its place in the permuted-then-contiguous
+                    // layout {D, H, S, B}
+                    ost[0] = 1; ost[1] = (int64_t)D * H; ost[2] = D; ost[3] = (int64_t)D * H * S;
+                    po = ost;
+                }
+                I.check(mgh_flash_attn_f16kv(I.ctx, (const float*)I.dev(q), (const float*)I.dev(t->src[1]),
+                                             (const float*)I.dev(t->src[2]), st, D, S, H, B, t->fparam[0],
+                                             (float*)out, po));
+                break;
+            }
+            case Op::GetRows: {
+                const Tensor* a = t->src[0];
+                const Tensor* ids = t->src[1];
+                if (a->type != Type::F32 || ids->type != Type::I32 || !a->is_contiguous() || !ids->is_contiguous())
+                    throw std::runtime_error("HipRuntime: GetRows needs an F32 table and I32 ids");
+                I.check(mgh_get_rows(I.ctx, (const float*)I.dev(a), a->ne[0], a->nelements() / a->ne[0],
+                                     (const int32_t*)I.dev(ids), ids->nelements(), (float*)out));
+                break;
+            }
+            case Op::Add: {
+                const Tensor* a = t->src[0];
+                const Tensor* b = t->src[1];
+                if (!a->is_contiguous() || !b->is_contiguous() || a->nelements() % b->nelements())
+                    throw std::runtime_error("HipRuntime: Add needs contiguous operands with a repeating second one");
+                I.check(mgh_add(I.ctx, (const float*)I.dev(a), (const float*)I.dev(b), b->nelements(), (float*)out,
+                                a->nelements()));
+                break;
+            }
+            case Op::Cont: {
+                if (fa_into.count(t)) break;                       // already written
+                int64_t st[4];
+                Impl::elem_strides(t->src[0], st);
+                const int64_t ne[4] = {t->ne[0], t->ne[1], t->ne[2], t->ne[3]};
+                I.check(mgh_copy_strided(I.ctx, (const float*)I.dev(t->src[0]), ne, st, (float*)out));
+                break;
+            }
+            default:
+                throw std::runtime_error(std::string("HipRuntime: unsupported op ") + std::to_string((int)t->op));
+        }
+
+        if (I.profiling) {
+            float ms = 0.f;
+            I.check(mgh_timer_stop(I.ctx, &ms));
+            auto& e = I.prof[op_name(t)];
+            e.first++;
+            e.second += ms;
+        }
+        // release roots whose last consumer was this node (never the final output)
+        for (const Tensor* s : t->src) {
+            if (!s) continue;
+            const Tensor* r = I.root(s);
+            if (r->op == Op::None || r == g.nodes.back() || last.at(r) != i) continue;
+            const auto a = I.addr.find(r);
+            if (a == I.addr.end() || !a->second) continue;
+            if (fa_target.count(r)) continue;                      // shares the cont's buffer
+            I.give(a->second);
+            a->second = nullptr;
+            const auto c = I.codes.find(r);
+            if (c != I.codes.end()) {
+                I.give(c->second.q);
+                I.give(c->second.dx);
+                I.give(c->second.sx);
+                I.codes.erase(c);
+            }
+        }
+    }
+
+    Tensor* outp = g.nodes.back();
+    const Tensor* ro = I.root(outp);
+    if (!outp->data) throw std::runtime_error("HipRuntime: output node has no host storage");
+    I.check(mgh_d2h(I.ctx, outp->data, I.dev(ro), outp->nbytes()));
+    for (auto& kv : I.addr)                                        // computed buffers back to the pool
+        if (kv.first->op != Op::None && kv.second && !fa_target.count(kv.first)) {
+            I.give(kv.second);
+            kv.second = nullptr;
+        }
+    for (auto& kv : I.codes) {
+        I.give(kv.second.q);
+        I.give(kv.second.dx);
+        I.give(kv.second.sx);
+    }
+    I.codes.clear();
+    I.addr.clear();
+}
+
+}  // namespace mg

@@ -1,0 +1,161 @@
+// mgr_api.cpp — C entry points (include/mgr.h) over Model + build_transformer + HipRuntime.
+#include "mgr.h"
+
+#include <cstdio>
+#include <cstring>
+#include <exception>
+#include <memory>
+#include <string>
+
+#include "mg-hip.hpp"
+#include "mg-model.hpp"
+#include "mg-transformer.hpp"
+
+namespace {
+thread_local std::string g_err;
+
+int fail(const std::exception& e) {
+    g_err = e.what();
+    return -1;
+}
+}  // namespace
+
+struct mgr_model {
+    std::unique_ptr<mg::Context> wctx;     // weight tensors (externals over the mmap)
+    std::unique_ptr<mg::Model> model;
+    std::unique_ptr<mg::HipRuntime> rt;
+    std::unique_ptr<mg::Context> gctx;     // per-forward graph; host data only for the output
+    size_t gctx_bytes = 0;
+};
+
+extern "C" {
+
+const char* mgr_last_error(void) { return g_err.c_str(); }
+
+int mgr_load(const char* path, int device, int algo, mgr_model** out) {
+    if (!path || !out) {
+        g_err = "mgr_load: null argument";
+        return -1;
+    }
+    try {
+        std::unique_ptr<mgr_model> m(new mgr_model());
+        m->wctx.reset(new mg::Context(16 << 20));
+        m->model = mg::Model::load(path, *m->wctx);
+        m->rt.reset(new mg::HipRuntime(device));
+        if (algo) m->rt->set_quant_algo(algo);
+        *out = m.release();
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e);
+    }
+}
+
+void mgr_free(mgr_model* m) { delete m; }
+
+int mgr_hparams(const mgr_model* m, int32_t o[7]) {
+    if (!m || !o) return -1;
+    const mg::HParams& h = m->model->hparams();
+    o[0] = h.n_layer; o[1] = h.n_head; o[2] = h.n_embd; o[3] = h.head_dim;
+    o[4] = h.vocab_size; o[5] = h.n_positions; o[6] = h.mask_token_id;
+    return 0;
+}
+
+const char* mgr_device_name(const mgr_model* m) { return m ? m->rt->device_name().c_str() : ""; }
+
+int mgr_forward(mgr_model* m, const int32_t* tokens, int S, int B, float* logits) {
+    if (!m || !tokens || S <= 0 || B <= 0) {
+        g_err = "mgr_forward: bad argument";
+        return -1;
+    }
+    try {
+        const mg::HParams& h = m->model->hparams();
+        // graph nodes keep host storage (the reference's Context semantics); the arena is
+        // not zero-filled, so only the token ids and the logits pages are ever touched
+        // per token: each layer's 10 n_embd-wide nodes and its n_ffn-wide node, 5 more
+        // n_embd-wide nodes around the layers and the logits (32-byte alignment slack)
+        const size_t per_tok = (size_t)h.n_layer * (10 * (size_t)h.n_embd + (size_t)h.n_ffn) +
+                               5 * (size_t)h.n_embd + (size_t)h.vocab_size;
+        const size_t need = (size_t)S * B * per_tok * 4 + (size_t)(h.n_layer * 16 + 16) * 64 + (64u << 20);
+        if (!m->gctx || m->gctx_bytes < need) {
+            m->gctx.reset(new mg::Context(need));
+            m->gctx_bytes = need;
+        }
+        m->gctx->reset();
+        mg::Tensor* tok = m->gctx->tensor2d(mg::Type::I32, S, B);
+        std::memcpy(tok->data, tokens, (size_t)S * B * sizeof(int32_t));
+        mg::Tensor* out = mg::build_transformer(*m->gctx, *m->model, tok);
+        mg::Graph g;
+        g.build_forward(out);
+        m->rt->invalidate(tok);               // new token ids at a reused host address
+        m->rt->compute(g);
+        if (logits) std::memcpy(logits, out->data, out->nbytes());
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e);
+    }
+}
+
+int mgr_profile_enable(mgr_model* m, int on) {
+    if (!m) return -1;
+    m->rt->profile_enable(on != 0);
+    m->rt->profile_reset();
+    return 0;
+}
+
+int mgr_profile_report(const mgr_model* m, char* buf, size_t cap) {
+    if (!m || !buf || !cap) return -1;
+    std::string s;
+    for (const mg::OpProfile& p : m->rt->profile_report()) {
+        char line[160];
+        std::snprintf(line, sizeof line, "%s %d %.4f\n", p.op.c_str(), p.count, p.ms);
+        s += line;
+    }
+    std::snprintf(buf, cap, "%s", s.c_str());
+    return 0;
+}
+
+int mgr_gguf_info(const char* path, int32_t o[7], int64_t* n_tensors) {
+    if (!path || !o) {
+        g_err = "mgr_gguf_info: null argument";
+        return -1;
+    }
+    try {
+        mg::Context c(16 << 20);
+        auto m = mg::Model::load(path, c);
+        const mg::HParams& h = m->hparams();
+        o[0] = h.n_layer; o[1] = h.n_head; o[2] = h.n_embd; o[3] = h.head_dim;
+        o[4] = h.vocab_size; o[5] = h.n_positions; o[6] = h.mask_token_id;
+        if (n_tensors) *n_tensors = (int64_t)m->n_tensors();
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e);
+    }
+}
+
+int mgr_graph_stats(const char* path, int S, int B, int32_t counts[32]) {
+    if (!path || !counts || S <= 0 || B <= 0) {
+        g_err = "mgr_graph_stats: bad argument";
+        return -1;
+    }
+    try {
+        mg::Context wc(16 << 20);
+        auto m = mg::Model::load(path, wc);
+        const mg::HParams& h = m->hparams();
+        const size_t per_tok = (size_t)h.n_layer * (10 * (size_t)h.n_embd + (size_t)h.n_ffn) +
+                               5 * (size_t)h.n_embd + (size_t)h.vocab_size;
+        // node storage is reserved, never touched (the arena is not zero-filled)
+        mg::Context big((size_t)S * B * per_tok * 4 + (64u << 20));
+        mg::Tensor* tok2 = big.tensor2d(mg::Type::I32, S, B);
+        std::memset(tok2->data, 0, (size_t)S * B * 4);
+        mg::Tensor* out = mg::build_transformer(big, *m, tok2);
+        mg::Graph g;
+        g.build_forward(out);
+        for (int i = 0; i < 32; i++) counts[i] = 0;
+        for (const mg::Tensor* t : g.nodes) counts[(int)t->op & 31]++;
+        return (int)g.nodes.size();
+    } catch (const std::exception& e) {
+        return fail(e);
+    }
+}
+
+}  // extern "C"

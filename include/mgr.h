@@ -1,0 +1,47 @@
+/* mgr.h — C entry points of the MI355X MaskGIT transformer runtime (lib/libmg_hip.so).
+ *
+ * A model handle owns a GGUF file (mg::Model::load), a HipRuntime and the graph context; a
+ * forward builds the reference's transformer graph (mg::build_transformer,
+ * src/mg-transformer.cpp:32-111) for the given tokens and runs it on the GPU — the path of
+ * the reference's TransformerFwd hook (include/mg-generate.hpp:15, tools/main.cpp:122-130).
+ * Status codes: 0 = OK, negative = error with mgr_last_error() set (per thread).
+ */
+#ifndef MGR_H
+#define MGR_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mgr_model mgr_model;
+
+/* algo: 1 = int8-dot FC (default), 2 = dequantized weights x fp16 activations */
+int mgr_load(const char* gguf_path, int device, int algo, mgr_model** out);
+void mgr_free(mgr_model* m);
+const char* mgr_last_error(void);
+/* n_layer, n_head, n_embd, head_dim, vocab_size, n_positions, mask_token_id */
+int mgr_hparams(const mgr_model* m, int32_t out[7]);
+const char* mgr_device_name(const mgr_model* m);
+
+/* tokens [B][S] (I32) -> logits [B][S][vocab_size] (fp32, host). logits may be NULL: the
+ * forward then runs without the final readback. */
+int mgr_forward(mgr_model* m, const int32_t* tokens, int S, int B, float* logits);
+
+/* per-op device-time profile of the following forwards (each node timed on its own) */
+int mgr_profile_enable(mgr_model* m, int on);
+/* writes up to cap rows "name count ms\n" into buf (NUL-terminated) */
+int mgr_profile_report(const mgr_model* m, char* buf, size_t cap);
+
+/* ---- host-only inspection (no device needed) ---- */
+/* parse a GGUF file: hparams as in mgr_hparams, and the tensor count */
+int mgr_gguf_info(const char* gguf_path, int32_t hparams_out[7], int64_t* n_tensors);
+/* build the forward graph for S x B tokens and count its nodes per op code
+ * (counts[op] for op in 0..31, mg::Op values); returns the node count or < 0 */
+int mgr_graph_stats(const char* gguf_path, int S, int B, int32_t counts[32]);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MGR_H */

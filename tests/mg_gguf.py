@@ -1,0 +1,137 @@
+"""GGUF v3 writer and synthetic MaskGIT transformer models (TEST INFRASTRUCTURE).
+
+Writes the layout the reference's converter produces (tools/convert_to_gguf.py:158-266):
+`maskgit.*` metadata, tensor dims innermost-first (reversed numpy shape), FC weights as
+F32 / Q8_0 / Q4_K blocks (quantized by the oracle's encoders, which are pinned to the
+reference encoder's bytes), everything else F32, 32-byte aligned data.
+
+Synthetic weights follow BASELINE's random-init recipe: FC weights ~N(0, 0.02), biases
+~N(0, 0.01), embeddings ~N(0, 0.02), LayerNorm gamma ~ 1 + N(0, 0.02), beta ~N(0, 0.01).
+"""
+from __future__ import annotations
+
+import struct
+
+import numpy as np
+
+import oracle
+
+GGML_F32, GGML_Q8_0, GGML_Q4_K = 0, 8, 12
+_U32, _I32, _F32, _STR = 4, 5, 6, 8
+ALIGN = 32
+
+FC_NAMES = ("attn_q", "attn_k", "attn_v", "attn_o", "ffn_up", "ffn_down")
+
+
+def _s(b: bytearray, text: str):
+    raw = text.encode()
+    b += struct.pack("<Q", len(raw)) + raw
+
+
+def write_gguf(path: str, meta: list, tensors: list) -> None:
+    """meta: [(key, kind, value)] with kind in {"u32", "i32", "f32", "str"};
+    tensors: [(name, numpy shape, ggml type, raw bytes)]."""
+    kv = bytearray()
+    for key, kind, val in meta:
+        _s(kv, key)
+        if kind == "u32":
+            kv += struct.pack("<II", _U32, val)
+        elif kind == "i32":
+            kv += struct.pack("<Ii", _I32, val)
+        elif kind == "f32":
+            kv += struct.pack("<If", _F32, val)
+        else:
+            kv += struct.pack("<I", _STR)
+            _s(kv, val)
+    info = bytearray()
+    offsets, off = [], 0
+    for name, shape, gtype, data in tensors:
+        offsets.append(off)
+        off = (off + len(data) + ALIGN - 1) // ALIGN * ALIGN
+    for (name, shape, gtype, data), o in zip(tensors, offsets):
+        _s(info, name)
+        info += struct.pack("<I", len(shape))
+        for d in reversed(shape):
+            info += struct.pack("<Q", int(d))
+        info += struct.pack("<IQ", gtype, o)
+    head = struct.pack("<IIQQ", 0x46554747, 3, len(tensors), len(meta)) + kv + info
+    pad = (-len(head)) % ALIGN
+    with open(path, "wb") as f:
+        f.write(head + b"\0" * pad)
+        pos = 0
+        for (name, shape, gtype, data), o in zip(tensors, offsets):
+            f.write(b"\0" * (o - pos))
+            f.write(data)
+            pos = o + len(data)
+
+
+def synthetic_model(n_layer: int = 2, quant: str = "f32", seed: int = 0, n_embd: int = 768,
+                    n_head: int = 16, n_ffn: int = 3072, vocab: int = 2025, n_pos: int = 257):
+    """Random-init MaskGIT transformer: returns (meta, float tensors dict, quant)."""
+    rng = np.random.default_rng(seed)
+    t = {}
+
+    def nrm(shape, s):
+        return (rng.standard_normal(shape) * s).astype(np.float32)
+
+    t["token_embd.weight"] = nrm((vocab, n_embd), 0.02)
+    t["pos_embd.weight"] = nrm((n_pos, n_embd), 0.02)
+    t["token_embd_norm.weight"] = 1 + nrm(n_embd, 0.02)
+    t["token_embd_norm.bias"] = nrm(n_embd, 0.01)
+    for l in range(n_layer):
+        p = f"blk.{l}."
+        for nm in FC_NAMES:
+            n_out = n_ffn if nm == "ffn_up" else n_embd
+            n_in = n_ffn if nm == "ffn_down" else n_embd
+            t[p + nm + ".weight"] = nrm((n_out, n_in), 0.02)
+            t[p + nm + ".bias"] = nrm(n_out, 0.01)
+        for nm in ("attn_norm", "ffn_norm"):
+            t[p + nm + ".weight"] = 1 + nrm(n_embd, 0.02)
+            t[p + nm + ".bias"] = nrm(n_embd, 0.01)
+    t["output_proj.weight"] = nrm((n_embd, n_embd), 0.02)
+    t["output_proj.bias"] = nrm(n_embd, 0.01)
+    t["output_norm.weight"] = 1 + nrm(n_embd, 0.02)
+    t["output_norm.bias"] = nrm(n_embd, 0.01)
+    t["output.bias"] = nrm(vocab, 0.01)
+    meta = [("general.architecture", "str", "maskgit"), ("general.name", "str", "synthetic"),
+            ("general.alignment", "u32", ALIGN), ("maskgit.n_layer", "u32", n_layer),
+            ("maskgit.n_head", "u32", n_head), ("maskgit.n_embd", "u32", n_embd),
+            ("maskgit.n_ffn", "u32", n_ffn), ("maskgit.head_dim", "u32", n_embd // n_head),
+            ("maskgit.vocab_size", "u32", vocab), ("maskgit.n_tokens", "u32", n_pos - 1),
+            ("maskgit.n_positions", "u32", n_pos), ("maskgit.mask_token_id", "i32", vocab - 1),
+            ("maskgit.layernorm_eps", "f32", 1e-12), ("maskgit.quant", "str", quant)]
+    return meta, t
+
+
+def is_fc(name: str) -> bool:
+    return name.endswith(tuple(n + ".weight" for n in FC_NAMES)) or name == "output_proj.weight"
+
+
+def encode(tensors: dict, quant: str) -> list:
+    """[(name, shape, ggml type, bytes)] with FC weights in the given format."""
+    out = []
+    for name, a in tensors.items():
+        if quant in ("q8_0", "q4_k") and is_fc(name):
+            wt = oracle.WTYPE_Q8_0 if quant == "q8_0" else oracle.WTYPE_Q4_K
+            out.append((name, a.shape, GGML_Q8_0 if quant == "q8_0" else GGML_Q4_K,
+                        oracle.quantize(wt, a).tobytes()))
+        else:
+            out.append((name, a.shape, GGML_F32, np.ascontiguousarray(a, np.float32).tobytes()))
+    return out
+
+
+def write_model(path: str, n_layer: int = 2, quant: str = "f32", seed: int = 0) -> dict:
+    """Write a synthetic model; returns the float tensors (pre-quantization)."""
+    meta, t = synthetic_model(n_layer, quant, seed)
+    write_gguf(path, meta, encode(t, quant))
+    return t
+
+
+def tokens(rng, S: int, B: int, vocab: int = 2025, n_codes: int = 1024, mask_id: int = 2024) -> np.ndarray:
+    """Token ids as MaskGIT feeds them: position 0 = class token 1024 + class, positions
+    1..S-1 codebook ids with half replaced by the mask id (mg-generate.cpp:48-59)."""
+    t = rng.integers(0, n_codes, (B, S)).astype(np.int32)
+    t[:, 0] = 1024 + rng.integers(0, 1000, B)
+    m = rng.random((B, S - 1)) < 0.5
+    t[:, 1:][m] = mask_id
+    return t

@@ -48,3 +48,29 @@ def test_package_has_no_cpu_fallback():
                 txt = open(os.path.join(dirpath, f)).read()
                 assert "import oracle" not in txt and "from oracle" not in txt, f
                 assert "mg_oracle" not in txt, f
+
+
+def _declared_mgr():
+    text = open(os.path.join(ROOT, "include", "mgr.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mgr_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_runtime_library_exports_every_declared_symbol():
+    from edge_maskgit_amd import runtime
+    lib = runtime.lib()
+    declared = _declared_mgr()
+    assert declared
+    missing = [s for s in declared if not hasattr(lib, s)]
+    assert not missing, missing
+    assert sorted(runtime.MGR_SYMBOLS) == declared
+
+
+def test_runtime_errors_without_device(tmp_path):
+    from edge_maskgit_amd import runtime
+    with pytest.raises(ema.MghError):
+        runtime.gguf_info(str(tmp_path / "missing.gguf"))
+    bad = tmp_path / "bad.gguf"
+    bad.write_bytes(b"NOTAGGUF" * 8)
+    with pytest.raises(ema.MghError):
+        runtime.gguf_info(str(bad))
