@@ -234,6 +234,88 @@ def measure(ctx, M, wtype, steps, warmup, rotate_gb, use_graphs=True, path="pack
     return ms_step, ms_gemms, host
 
 
+def write_synthetic_model(path, n_layer, wtype, seed=0):
+    """Random-init MaskGIT transformer GGUF (BASELINE cfg4/cfg5 recipe): FC weights ~N(0,0.02)
+    in Q8_0 / Q4_K blocks (bench-local encoders), embeddings ~N(0,0.02), biases ~N(0,0.01),
+    LN gamma ~1+N(0,0.02), beta ~N(0,0.01); hidden 768, 16 heads, MLP 3072, vocab 2025."""
+    from edge_maskgit_amd.gguf import GGML_F32, GGML_Q4_K, GGML_Q8_0, write_gguf
+    rng = np.random.default_rng(seed)
+    E, F, V, P = 768, 3072, 2025, 257
+    enc, gt = (synth_q8_0, GGML_Q8_0) if wtype == ema.WTYPE_Q8_0 else (synth_q4_k, GGML_Q4_K)
+    out = []
+
+    def f32(name, a):
+        out.append((name, a.shape, GGML_F32, np.ascontiguousarray(a, np.float32).tobytes()))
+
+    def nrm(shape, s):
+        return (rng.standard_normal(shape, dtype=np.float32) * np.float32(s)).astype(np.float32)
+
+    def fcw(name, n_out, n_in):
+        w = nrm((n_out, n_in), 0.02)
+        out.append((name, (n_out, n_in), gt, enc(w).tobytes()))
+
+    f32("token_embd.weight", nrm((V, E), 0.02))
+    f32("pos_embd.weight", nrm((P, E), 0.02))
+    f32("token_embd_norm.weight", 1 + nrm(E, 0.02))
+    f32("token_embd_norm.bias", nrm(E, 0.01))
+    for l in range(n_layer):
+        p = f"blk.{l}."
+        for nm, no, ni in (("attn_q", E, E), ("attn_k", E, E), ("attn_v", E, E), ("attn_o", E, E),
+                           ("ffn_up", F, E), ("ffn_down", E, F)):
+            fcw(p + nm + ".weight", no, ni)
+            f32(p + nm + ".bias", nrm(no, 0.01))
+        for nm in ("attn_norm", "ffn_norm"):
+            f32(p + nm + ".weight", 1 + nrm(E, 0.02))
+            f32(p + nm + ".bias", nrm(E, 0.01))
+    fcw("output_proj.weight", E, E)
+    f32("output_proj.bias", nrm(E, 0.01))
+    f32("output_norm.weight", 1 + nrm(E, 0.02))
+    f32("output_norm.bias", nrm(E, 0.01))
+    f32("output.bias", nrm(V, 0.01))
+    meta = [("general.architecture", "str", "maskgit"), ("general.alignment", "u32", 32),
+            ("maskgit.n_layer", "u32", n_layer), ("maskgit.n_head", "u32", 16),
+            ("maskgit.n_embd", "u32", E), ("maskgit.n_ffn", "u32", F), ("maskgit.head_dim", "u32", 48),
+            ("maskgit.vocab_size", "u32", V), ("maskgit.n_tokens", "u32", P - 1),
+            ("maskgit.n_positions", "u32", P), ("maskgit.mask_token_id", "i32", V - 1),
+            ("maskgit.layernorm_eps", "f32", 1e-12)]
+    write_gguf(path, meta, out)
+
+
+def synth_tokens(rng, B, S=257):
+    """cfg4 token ids: position 0 = class token 1024 + U[0,999]; positions 1..256 codebook ids
+    U[0,1023] with half replaced by the mask id 2024 (the reference's convention)."""
+    t = rng.integers(0, 1024, (B, S)).astype(np.int32)
+    t[:, 0] = 1024 + rng.integers(0, 1000, B)
+    t[:, 1:][rng.random((B, S - 1)) < 0.5] = 2024
+    return t
+
+
+def measure_forward(path, B, steps, warmup, algo=1, profile=False):
+    """Full transformer forward through the C++ HipRuntime (graph build + kernels + logits
+    readback), wall clock per call; and the same without the logits readback."""
+    from edge_maskgit_amd.runtime import TransformerRuntime
+    rng = np.random.default_rng(1)
+    tok = synth_tokens(rng, B)
+    with TransformerRuntime(path, algo=algo) as m:
+        for _ in range(max(1, warmup)):
+            m.forward(tok)                       # first call packs and uploads the weights
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            m.forward(tok)
+        ms = (time.perf_counter() - t0) / steps * 1e3
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            m.forward(tok, readback=False)
+        ms_nr = (time.perf_counter() - t0) / steps * 1e3
+        prof = None
+        if profile:
+            m.profile(True)
+            m.forward(tok, readback=False)
+            prof = {n: {"count": c, "ms": round(t, 3)} for n, c, t in m.profile_report()}
+            m.profile(False)
+    return ms, ms_nr, prof
+
+
 def cpu_baseline(host, M, wtype, budget_s=15.0):
     """The reference CPU executor (libmgref) on dequantized weights, single thread, over the
     same four GEMMs; rows are processed in chunks until the budget is spent."""
@@ -279,6 +361,10 @@ def main():
                     help="enqueue kernels one by one instead of replaying a captured HIP graph")
     ap.add_argument("--path", choices=["packed", "raw"], default="packed",
                     help="packed: device-native weight layout (production); raw: GGUF blocks as stored")
+    ap.add_argument("--no-fwd", action="store_true", help="skip the transformer forward (cfg4)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only run 10 plain device copies of BYTES (k_copy4d), to calibrate the "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters, and exit")
     ap.add_argument("--extra", action="store_true",
                     help="also measure Q8_0 M=4097 and Q4_K M=1025/4097 layers")
     a = ap.parse_args()
@@ -290,6 +376,16 @@ def main():
 
     ctx = ema.Context(0)
     log(f"[bench] device: {ctx.device_name}")
+    if a.copy_probe:
+        n = a.copy_probe // 4
+        src, dst = ctx.alloc(n * 4), ctx.alloc(n * 4)
+        ctx.fill_u32(src, 0x3F800000, n)
+        for _ in range(10):
+            ctx.copy_strided(src, (n, 1, 1, 1), (1, n, n, n), dst)
+        ctx.sync()
+        print(json.dumps({"copy_probe_bytes": n * 4, "launches": 10}), flush=True)
+        ctx.close()
+        return
     M, wtype = 1025, ema.WTYPE_Q8_0
     ms_step, ms_gemms, host = measure(ctx, M, wtype, a.steps, a.warmup, a.rotate_gb,
                                       use_graphs=not a.no_graphs, path=a.path)
@@ -312,6 +408,25 @@ def main():
                           "gemm_tops": round(layer_ops(mm) / (g * 1e-3) / 1e12, 2),
                           "frac_of_hbm_roofline": round(step_alg_bytes(mm, wt) / (HBM_PEAK_GBS * 1e9)
                                                         / (s * 1e-3), 4)}
+    if not a.no_fwd:
+        import tempfile
+        with tempfile.TemporaryDirectory() as d:
+            path = os.path.join(d, "cfg4_q8_0.gguf")
+            t0 = time.perf_counter()
+            write_synthetic_model(path, 24, ema.WTYPE_Q8_0)
+            log(f"[bench] cfg4 model written in {time.perf_counter() - t0:.1f} s")
+            fwd, fwd_nr, prof = measure_forward(path, 16, max(3, a.steps // 10), 2, profile=True)
+            extra["transformer_fwd_cfg4"] = {
+                "ms": round(fwd, 3), "ms_no_logits_readback": round(fwd_nr, 3),
+                "model": "24 layers Q8_0 random-init, hidden 768, 16 heads, MLP 3072, vocab 2025",
+                "batch": "16 images x 257 tokens (M=4112)", "algo": "int8-dot",
+                "per_op_device_ms": prof}
+            if a.extra:
+                path5 = os.path.join(d, "cfg5_q4_k.gguf")
+                write_synthetic_model(path5, 24, ema.WTYPE_Q4_K, seed=5)
+                f5, f5nr, _ = measure_forward(path5, 64, 3, 1)
+                extra["transformer_fwd_q4k_b64"] = {"ms": round(f5, 3), "ms_no_logits_readback": round(f5nr, 3),
+                                                    "batch": "64 x 257 tokens (M=16448), one decode step's forward"}
     cpu = None if a.no_cpu else cpu_baseline(host, M, wtype)
     line = {
         "metric": "Q8_0/Q4_K GEMM TOPS + % roofline at M=1025/4097; transformer fwd ms",

@@ -10,59 +10,13 @@ Synthetic weights follow BASELINE's random-init recipe: FC weights ~N(0, 0.02), 
 """
 from __future__ import annotations
 
-import struct
-
 import numpy as np
 
 import oracle
 
-GGML_F32, GGML_Q8_0, GGML_Q4_K = 0, 8, 12
-_U32, _I32, _F32, _STR = 4, 5, 6, 8
-ALIGN = 32
+from edge_maskgit_amd.gguf import ALIGN, GGML_F32, GGML_Q4_K, GGML_Q8_0, write_gguf  # noqa: F401
 
 FC_NAMES = ("attn_q", "attn_k", "attn_v", "attn_o", "ffn_up", "ffn_down")
-
-
-def _s(b: bytearray, text: str):
-    raw = text.encode()
-    b += struct.pack("<Q", len(raw)) + raw
-
-
-def write_gguf(path: str, meta: list, tensors: list) -> None:
-    """meta: [(key, kind, value)] with kind in {"u32", "i32", "f32", "str"};
-    tensors: [(name, numpy shape, ggml type, raw bytes)]."""
-    kv = bytearray()
-    for key, kind, val in meta:
-        _s(kv, key)
-        if kind == "u32":
-            kv += struct.pack("<II", _U32, val)
-        elif kind == "i32":
-            kv += struct.pack("<Ii", _I32, val)
-        elif kind == "f32":
-            kv += struct.pack("<If", _F32, val)
-        else:
-            kv += struct.pack("<I", _STR)
-            _s(kv, val)
-    info = bytearray()
-    offsets, off = [], 0
-    for name, shape, gtype, data in tensors:
-        offsets.append(off)
-        off = (off + len(data) + ALIGN - 1) // ALIGN * ALIGN
-    for (name, shape, gtype, data), o in zip(tensors, offsets):
-        _s(info, name)
-        info += struct.pack("<I", len(shape))
-        for d in reversed(shape):
-            info += struct.pack("<Q", int(d))
-        info += struct.pack("<IQ", gtype, o)
-    head = struct.pack("<IIQQ", 0x46554747, 3, len(tensors), len(meta)) + kv + info
-    pad = (-len(head)) % ALIGN
-    with open(path, "wb") as f:
-        f.write(head + b"\0" * pad)
-        pos = 0
-        for (name, shape, gtype, data), o in zip(tensors, offsets):
-            f.write(b"\0" * (o - pos))
-            f.write(data)
-            pos = o + len(data)
 
 
 def synthetic_model(n_layer: int = 2, quant: str = "f32", seed: int = 0, n_embd: int = 768,
