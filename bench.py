@@ -428,6 +428,10 @@ def main():
                 extra["transformer_fwd_q4k_b64"] = {"ms": round(f5, 3), "ms_no_logits_readback": round(f5nr, 3),
                                                     "batch": "64 x 257 tokens (M=16448), one decode step's forward"}
     cpu = None if a.no_cpu else cpu_baseline(host, M, wtype)
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", "traffic_cfg2_q8_m1025.json")
+    if a.path == "packed" and os.path.exists(tf):
+        traffic = json.load(open(tf)).get("traffic_bytes_per_step")   # rocprofv3 --pmc, scaled
     line = {
         "metric": "Q8_0/Q4_K GEMM TOPS + % roofline at M=1025/4097; transformer fwd ms",
         "value": round(value, 3),
@@ -447,7 +451,7 @@ def main():
                    "M": M, "weights": "Q8_0", "rotate_gb": a.rotate_gb,
                    "launch": "stream" if a.no_graphs else "hip_graph_per_step"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": KERNEL[a.path], "bytes_per_step": gb},
         "cpu_baseline": cpu,
         "extra": extra,
