@@ -8,17 +8,20 @@ layer's four Q8_0 FC GEMMs at M = 1025 tokens (32x32 grid + class token), fp32 a
     up    768 -> 3072  (+bias, GELU)
     down 3072 -> 768   (+bias +residual)
 A step runs each FC as the int8-dot path does it: per-32 activation quantization
-(k_quantize_act_q8, codes written as fp16) then the GEMM (k_gemm_q_f16x: block dots on fp16
-MFMA, exact), i.e. exactly what mgh_gemm_q_f32in runs, all inputs already resident in HBM. Each buffer set's step is captured once as a HIP graph and replayed (--no-graphs
-enqueues the kernels one by one instead). Buffers rotate over >= --rotate-gb of distinct sets so the 256 MB MALL and the L2s do
-not serve the timed reads. Synthetic data: x ~ N(0,1), W ~ N(0,0.02) quantized to Q8_0,
-biases ~ N(0,0.01), residuals ~ N(0,1), seeded.
+(k_quantize_act_q8, codes written as fp16) then the GEMM on weights in the device-native packed
+layout (k_gemm_qp: exact block dots on fp16 MFMA, per-block scales in registers), the weights
+packed once at upload as the reference uploads them once; all inputs already resident in HBM.
+Each buffer set's step is captured once as a HIP graph and replayed (--no-graphs enqueues the
+kernels one by one instead). Buffers rotate over >= --rotate-gb of distinct sets so the 256 MB
+MALL and the L2s do not serve the timed reads. Synthetic data: x ~ N(0,1), W ~ N(0,0.02)
+quantized to Q8_0, biases ~ N(0,0.01), residuals ~ N(0,1), seeded.
 
 value = 2*M*K*N summed over the four GEMMs / step time, in TOPS (int8 ops).
-roofline = the dominant kernel k_gemm_q_f16x, HBM-bound: algorithmic bytes of its launches
+roofline = the dominant kernel k_gemm_qp, HBM-bound: algorithmic bytes of its launches
 (quantized weights once + fp16 activation codes + fp32 block scales (+ block sums for Q4_K)
-+ fp32 output + bias + residual)
-divided by its average launch duration, timed with HIP events on the stream it runs on.
++ fp32 output + bias + residual) divided by its average launch duration, timed with HIP
+events on the stream it runs on; traffic = the measured HBM bytes of those launches
+(rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy).
 cpu_baseline = the reference's own CPU executor (mg-cpu k_mul_mat, single thread, built
 from the reference sources into oracle/_ref) on the dequantized weights, timed on this
 host over the same four GEMMs; if that library is absent, the C oracle's int8 path.
@@ -277,7 +280,8 @@ def write_synthetic_model(path, n_layer, wtype, seed=0):
             ("maskgit.n_embd", "u32", E), ("maskgit.n_ffn", "u32", F), ("maskgit.head_dim", "u32", 48),
             ("maskgit.vocab_size", "u32", V), ("maskgit.n_tokens", "u32", P - 1),
             ("maskgit.n_positions", "u32", P), ("maskgit.mask_token_id", "i32", V - 1),
-            ("maskgit.layernorm_eps", "f32", 1e-12)]
+            ("maskgit.layernorm_eps", "f32", 1e-12), ("maskgit.vqgan.codebook_size", "u32", 1024),
+            ("maskgit.sampling.choice_temperature", "f32", 4.5)]
     write_gguf(path, meta, out)
 
 
@@ -314,6 +318,41 @@ def measure_forward(path, B, steps, warmup, algo=1, profile=False):
             prof = {n: {"count": c, "ms": round(t, 3)} for n, c, t in m.profile_report()}
             m.profile(False)
     return ms, ms_nr, prof
+
+
+def measure_generate(path, B, n_steps=8, reps=2):
+    """cfg5: B images, n_steps device-resident decode steps (transformer forward in HBM ->
+    on-device sampling / confidence / re-mask), wall clock per generate; token grids only come
+    back at the end."""
+    from edge_maskgit_amd.runtime import TransformerRuntime
+    cls = (np.arange(B) * 37) % 1000
+    seeds = np.arange(B, dtype=np.uint64) + 42
+    with TransformerRuntime(path, algo=1) as m:
+        m.generate(cls, seeds, n_steps)          # packs and uploads the weights
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            m.generate(cls, seeds, n_steps)
+        return (time.perf_counter() - t0) / reps * 1e3
+
+
+def measure_decode_step(ctx, B, S=257, V=2025, reps=20):
+    """Device time of one mgh_decode_step (engine draws + sampling + re-mask) for B images on
+    logits already in HBM."""
+    rng = np.random.default_rng(2)
+    logits = ctx.upload((rng.standard_normal((B, S, V)) * 2).astype(np.float32))
+    tok = np.full((B, S), 2024, np.int32)
+    tok[:, 0] = 1024
+    d_tok, d_res = ctx.upload(tok), ctx.alloc(tok.nbytes)
+    state, work = ctx.alloc(ema.decode_state_bytes(B)), ctx.alloc(ema.decode_work_bytes(B, S))
+    ctx.decode_init(list(range(B)), state)
+    ctx.decode_step(state, work, logits, B, S, V, 1024, 2024, 256, 0, 8, 4.5, d_tok, d_res)
+    ctx.timer_start()
+    for _ in range(reps):
+        ctx.decode_step(state, work, logits, B, S, V, 1024, 2024, 256, 0, 8, 4.5, d_tok, d_res)
+    ms = ctx.timer_stop() / reps
+    for b in (logits, d_tok, d_res, state, work):
+        ctx.free(b)
+    return ms
 
 
 def cpu_baseline(host, M, wtype, budget_s=15.0):
@@ -427,6 +466,12 @@ def main():
                 f5, f5nr, _ = measure_forward(path5, 64, 3, 1)
                 extra["transformer_fwd_q4k_b64"] = {"ms": round(f5, 3), "ms_no_logits_readback": round(f5nr, 3),
                                                     "batch": "64 x 257 tokens (M=16448), one decode step's forward"}
+                gen = measure_generate(path5, 64)
+                extra["generate_cfg5"] = {
+                    "ms_per_generate": round(gen, 2), "ms_per_step": round(gen / 8, 3),
+                    "decode_step_device_ms": round(measure_decode_step(ctx, 64), 4),
+                    "workload": "64 images x 257 tokens, 8 steps, Q4_K 24 layers, int8-dot; "
+                                "forward + on-device sampling per step, grids read back once"}
     cpu = None if a.no_cpu else cpu_baseline(host, M, wtype)
     traffic = None
     tf = os.path.join(ROOT, "profiles", "traffic_cfg2_q8_m1025.json")

@@ -35,7 +35,8 @@ MGH_SYMBOLS = [
     "mgh_packed_weight_bytes", "mgh_pack_weights", "mgh_gemm_q_packed", "mgh_debug_block_dots_packed",
     "mgh_gemm_q_packed_f32in",
     "mgh_layernorm_affine", "mgh_flash_attn_f16kv", "mgh_gemm_f32", "mgh_get_rows", "mgh_add",
-    "mgh_copy_strided",
+    "mgh_copy_strided", "mgh_decode_state_bytes", "mgh_decode_work_bytes", "mgh_decode_init",
+    "mgh_decode_step",
 ]
 
 _lib = None
@@ -93,6 +94,12 @@ def lib():
         L.mgh_get_rows.argtypes = [P, P, I64, I64, P, I64, P]
         L.mgh_add.argtypes = [P, P, P, I64, P, I64]
         L.mgh_copy_strided.argtypes = [P, P, P, P, P]
+        L.mgh_decode_state_bytes.argtypes = [I]
+        L.mgh_decode_state_bytes.restype = SZ
+        L.mgh_decode_work_bytes.argtypes = [I, I]
+        L.mgh_decode_work_bytes.restype = SZ
+        L.mgh_decode_init.argtypes = [P, I, P, P]
+        L.mgh_decode_step.argtypes = [P, P, P, P, I, I, I, I, I, I, I, I, ctypes.c_float, P, P]
         L.mgh_graph_begin.argtypes = [P]
         L.mgh_graph_end.argtypes = [P, ctypes.POINTER(P)]
         L.mgh_graph_launch.argtypes = [P, P]
@@ -100,6 +107,14 @@ def lib():
         L.mgh_graph_destroy.restype = None
         _lib = L
     return _lib
+
+
+def decode_state_bytes(B: int) -> int:
+    return int(lib().mgh_decode_state_bytes(B))
+
+
+def decode_work_bytes(B: int, S: int) -> int:
+    return int(lib().mgh_decode_work_bytes(B, S))
 
 
 def packed_weight_bytes(wtype: int, N: int, K: int) -> int:
@@ -171,6 +186,13 @@ class Context:
         b = self.alloc(max(arr.nbytes, 1))
         self._check(lib().mgh_h2d(self.h, b.p, arr.ctypes.data_as(ctypes.c_void_p), arr.nbytes))
         return b
+
+    def write(self, buf: DeviceBuffer, arr: np.ndarray):
+        """Copy a host array into the start of an existing device buffer."""
+        arr = np.ascontiguousarray(arr)
+        if arr.nbytes > buf.nbytes:
+            raise ValueError("write: array larger than the buffer")
+        self._check(lib().mgh_h2d(self.h, buf.p, arr.ctypes.data_as(ctypes.c_void_p), arr.nbytes))
 
     def download(self, buf: DeviceBuffer, shape, dtype) -> np.ndarray:
         out = np.empty(shape, dtype)
@@ -258,6 +280,18 @@ class Context:
         P = self._ptr
         self._check(lib().mgh_copy_strided(self.h, P(a), (ctypes.c_int64 * 4)(*ne),
                                            (ctypes.c_int64 * 4)(*strides), P(out)))
+
+    def decode_init(self, seeds, state):
+        """seeds: host sequence of B uint64 seeds; state: mgh_decode_state_bytes(B) bytes."""
+        sd = (ctypes.c_uint64 * len(seeds))(*[int(v) for v in seeds])
+        self._check(lib().mgh_decode_init(self.h, len(seeds), sd, self._ptr(state)))
+
+    def decode_step(self, state, work, logits, B, S, V, codebook, mask_id, n_tokens, step, n_steps,
+                    choice_temp, tokens, result):
+        P = self._ptr
+        self._check(lib().mgh_decode_step(self.h, P(state), P(work), P(logits), B, S, V, codebook,
+                                          mask_id, n_tokens, step, n_steps, choice_temp, P(tokens),
+                                          P(result)))
 
     def gemm_q_packed_f32in(self, algo, wtype, wp, N, K, x, M, bias, act, resid, y):
         P = self._ptr

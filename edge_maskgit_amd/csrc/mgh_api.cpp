@@ -610,6 +610,47 @@ int mgh_copy_strided(mgh_ctx* c, const float* a, const int64_t ne[4], const int6
     return MGH_OK;
 }
 
+size_t mgh_decode_state_bytes(int B) { return B > 0 ? mgh::decode_state_bytes(B) : 0; }
+
+size_t mgh_decode_work_bytes(int B, int S) { return B > 0 && S > 0 ? mgh::decode_work_bytes(B, S) : 0; }
+
+int mgh_decode_init(mgh_ctx* c, int B, const uint64_t* seeds, void* state) {
+    if (!c) return MGH_ERR_ARG;
+    if (B <= 0) return fail(c, MGH_ERR_ARG, "decode_init: need B > 0");
+    if (!seeds || !state) return fail(c, MGH_ERR_ARG, "decode_init: null pointer");
+    if ((uintptr_t)state % 8) return fail(c, MGH_ERR_ARG, "decode_init: state must be 8-byte aligned");
+    if (int r = set_dev(c)) return r;
+    // seed b goes to word 0 of image b's state block; the kernel expands it in place
+    const size_t pitch = mgh::decode_state_bytes(1);
+    MGH_HIP(c, hipMemcpy2DAsync(state, pitch, seeds, sizeof(uint64_t), sizeof(uint64_t), (size_t)B,
+                                hipMemcpyHostToDevice, c->stream), "decode_init: seed copy");
+    MGH_HIP(c, mgh::launch_decode_seed(B, state, c->stream), "k_mt64_seed");
+    MGH_HIP(c, hipStreamSynchronize(c->stream), "decode_init");
+    return MGH_OK;
+}
+
+int mgh_decode_step(mgh_ctx* c, void* state, void* work, const float* logits, int B, int S, int V,
+                    int codebook, int mask_id, int n_tokens, int step, int n_steps,
+                    float choice_temp, int32_t* tokens, int32_t* result) {
+    if (!c) return MGH_ERR_ARG;
+    if (B <= 0 || S <= 0 || V <= 0) return fail(c, MGH_ERR_ARG, "decode_step: need B, S, V > 0");
+    if (S > 512) return fail(c, MGH_ERR_UNSUPPORTED, "decode_step: at most 512 positions per image");
+    if (codebook <= 0 || codebook % 64 || codebook > 1024 || codebook > V)
+        return fail(c, MGH_ERR_UNSUPPORTED, "decode_step: codebook must be a multiple of 64, <= 1024 and <= V");
+    if (n_steps <= 0 || step < 0 || step >= n_steps)
+        return fail(c, MGH_ERR_ARG, "decode_step: need 0 <= step < n_steps");
+    if (!state || !work || !logits || !tokens || !result) return fail(c, MGH_ERR_ARG, "decode_step: null pointer");
+    if ((uintptr_t)state % 8 || (uintptr_t)work % 256)
+        return fail(c, MGH_ERR_ARG, "decode_step: state must be 8-byte and work 256-byte aligned");
+    if (int r = set_dev(c)) return r;
+    mgh::DecodeArgs a{};
+    a.logits = logits; a.tokens = tokens; a.result = result;
+    a.B = B; a.S = S; a.V = V; a.CB = codebook; a.mask_id = mask_id; a.n_tokens = n_tokens;
+    a.step = step; a.n_steps = n_steps; a.choice_temp = choice_temp;
+    MGH_HIP(c, mgh::launch_decode_step(a, state, work, c->stream), "decode_step");
+    return MGH_OK;
+}
+
 int mgh_debug_block_dots(mgh_ctx* c, int wtype, const void* w, int N, int K, const int8_t* qx,
                          int M, int32_t* out) {
     if (!c) return MGH_ERR_ARG;

@@ -107,4 +107,23 @@ struct QpPlan {
 };
 QpPlan gemm_qp_plan(int M, int N, int K);
 
+// Iterative decoding (k_decode.hip). Per image: mt19937_64 state (312 words + index) in
+// `state`; per step 2*S engine outputs, softmax/categorical per position, confidence and
+// re-mask per image. The launcher carves draws/sampled/selp out of `work`.
+struct DecodeArgs {
+    const float* logits;   // [B][S][V]
+    int32_t* tokens;       // [B][S] in/out
+    int32_t* result;       // [B][S] samples before re-masking
+    uint64_t* draws;       // [B][2S]
+    int32_t* sampled;      // [B][S]
+    float* selp;           // [B][S]
+    int B, S, V, CB, mask_id, n_tokens, step, n_steps;
+    float choice_temp;
+};
+size_t decode_state_bytes(int B);
+size_t decode_work_bytes(int B, int S);
+// seeds are read from word 0 of each image's state block (the caller puts them there)
+hipError_t launch_decode_seed(int B, void* state, hipStream_t s);
+hipError_t launch_decode_step(DecodeArgs a, void* state, void* work, hipStream_t s);
+
 }  // namespace mgh

@@ -8,7 +8,9 @@
 //     flash-attention -> permute -> cont chains (attention writes the merged layout).
 //  2. Run the nodes in order; device buffers of computed roots come from a size-bucketed
 //     pool and return to it after their last consumer.
-//  3. Copy the final node to its host data and wait (the reference's readback, :1622-1642).
+//  3. Copy the final node to its host data and wait (the reference's readback, :1622-1642);
+//     compute_device() instead keeps the result in HBM for device-side consumers (the
+//     decode step) and returns without waiting.
 // Leaves are uploaded once per (host address, byte size) and kept; quantized weights are
 // packed on upload (mgh_pack_weights). Supported ops: MulMat (Q8_0, Q4_K, F32 weights),
 // Norm (plain or affine), FlashAttention, GetRows, Add, Cont, Reshape, View, Permute.
@@ -57,6 +59,11 @@ struct HipRuntime::Impl {
     std::multimap<size_t, void*> pool;
     // unit gamma / zero beta per D for plain Norm nodes
     std::map<int64_t, std::pair<void*, void*>> unit_affine;
+
+    // leaves bound to caller-owned device memory for the next compute
+    std::unordered_map<const Tensor*, void*> bound;
+    // final result of the last compute_device, returned to the pool by the next compute
+    void* held = nullptr;
 
     // per-compute state
     std::unordered_map<const Tensor*, void*> addr;            // device address of a tensor
@@ -117,7 +124,8 @@ struct HipRuntime::Impl {
         if (r->op == Op::None) {
             const auto it = addr.find(r);
             if (it != addr.end()) return it->second;
-            void* d = upload_leaf(r, false);
+            const auto b = bound.find(r);
+            void* d = b != bound.end() ? b->second : upload_leaf(r, false);
             addr[r] = d;
             return d;
         }
@@ -157,6 +165,7 @@ HipRuntime::~HipRuntime() {
     mgh_sync(p_->ctx);
     for (auto& kv : p_->leaves) mgh_free(p_->ctx, kv.second);
     for (auto& kv : p_->pool) mgh_free(p_->ctx, kv.second);
+    if (p_->held) mgh_free(p_->ctx, p_->held);
     for (auto& kv : p_->unit_affine) {
         mgh_free(p_->ctx, kv.second.first);
         mgh_free(p_->ctx, kv.second.second);
@@ -195,9 +204,27 @@ void HipRuntime::set_quant_algo(int algo) {
     p_->algo = algo;
 }
 
-void HipRuntime::compute(Graph& g) {
+void HipRuntime::bind_device(const Tensor* t, void* d) {
+    if (!t || t->op != Op::None) throw std::runtime_error("HipRuntime::bind_device: needs a leaf tensor");
+    p_->bound[t] = d;
+}
+
+mgh_ctx* HipRuntime::context() const { return p_->ctx; }
+
+void HipRuntime::compute(Graph& g) { run(g, true); }
+
+const void* HipRuntime::compute_device(Graph& g) { return run(g, false); }
+
+const void* HipRuntime::run(Graph& g, bool readback) {
     Impl& I = *p_;
-    if (g.nodes.empty()) return;
+    if (I.held) {
+        I.give(I.held);
+        I.held = nullptr;
+    }
+    if (g.nodes.empty()) {
+        I.bound.clear();
+        return nullptr;
+    }
     I.addr.clear();
     I.codes.clear();
     const int n = (int)g.nodes.size();
@@ -396,10 +423,16 @@ void HipRuntime::compute(Graph& g) {
 
     Tensor* outp = g.nodes.back();
     const Tensor* ro = I.root(outp);
-    if (!outp->data) throw std::runtime_error("HipRuntime: output node has no host storage");
-    I.check(mgh_d2h(I.ctx, outp->data, I.dev(ro), outp->nbytes()));
+    void* result = I.dev(ro);
+    if (readback) {
+        if (!outp->data) throw std::runtime_error("HipRuntime: output node has no host storage");
+        I.check(mgh_d2h(I.ctx, outp->data, result, outp->nbytes()));
+    } else {
+        I.held = result;                                           // kept until the next compute
+    }
+    I.bound.clear();
     for (auto& kv : I.addr)                                        // computed buffers back to the pool
-        if (kv.first->op != Op::None && kv.second && !fa_target.count(kv.first)) {
+        if (kv.first->op != Op::None && kv.second && kv.second != I.held && !fa_target.count(kv.first)) {
             I.give(kv.second);
             kv.second = nullptr;
         }
@@ -410,6 +443,7 @@ void HipRuntime::compute(Graph& g) {
     }
     I.codes.clear();
     I.addr.clear();
+    return readback ? nullptr : result;
 }
 
 }  // namespace mg

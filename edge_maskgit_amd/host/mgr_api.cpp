@@ -5,9 +5,12 @@
 #include <cstring>
 #include <exception>
 #include <memory>
+#include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "mg-hip.hpp"
+#include "mgh.h"
 #include "mg-model.hpp"
 #include "mg-transformer.hpp"
 
@@ -26,7 +29,56 @@ struct mgr_model {
     std::unique_ptr<mg::HipRuntime> rt;
     std::unique_ptr<mg::Context> gctx;     // per-forward graph; host data only for the output
     size_t gctx_bytes = 0;
+    // device buffers of mgr_generate, grown on demand: tokens, result [B][S] i32, engine
+    // states, per-step work
+    void* d_tok = nullptr;
+    void* d_res = nullptr;
+    void* d_state = nullptr;
+    void* d_work = nullptr;
+    size_t cap_tok = 0, cap_res = 0, cap_state = 0, cap_work = 0;
+
+    ~mgr_model() {
+        if (!rt) return;
+        mgh_ctx* c = rt->context();
+        mgh_sync(c);
+        for (void* p : {d_tok, d_res, d_state, d_work})
+            if (p) mgh_free(c, p);
+    }
+
+    // reserves the graph arena for S x B tokens: graph nodes keep host storage (the
+    // reference's Context semantics); the arena is not zero-filled, so only the token ids and
+    // the logits pages are ever touched. Per token: each layer's 10 n_embd-wide nodes and its
+    // n_ffn-wide node, 5 more n_embd-wide nodes around the layers and the logits (plus
+    // alignment slack)
+    void reserve_graph(int S, int B) {
+        const mg::HParams& h = model->hparams();
+        const size_t per_tok = (size_t)h.n_layer * (10 * (size_t)h.n_embd + (size_t)h.n_ffn) +
+                               5 * (size_t)h.n_embd + (size_t)h.vocab_size;
+        const size_t need = (size_t)S * B * per_tok * 4 + (size_t)(h.n_layer * 16 + 16) * 64 + (64u << 20);
+        if (!gctx || gctx_bytes < need) {
+            gctx.reset(new mg::Context(need));
+            gctx_bytes = need;
+        }
+        gctx->reset();
+    }
 };
+
+namespace {
+
+void grow(mgh_ctx* c, void** p, size_t* cap, size_t need) {
+    if (*cap >= need) return;
+    if (*p && mgh_free(c, *p) != MGH_OK) throw std::runtime_error(mgh_last_error(c));
+    *p = nullptr;
+    *cap = 0;
+    if (mgh_alloc(c, need, p) != MGH_OK) throw std::runtime_error(mgh_last_error(c));
+    *cap = need;
+}
+
+void check(mgh_ctx* c, int rc) {
+    if (rc != MGH_OK) throw std::runtime_error(std::string("mgr_generate: ") + mgh_last_error(c));
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -60,6 +112,15 @@ int mgr_hparams(const mgr_model* m, int32_t o[7]) {
     return 0;
 }
 
+int mgr_decode_params(const mgr_model* m, int32_t* n_tokens, int32_t* codebook, float* choice_temperature) {
+    if (!m) return -1;
+    const mg::HParams& h = m->model->hparams();
+    if (n_tokens) *n_tokens = h.n_tokens;
+    if (codebook) *codebook = h.vq_codebook_size;
+    if (choice_temperature) *choice_temperature = h.choice_temperature;
+    return 0;
+}
+
 const char* mgr_device_name(const mgr_model* m) { return m ? m->rt->device_name().c_str() : ""; }
 
 int mgr_forward(mgr_model* m, const int32_t* tokens, int S, int B, float* logits) {
@@ -68,19 +129,7 @@ int mgr_forward(mgr_model* m, const int32_t* tokens, int S, int B, float* logits
         return -1;
     }
     try {
-        const mg::HParams& h = m->model->hparams();
-        // graph nodes keep host storage (the reference's Context semantics); the arena is
-        // not zero-filled, so only the token ids and the logits pages are ever touched
-        // per token: each layer's 10 n_embd-wide nodes and its n_ffn-wide node, 5 more
-        // n_embd-wide nodes around the layers and the logits (32-byte alignment slack)
-        const size_t per_tok = (size_t)h.n_layer * (10 * (size_t)h.n_embd + (size_t)h.n_ffn) +
-                               5 * (size_t)h.n_embd + (size_t)h.vocab_size;
-        const size_t need = (size_t)S * B * per_tok * 4 + (size_t)(h.n_layer * 16 + 16) * 64 + (64u << 20);
-        if (!m->gctx || m->gctx_bytes < need) {
-            m->gctx.reset(new mg::Context(need));
-            m->gctx_bytes = need;
-        }
-        m->gctx->reset();
+        m->reserve_graph(S, B);
         mg::Tensor* tok = m->gctx->tensor2d(mg::Type::I32, S, B);
         std::memcpy(tok->data, tokens, (size_t)S * B * sizeof(int32_t));
         mg::Tensor* out = mg::build_transformer(*m->gctx, *m->model, tok);
@@ -89,6 +138,57 @@ int mgr_forward(mgr_model* m, const int32_t* tokens, int S, int B, float* logits
         m->rt->invalidate(tok);               // new token ids at a reused host address
         m->rt->compute(g);
         if (logits) std::memcpy(logits, out->data, out->nbytes());
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e);
+    }
+}
+
+int mgr_generate(mgr_model* m, const int32_t* class_ids, const uint64_t* seeds, int B, int steps,
+                 float temperature, int32_t* out_tokens) {
+    if (!m || !class_ids || !seeds || !out_tokens || B <= 0 || steps <= 0) {
+        g_err = "mgr_generate: bad argument";
+        return -1;
+    }
+    try {
+        const mg::HParams& h = m->model->hparams();
+        const int CB = h.vq_codebook_size, MASK = h.mask_token_id, S = h.n_tokens + 1;
+        if (CB <= 0) throw std::runtime_error("mgr_generate: model has no maskgit.vqgan.codebook_size");
+        if (S > h.n_positions) throw std::runtime_error("mgr_generate: n_tokens + 1 exceeds n_positions");
+        for (int b = 0; b < B; b++)
+            if (class_ids[b] < 0 || class_ids[b] + CB >= h.vocab_size)
+                throw std::runtime_error("mgr_generate: class id out of range");
+        const float temp = temperature < 0 ? h.choice_temperature : temperature;
+        mgh_ctx* c = m->rt->context();
+        const size_t ntok = (size_t)B * S * sizeof(int32_t);
+        grow(c, &m->d_tok, &m->cap_tok, ntok);
+        grow(c, &m->d_res, &m->cap_res, ntok);
+        grow(c, &m->d_state, &m->cap_state, mgh_decode_state_bytes(B));
+        grow(c, &m->d_work, &m->cap_work, mgh_decode_work_bytes(B, S));
+
+        // class token at position 0, every image position masked (mg-generate.cpp:56-59)
+        std::vector<int32_t> tok((size_t)B * S, MASK);
+        for (int b = 0; b < B; b++) tok[(size_t)b * S] = class_ids[b] + CB;
+        check(c, mgh_h2d(c, m->d_tok, tok.data(), ntok));
+        check(c, mgh_decode_init(c, B, seeds, m->d_state));
+
+        // one graph for every step; its token leaf reads the device token buffer
+        m->reserve_graph(S, B);
+        mg::Tensor* tl = m->gctx->tensor2d(mg::Type::I32, S, B);
+        mg::Tensor* out = mg::build_transformer(*m->gctx, *m->model, tl);
+        mg::Graph g;
+        g.build_forward(out);
+        for (int step = 0; step < steps; step++) {
+            m->rt->bind_device(tl, m->d_tok);
+            const float* logits = (const float*)m->rt->compute_device(g);
+            check(c, mgh_decode_step(c, m->d_state, m->d_work, logits, B, S, h.vocab_size, CB, MASK,
+                                     h.n_tokens, step, steps, temp, (int32_t*)m->d_tok,
+                                     (int32_t*)m->d_res));
+        }
+        check(c, mgh_d2h(c, tok.data(), m->d_res, ntok));
+        for (int b = 0; b < B; b++)
+            std::memcpy(out_tokens + (size_t)b * h.n_tokens, tok.data() + (size_t)b * S + 1,
+                        (size_t)h.n_tokens * sizeof(int32_t));
         return 0;
     } catch (const std::exception& e) {
         return fail(e);

@@ -16,7 +16,7 @@ from . import LIB_DIR, MghError
 
 MGR_SYMBOLS = ["mgr_load", "mgr_free", "mgr_last_error", "mgr_hparams", "mgr_device_name",
                "mgr_forward", "mgr_profile_enable", "mgr_profile_report", "mgr_gguf_info",
-               "mgr_graph_stats"]
+               "mgr_graph_stats", "mgr_decode_params", "mgr_generate"]
 
 _lib = None
 
@@ -41,6 +41,8 @@ def lib():
         L.mgr_profile_report.argtypes = [P, ctypes.c_char_p, ctypes.c_size_t]
         L.mgr_gguf_info.argtypes = [ctypes.c_char_p, P, ctypes.POINTER(ctypes.c_int64)]
         L.mgr_graph_stats.argtypes = [ctypes.c_char_p, I, I, P]
+        L.mgr_decode_params.argtypes = [P, P, P, P]
+        L.mgr_generate.argtypes = [P, P, P, I, I, ctypes.c_float, P]
         _lib = L
     return _lib
 
@@ -82,6 +84,9 @@ class TransformerRuntime:
         hp = np.zeros(7, np.int32)
         _check(lib().mgr_hparams(self.h, hp.ctypes.data_as(ctypes.c_void_p)))
         self.hparams = dict(zip(HPARAM_NAMES, (int(v) for v in hp)))
+        nt, cb, ct = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_float()
+        _check(lib().mgr_decode_params(self.h, ctypes.byref(nt), ctypes.byref(cb), ctypes.byref(ct)))
+        self.hparams.update(n_tokens=nt.value, codebook_size=cb.value, choice_temperature=ct.value)
 
     def close(self):
         if self.h:
@@ -107,6 +112,19 @@ class TransformerRuntime:
         out = np.empty((B, S, self.hparams["vocab_size"]), np.float32) if readback else None
         _check(lib().mgr_forward(self.h, tok.ctypes.data_as(ctypes.c_void_p), S, B,
                                  None if out is None else out.ctypes.data_as(ctypes.c_void_p)))
+        return out
+
+    def generate(self, class_ids, seeds, steps: int = 8, temperature: float = -1.0) -> np.ndarray:
+        """Iterative decoding on the device (mgr_generate): one image per class id / seed;
+        returns the final token grids int32 [B][n_tokens]."""
+        cls = np.ascontiguousarray(class_ids, dtype=np.int32).reshape(-1)
+        sd = np.ascontiguousarray(seeds, dtype=np.uint64).reshape(-1)
+        if cls.shape != sd.shape:
+            raise ValueError("one seed per class id")
+        out = np.empty((cls.size, self.hparams["n_tokens"]), np.int32)
+        _check(lib().mgr_generate(self.h, cls.ctypes.data_as(ctypes.c_void_p),
+                                  sd.ctypes.data_as(ctypes.c_void_p), cls.size, steps, temperature,
+                                  out.ctypes.data_as(ctypes.c_void_p)))
         return out
 
     def profile(self, on: bool = True):

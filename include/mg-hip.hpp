@@ -16,6 +16,8 @@
 #include <string>
 #include <vector>
 
+struct mgh_ctx;
+
 namespace mg {
 
 struct OpProfile {
@@ -51,7 +53,21 @@ public:
     // 2 = dequantized weights x fp16 activations (its dequant-fused path).
     void set_quant_algo(int algo);
 
+    // ---- device-resident decoding: additions with no counterpart in OpenCLRuntime ----
+    // For the next compute only, leaf `t` reads caller-owned device memory `d` (for example
+    // token ids that an on-device decode step rewrites between forwards) instead of its host
+    // data.
+    void bind_device(const Tensor* t, void* d);
+    // compute() without the final readback: returns the device address of the final node's
+    // result, which stays valid until the next compute call. Kernels are only enqueued.
+    const void* compute_device(Graph& g);
+    // the libmgh context whose stream runs the graph (work enqueued on it is ordered after
+    // the graph's kernels)
+    mgh_ctx* context() const;
+
 private:
+    const void* run(Graph& g, bool readback);
+
     struct Impl;
     std::unique_ptr<Impl> p_;
 };

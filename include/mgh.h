@@ -186,6 +186,25 @@ int mgh_add(mgh_ctx* ctx, const float* d_a, const float* d_b, int64_t nb, float*
 int mgh_copy_strided(mgh_ctx* ctx, const float* d_a, const int64_t ne[4], const int64_t strides[4],
                      float* d_out);
 
+/* ---- iterative decoding on the device: one step of the reference's generate() loop,
+ *      src/mg-generate.cpp:82-121, for B images whose logits [B][S][V] are already in HBM.
+ *      Image b draws from std::mt19937_64(seeds[b]) through uniform_real_distribution<double>
+ *      in the reference's order (S categorical draws, then S Gumbel draws per step), samples
+ *      every position over the first `codebook` logits (softmax, :89-97), keeps known tokens
+ *      (:98-100), applies the cosine schedule with n_tokens unknown positions at the start
+ *      (:104-110) and re-masks the lowest-confidence samples (:112-119). `tokens` [B][S] is
+ *      updated in place; `result` [B][S] receives the step's samples before re-masking (the
+ *      reference's `result`). `state` (mgh_decode_state_bytes, 8-byte aligned) carries the
+ *      engines across steps; `work` (mgh_decode_work_bytes, 256-byte aligned) is per-step
+ *      scratch. Limits: S <= 512, codebook a multiple of 64 and <= 1024. ---- */
+size_t mgh_decode_state_bytes(int B);
+size_t mgh_decode_work_bytes(int B, int S);
+/* seeds: host array of B seeds; the state is ready when the call returns */
+int mgh_decode_init(mgh_ctx* ctx, int B, const uint64_t* seeds, void* d_state);
+int mgh_decode_step(mgh_ctx* ctx, void* d_state, void* d_work, const float* d_logits, int B, int S,
+                    int V, int codebook, int mask_id, int n_tokens, int step, int n_steps,
+                    float choice_temp, int32_t* d_tokens, int32_t* d_result);
+
 /* ---- debug: the int32 per-block dot products exactly as the production GEMM's MFMA
  *      computes them, out[m][n][t] (t = K/32 blocks). The reference has no counterpart;
  *      it exposes the quantity mg-opencl.cpp:472-478 / :571-576 accumulates. ---- */

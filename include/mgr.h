@@ -24,10 +24,24 @@ const char* mgr_last_error(void);
 /* n_layer, n_head, n_embd, head_dim, vocab_size, n_positions, mask_token_id */
 int mgr_hparams(const mgr_model* m, int32_t out[7]);
 const char* mgr_device_name(const mgr_model* m);
+/* decoding parameters: image positions, VQGAN codebook size, default choice temperature
+ * (maskgit.n_tokens, maskgit.vqgan.codebook_size, maskgit.sampling.choice_temperature) */
+int mgr_decode_params(const mgr_model* m, int32_t* n_tokens, int32_t* codebook, float* choice_temperature);
 
 /* tokens [B][S] (I32) -> logits [B][S][vocab_size] (fp32, host). logits may be NULL: the
  * forward then runs without the final readback. */
 int mgr_forward(mgr_model* m, const int32_t* tokens, int S, int B, float* logits);
+
+/* Iterative decoding of B images on the device: the reference's generate() loop
+ * (src/mg-generate.cpp:39-121) without the VQGAN decode. Image b starts from class token
+ * class_ids[b] + codebook and all n_tokens positions masked, draws from
+ * std::mt19937_64(seeds[b]) in the reference's order and runs `steps` transformer forwards,
+ * each followed by the on-device sampling / confidence / re-mask step (mgh_decode_step); the
+ * logits never leave HBM. temperature < 0 selects the model's choice temperature.
+ * out_tokens [B][n_tokens] receives the final grid (the reference's result without the
+ * class token, the input of its VQGAN decode). */
+int mgr_generate(mgr_model* m, const int32_t* class_ids, const uint64_t* seeds, int B, int steps,
+                 float temperature, int32_t* out_tokens);
 
 /* per-op device-time profile of the following forwards (each node timed on its own) */
 int mgr_profile_enable(mgr_model* m, int on);

@@ -19,6 +19,12 @@ Parity pins (what checks each function; see tests/test_oracle.py):
   gemm_f32            reference CPU executor (libmgref) bit-exact
   layernorm_affine    reference CPU executor bit-exact
   attention           reference CPU executor (f32); f16kv = f32 path on rounded inputs
+  mt64_draws          the C++ standard's known answer (10000th output of seed 5489)
+  uniform_draws       generate_canonical closed form over the engine's raw outputs
+  decode_step         closed forms on uniform logits (categorical index = ceil(1024 u) - 1,
+                      re-masked set = smallest Gumbel draws), argmax limit, temperature-0
+                      ordering by probability, cosine-schedule counts, known-token rules
+                      (tests/test_oracle_decode.py)
 """
 from __future__ import annotations
 
@@ -74,6 +80,15 @@ def lib():
         L.mgo_attention.argtypes = [P, P, P, P, I64, I64, I64, I64, ctypes.c_float, ctypes.c_int, P]
         L.mgo_get_rows.argtypes = [P, I64, I64, P, I64, P]
         L.mgo_merge_heads.argtypes = [P, I64, I64, I64, I64, P]
+        U64 = ctypes.c_uint64
+        L.mgo_mt64_draws.argtypes = [U64, I64, P]
+        L.mgo_mt64_draws.restype = None
+        L.mgo_uniform_draws.argtypes = [U64, ctypes.c_double, ctypes.c_double, I64, P]
+        L.mgo_uniform_draws.restype = None
+        L.mgo_decode_step.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_float, P, I64, P, P]
+        L.mgo_decode_step.restype = None
         _lib = L
     return _lib
 
@@ -245,3 +260,30 @@ def merge_heads(a, D, S, H, B) -> np.ndarray:
     o = np.empty(D * S * H * B, np.float32)
     lib().mgo_merge_heads(_p(a), D, S, H, B, _p(o))
     return o
+
+
+# ---- iterative decoding (src/mg-generate.cpp:82-121) -----------------------------
+def mt64_draws(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.uint64)
+    lib().mgo_mt64_draws(seed, n, _p(out))
+    return out
+
+
+def uniform_draws(seed: int, a: float, b: float, n: int) -> np.ndarray:
+    out = np.empty(n, np.float64)
+    lib().mgo_uniform_draws(seed, a, b, n, _p(out))
+    return out
+
+
+def decode_step(logits, tokens, step: int, n_steps: int, seeds, draws_before: int,
+                codebook: int = 1024, mask_id: int = 2024, n_tokens: int = 256,
+                choice_temp: float = 4.5):
+    """One decoding step for B images; returns (new tokens, step samples before re-masking)."""
+    logits = _f32(logits)
+    B, S, V = logits.shape
+    tok = np.ascontiguousarray(tokens, np.int32).copy()
+    res = np.empty_like(tok)
+    sd = np.ascontiguousarray(seeds, np.uint64)
+    lib().mgo_decode_step(_p(logits), B, S, V, codebook, mask_id, n_tokens, step, n_steps,
+                          choice_temp, _p(sd), draws_before, _p(tok), _p(res))
+    return tok, res

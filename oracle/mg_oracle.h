@@ -93,6 +93,14 @@ void mgo_merge_heads(const float* a, int64_t D, int64_t S, int64_t H, int64_t B,
 /* library self-description */
 int mgo_version(void);
 
+/* ---- iterative decoding (mg_oracle_decode.cpp; src/mg-generate.cpp:82-121) ----
+ * std::mt19937_64 / std::uniform_real_distribution<double> exactly as the reference calls them */
+void mgo_mt64_draws(uint64_t seed, int64_t n, uint64_t* out);
+void mgo_uniform_draws(uint64_t seed, double a, double b, int64_t n, double* out);
+void mgo_decode_step(const float* logits, int B, int S, int V, int CB, int mask_id, int n_tokens,
+                     int step, int n_steps, float choice_temp, const uint64_t* seeds,
+                     int64_t draws_before, int32_t* tokens, int32_t* result);
+
 #ifdef __cplusplus
 }
 #endif

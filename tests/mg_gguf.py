@@ -53,7 +53,9 @@ def synthetic_model(n_layer: int = 2, quant: str = "f32", seed: int = 0, n_embd:
             ("maskgit.n_ffn", "u32", n_ffn), ("maskgit.head_dim", "u32", n_embd // n_head),
             ("maskgit.vocab_size", "u32", vocab), ("maskgit.n_tokens", "u32", n_pos - 1),
             ("maskgit.n_positions", "u32", n_pos), ("maskgit.mask_token_id", "i32", vocab - 1),
-            ("maskgit.layernorm_eps", "f32", 1e-12), ("maskgit.quant", "str", quant)]
+            ("maskgit.layernorm_eps", "f32", 1e-12), ("maskgit.quant", "str", quant),
+            ("maskgit.vqgan.codebook_size", "u32", 1024),
+            ("maskgit.sampling.choice_temperature", "f32", 4.5)]
     return meta, t
 
 
