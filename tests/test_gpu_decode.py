@@ -49,7 +49,7 @@ def _run(ctx, logits_fn, tok0, seeds, n_steps, CB=1024, n_tokens=256, choice_tem
     ctx.decode_init(seeds, state)
     d_log = None
     tok_ref = tok0.copy()
-    for step in (range(n_steps) if steps is None else steps):
+    for i, step in enumerate(range(n_steps) if steps is None else steps):
         logits = logits_fn(step, tok_ref)
         V = logits.shape[2]
         if d_log is None:
@@ -59,7 +59,7 @@ def _run(ctx, logits_fn, tok0, seeds, n_steps, CB=1024, n_tokens=256, choice_tem
                         choice_temp, d_tok, d_res)
         got_tok = ctx.download(d_tok, tok0.shape, np.int32)
         got_res = ctx.download(d_res, tok0.shape, np.int32)
-        draws_before = 2 * S * step
+        draws_before = 2 * S * i          # the device engines advance once per call
         tok_ref, res_ref = oracle.decode_step(logits, tok_ref, step, n_steps, seeds, draws_before,
                                               codebook=CB, mask_id=mask_id, n_tokens=n_tokens,
                                               choice_temp=choice_temp)
