@@ -36,7 +36,8 @@ MGH_SYMBOLS = [
     "mgh_gemm_q_packed_f32in",
     "mgh_layernorm_affine", "mgh_flash_attn_f16kv", "mgh_gemm_f32", "mgh_get_rows", "mgh_add",
     "mgh_copy_strided", "mgh_decode_state_bytes", "mgh_decode_work_bytes", "mgh_decode_init",
-    "mgh_decode_step",
+    "mgh_decode_step", "mgh_packed_weight_bytes_f16", "mgh_pack_weights_f16", "mgh_f32_to_f16",
+    "mgh_gemm_h16", "mgh_gemm_h16_f32in",
 ]
 
 _lib = None
@@ -94,6 +95,12 @@ def lib():
         L.mgh_get_rows.argtypes = [P, P, I64, I64, P, I64, P]
         L.mgh_add.argtypes = [P, P, P, I64, P, I64]
         L.mgh_copy_strided.argtypes = [P, P, P, P, P]
+        L.mgh_packed_weight_bytes_f16.argtypes = [I, I]
+        L.mgh_packed_weight_bytes_f16.restype = SZ
+        L.mgh_pack_weights_f16.argtypes = [P, I, P, I, I, P]
+        L.mgh_f32_to_f16.argtypes = [P, P, I64, P]
+        L.mgh_gemm_h16.argtypes = [P, P, I, I, P, I, P, I, P, P]
+        L.mgh_gemm_h16_f32in.argtypes = [P, P, I, I, P, I, P, I, P, P]
         L.mgh_decode_state_bytes.argtypes = [I]
         L.mgh_decode_state_bytes.restype = SZ
         L.mgh_decode_work_bytes.argtypes = [I, I]
@@ -107,6 +114,10 @@ def lib():
         L.mgh_graph_destroy.restype = None
         _lib = L
     return _lib
+
+
+def packed_weight_bytes_f16(N: int, K: int) -> int:
+    return int(lib().mgh_packed_weight_bytes_f16(N, K))
 
 
 def decode_state_bytes(B: int) -> int:
@@ -280,6 +291,20 @@ class Context:
         P = self._ptr
         self._check(lib().mgh_copy_strided(self.h, P(a), (ctypes.c_int64 * 4)(*ne),
                                            (ctypes.c_int64 * 4)(*strides), P(out)))
+
+    def pack_weights_f16(self, wtype, w, N, K, wp16):
+        self._check(lib().mgh_pack_weights_f16(self.h, wtype, self._ptr(w), N, K, self._ptr(wp16)))
+
+    def f32_to_f16(self, x, n, x16):
+        self._check(lib().mgh_f32_to_f16(self.h, self._ptr(x), n, self._ptr(x16)))
+
+    def gemm_h16(self, wp16, N, K, x16, M, bias, act, resid, y):
+        P = self._ptr
+        self._check(lib().mgh_gemm_h16(self.h, P(wp16), N, K, P(x16), M, P(bias), act, P(resid), P(y)))
+
+    def gemm_h16_f32in(self, wp16, N, K, x, M, bias, act, resid, y):
+        P = self._ptr
+        self._check(lib().mgh_gemm_h16_f32in(self.h, P(wp16), N, K, P(x), M, P(bias), act, P(resid), P(y)))
 
     def decode_init(self, seeds, state):
         """seeds: host sequence of B uint64 seeds; state: mgh_decode_state_bytes(B) bytes."""

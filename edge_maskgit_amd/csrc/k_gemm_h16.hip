@@ -1,0 +1,380 @@
+// k_gemm_h16.hip — the dequantize-fused FC path: Q8_0 / Q4_K weights dequantized once at
+// upload into fp16, activations in fp16, fp32 accumulation on MFMA, fused epilogue.
+//
+// Semantics: the reference's fp16-slab dequant GEMMs k_mul_mat_q8_0_t2_h / k_mul_mat_q4k_t2_h
+// (src/mg-opencl/mg-opencl.cpp:320-411): every weight is expanded to its float value
+//   Q8_0: w = d * q            Q4_K: w = (d * sc) * q - dmin * m      (fp32, then to fp16)
+// and the activations are rounded to fp16 (vstore_half_rte); the products accumulate in fp32,
+// then y = act(acc + bias) + resid (mg-opencl.cpp:485-491). The outputs stay within 1e-3 of
+// max|y| of the dequantize-then-F32 product (mg-cpu.cpp:48-72); the only rounding is the
+// fp16 storage of the two operands and the fp32 summation.
+//
+// gfx950 mapping
+//  * y tile 128 weight rows x BM activation rows per 256-thread workgroup (2 x 2 waves, each
+//    64 x BM/2 outputs as 4 x BM/32 v_mfma_f32_16x16x32_f16 tiles); K stage 64.
+//  * Operands move with global_load_lds (16 bytes per lane) straight into a double-buffered
+//    LDS ring: one instruction moves 8 whole 128-byte row segments, XOR-swizzled so the MFMA
+//    fragment reads are bank-conflict free (the layout of k_gemm_qp.hip).
+//  * Software pipeline: the fragments of the next K half are read from LDS while the current
+//    half's MFMAs issue; the stage boundary (vmcnt wait, barrier, next DMA, first fragment
+//    reads of the new stage) sits between two halves of the second K half's MFMAs, so the MFMA
+//    pipe keeps work while the wave waits.
+//  * K rotation: output tiles that share operand rows start their K loop at different stages,
+//    so the first touch of each K slice (an L2 miss) is spread over the kernel instead of
+//    being paid by every tile in the same step.
+//  * Epilogue through LDS: the accumulator tile is transposed in two halves and leaves as whole
+//    rows (512 bytes per 32 lanes) with streaming (non-temporal) stores; bias, activation and
+//    residual are applied on the way out.
+//  * Split-K for shapes with too few tiles: each split writes its partial tile row-major into a
+//    workspace (same transposed path) and k_gemm_h16_reduce sums the splits in split order
+//    (deterministic) and applies the epilogue.
+#include <algorithm>
+
+#include "mgh_common.h"
+#include "mgh_kernels.h"
+
+namespace mgh {
+
+namespace {
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int NT = 256;
+constexpr int BN = 128;
+
+template <int BM>
+struct HLds {
+    u32x4 w[2][BN * 8];     // [stage][row][8 swizzled 16-byte chunks] fp16
+    u32x4 x[2][BM * 8];
+};
+
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <int ACT>
+__device__ __forceinline__ float act_h(float v) {
+    if (ACT == 1) return 0.5f * v * (1.0f + erff(v * 0.70710678f));
+    if (ACT == 2) return v / (1.0f + expf(-v));
+    return v;
+}
+
+__device__ __forceinline__ void tile_origin(int lt, int tiles_m, int tiles_n, int bm, int& m0, int& n0) {
+    const int panel = lt / (8 * tiles_n);
+    const int pm = min(8, tiles_m - panel * 8);
+    const int rem = lt - panel * 8 * tiles_n;
+    m0 = (panel * 8 + rem % pm) * bm;
+    n0 = (rem / pm) * BN;
+}
+
+__device__ __forceinline__ uint32_t f16_bits(float v) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+// One thread per 32-value block: the block's 32 dequantized values as fp16 (4 x 16 bytes).
+template <int WTYPE>
+__global__ __launch_bounds__(256) void k_pack_w16(const uint8_t* __restrict__ w, u32x4* __restrict__ out,
+                                                  int N, int K) {
+#pragma clang fp contract(off)
+    const int T = K / 32;
+    const int64_t blk = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (blk >= (int64_t)N * T) return;
+    const int64_t n = blk / T;
+    const int t = (int)(blk - n * T);
+    float v[32];
+    if (WTYPE == 8) {
+        const uint8_t* b = w + blk * 34;
+        const float d = h2f((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = d * (float)(int8_t)b[2 + i];
+    } else {
+        const uint8_t* sb = w + (n * (T / 8) + t / 8) * 144;
+        const int j = t & 7;
+        const uint8_t* sc12 = sb + 4;
+        uint32_t sc, mn;
+        if (j < 4) {
+            sc = sc12[j] & 63u;
+            mn = sc12[j + 4] & 63u;
+        } else {
+            sc = (sc12[j + 4] & 0xFu) | ((uint32_t)(sc12[j - 4] >> 6) << 4);
+            mn = (uint32_t)(sc12[j + 4] >> 4) | ((uint32_t)(sc12[j] >> 6) << 4);
+        }
+        const float d = h2f((uint32_t)sb[0] | ((uint32_t)sb[1] << 8));
+        const float dmin = h2f((uint32_t)sb[2] | ((uint32_t)sb[3] << 8));
+        const float s = d * (float)sc, m = dmin * (float)mn;
+        const uint8_t* qs = sb + 16 + 32 * (j >> 1);
+        const int sh = 4 * (j & 1);
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = s * (float)((qs[i] >> sh) & 15) - m;
+    }
+    u32x4* dst = out + blk * 4;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        u32x4 c;
+#pragma unroll
+        for (int e = 0; e < 4; e++) c[e] = f16_bits(v[8 * q + 2 * e]) | (f16_bits(v[8 * q + 2 * e + 1]) << 16);
+        dst[q] = c;
+    }
+}
+
+// fp32 -> fp16 (round to nearest even), 8 values per thread
+__global__ __launch_bounds__(256) void k_f32_to_f16(const f32x4* __restrict__ x, u32x4* __restrict__ h,
+                                                    int64_t n8) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n8) return;
+    const f32x4 a = x[2 * i], b = x[2 * i + 1];
+    h[i] = u32x4{f16_bits(a[0]) | (f16_bits(a[1]) << 16), f16_bits(a[2]) | (f16_bits(a[3]) << 16),
+                 f16_bits(b[0]) | (f16_bits(b[1]) << 16), f16_bits(b[2]) | (f16_bits(b[3]) << 16)};
+}
+
+}  // namespace
+
+// y[M][N] = act(x16[M][K] . w16[N][K]^T + bias) + resid, or (PART) the raw partial tile of
+// split ks over its K range into ws.
+template <int ACT, int BM, bool PART>
+__global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
+    constexpr int J = BM / 32;                  // 16-row activation subtiles per wave
+    constexpr int CW = BN / 32, CX = BM / 32;   // DMA instructions per wave and stage
+    constexpr int MID = 2 * J;                  // second-half MFMAs issued before the boundary
+    __shared__ HLds<BM> L;
+
+    const int K = g.K, M = g.M, N = g.N;
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const int splits = PART ? g.splits : 1;
+    const int lfull = xcd_remap(blockIdx.x, tiles_m * tiles_n * splits);
+    const int lt = lfull / splits, ks = lfull - lt * splits;
+    int m0, n0;
+    tile_origin(lt, tiles_m, tiles_n, BM, m0, n0);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wn = wave & 1, wm = wave >> 1;
+    const int l16 = lane & 15, lq = lane >> 4;
+
+    // row r's 128-byte stage segment lives at LDS slots r*8 + (chunk ^ ((r >> 1) & 7)); one
+    // DMA instruction moves rows 8c .. 8c+7 (lane l: row 8c + l/8, chunk (l & 7) ^ swizzle)
+    const uint8_t* srcw[CW];
+    const uint8_t* srcx[CX];
+#pragma unroll
+    for (int q = 0; q < CW; q++) {
+        const int c = wave + 4 * q;
+        const int n = min(n0 + 8 * c + (lane >> 3), N - 1);
+        srcw[q] = (const uint8_t*)g.w + (size_t)n * K * 2 + ((lane & 7) ^ ((4 * c + (lane >> 4)) & 7)) * 16;
+    }
+#pragma unroll
+    for (int q = 0; q < CX; q++) {
+        const int c = wave + 4 * q;
+        const int m = min(m0 + 8 * c + (lane >> 3), M - 1);
+        srcx[q] = (const uint8_t*)g.x + (size_t)m * K * 2 + ((lane & 7) ^ ((4 * c + (lane >> 4)) & 7)) * 16;
+    }
+    const int S = K / 64;
+    const int s_beg = (int)((int64_t)ks * S / splits), s_end = (int)((int64_t)(ks + 1) * S / splits);
+    const int SL = s_end - s_beg;
+    const int s0 = ((m0 / BM) + 4 * (n0 / BN)) % SL;          // K rotation
+    auto kst = [&](int s) { int v = s + s0; return s_beg + (v >= SL ? v - SL : v); };
+    auto dma_stage = [&](int st, int s) {
+        const size_t ofs = (size_t)kst(s) * 128;
+#pragma unroll
+        for (int d = 0; d < CW; d++) dma16(srcw[d] + ofs, &L.w[st][(wave + 4 * d) * 64]);
+#pragma unroll
+        for (int d = 0; d < CX; d++) dma16(srcx[d] + ofs, &L.x[st][(wave + 4 * d) * 64]);
+    };
+    auto frag = [&](const u32x4* B, int r0, int kb) {
+        return __builtin_bit_cast(f16x8, B[(r0 + l16) * 8 + ((4 * kb + lq) ^ ((l16 >> 1) & 7))]);
+    };
+
+    f32x4 acc[4][J];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < J; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    f16x8 a[2][4], b[2][J];
+
+    dma_stage(0, 0);
+    dma_stage(1, min(1, SL - 1));
+    wait_vm<CW + CX>();                         // stage 0 has landed (mine) ...
+    __syncthreads();                            // ... and everyone's
+#pragma unroll
+    for (int i = 0; i < 4; i++) a[0][i] = frag(L.w[0], 64 * wn + 16 * i, 0);
+#pragma unroll
+    for (int j = 0; j < J; j++) b[0][j] = frag(L.x[0], (BM / 2) * wm + 16 * j, 0);
+
+    int st = 0;
+    for (int s = 0; s < SL; s++) {
+        const int stn = st ^ 1;
+        // K half 0: MFMAs on a/b[0] while the fragments of half 1 are read
+#pragma unroll
+        for (int i = 0; i < 4; i++) a[1][i] = frag(L.w[st], 64 * wn + 16 * i, 1);
+#pragma unroll
+        for (int j = 0; j < J; j++) b[1][j] = frag(L.x[st], (BM / 2) * wm + 16 * j, 1);
+#pragma unroll
+        for (int j = 0; j < J; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0][i], b[0][j], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 4 + J; t++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4 * J - (4 + J), 0);
+        // K half 1: MID MFMAs, the stage boundary, the rest
+#pragma unroll
+        for (int q = 0; q < MID; q++)
+            acc[q % 4][q / 4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1][q % 4], b[1][q / 4], acc[q % 4][q / 4], 0, 0, 0);
+        if (s + 1 < SL) {
+            wait_vm0();                         // stage s+1 (requested one stage ago) landed
+            __syncthreads();                    // for every wave; stage s is no longer read
+            if (s + 2 < SL) dma_stage(st, s + 2);
+#pragma unroll
+            for (int i = 0; i < 4; i++) a[0][i] = frag(L.w[stn], 64 * wn + 16 * i, 0);
+#pragma unroll
+            for (int j = 0; j < J; j++) b[0][j] = frag(L.x[stn], (BM / 2) * wm + 16 * j, 0);
+        }
+#pragma unroll
+        for (int q = MID; q < 4 * J; q++)
+            acc[q % 4][q / 4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1][q % 4], b[1][q / 4], acc[q % 4][q / 4], 0, 0, 0);
+        st = stn;
+    }
+    wait_vm0();
+
+    // epilogue: the tile leaves through LDS as whole rows, in two halves of BM/2 rows
+    constexpr int P = BN + 4;                   // padded row pitch (floats)
+    constexpr int HR = BM / 2;
+    static_assert(HR * P * 4 <= (int)sizeof(HLds<BM>), "transpose buffer fits the ring");
+    float* T = (float*)&L;
+    const int c = 4 * (tid & 31);               // this thread's 4 columns
+    const int n = n0 + c;
+    f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+    if (!PART && g.bias && n < N) bv = *(const f32x4*)(g.bias + n);
+    float* part = PART ? g.ws + ((size_t)lt * splits + ks) * (size_t)BM * BN : nullptr;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        __syncthreads();                        // ring / previous half no longer read
+        if (wm == h) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < J; j++)
+                    *(f32x4*)&T[(16 * j + l16) * P + 64 * wn + 16 * i + 4 * lq] = acc[i][j];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int p = 0; p < HR / 8; p++) {
+            const int r = 8 * p + (tid >> 5);
+            const f32x4 v = *(const f32x4*)&T[r * P + c];
+            if (PART) {
+                __builtin_nontemporal_store(v, (f32x4*)(part + (size_t)(HR * h + r) * BN + c));
+                continue;
+            }
+            const int m = m0 + HR * h + r;
+            if (m >= M || n >= N) continue;
+            f32x4 o = v + bv;
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = act_h<ACT>(o[e]);
+            const size_t idx = (size_t)m * N + n;
+            if (g.resid) o += *(const f32x4*)(g.resid + idx);
+            __builtin_nontemporal_store(o, (f32x4*)(g.y + idx));
+        }
+    }
+}
+
+// Split-K epilogue: one thread per output float4; sums the splits' row-major partial tiles in
+// split order, then +bias -> act -> +resid.
+template <int ACT, int BM>
+__global__ __launch_bounds__(256) void k_gemm_h16_reduce(GemmH16Args g) {
+    const int M = g.M, N = g.N, splits = g.splits;
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const size_t idx4 = (size_t)blockIdx.x * 256 + threadIdx.x;
+    constexpr int Q = BM * BN / 4;              // float4s per tile
+    const int lt = (int)(idx4 / Q);
+    if (lt >= tiles_m * tiles_n) return;
+    const int q = (int)(idx4 - (size_t)lt * Q);
+    const int r = q / (BN / 4), c = 4 * (q % (BN / 4));
+    int m0, n0;
+    tile_origin(lt, tiles_m, tiles_n, BM, m0, n0);
+    const int m = m0 + r, n = n0 + c;
+    if (m >= M || n >= N) return;
+    const f32x4* part = (const f32x4*)(g.ws + (size_t)lt * splits * BM * BN) + q;
+    f32x4 v = __builtin_nontemporal_load(part);
+    for (int k = 1; k < splits; k++) v += __builtin_nontemporal_load(part + (size_t)k * Q);
+    if (g.bias) v += *(const f32x4*)(g.bias + n);
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = act_h<ACT>(v[e]);
+    const size_t o = (size_t)m * N + n;
+    if (g.resid) v += *(const f32x4*)(g.resid + o);
+    __builtin_nontemporal_store(v, (f32x4*)(g.y + o));
+}
+
+H16Plan gemm_h16_plan(int M, int N, int K) {
+    H16Plan p{};
+    const int tn = (N + BN - 1) / BN;
+    const int t128 = ((M + 127) / 128) * tn;
+    // 128-row activation tiles once there are about two per CU; below that the 64-row tile
+    // (1.5x the operand traffic per flop, but twice the workgroups) measured faster
+    p.bm = t128 >= 512 ? 128 : 64;
+    const int tiles = ((M + p.bm - 1) / p.bm) * tn;
+    const int S = K / 64;
+    p.splits = 1;
+    // split K while there are fewer workgroups than about 1.5 per CU and each split keeps
+    // >= 12 stages (K >= 768)
+    while (tiles * p.splits * 2 <= 384 && S / (p.splits * 2) >= 12) p.splits *= 2;
+    p.ws_bytes = p.splits > 1 ? (size_t)tiles * p.splits * p.bm * BN * 4 : 0;
+    return p;
+}
+
+size_t packed_weight_bytes_f16(int64_t N, int64_t K) { return (size_t)(2 * N * K); }
+
+hipError_t launch_pack_weights_f16(int wtype, const void* w, void* out, int N, int K, hipStream_t s) {
+    const int64_t blocks = (int64_t)N * (K / 32);
+    if (blocks == 0) return hipSuccess;
+    const dim3 grid((unsigned)((blocks + 255) / 256)), block(256);
+    if (wtype == 8)
+        hipLaunchKernelGGL(k_pack_w16<8>, grid, block, 0, s, (const uint8_t*)w, (u32x4*)out, N, K);
+    else if (wtype == 12)
+        hipLaunchKernelGGL(k_pack_w16<12>, grid, block, 0, s, (const uint8_t*)w, (u32x4*)out, N, K);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_f32_to_f16(const float* x, _Float16* h, int64_t n, hipStream_t s) {
+    const int64_t n8 = n / 8;
+    if (n8 == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_f32_to_f16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s,
+                       (const f32x4*)x, (u32x4*)h, n8);
+    return hipGetLastError();
+}
+
+template <int BMV>
+static hipError_t launch_h16_t(const GemmH16Args& a, hipStream_t s) {
+    const int tiles = ((a.M + BMV - 1) / BMV) * ((a.N + BN - 1) / BN);
+    const int splits = std::max(a.splits, 1);
+    const dim3 block(NT);
+    if (splits > 1) {
+        hipLaunchKernelGGL((k_gemm_h16<0, BMV, true>), dim3(tiles * splits), block, 0, s, a);
+        const size_t n4 = (size_t)tiles * BMV * BN / 4;
+        const dim3 rg((unsigned)((n4 + 255) / 256));
+        if (a.act == 1) hipLaunchKernelGGL((k_gemm_h16_reduce<1, BMV>), rg, block, 0, s, a);
+        else if (a.act == 2) hipLaunchKernelGGL((k_gemm_h16_reduce<2, BMV>), rg, block, 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_h16_reduce<0, BMV>), rg, block, 0, s, a);
+    } else {
+        if (a.act == 1) hipLaunchKernelGGL((k_gemm_h16<1, BMV, false>), dim3(tiles), block, 0, s, a);
+        else if (a.act == 2) hipLaunchKernelGGL((k_gemm_h16<2, BMV, false>), dim3(tiles), block, 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_h16<0, BMV, false>), dim3(tiles), block, 0, s, a);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_h16(int bm, const GemmH16Args& a, hipStream_t s) {
+    if (bm == 128) return launch_h16_t<128>(a, s);
+    if (bm == 64) return launch_h16_t<64>(a, s);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace mgh

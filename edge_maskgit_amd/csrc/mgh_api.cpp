@@ -135,6 +135,32 @@ int run_gemm_qp(mgh_ctx* c, int wtype, mgh::GemmArgs a, bool dbg) {
     return MGH_OK;
 }
 
+// The fp16 dequantize-fused GEMM with its split-K plan (workspace from the context).
+int run_gemm_h16(mgh_ctx* c, mgh::GemmH16Args a) {
+    const mgh::H16Plan p = mgh::gemm_h16_plan(a.M, a.N, a.K);
+    a.splits = p.splits;
+    if (p.splits > 1) {
+        if (int r = ensure_qp_ws(c, p.ws_bytes)) return r;
+        a.ws = (float*)c->qp_ws;
+    }
+    MGH_HIP(c, mgh::launch_gemm_h16(p.bm, a, c->stream), "k_gemm_h16");
+    return MGH_OK;
+}
+
+int check_h16(mgh_ctx* c, const char* fn, const void* wp, int N, int K, const void* x, int M,
+              const float* bias, int act, const float* resid, const float* y) {
+    if (N <= 0 || K <= 0 || M < 0) return fail(c, MGH_ERR_ARG, std::string(fn) + ": shape must have N>0, K>0, M>=0");
+    if (act < 0 || act > 2) return fail(c, MGH_ERR_ARG, "act must be 0 (none), 1 (gelu) or 2 (silu)");
+    if (K % 64) return fail(c, MGH_ERR_UNSUPPORTED, std::string(fn) + ": needs K % 64 == 0");
+    if (N % 4) return fail(c, MGH_ERR_UNSUPPORTED, std::string(fn) + ": needs N % 4 == 0");
+    if (M == 0) return MGH_OK;
+    if (!wp || !x || !y) return fail(c, MGH_ERR_ARG, std::string(fn) + ": null pointer");
+    if (!aligned16(wp) || !aligned16(x) || !aligned16(bias) || !aligned16(resid) || !aligned16(y))
+        return fail(c, MGH_ERR_ARG, std::string(fn) + ": operands must be 16-byte aligned");
+    return MGH_OK;
+}
+
+
 // Streamed kernel when K is a multiple of 256 and every streamed operand is 16-byte aligned
 // (its 16-byte direct-to-LDS loads and vector scale loads need both); general kernel otherwise.
 hipError_t launch_gemm(int wtype, const mgh::GemmArgs& a, bool dbg, hipStream_t s) {
@@ -649,6 +675,59 @@ int mgh_decode_step(mgh_ctx* c, void* state, void* work, const float* logits, in
     a.step = step; a.n_steps = n_steps; a.choice_temp = choice_temp;
     MGH_HIP(c, mgh::launch_decode_step(a, state, work, c->stream), "decode_step");
     return MGH_OK;
+}
+
+size_t mgh_packed_weight_bytes_f16(int N, int K) {
+    return N > 0 && K > 0 ? mgh::packed_weight_bytes_f16(N, K) : 0;
+}
+
+int mgh_pack_weights_f16(mgh_ctx* c, int wtype, const void* w, int N, int K, void* wp16) {
+    if (!c) return MGH_ERR_ARG;
+    if (int r = check_quant_shape(c, wtype, N, K, 0)) return r;
+    if (!w || !wp16) return fail(c, MGH_ERR_ARG, "pack_weights_f16: null pointer");
+    if (!aligned16(wp16)) return fail(c, MGH_ERR_ARG, "pack_weights_f16: output must be 16-byte aligned");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_pack_weights_f16(wtype, w, wp16, N, K, c->stream), "k_pack_w16");
+    return MGH_OK;
+}
+
+int mgh_f32_to_f16(mgh_ctx* c, const float* x, int64_t n, void* x16) {
+    if (!c) return MGH_ERR_ARG;
+    if (n < 0 || n % 8) return fail(c, MGH_ERR_ARG, "f32_to_f16: n must be a non-negative multiple of 8");
+    if (n == 0) return MGH_OK;
+    if (!x || !x16 || !aligned16(x) || !aligned16(x16))
+        return fail(c, MGH_ERR_ARG, "f32_to_f16: pointers must be non-null and 16-byte aligned");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_f32_to_f16(x, (_Float16*)x16, n, c->stream), "k_f32_to_f16");
+    return MGH_OK;
+}
+
+int mgh_gemm_h16(mgh_ctx* c, const void* wp16, int N, int K, const void* x16, int M,
+                 const float* bias, int act, const float* resid, float* y) {
+    if (!c) return MGH_ERR_ARG;
+    if (int r = check_h16(c, "gemm_h16", wp16, N, K, x16, M, bias, act, resid, y)) return r;
+    if (M == 0) return MGH_OK;
+    if (int r = set_dev(c)) return r;
+    mgh::GemmH16Args a{};
+    a.x = (const _Float16*)x16; a.w = (const _Float16*)wp16;
+    a.bias = bias; a.resid = resid; a.y = y;
+    a.M = M; a.N = N; a.K = K; a.act = act;
+    return run_gemm_h16(c, a);
+}
+
+int mgh_gemm_h16_f32in(mgh_ctx* c, const void* wp16, int N, int K, const float* x, int M,
+                       const float* bias, int act, const float* resid, float* y) {
+    if (!c) return MGH_ERR_ARG;
+    if (int r = check_h16(c, "gemm_h16_f32in", wp16, N, K, x, M, bias, act, resid, y)) return r;
+    if (M == 0) return MGH_OK;
+    if (int r = set_dev(c)) return r;
+    if (int r = ensure_scratch(c, round256((size_t)M * K * 2))) return r;
+    MGH_HIP(c, mgh::launch_f32_to_f16(x, (_Float16*)c->scratch, (int64_t)M * K, c->stream), "k_f32_to_f16");
+    mgh::GemmH16Args a{};
+    a.x = (const _Float16*)c->scratch; a.w = (const _Float16*)wp16;
+    a.bias = bias; a.resid = resid; a.y = y;
+    a.M = M; a.N = N; a.K = K; a.act = act;
+    return run_gemm_h16(c, a);
 }
 
 int mgh_debug_block_dots(mgh_ctx* c, int wtype, const void* w, int N, int K, const int8_t* qx,

@@ -126,4 +126,26 @@ size_t decode_work_bytes(int B, int S);
 hipError_t launch_decode_seed(int B, void* state, hipStream_t s);
 hipError_t launch_decode_step(DecodeArgs a, void* state, void* work, hipStream_t s);
 
+// Dequantize-fused fp16 path (k_gemm_h16.hip): weights dequantized once into fp16 [N][K],
+// fp16 activations, fp32 accumulation, y = act(x . w^T + bias) + resid. K % 64 == 0,
+// N % 4 == 0, 16-byte aligned operands.
+struct GemmH16Args {
+    const _Float16* x;     // [M][K]
+    const _Float16* w;     // [N][K]
+    const float* bias;     // [N] or null
+    const float* resid;    // [M][N] or null
+    float* y;              // [M][N]
+    float* ws;             // split-K partial tiles (H16Plan::ws_bytes)
+    int M, N, K, splits, act;
+};
+struct H16Plan {
+    int bm, splits;
+    size_t ws_bytes;
+};
+H16Plan gemm_h16_plan(int M, int N, int K);
+size_t packed_weight_bytes_f16(int64_t N, int64_t K);
+hipError_t launch_pack_weights_f16(int wtype, const void* w, void* out, int N, int K, hipStream_t s);
+hipError_t launch_f32_to_f16(const float* x, _Float16* h, int64_t n, hipStream_t s);
+hipError_t launch_gemm_h16(int bm, const GemmH16Args& a, hipStream_t s);
+
 }  // namespace mgh

@@ -75,7 +75,7 @@ void grow(mgh_ctx* c, void** p, size_t* cap, size_t need) {
 }
 
 void check(mgh_ctx* c, int rc) {
-    if (rc != MGH_OK) throw std::runtime_error(std::string("mgr_generate: ") + mgh_last_error(c));
+    if (rc != MGH_OK) throw std::runtime_error(std::string("mgr: ") + mgh_last_error(c));
 }
 
 }  // namespace
@@ -136,8 +136,10 @@ int mgr_forward(mgr_model* m, const int32_t* tokens, int S, int B, float* logits
         mg::Graph g;
         g.build_forward(out);
         m->rt->invalidate(tok);               // new token ids at a reused host address
-        m->rt->compute(g);
-        if (logits) std::memcpy(logits, out->data, out->nbytes());
+        // the logits go straight from HBM to the caller's buffer (or stay on the device)
+        const void* d = m->rt->compute_device(g);
+        mgh_ctx* c = m->rt->context();
+        check(c, logits ? mgh_d2h(c, logits, d, out->nbytes()) : mgh_sync(c));
         return 0;
     } catch (const std::exception& e) {
         return fail(e);

@@ -186,6 +186,24 @@ int mgh_add(mgh_ctx* ctx, const float* d_a, const float* d_b, int64_t nb, float*
 int mgh_copy_strided(mgh_ctx* ctx, const float* d_a, const int64_t ne[4], const int64_t strides[4],
                      float* d_out);
 
+/* ---- dequantize-fused fp16 FC path: the reference's fp16-slab dequant GEMMs
+ *      k_mul_mat_q8_0_t2_h / k_mul_mat_q4k_t2_h (src/mg-opencl/mg-opencl.cpp:320-411).
+ *      mgh_pack_weights_f16 expands raw Q8_0 / Q4_K blocks once into fp16 [N][K]
+ *      (w = d*q, resp. (d*sc)*q - dmin*m in fp32, rounded to nearest fp16; buffer size
+ *      mgh_packed_weight_bytes_f16). mgh_gemm_h16 computes
+ *      y[M][N] = act(x16[M][K] . w16^T + bias) + resid with fp16 activations (for example
+ *      from mgh_layernorm_affine with MGH_EMIT_DEQ_F16 or mgh_f32_to_f16) and fp32
+ *      accumulation; mgh_gemm_h16_f32in rounds fp32 activations to fp16 first (context
+ *      scratch). K % 64 == 0, N % 4 == 0, 16-byte aligned operands. ---- */
+size_t mgh_packed_weight_bytes_f16(int N, int K);
+int mgh_pack_weights_f16(mgh_ctx* ctx, int wtype, const void* d_w, int N, int K, void* d_wp16);
+/* x -> fp16 (round to nearest even); n % 8 == 0 */
+int mgh_f32_to_f16(mgh_ctx* ctx, const float* d_x, int64_t n, void* d_x16);
+int mgh_gemm_h16(mgh_ctx* ctx, const void* d_wp16, int N, int K, const void* d_x16, int M,
+                 const float* d_bias, int act, const float* d_resid, float* d_y);
+int mgh_gemm_h16_f32in(mgh_ctx* ctx, const void* d_wp16, int N, int K, const float* d_x, int M,
+                       const float* d_bias, int act, const float* d_resid, float* d_y);
+
 /* ---- iterative decoding on the device: one step of the reference's generate() loop,
  *      src/mg-generate.cpp:82-121, for B images whose logits [B][S][V] are already in HBM.
  *      Image b draws from std::mt19937_64(seeds[b]) through uniform_real_distribution<double>

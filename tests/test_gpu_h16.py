@@ -1,0 +1,149 @@
+"""GPU parity of the dequantize-fused fp16 FC path: mgh_pack_weights_f16, mgh_f32_to_f16,
+mgh_gemm_h16 / mgh_gemm_h16_f32in (k_gemm_h16.hip).
+
+Bars:
+  * packed weights: the oracle's dequantization (pinned to the reference decoder) rounded to
+    fp16, bit for bit; the activation rounding: numpy's IEEE round-to-nearest-even, bit for bit;
+  * the GEMM itself: against a float64 product of the same fp16 operands (+ bias, activation,
+    residual in float64), max|y - ref| <= 1e-5 * max|ref| — only the fp32 accumulation order
+    differs, so a wrong index, a dropped K stage or a mis-summed split shows as O(1);
+  * the path as a whole: within 1e-3 * max|y| of the reference's dequantize-then-F32 product on
+    the fp32 activations (oracle.gemm_q_deq_f32 = mg-cpu.cpp:48-72 semantics);
+  * repeated calls are bit-identical (split-K partials are summed in a fixed order).
+"""
+import numpy as np
+import pytest
+from scipy.special import erf
+
+import edge_maskgit_amd as ema
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = ema.Context(0)
+    yield c
+    c.close()
+
+
+def _rel(y, ref):
+    return float(np.abs(y - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def _act64(v, act):
+    if act == 1:
+        return 0.5 * v * (1.0 + erf(v / np.sqrt(2.0)))
+    if act == 2:
+        return v / (1.0 + np.exp(-v))
+    return v
+
+
+def _pack16(ctx, wtype, wq, N, K):
+    dW = ctx.upload(wq)
+    dP = ctx.alloc(ema.packed_weight_bytes_f16(N, K))
+    ctx.pack_weights_f16(wtype, dW, N, K, dP)
+    ctx.free(dW)
+    return dP
+
+
+@pytest.mark.parametrize("wtype", [ema.WTYPE_Q8_0, ema.WTYPE_Q4_K])
+@pytest.mark.parametrize("N,K", [(1, 256), (96, 512), (2304, 768), (768, 3072)])
+def test_pack_f16_matches_oracle(ctx, wtype, N, K):
+    print(f"pack_f16 wtype={wtype} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(N + K + wtype)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    w[0, :32] = 0.0
+    wq = oracle.quantize(wtype, w)
+    assert ema.packed_weight_bytes_f16(N, K) == 2 * N * K
+    dP = _pack16(ctx, wtype, wq, N, K)
+    got = ctx.download(dP, (N, K), np.float16)
+    ctx.free(dP)
+    want = oracle.dequant(wtype, wq, N, K).astype(np.float16)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+def test_f32_to_f16_rounding(ctx):
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(4096 * 8) * np.exp(rng.uniform(-20, 12, 4096 * 8))).astype(np.float32)
+    x[:8] = [0.0, -0.0, 65504.0, 65520.0, 1e-8, -6.1e-5, np.float32(2049.0), np.float32(2051.0)]
+    dX, dH = ctx.upload(x), ctx.alloc(x.size * 2)
+    ctx.f32_to_f16(dX, x.size, dH)
+    got = ctx.download(dH, x.shape, np.float16)
+    ctx.free(dX)
+    ctx.free(dH)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+SHAPES = [(1, 4, 64), (7, 132, 256), (65, 128, 768), (257, 3072, 768), (1025, 2304, 768),
+          (1025, 768, 768), (1025, 768, 3072), (300, 256, 3072), (4097, 768, 3072)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("act,res", [(0, False), (1, False), (0, True), (2, True)])
+def test_gemm_h16_vs_float64(ctx, M, N, K, act, res):
+    if (M, N, K) == (4097, 768, 3072) and (act, res) != (0, True):
+        pytest.skip("one epilogue at the largest shape")
+    print(f"gemm_h16 M={M} N={N} K={K} act={act} resid={res}", flush=True)
+    rng = np.random.default_rng(M * 7 + N * 3 + K + act)
+    w16 = (rng.standard_normal((N, K)) * 0.02).astype(np.float16)
+    x16 = rng.standard_normal((M, K)).astype(np.float16)
+    bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+    resid = rng.standard_normal((M, N)).astype(np.float32) if res else None
+    dW, dX, dB = ctx.upload(w16), ctx.upload(x16), ctx.upload(bias)
+    dR = ctx.upload(resid) if res else None
+    dY = ctx.alloc(M * N * 4)
+    ctx.gemm_h16(dW, N, K, dX, M, dB, act, dR, dY)
+    y = ctx.download(dY, (M, N), np.float32)
+    ctx.gemm_h16(dW, N, K, dX, M, dB, act, dR, dY)
+    y2 = ctx.download(dY, (M, N), np.float32)
+    for t in (dW, dX, dB, dR, dY):
+        if t is not None:
+            ctx.free(t)
+    ref = _act64(x16.astype(np.float64) @ w16.astype(np.float64).T + bias, act)
+    if res:
+        ref = ref + resid
+    err = _rel(y, ref)
+    print(f"  rel err vs float64 {err:.2e}")
+    assert err <= 1e-5
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+
+
+@pytest.mark.parametrize("wtype", [ema.WTYPE_Q8_0, ema.WTYPE_Q4_K])
+@pytest.mark.parametrize("M,N,K,act,res", [(257, 768, 768, 0, True), (1025, 3072, 768, 1, False),
+                                           (1025, 768, 3072, 0, True), (64, 2304, 768, 0, False)])
+def test_gemm_h16_f32in_vs_dequant_f32(ctx, wtype, M, N, K, act, res):
+    print(f"gemm_h16_f32in wtype={wtype} M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M + N + K + wtype)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    wq = oracle.quantize(wtype, w)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+    resid = rng.standard_normal((M, N)).astype(np.float32) if res else None
+    dP = _pack16(ctx, wtype, wq, N, K)
+    dX, dB, dY = ctx.upload(x), ctx.upload(bias), ctx.alloc(M * N * 4)
+    dR = ctx.upload(resid) if res else None
+    ctx.gemm_h16_f32in(dP, N, K, dX, M, dB, act, dR, dY)
+    y = ctx.download(dY, (M, N), np.float32)
+    for t in (dP, dX, dB, dR, dY):
+        if t is not None:
+            ctx.free(t)
+    ref = oracle.gemm_q_deq_f32(wtype, wq, N, K, x, bias=bias, act=act, resid=resid)
+    err = _rel(y, ref)
+    print(f"  rel err vs dequantize-then-F32 {err:.2e}")
+    assert err <= 1e-3
+
+
+def test_gemm_h16_rejects_bad_args(ctx):
+    buf = ctx.alloc(1 << 20)
+    for (N, K) in [(6, 64), (8, 96), (0, 64)]:
+        with pytest.raises(ema.MghError):
+            ctx.gemm_h16(buf, N, K, buf, 4, None, 0, None, buf)
+    with pytest.raises(ema.MghError):
+        ctx.gemm_h16(buf, 8, 64, buf, 4, None, 3, None, buf)
+    with pytest.raises(ema.MghError):
+        ctx.f32_to_f16(buf, 12, buf)
+    ctx.free(buf)
