@@ -7,21 +7,28 @@ layer's four Q8_0 FC GEMMs at M = 1025 tokens (32x32 grid + class token), fp32 a
     out   768 -> 768   (+bias +residual)
     up    768 -> 3072  (+bias, GELU)
     down 3072 -> 768   (+bias +residual)
-A step runs each FC as the int8-dot path does it: per-32 activation quantization
-(k_quantize_act_q8, codes written as fp16) then the GEMM on weights in the device-native packed
-layout (k_gemm_qp: exact block dots on fp16 MFMA, per-block scales in registers), the weights
-packed once at upload as the reference uploads them once; all inputs already resident in HBM.
+A step runs each FC of the chosen production path, all inputs already resident in HBM, the
+weights prepared once at upload (outside the timed region, as the reference uploads each
+weight once):
+  --path h16 (default, the dequantize-fused path; it meets the 1e-3 * max|y| bar against the
+    reference's dequantize-then-F32 product): x rounded to fp16 (k_f32_to_f16), then k_gemm_h16
+    on the weights dequantized to fp16 at upload: fp16 MFMA, fp32 accumulation, fused
+    bias/GELU/residual epilogue;
+  --path packed (the int8-dot path, bit-exact int32 block dots of the reference's int8
+    kernels): per-32 int8 activation quantization (k_quantize_act_q8, codes as fp16), then
+    k_gemm_qp on the packed codes with per-block scales applied in fp32.
+The other path is measured on the same workload and reported under extra.
 Each buffer set's step is captured once as a HIP graph and replayed (--no-graphs enqueues the
 kernels one by one instead). Buffers rotate over >= --rotate-gb of distinct sets so the 256 MB
 MALL and the L2s do not serve the timed reads. Synthetic data: x ~ N(0,1), W ~ N(0,0.02)
 quantized to Q8_0, biases ~ N(0,0.01), residuals ~ N(0,1), seeded.
 
-value = 2*M*K*N summed over the four GEMMs / step time, in TOPS (int8 ops).
-roofline = the dominant kernel k_gemm_qp, HBM-bound: algorithmic bytes of its launches
-(quantized weights once + fp16 activation codes + fp32 block scales (+ block sums for Q4_K)
-+ fp32 output + bias + residual) divided by its average launch duration, timed with HIP
-events on the stream it runs on; traffic = the measured HBM bytes of those launches
-(rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy).
+value = 2*M*K*N summed over the four GEMMs / step time, in TOPS.
+roofline = the dominant kernel (k_gemm_h16, resp. k_gemm_qp), HBM-bound: algorithmic bytes of
+its launches (quantized weights once + fp16 activations (+ block scales on the int8 path) +
+fp32 output + bias + residual) divided by its average launch duration, timed with HIP events
+on the stream it runs on; traffic = the measured HBM bytes of those launches (rocprofv3
+FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy), from profiles/.
 cpu_baseline = the reference's own CPU executor (mg-cpu k_mul_mat, single thread, built
 from the reference sources into oracle/_ref) on the dequantized weights, timed on this
 host over the same four GEMMs; if that library is absent, the C oracle's int8 path.
@@ -52,7 +59,15 @@ LAYER = [  # name, N, K, act, residual
 ]
 
 
-KERNEL = {"packed": "k_gemm_qp", "raw": "k_gemm_q_f16x"}
+KERNEL = {"packed": "k_gemm_qp", "raw": "k_gemm_q_f16x", "h16": "k_gemm_h16"}
+PATH_NAME = {"packed": "int8_dot", "raw": "int8_dot_raw", "h16": "dequant_f16"}
+WORKLOAD_PATH = {
+    "h16": "dequantize-fused path (weights dequantized once to fp16 at upload; per FC: fp32 -> "
+           "fp16 activation rounding + fp16 MFMA GEMM with fp32 accumulation and fused epilogue)",
+    "packed": "int8-dot path (per FC: per-32 int8 activation quantization + exact block dots with "
+              "per-block scales applied in fp32)",
+    "raw": "int8-dot path on GGUF blocks as stored"}
+ALGO = {"packed": 1, "raw": 1, "h16": 2}
 
 
 def log(*a):
@@ -66,9 +81,11 @@ def row_bytes(wtype, K):
 class LayerSet:
     """One set of device buffers for the four FC GEMMs of a layer.
 
-    path "packed" (production): weights rewritten once at upload into the device-native layout
-    (mgh_pack_weights, outside the timed region, as the reference uploads each weight once),
-    then per FC: quantizer (fp16 codes) + mgh_gemm_q_packed.
+    path "packed" (int8-dot production path): weights rewritten once at upload into the
+    device-native layout (mgh_pack_weights, outside the timed region, as the reference uploads
+    each weight once), then per FC: quantizer (fp16 codes) + mgh_gemm_q_packed.
+    path "h16" (dequantize-fused production path): weights dequantized once at upload into
+    fp16 (mgh_pack_weights_f16), then per FC: fp32 -> fp16 activations + mgh_gemm_h16.
     path "raw": GGUF blocks as stored, per FC: quantizer + mgh_gemm_q_codes16."""
 
     def __init__(self, ctx, host, M, wtype, path="packed"):
@@ -80,7 +97,13 @@ class LayerSet:
         for (name, N, K, act, res), h in zip(LAYER, host):
             nb = K // 32
             w = ctx.upload(h["wq"])
-            if path == "packed":
+            if path == "h16":
+                wp = ctx.alloc(ema.packed_weight_bytes_f16(N, K))
+                ctx.pack_weights_f16(wtype, w, N, K, wp)
+                ctx.sync()
+                ctx.free(w)
+                w = wp
+            elif path == "packed":
                 wp = ctx.alloc(ema.packed_weight_bytes(wtype, N, K))
                 ctx.pack_weights(wtype, w, N, K, wp)
                 ctx.sync()
@@ -94,6 +117,9 @@ class LayerSet:
 
     def _gemm(self, d):
         c = self.ctx
+        if self.path == "h16":
+            c.gemm_h16(d["w"], d["N"], d["K"], d["qx"], self.M, d["b"], d["act"], d["r"], d["y"])
+            return
         f = c.gemm_q_packed if self.path == "packed" else c.gemm_q_codes16
         f(self.wtype, d["w"], d["N"], d["K"], d["qx"], d["dx"], d["sx"], self.M,
           d["b"], d["act"], d["r"], d["y"])
@@ -101,7 +127,10 @@ class LayerSet:
     def step(self):
         c = self.ctx
         for d in self.g:
-            c.quantize_act_q8_codes16(d["x"], self.M, d["K"], d["qx"], d["dx"], d["sx"])
+            if self.path == "h16":
+                c.f32_to_f16(d["x"], self.M * d["K"], d["qx"])
+            else:
+                c.quantize_act_q8_codes16(d["x"], self.M, d["K"], d["qx"], d["dx"], d["sx"])
             self._gemm(d)
 
     def gemms_only(self):
@@ -161,14 +190,16 @@ def layer_ops(M):
     return sum(2.0 * M * N * K for _, N, K, _, _ in LAYER)
 
 
-def gemm_alg_bytes(M, wtype):
-    """Algorithmic HBM bytes of the four k_gemm_q_i8 launches of one step."""
+def gemm_alg_bytes(M, wtype, path="h16"):
+    """Algorithmic HBM bytes of the four GEMM launches of one step: the quantized weights
+    once, the fp16 activations (int8-dot path: fp16 codes + fp32 block scales (+ block sums for
+    Q4_K)), the fp32 output, bias and residual."""
     tot = 0
     for _, N, K, act, res in LAYER:
         nb = K // 32
-        tot += N * row_bytes(wtype, K) + M * K * 2 + M * nb * 4 + M * N * 4 + N * 4
-        if wtype == ema.WTYPE_Q4_K:
-            tot += M * nb * 4
+        tot += N * row_bytes(wtype, K) + M * K * 2 + M * N * 4 + N * 4
+        if path != "h16":
+            tot += M * nb * 4 * (2 if wtype == ema.WTYPE_Q4_K else 1)
         if res:
             tot += M * N * 4
     return tot
@@ -320,14 +351,14 @@ def measure_forward(path, B, steps, warmup, algo=1, profile=False):
     return ms, ms_nr, prof
 
 
-def measure_generate(path, B, n_steps=8, reps=2):
+def measure_generate(path, B, n_steps=8, reps=2, algo=1):
     """cfg5: B images, n_steps device-resident decode steps (transformer forward in HBM ->
     on-device sampling / confidence / re-mask), wall clock per generate; token grids only come
     back at the end."""
     from edge_maskgit_amd.runtime import TransformerRuntime
     cls = (np.arange(B) * 37) % 1000
     seeds = np.arange(B, dtype=np.uint64) + 42
-    with TransformerRuntime(path, algo=1) as m:
+    with TransformerRuntime(path, algo=algo) as m:
         m.generate(cls, seeds, n_steps)          # packs and uploads the weights
         t0 = time.perf_counter()
         for _ in range(reps):
@@ -398,8 +429,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-graphs", action="store_true",
                     help="enqueue kernels one by one instead of replaying a captured HIP graph")
-    ap.add_argument("--path", choices=["packed", "raw"], default="packed",
-                    help="packed: device-native weight layout (production); raw: GGUF blocks as stored")
+    ap.add_argument("--path", choices=["packed", "h16", "raw"], default="h16",
+                    help="packed: int8-dot path on the device-native weight layout; h16: "
+                         "dequantize-fused fp16 path; raw: int8-dot on GGUF blocks as stored")
     ap.add_argument("--no-fwd", action="store_true", help="skip the transformer forward (cfg4)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run 10 plain device copies of BYTES (k_copy4d), to calibrate the "
@@ -430,7 +462,7 @@ def main():
                                       use_graphs=not a.no_graphs, path=a.path)
     ops = layer_ops(M)
     value = ops / (ms_step * 1e-3) / 1e12
-    gb = gemm_alg_bytes(M, wtype)
+    gb = gemm_alg_bytes(M, wtype, a.path)
     achieved = gb / (ms_gemms * 1e-3) / 1e9
     extra = {"gemm_only_ms_per_step": round(ms_gemms, 5),
              "gemm_tops": round(ops / (ms_gemms * 1e-3) / 1e12, 2),
@@ -438,6 +470,12 @@ def main():
              "step_hbm_roofline_us": round(step_alg_bytes(M, wtype) / (HBM_PEAK_GBS * 1e9) * 1e6, 2),
              "step_frac_of_hbm_roofline": round(step_alg_bytes(M, wtype) / (HBM_PEAK_GBS * 1e9)
                                                 / (ms_step * 1e-3), 4)}
+    # the other production path on the same workload
+    other = "packed" if a.path == "h16" else "h16"
+    so, go, _ = measure(ctx, M, wtype, a.steps, a.warmup, a.rotate_gb, use_graphs=not a.no_graphs, path=other)
+    extra[f"cfg2_{PATH_NAME[other]}"] = {
+        "ms_per_step": round(so, 5), "tops": round(ops / (so * 1e-3) / 1e12, 2),
+        "gemm_tops": round(ops / (go * 1e-3) / 1e12, 2), "kernel": KERNEL[other]}
     if a.extra:
         for (mm, wt) in ((4097, ema.WTYPE_Q8_0), (1025, ema.WTYPE_Q4_K), (4097, ema.WTYPE_Q4_K)):
             s, g, _ = measure(ctx, mm, wt, max(10, a.steps // 2), a.warmup, a.rotate_gb,
@@ -454,28 +492,31 @@ def main():
             t0 = time.perf_counter()
             write_synthetic_model(path, 24, ema.WTYPE_Q8_0)
             log(f"[bench] cfg4 model written in {time.perf_counter() - t0:.1f} s")
-            fwd, fwd_nr, prof = measure_forward(path, 16, max(3, a.steps // 10), 2, profile=True)
+            fwd4 = {}
+            for pth in (a.path, other):
+                fwd, fwd_nr, prof = measure_forward(path, 16, max(3, a.steps // 10), 2, algo=ALGO[pth],
+                                                    profile=True)
+                fwd4[PATH_NAME[pth]] = {"ms": round(fwd, 3), "ms_no_logits_readback": round(fwd_nr, 3),
+                                        "per_op_device_ms": prof}
             extra["transformer_fwd_cfg4"] = {
-                "ms": round(fwd, 3), "ms_no_logits_readback": round(fwd_nr, 3),
                 "model": "24 layers Q8_0 random-init, hidden 768, 16 heads, MLP 3072, vocab 2025",
-                "batch": "16 images x 257 tokens (M=4112)", "algo": "int8-dot",
-                "per_op_device_ms": prof}
+                "batch": "16 images x 257 tokens (M=4112)", **fwd4}
             if a.extra:
                 path5 = os.path.join(d, "cfg5_q4_k.gguf")
                 write_synthetic_model(path5, 24, ema.WTYPE_Q4_K, seed=5)
-                f5, f5nr, _ = measure_forward(path5, 64, 3, 1)
+                f5, f5nr, _ = measure_forward(path5, 64, 3, 1, algo=ALGO[a.path])
                 extra["transformer_fwd_q4k_b64"] = {"ms": round(f5, 3), "ms_no_logits_readback": round(f5nr, 3),
                                                     "batch": "64 x 257 tokens (M=16448), one decode step's forward"}
-                gen = measure_generate(path5, 64)
+                gen = measure_generate(path5, 64, algo=ALGO[a.path])
                 extra["generate_cfg5"] = {
                     "ms_per_generate": round(gen, 2), "ms_per_step": round(gen / 8, 3),
                     "decode_step_device_ms": round(measure_decode_step(ctx, 64), 4),
-                    "workload": "64 images x 257 tokens, 8 steps, Q4_K 24 layers, int8-dot; "
+                    "workload": f"64 images x 257 tokens, 8 steps, Q4_K 24 layers, {PATH_NAME[a.path]}; "
                                 "forward + on-device sampling per step, grids read back once"}
     cpu = None if a.no_cpu else cpu_baseline(host, M, wtype)
     traffic = None
-    tf = os.path.join(ROOT, "profiles", "traffic_cfg2_q8_m1025.json")
-    if a.path == "packed" and os.path.exists(tf):
+    tf = os.path.join(ROOT, "profiles", f"traffic_{KERNEL[a.path]}_cfg2_q8_m1025.json")
+    if os.path.exists(tf):
         traffic = json.load(open(tf)).get("traffic_bytes_per_step")   # rocprofv3 --pmc, scaled
     line = {
         "metric": "Q8_0/Q4_K GEMM TOPS + % roofline at M=1025/4097; transformer fwd ms",
@@ -488,11 +529,12 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
+        "dtype": "f16" if a.path == "h16" else "int8",
         "data": "synthetic",
         "config": {"workload": "cfg2: one MaskGIT layer's four Q8_0 FC GEMMs (QKV 768->2304, "
                                "out 768->768 +resid, up 768->3072 +GELU, down 3072->768 +resid), "
-                               "M=1025, fp32 activations, int8-dot path (quantize + GEMM)",
+                               "M=1025, fp32 activations and outputs, " + WORKLOAD_PATH[a.path],
+                   "path": PATH_NAME[a.path],
                    "M": M, "weights": "Q8_0", "rotate_gb": a.rotate_gb,
                    "launch": "stream" if a.no_graphs else "hip_graph_per_step"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,

@@ -4,7 +4,8 @@
 //
 // Per compute():
 //  1. Plan: every node's storage root (views alias their source), each root's last consumer,
-//     the LayerNorm nodes whose output feeds int8-dot FC layers (fused operand), and the
+//     the LayerNorm nodes whose output feeds quantized FC layers (fused operand: int8 codes for
+//     the int8-dot path, fp16 values for the dequantize-fused path), and the
 //     flash-attention -> permute -> cont chains (attention writes the merged layout).
 //  2. Run the nodes in order; device buffers of computed roots come from a size-bucketed
 //     pool and return to it after their last consumer.
@@ -12,7 +13,8 @@
 //     compute_device() instead keeps the result in HBM for device-side consumers (the
 //     decode step) and returns without waiting.
 // Leaves are uploaded once per (host address, byte size) and kept; quantized weights are
-// packed on upload (mgh_pack_weights). Supported ops: MulMat (Q8_0, Q4_K, F32 weights),
+// packed on upload (mgh_pack_weights for the int8-dot path, mgh_pack_weights_f16 for the
+// dequantize-fused path). Supported ops: MulMat (Q8_0, Q4_K, F32 weights),
 // Norm (plain or affine), FlashAttention, GetRows, Add, Cont, Reshape, View, Permute.
 #include "mg-hip.hpp"
 
@@ -53,7 +55,7 @@ struct HipRuntime::Impl {
     bool profiling = false;
     std::map<std::string, std::pair<int, double>> prof;
 
-    // leaf uploads: (host address, bytes, packed?) -> device pointer
+    // leaf uploads: (host address, bytes, layout) -> device pointer
     std::map<std::tuple<const void*, size_t, int>, void*> leaves;
     // free device buffers by size
     std::multimap<size_t, void*> pool;
@@ -68,7 +70,7 @@ struct HipRuntime::Impl {
     // per-compute state
     std::unordered_map<const Tensor*, void*> addr;            // device address of a tensor
     struct Codes { void* q = nullptr; void* dx = nullptr; void* sx = nullptr; size_t bytes = 0; };
-    std::unordered_map<const Tensor*, Codes> codes;           // fused int8-dot operand of a Norm node
+    std::unordered_map<const Tensor*, Codes> codes;           // fused FC operand of a Norm node
 
     void check(int rc) {
         if (rc != MGH_OK) throw std::runtime_error(std::string("HipRuntime: ") + mgh_last_error(ctx));
@@ -90,9 +92,11 @@ struct HipRuntime::Impl {
     void give(void* p) { pool.emplace(alloc_size.at(p), p); }
     std::unordered_map<void*, size_t> alloc_size;
 
-    void* upload_leaf(const Tensor* t, bool packed) {
+    // layout 0: the leaf's bytes as stored; 1: quantized weight in the int8-dot packed layout
+    // (mgh_pack_weights); 2: quantized weight dequantized into fp16 (mgh_pack_weights_f16)
+    void* upload_leaf(const Tensor* t, int layout) {
         const size_t n = t->nbytes();
-        const auto key = std::make_tuple((const void*)t->data, n, packed ? (int)t->type : -1);
+        const auto key = std::make_tuple((const void*)t->data, n, layout ? 100 * layout + (int)t->type : -1);
         const auto it = leaves.find(key);
         if (it != leaves.end()) return it->second;
         if (!t->data) throw std::runtime_error("HipRuntime: leaf '" + t->name + "' has no host data");
@@ -100,13 +104,13 @@ struct HipRuntime::Impl {
         check(mgh_alloc(ctx, n, &raw));
         check(mgh_h2d(ctx, raw, t->data, n));
         void* d = raw;
-        if (packed) {
+        if (layout) {
             const int wt = t->type == Type::Q8_0 ? MGH_WTYPE_Q8_0 : MGH_WTYPE_Q4_K;
             const int K = (int)t->ne[0], N = (int)(t->nelements() / t->ne[0]);
-            const size_t pb = mgh_packed_weight_bytes(wt, N, K);
+            const size_t pb = layout == 2 ? mgh_packed_weight_bytes_f16(N, K) : mgh_packed_weight_bytes(wt, N, K);
             if (!pb) throw std::runtime_error("HipRuntime: unsupported quantized weight shape for '" + t->name + "'");
             check(mgh_alloc(ctx, pb, &d));
-            check(mgh_pack_weights(ctx, wt, raw, N, K, d));
+            check(layout == 2 ? mgh_pack_weights_f16(ctx, wt, raw, N, K, d) : mgh_pack_weights(ctx, wt, raw, N, K, d));
             check(mgh_free(ctx, raw));
         }
         leaves[key] = d;
@@ -125,7 +129,7 @@ struct HipRuntime::Impl {
             const auto it = addr.find(r);
             if (it != addr.end()) return it->second;
             const auto b = bound.find(r);
-            void* d = b != bound.end() ? b->second : upload_leaf(r, false);
+            void* d = b != bound.end() ? b->second : upload_leaf(r, 0);
             addr[r] = d;
             return d;
         }
@@ -295,8 +299,16 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                 const float* bias = (const float*)I.dev(t->src[2]);
                 const float* resid = (const float*)I.dev(t->src[3]);
                 const int act = t->iparam[0];
-                if (quant(w)) {
-                    void* wp = I.upload_leaf(w, true);
+                if (quant(w) && I.algo == MGH_ALGO_DEQ_F16) {
+                    void* wp = I.upload_leaf(w, 2);
+                    const auto c = I.codes.find(I.root(x));
+                    if (c != I.codes.end())
+                        I.check(mgh_gemm_h16(I.ctx, wp, N, K, c->second.q, M, bias, act, resid, (float*)out));
+                    else
+                        I.check(mgh_gemm_h16_f32in(I.ctx, wp, N, K, (const float*)I.dev(x), M, bias, act, resid,
+                                                   (float*)out));
+                } else if (quant(w)) {
+                    void* wp = I.upload_leaf(w, 1);
                     const auto c = I.codes.find(I.root(x));
                     if (c != I.codes.end())
                         I.check(mgh_gemm_q_packed(I.ctx, w->type == Type::Q8_0 ? MGH_WTYPE_Q8_0 : MGH_WTYPE_Q4_K,
@@ -328,10 +340,11 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                 }
                 int emit = MGH_EMIT_NONE;
                 Impl::Codes cd;
-                // one int8-dot operand for every quantized FC that reads this LN (flat 32-blocks,
-                // so any FC row length that is a multiple of 32 reads the same codes)
-                if (I.algo == MGH_ALGO_INT8 && fc_uses.count(t)) {
-                    emit = MGH_EMIT_INT8;
+                // one FC operand for every quantized FC that reads this LN: int8 codes (flat
+                // 32-blocks, so any FC row length that is a multiple of 32 reads the same codes),
+                // or for the dequantize-fused path the fp16-rounded y
+                if ((I.algo == MGH_ALGO_INT8 || I.algo == MGH_ALGO_DEQ_F16) && fc_uses.count(t)) {
+                    emit = I.algo == MGH_ALGO_INT8 ? MGH_EMIT_INT8 : MGH_EMIT_DEQ_F16;
                     const size_t T = (size_t)D / 32;
                     cd.q = I.take((size_t)rows * D * 2);
                     cd.dx = I.take((size_t)rows * T * 4);
