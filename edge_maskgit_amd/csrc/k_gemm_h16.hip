@@ -42,10 +42,11 @@ typedef __attribute__((address_space(3))) void lds_void;
 constexpr int NT = 256;
 constexpr int BN = 128;
 
-template <int BM>
+// XF32: the activation stage holds fp32 rows (16 chunks of 16 bytes) instead of fp16 ones
+template <int BM, bool XF32>
 struct HLds {
-    u32x4 w[2][BN * 8];     // [stage][row][8 swizzled 16-byte chunks] fp16
-    u32x4 x[2][BM * 8];
+    u32x4 w[2][BN * 8];                  // [stage][row][8 swizzled 16-byte chunks] fp16
+    u32x4 x[2][BM * (XF32 ? 16 : 8)];
 };
 
 __device__ __forceinline__ void dma16(const void* g, void* lds) {
@@ -136,13 +137,18 @@ __global__ __launch_bounds__(256) void k_f32_to_f16(const f32x4* __restrict__ x,
 }  // namespace
 
 // y[M][N] = act(x16[M][K] . w16[N][K]^T + bias) + resid, or (PART) the raw partial tile of
-// split ks over its K range into ws.
-template <int ACT, int BM, bool PART>
+// split ks over its K range into ws. XF32: the activations arrive as fp32 (g.xf) and are
+// rounded to fp16 (nearest even, as k_f32_to_f16) when the MFMA fragments are read from LDS;
+// their stage rows are 256 bytes (16 chunks, swizzle chunk ^ (row & 15)).
+template <int ACT, int BM, bool PART, bool XF32>
 __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
     constexpr int J = BM / 32;                  // 16-row activation subtiles per wave
-    constexpr int CW = BN / 32, CX = BM / 32;   // DMA instructions per wave and stage
+    constexpr int CW = BN / 32;                 // weight DMA instructions per wave and stage
+    constexpr int CX = XF32 ? BM / 16 : BM / 32;  // activation DMA instructions per wave and stage
     constexpr int MID = 2 * J;                  // second-half MFMAs issued before the boundary
-    __shared__ HLds<BM> L;
+    constexpr int NR = 4 + (XF32 ? 2 : 1) * J;  // LDS reads per K half
+    static_assert(NR <= 4 * J, "read/MFMA interleave");
+    __shared__ HLds<BM, XF32> L;
 
     const int K = g.K, M = g.M, N = g.N;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
@@ -169,8 +175,14 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
 #pragma unroll
     for (int q = 0; q < CX; q++) {
         const int c = wave + 4 * q;
-        const int m = min(m0 + 8 * c + (lane >> 3), M - 1);
-        srcx[q] = (const uint8_t*)g.x + (size_t)m * K * 2 + ((lane & 7) ^ ((4 * c + (lane >> 4)) & 7)) * 16;
+        if (XF32) {                             // 4 rows of 256 bytes per instruction
+            const int r = 4 * c + (lane >> 4);
+            const int m = min(m0 + r, M - 1);
+            srcx[q] = (const uint8_t*)g.xf + (size_t)m * K * 4 + ((lane & 15) ^ (r & 15)) * 16;
+        } else {
+            const int m = min(m0 + 8 * c + (lane >> 3), M - 1);
+            srcx[q] = (const uint8_t*)g.x + (size_t)m * K * 2 + ((lane & 7) ^ ((4 * c + (lane >> 4)) & 7)) * 16;
+        }
     }
     const int S = K / 64;
     const int s_beg = (int)((int64_t)ks * S / splits), s_end = (int)((int64_t)(ks + 1) * S / splits);
@@ -182,10 +194,19 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
 #pragma unroll
         for (int d = 0; d < CW; d++) dma16(srcw[d] + ofs, &L.w[st][(wave + 4 * d) * 64]);
 #pragma unroll
-        for (int d = 0; d < CX; d++) dma16(srcx[d] + ofs, &L.x[st][(wave + 4 * d) * 64]);
+        for (int d = 0; d < CX; d++) dma16(srcx[d] + (XF32 ? 2 : 1) * ofs, &L.x[st][(wave + 4 * d) * 64]);
     };
     auto frag = [&](const u32x4* B, int r0, int kb) {
         return __builtin_bit_cast(f16x8, B[(r0 + l16) * 8 + ((4 * kb + lq) ^ ((l16 >> 1) & 7))]);
+    };
+    // activation fragment: fp16 rows as stored, or fp32 rows rounded to fp16 on the way in
+    auto xfrag = [&](const u32x4* B, int r0, int kb) {
+        if (!XF32) return frag(B, r0, kb);
+        const int r = r0 + l16, c = 8 * kb + 2 * lq;  // r0 % 16 == 0, so r & 15 == l16
+        const f32x4 v0 = __builtin_bit_cast(f32x4, B[r * 16 + (c ^ l16)]);
+        const f32x4 v1 = __builtin_bit_cast(f32x4, B[r * 16 + ((c + 1) ^ l16)]);
+        return f16x8{(_Float16)v0[0], (_Float16)v0[1], (_Float16)v0[2], (_Float16)v0[3],
+                     (_Float16)v1[0], (_Float16)v1[1], (_Float16)v1[2], (_Float16)v1[3]};
     };
 
     f32x4 acc[4][J];
@@ -202,7 +223,7 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
 #pragma unroll
     for (int i = 0; i < 4; i++) a[0][i] = frag(L.w[0], 64 * wn + 16 * i, 0);
 #pragma unroll
-    for (int j = 0; j < J; j++) b[0][j] = frag(L.x[0], (BM / 2) * wm + 16 * j, 0);
+    for (int j = 0; j < J; j++) b[0][j] = xfrag(L.x[0], (BM / 2) * wm + 16 * j, 0);
 
     int st = 0;
     for (int s = 0; s < SL; s++) {
@@ -211,18 +232,18 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
 #pragma unroll
         for (int i = 0; i < 4; i++) a[1][i] = frag(L.w[st], 64 * wn + 16 * i, 1);
 #pragma unroll
-        for (int j = 0; j < J; j++) b[1][j] = frag(L.x[st], (BM / 2) * wm + 16 * j, 1);
+        for (int j = 0; j < J; j++) b[1][j] = xfrag(L.x[st], (BM / 2) * wm + 16 * j, 1);
 #pragma unroll
         for (int j = 0; j < J; j++)
 #pragma unroll
             for (int i = 0; i < 4; i++)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0][i], b[0][j], acc[i][j], 0, 0, 0);
 #pragma unroll
-        for (int t = 0; t < 4 + J; t++) {
+        for (int t = 0; t < NR; t++) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 4 * J - (4 + J), 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4 * J - NR, 0);
         // K half 1: MID MFMAs, the stage boundary, the rest
 #pragma unroll
         for (int q = 0; q < MID; q++)
@@ -234,7 +255,7 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
 #pragma unroll
             for (int i = 0; i < 4; i++) a[0][i] = frag(L.w[stn], 64 * wn + 16 * i, 0);
 #pragma unroll
-            for (int j = 0; j < J; j++) b[0][j] = frag(L.x[stn], (BM / 2) * wm + 16 * j, 0);
+            for (int j = 0; j < J; j++) b[0][j] = xfrag(L.x[stn], (BM / 2) * wm + 16 * j, 0);
         }
 #pragma unroll
         for (int q = MID; q < 4 * J; q++)
@@ -246,7 +267,7 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
     // epilogue: the tile leaves through LDS as whole rows, in two halves of BM/2 rows
     constexpr int P = BN + 4;                   // padded row pitch (floats)
     constexpr int HR = BM / 2;
-    static_assert(HR * P * 4 <= (int)sizeof(HLds<BM>), "transpose buffer fits the ring");
+    static_assert(HR * P * 4 <= (int)sizeof(HLds<BM, XF32>), "transpose buffer fits the ring");
     float* T = (float*)&L;
     const int c = 4 * (tid & 31);               // this thread's 4 columns
     const int n = n0 + c;
@@ -351,29 +372,30 @@ hipError_t launch_f32_to_f16(const float* x, _Float16* h, int64_t n, hipStream_t
     return hipGetLastError();
 }
 
-template <int BMV>
+template <int BMV, bool XF32>
 static hipError_t launch_h16_t(const GemmH16Args& a, hipStream_t s) {
     const int tiles = ((a.M + BMV - 1) / BMV) * ((a.N + BN - 1) / BN);
     const int splits = std::max(a.splits, 1);
     const dim3 block(NT);
     if (splits > 1) {
-        hipLaunchKernelGGL((k_gemm_h16<0, BMV, true>), dim3(tiles * splits), block, 0, s, a);
+        hipLaunchKernelGGL((k_gemm_h16<0, BMV, true, XF32>), dim3(tiles * splits), block, 0, s, a);
         const size_t n4 = (size_t)tiles * BMV * BN / 4;
         const dim3 rg((unsigned)((n4 + 255) / 256));
         if (a.act == 1) hipLaunchKernelGGL((k_gemm_h16_reduce<1, BMV>), rg, block, 0, s, a);
         else if (a.act == 2) hipLaunchKernelGGL((k_gemm_h16_reduce<2, BMV>), rg, block, 0, s, a);
         else hipLaunchKernelGGL((k_gemm_h16_reduce<0, BMV>), rg, block, 0, s, a);
     } else {
-        if (a.act == 1) hipLaunchKernelGGL((k_gemm_h16<1, BMV, false>), dim3(tiles), block, 0, s, a);
-        else if (a.act == 2) hipLaunchKernelGGL((k_gemm_h16<2, BMV, false>), dim3(tiles), block, 0, s, a);
-        else hipLaunchKernelGGL((k_gemm_h16<0, BMV, false>), dim3(tiles), block, 0, s, a);
+        if (a.act == 1) hipLaunchKernelGGL((k_gemm_h16<1, BMV, false, XF32>), dim3(tiles), block, 0, s, a);
+        else if (a.act == 2) hipLaunchKernelGGL((k_gemm_h16<2, BMV, false, XF32>), dim3(tiles), block, 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_h16<0, BMV, false, XF32>), dim3(tiles), block, 0, s, a);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_gemm_h16(int bm, const GemmH16Args& a, hipStream_t s) {
-    if (bm == 128) return launch_h16_t<128>(a, s);
-    if (bm == 64) return launch_h16_t<64>(a, s);
+    const bool xf = a.xf != nullptr;
+    if (bm == 128) return xf ? launch_h16_t<128, true>(a, s) : launch_h16_t<128, false>(a, s);
+    if (bm == 64) return xf ? launch_h16_t<64, true>(a, s) : launch_h16_t<64, false>(a, s);
     return hipErrorInvalidValue;
 }
 

@@ -721,10 +721,8 @@ int mgh_gemm_h16_f32in(mgh_ctx* c, const void* wp16, int N, int K, const float* 
     if (int r = check_h16(c, "gemm_h16_f32in", wp16, N, K, x, M, bias, act, resid, y)) return r;
     if (M == 0) return MGH_OK;
     if (int r = set_dev(c)) return r;
-    if (int r = ensure_scratch(c, round256((size_t)M * K * 2))) return r;
-    MGH_HIP(c, mgh::launch_f32_to_f16(x, (_Float16*)c->scratch, (int64_t)M * K, c->stream), "k_f32_to_f16");
     mgh::GemmH16Args a{};
-    a.x = (const _Float16*)c->scratch; a.w = (const _Float16*)wp16;
+    a.xf = x; a.w = (const _Float16*)wp16;
     a.bias = bias; a.resid = resid; a.y = y;
     a.M = M; a.N = N; a.K = K; a.act = act;
     return run_gemm_h16(c, a);

@@ -130,7 +130,8 @@ hipError_t launch_decode_step(DecodeArgs a, void* state, void* work, hipStream_t
 // fp16 activations, fp32 accumulation, y = act(x . w^T + bias) + resid. K % 64 == 0,
 // N % 4 == 0, 16-byte aligned operands.
 struct GemmH16Args {
-    const _Float16* x;     // [M][K]
+    const _Float16* x;     // [M][K] fp16 activations, or
+    const float* xf;       // [M][K] fp32 activations rounded to fp16 in the kernel (x unused)
     const _Float16* w;     // [N][K]
     const float* bias;     // [N] or null
     const float* resid;    // [M][N] or null

@@ -137,6 +137,27 @@ def test_gemm_h16_f32in_vs_dequant_f32(ctx, wtype, M, N, K, act, res):
     assert err <= 1e-3
 
 
+@pytest.mark.parametrize("M,N,K,act", [(65, 128, 768, 0), (1025, 2304, 768, 1), (1025, 768, 3072, 0),
+                                       (4097, 3072, 768, 2)])
+def test_gemm_h16_f32in_equals_rounded_operand(ctx, M, N, K, act):
+    """The in-kernel fp32 -> fp16 rounding (XF32 variant) gives the same bits as rounding with
+    mgh_f32_to_f16 first and running the fp16-operand kernel."""
+    print(f"gemm_h16 f32in == f32_to_f16 + gemm_h16: M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M + 3 * N + K)
+    w16 = (rng.standard_normal((N, K)) * 0.02).astype(np.float16)
+    x = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+    dW, dX, dB = ctx.upload(w16), ctx.upload(x), ctx.upload(bias)
+    dH, dY1, dY2 = ctx.alloc(M * K * 2), ctx.alloc(M * N * 4), ctx.alloc(M * N * 4)
+    ctx.gemm_h16_f32in(dW, N, K, dX, M, dB, act, None, dY1)
+    ctx.f32_to_f16(dX, M * K, dH)
+    ctx.gemm_h16(dW, N, K, dH, M, dB, act, None, dY2)
+    y1, y2 = ctx.download(dY1, (M, N), np.float32), ctx.download(dY2, (M, N), np.float32)
+    for t in (dW, dX, dB, dH, dY1, dY2):
+        ctx.free(t)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+
+
 def test_gemm_h16_rejects_bad_args(ctx):
     buf = ctx.alloc(1 << 20)
     for (N, K) in [(6, 64), (8, 96), (0, 64)]:
