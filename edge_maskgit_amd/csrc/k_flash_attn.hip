@@ -21,6 +21,8 @@
 //    fp32 probabilities are applied to ~2^-22 — the reference multiplies them in fp32.
 // LDS rows are padded (K: D+8 halves, V^T: 72 halves) so the fragment reads are
 // bank-conflict free.
+#include <algorithm>
+
 #include "mgh_common.h"
 #include "mgh_kernels.h"
 
@@ -155,10 +157,162 @@ __global__ __launch_bounds__(256) void k_flash_attn_f16kv(FaArgs a) {
     }
 }
 
+
+// Whole-head variant for S <= 16*KT: one workgroup per (h, b) stages the head's K (row-major)
+// and V (transposed) once in LDS as fp16, then each wave takes 16-query tiles and computes all
+// scores of a tile in registers, a plain (not online) max-subtracted softmax over the row —
+// the order of the reference CPU kernel — and P . V. K/V are read once per head instead of
+// once per query tile, with 16-byte loads (needs unit d stride and 16-byte aligned rows).
+// at most NW waves (a workgroup takes min(NW, ~half the query tiles) waves), so the score
+// registers (4 * KT per lane) fit without spilling
+template <int KT>
+constexpr int kHeadWaves = KT <= 17 ? (KT + 1) / 2 : 8;
+
+template <int DC, int KT>
+__global__ __launch_bounds__(64 * kHeadWaves<KT>) void k_attn_head(FaArgs a) {
+    constexpr int D = 16 * DC;
+    constexpr int KLD = D + 8;         // K row stride (halves)
+    constexpr int SP = 16 * KT;        // keys, padded
+    constexpr int VT = SP + 8;         // V^T row stride (halves)
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[SP * KLD];
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[D * VT];
+
+    const int S = a.S;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int64_t base = (int64_t)b * a.st[3] + (int64_t)h * a.st[2];
+
+    for (int idx = tid; idx < SP * (D / 4); idx += blockDim.x) {
+        const int t = idx / (D / 4), d = 4 * (idx - t * (D / 4));
+        f32x4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+        if (t < S) {
+            const int64_t off = base + (int64_t)t * a.st[1] + d;
+            kv = *(const f32x4*)(a.k + off);
+            vv = *(const f32x4*)(a.v + off);
+        }
+        *(f16x4*)&Ks[t * KLD + d] = f16x4{(_Float16)kv[0], (_Float16)kv[1], (_Float16)kv[2], (_Float16)kv[3]};
+#pragma unroll
+        for (int j = 0; j < 4; j++) Vt[(d + j) * VT + t] = (_Float16)vv[j];
+    }
+    __syncthreads();
+
+    const int nqt = (S + 15) / 16;
+    for (int qt = wave; qt < nqt; qt += nw) {
+        const int q0 = 16 * qt;
+        // Q as the B operand: lane = query q0 + l16, k = d = 16c + 4lg + j
+        f16x4 qf[DC];
+        {
+            const int qi = min(q0 + l16, S - 1);
+            const float* qrow = a.q + base + (int64_t)qi * a.st[1];
+#pragma unroll
+            for (int c = 0; c < DC; c++) {
+                const f32x4 v = *(const f32x4*)(qrow + 16 * c + 4 * lg);
+                qf[c] = f16x4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+            }
+        }
+        // scores: register r of key tile t holds key 16t + 4lg + r of query q0 + l16
+        f32x4 sc[KT];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < KT; t++) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < DC; c++) {
+                const f16x4 kf = *(const f16x4*)&Ks[(16 * t + l16) * KLD + 16 * c + 4 * lg];
+                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kf, qf[c], acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                sc[t][r] = 16 * t + 4 * lg + r < S ? acc[r] * a.scale : -INFINITY;
+                mx = fmaxf(mx, sc[t][r]);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep the K fragment loads per key tile
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        float ps = 0.f;
+#pragma unroll
+        for (int t = 0; t < KT; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float p = sc[t][r] == -INFINITY ? 0.f : expf(sc[t][r] - mx);
+                sc[t][r] = p;
+                ps += p;
+            }
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        // O += P . V, P = hi + lo in fp16 (A operand: query l16, keys 16t + 4lg + j)
+        f32x4 O[DC];
+#pragma unroll
+        for (int c = 0; c < DC; c++) O[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < KT; t++) {
+            f16x4 ph, pl;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                ph[j] = (_Float16)sc[t][j];
+                pl[j] = (_Float16)(sc[t][j] - (float)ph[j]);
+            }
+#pragma unroll
+            for (int c = 0; c < DC; c++) {
+                const f16x4 vf = *(const f16x4*)&Vt[(16 * c + l16) * VT + 16 * t + 4 * lg];
+                O[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vf, O[c], 0, 0, 0);
+                O[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vf, O[c], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep the V fragment loads per key tile (registers)
+        }
+        // O register r: query q0 + 4lg + r, d = 16c + l16; its row sum sits in lane 4lg + r
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float inv = 1.f / __shfl(ps, 4 * lg + r);
+            const int qi = q0 + 4 * lg + r;
+            if (qi >= S) continue;
+            float* orow = a.o + (int64_t)b * a.os[3] + (int64_t)h * a.os[2] + (int64_t)qi * a.os[1];
+#pragma unroll
+            for (int c = 0; c < DC; c++) orow[(int64_t)(16 * c + l16) * a.os[0]] = O[c][r] * inv;
+        }
+    }
+}
+
+template <int DC, int KT>
+void launch_head_t(const FaArgs& a, hipStream_t s) {
+    const int nqt = (a.S + 15) / 16;
+    const int nw = std::min(kHeadWaves<KT>, std::max(1, (nqt + 1) / 2));  // ~2 query tiles per wave
+    hipLaunchKernelGGL((k_attn_head<DC, KT>), dim3((unsigned)a.H, (unsigned)a.B), dim3((unsigned)(64 * nw)),
+                       0, s, a);
+}
+
+template <int DC>
+hipError_t launch_head(const FaArgs& a, hipStream_t s) {
+    const int kt = (a.S + 15) / 16;
+    if (kt <= 4) launch_head_t<DC, 4>(a, s);
+    else if (kt <= 8) launch_head_t<DC, 8>(a, s);
+    else if (kt <= 17) launch_head_t<DC, 17>(a, s);
+    else if (kt <= 24) launch_head_t<DC, 24>(a, s);
+    else launch_head_t<DC, 32>(a, s);
+    return hipGetLastError();
+}
+
+bool head_ok(const FaArgs& a, int D) {
+    auto al = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+    return a.S <= 512 && a.st[0] == 1 && a.st[1] % 4 == 0 && a.st[2] % 4 == 0 && a.st[3] % 4 == 0 &&
+           D % 16 == 0 && al(a.q) && al(a.k) && al(a.v) && a.H <= 65535 && a.B <= 65535;
+}
+
 }  // namespace
 
 hipError_t launch_flash_attn_f16kv(const FaArgs& a, int D, hipStream_t s) {
     if (a.S <= 0 || a.H <= 0 || a.B <= 0) return hipSuccess;
+    if (head_ok(a, D)) {
+        switch (D) {
+            case 16: return launch_head<1>(a, s);
+            case 32: return launch_head<2>(a, s);
+            case 48: return launch_head<3>(a, s);
+            case 64: return launch_head<4>(a, s);
+            default: break;
+        }
+    }
     const dim3 grid((unsigned)((a.S + 63) / 64), (unsigned)a.H, (unsigned)a.B), block(256);
     switch (D) {
         case 16: hipLaunchKernelGGL(k_flash_attn_f16kv<1>, grid, block, 0, s, a); break;

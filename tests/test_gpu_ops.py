@@ -107,8 +107,11 @@ def _qkv(rng, D, S, H, B):
     return [rng.standard_normal(shape).astype(np.float32) for _ in range(3)]
 
 
+# S <= 512 runs the whole-head kernel (K/V of a head resident in LDS), longer sequences the
+# chunked online-softmax kernel
 @pytest.mark.parametrize("D,S,H,B", [(48, 1, 2, 1), (48, 17, 2, 1), (48, 64, 3, 2), (48, 65, 2, 1),
-                                     (48, 257, 16, 2), (64, 130, 4, 1), (16, 40, 1, 1)])
+                                     (48, 257, 16, 2), (64, 130, 4, 1), (16, 40, 1, 1), (32, 300, 2, 1),
+                                     (48, 512, 2, 1), (64, 512, 1, 1), (48, 513, 2, 1), (48, 1025, 1, 1)])
 def test_flash_attn_vs_oracle(ctx, D, S, H, B):
     print(f"flash_attn D={D} S={S} H={H} B={B}", flush=True)
     rng = np.random.default_rng(D * S + H + B)
