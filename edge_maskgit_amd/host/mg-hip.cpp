@@ -67,8 +67,13 @@ struct HipRuntime::Impl {
     // final result of the last compute_device, returned to the pool by the next compute
     void* held = nullptr;
 
+    // row-concatenated weights / biases of fused FC groups, keyed by the members' host data
+    std::map<std::vector<const void*>, void*> fused_w, fused_b;
+
     // per-compute state
     std::unordered_map<const Tensor*, void*> addr;            // device address of a tensor
+    std::unordered_map<const Tensor*, int64_t> pitch;         // row pitch of a fused FC output
+    std::unordered_map<const Tensor*, const Tensor*> owner;   // fused FC output -> group leader
     struct Codes { void* q = nullptr; void* dx = nullptr; void* sx = nullptr; size_t bytes = 0; };
     std::unordered_map<const Tensor*, Codes> codes;           // fused FC operand of a Norm node
 
@@ -122,6 +127,64 @@ struct HipRuntime::Impl {
         return t;
     }
 
+    // fp16 weights of a fused FC group, rows concatenated in member order (cached)
+    void* fused_weight(const std::vector<Tensor*>& grp, int K, int64_t Nt) {
+        std::vector<const void*> key;
+        for (const Tensor* m : grp) key.push_back(m->src[0]->data);
+        const auto it = fused_w.find(key);
+        if (it != fused_w.end()) return it->second;
+        void* d = nullptr;
+        check(mgh_alloc(ctx, mgh_packed_weight_bytes_f16((int)Nt, K), &d));
+        int64_t off = 0;
+        for (const Tensor* m : grp) {
+            const Tensor* w = m->src[0];
+            if (!w->data) throw std::runtime_error("HipRuntime: leaf '" + w->name + "' has no host data");
+            const int N = (int)w->ne[1];
+            void* raw = nullptr;
+            check(mgh_alloc(ctx, w->nbytes(), &raw));
+            check(mgh_h2d(ctx, raw, w->data, w->nbytes()));
+            check(mgh_pack_weights_f16(ctx, w->type == Type::Q8_0 ? MGH_WTYPE_Q8_0 : MGH_WTYPE_Q4_K, raw, N, K,
+                                       (char*)d + (size_t)off * K * 2));
+            check(mgh_sync(ctx));
+            check(mgh_free(ctx, raw));
+            off += N;
+        }
+        return fused_w[key] = d;
+    }
+
+    // biases of a fused FC group, concatenated (zeros for members without one)
+    void* fused_bias(const std::vector<Tensor*>& grp, int64_t Nt) {
+        std::vector<const void*> key;
+        for (const Tensor* m : grp) key.push_back(m->src[2] ? m->src[2]->data : nullptr);
+        const auto it = fused_b.find(key);
+        if (it != fused_b.end()) return it->second;
+        std::vector<float> h((size_t)Nt, 0.0f);
+        int64_t off = 0;
+        for (const Tensor* m : grp) {
+            const Tensor* b = m->src[2];
+            const int64_t N = m->src[0]->ne[1];
+            if (b) {
+                if (b->type != Type::F32 || b->nelements() != N || !b->data)
+                    throw std::runtime_error("HipRuntime: fused FC bias must be F32 [N] with host data");
+                std::memcpy(h.data() + off, b->data, (size_t)N * 4);
+            }
+            off += N;
+        }
+        void* d = nullptr;
+        check(mgh_alloc(ctx, (size_t)Nt * 4, &d));
+        check(mgh_h2d(ctx, d, h.data(), (size_t)Nt * 4));
+        return fused_b[key] = d;
+    }
+
+    // element strides of a view of a fused FC output: whole-row strides scale to the wide pitch
+    void widen(const Tensor* v, int64_t st[4]) const {
+        const auto p = pitch.find(root(v));
+        if (p == pitch.end()) return;
+        const int64_t rowlen = root(v)->ne[0];
+        for (int i = 0; i < 4; i++)
+            if (st[i] >= rowlen && st[i] % rowlen == 0) st[i] = st[i] / rowlen * p->second;
+    }
+
     void* dev(const Tensor* t) {
         if (!t) return nullptr;
         const Tensor* r = root(t);
@@ -168,6 +231,8 @@ HipRuntime::~HipRuntime() {
     if (!p_ || !p_->ctx) return;
     mgh_sync(p_->ctx);
     for (auto& kv : p_->leaves) mgh_free(p_->ctx, kv.second);
+    for (auto& kv : p_->fused_w) mgh_free(p_->ctx, kv.second);
+    for (auto& kv : p_->fused_b) mgh_free(p_->ctx, kv.second);
     for (auto& kv : p_->pool) mgh_free(p_->ctx, kv.second);
     if (p_->held) mgh_free(p_->ctx, p_->held);
     for (auto& kv : p_->unit_affine) {
@@ -189,6 +254,15 @@ void HipRuntime::invalidate(Tensor* t) {
             ++it;
         }
     }
+    for (auto* m : {&p_->fused_w, &p_->fused_b})
+        for (auto it = m->begin(); it != m->end();) {
+            if (std::find(it->first.begin(), it->first.end(), (const void*)t->data) != it->first.end()) {
+                mgh_free(p_->ctx, it->second);
+                it = m->erase(it);
+            } else {
+                ++it;
+            }
+        }
 }
 
 bool HipRuntime::import_host_region(void*, size_t) { return false; }
@@ -267,16 +341,107 @@ const void* HipRuntime::run(Graph& g, bool readback) {
     std::unordered_map<const Tensor*, const Tensor*> fa_target;  // FA -> cont it writes
     for (auto& kv : fa_into) fa_target[kv.second] = kv.first;
 
+    // dequantize-fused path: quantized FCs that read the same activations and feed only the
+    // attention (q, k, v: mg-transformer.cpp:59-70) run as one GEMM on row-concatenated
+    // weights; each output is a column range of the wide result, which the attention reads
+    // through its strides
+    std::vector<std::vector<Tensor*>> groups;
+    std::unordered_map<const Tensor*, int> grp_of;
+    I.pitch.clear();
+    I.owner.clear();
+    if (I.algo == MGH_ALGO_DEQ_F16) {
+        std::unordered_map<const Tensor*, std::vector<const Tensor*>> cons;   // root -> consumer nodes
+        for (const Tensor* t : g.nodes) {
+            if (is_view_op(t->op)) continue;
+            for (const Tensor* s : t->src)
+                if (s) cons[I.root(s)].push_back(t);
+        }
+        std::map<std::tuple<const Tensor*, int, int64_t, int>, int> key_grp;
+        for (Tensor* t : g.nodes) {
+            if (t->op != Op::MulMat || !quant(t->src[0]) || t->src[3] || t != I.root(t)) continue;
+            bool fa_only = !cons[t].empty();
+            for (const Tensor* c : cons[t]) fa_only = fa_only && c->op == Op::FlashAttention;
+            if (!fa_only || t == g.nodes.back()) continue;
+            const Tensor* w = t->src[0];
+            const auto key = std::make_tuple(I.root(t->src[1]), (int)w->type, w->ne[0], t->iparam[0]);
+            auto it = key_grp.find(key);
+            if (it == key_grp.end()) {
+                key_grp[key] = (int)groups.size();
+                groups.push_back({t});
+            } else {
+                groups[it->second].push_back(t);
+            }
+        }
+        for (size_t gi = 0; gi < groups.size(); gi++) {
+            if (groups[gi].size() < 2) continue;
+            const Tensor* lead = groups[gi][0];
+            for (Tensor* m : groups[gi]) {
+                grp_of[m] = (int)gi;
+                last[lead] = std::max(last[lead], last.count(m) ? last[m] : 0);
+            }
+        }
+    }
+
+    // release roots whose last consumer was node i (never the final output)
+    auto release_after = [&](int i, const Tensor* t) {
+        for (const Tensor* s : t->src) {
+            if (!s) continue;
+            const Tensor* r = I.root(s);
+            if (r->op == Op::None || r == g.nodes.back() || last.at(r) != i) continue;
+            const auto a = I.addr.find(r);
+            if (a == I.addr.end() || !a->second) continue;
+            if (fa_target.count(r)) continue;                      // shares the cont's buffer
+            const auto ow = I.owner.find(r);
+            if (ow != I.owner.end() && ow->second != r) continue;   // column range of a fused output
+            I.give(a->second);
+            a->second = nullptr;
+            const auto c = I.codes.find(r);
+            if (c != I.codes.end()) {
+                I.give(c->second.q);
+                I.give(c->second.dx);
+                I.give(c->second.sx);
+                I.codes.erase(c);
+            }
+        }
+    };
+
     // ---- run ----
     for (int i = 0; i < n; i++) {
         Tensor* t = g.nodes[i];
         if (is_view_op(t->op)) continue;
         if (t->type != Type::F32 && t->op != Op::GetRows)
             throw std::runtime_error("HipRuntime: only F32 results are supported");
+        if (grp_of.count(t) && I.addr.count(t)) {                 // computed with its group
+            release_after(i, t);
+            continue;
+        }
         if (I.profiling) I.check(mgh_timer_start(I.ctx));
 
         void* out = nullptr;
-        if (t->op == Op::Cont && fa_into.count(t)) {
+        if (grp_of.count(t)) {
+            const std::vector<Tensor*>& grp = groups[grp_of.at(t)];
+            const Tensor* x = t->src[1];
+            const int K = (int)t->src[0]->ne[0];
+            const int M = (int)(x->nelements() / K);
+            int64_t Nt = 0;
+            for (const Tensor* m : grp) Nt += m->src[0]->ne[1];
+            out = I.take((size_t)M * Nt * 4);
+            void* wp = I.fused_weight(grp, K, Nt);
+            const float* bias = (const float*)I.fused_bias(grp, Nt);
+            const auto c = I.codes.find(I.root(x));
+            if (c != I.codes.end())
+                I.check(mgh_gemm_h16(I.ctx, wp, (int)Nt, K, c->second.q, M, bias, t->iparam[0], nullptr, (float*)out));
+            else
+                I.check(mgh_gemm_h16_f32in(I.ctx, wp, (int)Nt, K, (const float*)I.dev(x), M, bias, t->iparam[0],
+                                           nullptr, (float*)out));
+            int64_t off = 0;
+            for (const Tensor* m : grp) {
+                I.addr[m] = (float*)out + off;
+                I.pitch[m] = Nt;
+                I.owner[m] = grp[0];
+                off += m->src[0]->ne[1];
+            }
+        } else if (t->op == Op::Cont && fa_into.count(t)) {
             out = I.dev(fa_into.at(t));                         // written by the attention
             I.addr[t] = out;
         } else if (t->op == Op::FlashAttention && fa_target.count(t)) {
@@ -288,7 +453,9 @@ const void* HipRuntime::run(Graph& g, bool readback) {
             I.addr[t] = out;
         }
 
-        switch (t->op) {
+        switch (grp_of.count(t) ? Op::None : t->op) {
+            case Op::None:
+                break;
             case Op::MulMat: {
                 const Tensor* w = t->src[0];
                 const Tensor* x = t->src[1];
@@ -361,6 +528,9 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                 Impl::elem_strides(q, st);
                 Impl::elem_strides(t->src[1], sk);
                 Impl::elem_strides(t->src[2], sv);
+                I.widen(q, st);
+                I.widen(t->src[1], sk);
+                I.widen(t->src[2], sv);
                 if (!std::equal(st, st + 4, sk) || !std::equal(st, st + 4, sv))
                     throw std::runtime_error("HipRuntime: FlashAttention needs q, k, v with equal strides");
                 const int D = (int)q->ne[0], S = (int)q->ne[1], H = (int)q->ne[2], B = (int)q->ne[3];
@@ -414,24 +584,7 @@ const void* HipRuntime::run(Graph& g, bool readback) {
             e.first++;
             e.second += ms;
         }
-        // release roots whose last consumer was this node (never the final output)
-        for (const Tensor* s : t->src) {
-            if (!s) continue;
-            const Tensor* r = I.root(s);
-            if (r->op == Op::None || r == g.nodes.back() || last.at(r) != i) continue;
-            const auto a = I.addr.find(r);
-            if (a == I.addr.end() || !a->second) continue;
-            if (fa_target.count(r)) continue;                      // shares the cont's buffer
-            I.give(a->second);
-            a->second = nullptr;
-            const auto c = I.codes.find(r);
-            if (c != I.codes.end()) {
-                I.give(c->second.q);
-                I.give(c->second.dx);
-                I.give(c->second.sx);
-                I.codes.erase(c);
-            }
-        }
+        release_after(i, t);
     }
 
     Tensor* outp = g.nodes.back();
@@ -445,7 +598,8 @@ const void* HipRuntime::run(Graph& g, bool readback) {
     }
     I.bound.clear();
     for (auto& kv : I.addr)                                        // computed buffers back to the pool
-        if (kv.first->op != Op::None && kv.second && kv.second != I.held && !fa_target.count(kv.first)) {
+        if (kv.first->op != Op::None && kv.second && kv.second != I.held && !fa_target.count(kv.first) &&
+            !(I.owner.count(kv.first) && I.owner.at(kv.first) != kv.first)) {
             I.give(kv.second);
             kv.second = nullptr;
         }

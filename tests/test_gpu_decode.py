@@ -145,10 +145,11 @@ def q4_model(tmp_path_factory):
     return p
 
 
-def test_generate_matches_host_loop(q4_model):
+@pytest.mark.parametrize("algo", [1, 2])
+def test_generate_matches_host_loop(q4_model, algo):
     classes, seeds, steps = [207, 3], [42, 2**40 + 1], 8
-    print("generate B=2 (q4_k, 2 layers) vs host loop", flush=True)
-    with rt.TransformerRuntime(q4_model, algo=1) as m:
+    print(f"generate B=2 (q4_k, 2 layers, algo {algo}) vs host loop", flush=True)
+    with rt.TransformerRuntime(q4_model, algo=algo) as m:
         got = m.generate(classes, seeds, steps)
         again = m.generate(classes, seeds, steps)
         other = m.generate(classes, [7, 8], steps)
