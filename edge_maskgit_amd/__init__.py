@@ -37,7 +37,7 @@ MGH_SYMBOLS = [
     "mgh_layernorm_affine", "mgh_flash_attn_f16kv", "mgh_gemm_f32", "mgh_get_rows", "mgh_add",
     "mgh_copy_strided", "mgh_decode_state_bytes", "mgh_decode_work_bytes", "mgh_decode_init",
     "mgh_decode_step", "mgh_packed_weight_bytes_f16", "mgh_pack_weights_f16", "mgh_f32_to_f16",
-    "mgh_gemm_h16", "mgh_gemm_h16_f32in",
+    "mgh_gemm_h16", "mgh_gemm_h16_f32in", "mgh_gemm_h16_y16", "mgh_flash_attn_f16kv_o16",
 ]
 
 _lib = None
@@ -101,6 +101,8 @@ def lib():
         L.mgh_f32_to_f16.argtypes = [P, P, I64, P]
         L.mgh_gemm_h16.argtypes = [P, P, I, I, P, I, P, I, P, P]
         L.mgh_gemm_h16_f32in.argtypes = [P, P, I, I, P, I, P, I, P, P]
+        L.mgh_gemm_h16_y16.argtypes = [P, P, I, I, P, I, P, I, P, P]
+        L.mgh_flash_attn_f16kv_o16.argtypes = [P, P, P, P, P, I, I, I, I, ctypes.c_float, P, P]
         L.mgh_decode_state_bytes.argtypes = [I]
         L.mgh_decode_state_bytes.restype = SZ
         L.mgh_decode_work_bytes.argtypes = [I, I]
@@ -301,6 +303,16 @@ class Context:
     def gemm_h16(self, wp16, N, K, x16, M, bias, act, resid, y):
         P = self._ptr
         self._check(lib().mgh_gemm_h16(self.h, P(wp16), N, K, P(x16), M, P(bias), act, P(resid), P(y)))
+
+    def gemm_h16_y16(self, wp16, N, K, x16, M, bias, act, resid, y16):
+        P = self._ptr
+        self._check(lib().mgh_gemm_h16_y16(self.h, P(wp16), N, K, P(x16), M, P(bias), act, P(resid), P(y16)))
+
+    def flash_attn_f16kv_o16(self, q, k, v, strides, D, S, H, B, scale, o16, o_strides=None):
+        P = self._ptr
+        st = (ctypes.c_int64 * 4)(*strides)
+        ost = None if o_strides is None else (ctypes.c_int64 * 4)(*o_strides)
+        self._check(lib().mgh_flash_attn_f16kv_o16(self.h, P(q), P(k), P(v), st, D, S, H, B, scale, P(o16), ost))
 
     def gemm_h16_f32in(self, wp16, N, K, x, M, bias, act, resid, y):
         P = self._ptr

@@ -151,9 +151,13 @@ __global__ __launch_bounds__(256) void k_flash_attn_f16kv(FaArgs a) {
         const float inv = 1.f / __shfl(l, 4 * lg + r);
         const int qi = q0w + 4 * lg + r;
         if (qi >= S) continue;
-        float* orow = a.o + (int64_t)b * a.os[3] + (int64_t)h * a.os[2] + (int64_t)qi * a.os[1];
+        const int64_t ro = (int64_t)b * a.os[3] + (int64_t)h * a.os[2] + (int64_t)qi * a.os[1];
 #pragma unroll
-        for (int c = 0; c < DC; c++) orow[(int64_t)(16 * c + l16) * a.os[0]] = O[c][r] * inv;
+        for (int c = 0; c < DC; c++) {
+            const int64_t e = ro + (int64_t)(16 * c + l16) * a.os[0];
+            if (a.o16) a.o16[e] = (_Float16)(O[c][r] * inv);
+            else a.o[e] = O[c][r] * inv;
+        }
     }
 }
 
@@ -282,9 +286,13 @@ __global__ __launch_bounds__(64 * kHeadWaves<KT>) void k_attn_head(FaArgs a) {
             const float inv = 1.f / __shfl(ps, 4 * lg + r);
             const int qi = q0 + 4 * lg + r;
             if (qi >= S) continue;
-            float* orow = a.o + (int64_t)b * a.os[3] + (int64_t)h * a.os[2] + (int64_t)qi * a.os[1];
+            const int64_t ro = (int64_t)b * a.os[3] + (int64_t)h * a.os[2] + (int64_t)qi * a.os[1];
 #pragma unroll
-            for (int c = 0; c < DC; c++) orow[(int64_t)(16 * c + l16) * a.os[0]] = O[c][r] * inv;
+            for (int c = 0; c < DC; c++) {
+                const int64_t e = ro + (int64_t)(16 * c + l16) * a.os[0];
+                if (a.o16) a.o16[e] = (_Float16)(O[c][r] * inv);
+                else a.o[e] = O[c][r] * inv;
+            }
         }
     }
 }

@@ -24,7 +24,8 @@
 //    being paid by every tile in the same step.
 //  * Epilogue through LDS: the accumulator tile is transposed in two halves and leaves as whole
 //    rows (512 bytes per 32 lanes) with streaming (non-temporal) stores; bias, activation and
-//    residual are applied on the way out.
+//    residual are applied on the way out. With y16 the result is stored rounded to fp16 (the
+//    operand form of a following dequantize-fused FC, which would round it to fp16 anyway).
 //  * Split-K for shapes with too few tiles: each split writes its partial tile row-major into a
 //    workspace (same transposed path) and k_gemm_h16_reduce sums the splits in split order
 //    (deterministic) and applies the epilogue.
@@ -38,6 +39,7 @@ namespace mgh {
 namespace {
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int NT = 256;
 constexpr int BN = 128;
@@ -300,7 +302,11 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
             for (int e = 0; e < 4; e++) o[e] = act_h<ACT>(o[e]);
             const size_t idx = (size_t)m * N + n;
             if (g.resid) o += *(const f32x4*)(g.resid + idx);
-            __builtin_nontemporal_store(o, (f32x4*)(g.y + idx));
+            if (g.y16)
+                __builtin_nontemporal_store(f16x4{(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]},
+                                            (f16x4*)(g.y16 + idx));
+            else
+                __builtin_nontemporal_store(o, (f32x4*)(g.y + idx));
         }
     }
 }
@@ -329,7 +335,11 @@ __global__ __launch_bounds__(256) void k_gemm_h16_reduce(GemmH16Args g) {
     for (int e = 0; e < 4; e++) v[e] = act_h<ACT>(v[e]);
     const size_t o = (size_t)m * N + n;
     if (g.resid) v += *(const f32x4*)(g.resid + o);
-    __builtin_nontemporal_store(v, (f32x4*)(g.y + o));
+    if (g.y16)
+        __builtin_nontemporal_store(f16x4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]},
+                                    (f16x4*)(g.y16 + o));
+    else
+        __builtin_nontemporal_store(v, (f32x4*)(g.y + o));
 }
 
 H16Plan gemm_h16_plan(int M, int N, int K) {

@@ -559,19 +559,22 @@ int mgh_layernorm_affine(mgh_ctx* c, const float* x, const float* g, const float
     return MGH_OK;
 }
 
-int mgh_flash_attn_f16kv(mgh_ctx* c, const float* q, const float* k, const float* v,
-                         const int64_t st[4], int D, int S, int H, int B, float scale, float* o,
-                         const int64_t ost[4]) {
+}  // extern "C"
+
+namespace {
+
+int flash_attn(mgh_ctx* c, const float* q, const float* k, const float* v, const int64_t st[4], int D, int S,
+               int H, int B, float scale, float* o, _Float16* o16, const int64_t ost[4]) {
     if (!c) return MGH_ERR_ARG;
     if (S < 0 || H < 0 || B < 0) return fail(c, MGH_ERR_ARG, "flash_attn: negative shape");
     if (D != 16 && D != 32 && D != 48 && D != 64)
         return fail(c, MGH_ERR_UNSUPPORTED, "flash_attn: D must be 16, 32, 48 or 64");
     if (S == 0 || H == 0 || B == 0) return MGH_OK;
-    if (!q || !k || !v || !o || !st) return fail(c, MGH_ERR_ARG, "flash_attn: null pointer");
+    if (!q || !k || !v || (!o && !o16) || !st) return fail(c, MGH_ERR_ARG, "flash_attn: null pointer");
     if (H > 65535 || B > 65535) return fail(c, MGH_ERR_UNSUPPORTED, "flash_attn: H and B must be <= 65535");
     if (int r = set_dev(c)) return r;
     mgh::FaArgs a{};
-    a.q = q; a.k = k; a.v = v; a.o = o;
+    a.q = q; a.k = k; a.v = v; a.o = o; a.o16 = o16;
     for (int i = 0; i < 4; i++) a.st[i] = st[i];
     if (ost) {
         for (int i = 0; i < 4; i++) a.os[i] = ost[i];
@@ -581,6 +584,22 @@ int mgh_flash_attn_f16kv(mgh_ctx* c, const float* q, const float* k, const float
     a.S = S; a.H = H; a.B = B; a.scale = scale;
     MGH_HIP(c, mgh::launch_flash_attn_f16kv(a, D, c->stream), "k_flash_attn_f16kv");
     return MGH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mgh_flash_attn_f16kv(mgh_ctx* c, const float* q, const float* k, const float* v,
+                         const int64_t st[4], int D, int S, int H, int B, float scale, float* o,
+                         const int64_t ost[4]) {
+    return flash_attn(c, q, k, v, st, D, S, H, B, scale, o, nullptr, ost);
+}
+
+int mgh_flash_attn_f16kv_o16(mgh_ctx* c, const float* q, const float* k, const float* v,
+                             const int64_t st[4], int D, int S, int H, int B, float scale, void* o16,
+                             const int64_t ost[4]) {
+    return flash_attn(c, q, k, v, st, D, S, H, B, scale, nullptr, (_Float16*)o16, ost);
 }
 
 int mgh_gemm_f32(mgh_ctx* c, const float* w, int N, int K, const float* x, int M, const float* bias,
@@ -711,6 +730,19 @@ int mgh_gemm_h16(mgh_ctx* c, const void* wp16, int N, int K, const void* x16, in
     mgh::GemmH16Args a{};
     a.x = (const _Float16*)x16; a.w = (const _Float16*)wp16;
     a.bias = bias; a.resid = resid; a.y = y;
+    a.M = M; a.N = N; a.K = K; a.act = act;
+    return run_gemm_h16(c, a);
+}
+
+int mgh_gemm_h16_y16(mgh_ctx* c, const void* wp16, int N, int K, const void* x16, int M,
+                     const float* bias, int act, const float* resid, void* y16) {
+    if (!c) return MGH_ERR_ARG;
+    if (int r = check_h16(c, "gemm_h16_y16", wp16, N, K, x16, M, bias, act, resid, (const float*)y16)) return r;
+    if (M == 0) return MGH_OK;
+    if (int r = set_dev(c)) return r;
+    mgh::GemmH16Args a{};
+    a.x = (const _Float16*)x16; a.w = (const _Float16*)wp16;
+    a.bias = bias; a.resid = resid; a.y16 = (_Float16*)y16;
     a.M = M; a.N = N; a.K = K; a.act = act;
     return run_gemm_h16(c, a);
 }

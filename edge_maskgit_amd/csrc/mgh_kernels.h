@@ -63,6 +63,7 @@ struct FaArgs {
     const float* k;
     const float* v;
     float* o;
+    _Float16* o16;         // fp16 output instead of o when set
     int64_t st[4];         // q/k/v element strides for d, s, h, b
     int64_t os[4];         // output element strides for d, s, h, b
     int S, H, B;
@@ -136,6 +137,7 @@ struct GemmH16Args {
     const float* bias;     // [N] or null
     const float* resid;    // [M][N] or null
     float* y;              // [M][N]
+    _Float16* y16;         // [M][N] fp16 output instead of y when set
     float* ws;             // split-K partial tiles (H16Plan::ws_bytes)
     int M, N, K, splits, act;
 };

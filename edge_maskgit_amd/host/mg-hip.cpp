@@ -5,7 +5,9 @@
 // Per compute():
 //  1. Plan: every node's storage root (views alias their source), each root's last consumer,
 //     the LayerNorm nodes whose output feeds quantized FC layers (fused operand: int8 codes for
-//     the int8-dot path, fp16 values for the dequantize-fused path), and the
+//     the int8-dot path, fp16 values for the dequantize-fused path), on the dequantize-fused
+//     path the FC groups that share their input (q/k/v: one GEMM) and the attention / FC
+//     outputs read only by FCs (stored as fp16), and the
 //     flash-attention -> permute -> cont chains (attention writes the merged layout).
 //  2. Run the nodes in order; device buffers of computed roots come from a size-bucketed
 //     pool and return to it after their last consumer.
@@ -24,6 +26,7 @@
 #include <stdexcept>
 #include <tuple>
 #include <unordered_map>
+#include <unordered_set>
 
 #include "mgh.h"
 
@@ -94,7 +97,9 @@ struct HipRuntime::Impl {
         alloc_size[p] = bytes;
         return p;
     }
-    void give(void* p) { pool.emplace(alloc_size.at(p), p); }
+    void give(void* p) {
+        if (p) pool.emplace(alloc_size.at(p), p);
+    }
     std::unordered_map<void*, size_t> alloc_size;
 
     // layout 0: the leaf's bytes as stored; 1: quantized weight in the int8-dot packed layout
@@ -405,6 +410,30 @@ const void* HipRuntime::run(Graph& g, bool readback) {
         }
     };
 
+    // dequantize-fused path: an attention output or an FC output whose only consumers are
+    // dequantize-fused FCs reading it as their activations is stored as fp16 directly (the
+    // consumers would round it to fp16 on their way in; the result is identical)
+    std::unordered_set<const Tensor*> emit16;
+    if (I.algo == MGH_ALGO_DEQ_F16) {
+        std::unordered_map<const Tensor*, std::vector<const Tensor*>> cons;
+        for (const Tensor* t : g.nodes) {
+            if (is_view_op(t->op)) continue;
+            for (const Tensor* s : t->src)
+                if (s) cons[I.root(s)].push_back(t);
+        }
+        for (const Tensor* t : g.nodes) {
+            if (t == g.nodes.back() || is_view_op(t->op) || grp_of.count(t)) continue;
+            const bool fa_out = t->op == Op::Cont && fa_into.count(t);
+            const bool fc_out = t->op == Op::MulMat && quant(t->src[0]);
+            if (!fa_out && !fc_out) continue;
+            bool ok = !cons[t].empty();
+            for (const Tensor* c : cons[t])
+                ok = ok && c->op == Op::MulMat && quant(c->src[0]) && I.root(c->src[1]) == t &&
+                     I.root(c->src[0]) != t;
+            if (ok) emit16.insert(t);
+        }
+    }
+
     // ---- run ----
     for (int i = 0; i < n; i++) {
         Tensor* t = g.nodes[i];
@@ -469,7 +498,12 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                 if (quant(w) && I.algo == MGH_ALGO_DEQ_F16) {
                     void* wp = I.upload_leaf(w, 2);
                     const auto c = I.codes.find(I.root(x));
-                    if (c != I.codes.end())
+                    if (c != I.codes.end() && emit16.count(t)) {
+                        Impl::Codes cd;
+                        cd.q = I.take((size_t)M * N * 2);
+                        I.check(mgh_gemm_h16_y16(I.ctx, wp, N, K, c->second.q, M, bias, act, resid, cd.q));
+                        I.codes[t] = cd;
+                    } else if (c != I.codes.end())
                         I.check(mgh_gemm_h16(I.ctx, wp, N, K, c->second.q, M, bias, act, resid, (float*)out));
                     else
                         I.check(mgh_gemm_h16_f32in(I.ctx, wp, N, K, (const float*)I.dev(x), M, bias, act, resid,
@@ -542,9 +576,18 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                     ost[0] = 1; ost[1] = (int64_t)D * H; ost[2] = D; ost[3] = (int64_t)D * H * S;
                     po = ost;
                 }
-                I.check(mgh_flash_attn_f16kv(I.ctx, (const float*)I.dev(q), (const float*)I.dev(t->src[1]),
-                                             (const float*)I.dev(t->src[2]), st, D, S, H, B, t->fparam[0],
-                                             (float*)out, po));
+                if (po && emit16.count(fa_target.at(t))) {
+                    Impl::Codes cd;
+                    cd.q = I.take((size_t)D * S * H * B * 2);
+                    I.check(mgh_flash_attn_f16kv_o16(I.ctx, (const float*)I.dev(q), (const float*)I.dev(t->src[1]),
+                                                     (const float*)I.dev(t->src[2]), st, D, S, H, B, t->fparam[0],
+                                                     cd.q, po));
+                    I.codes[fa_target.at(t)] = cd;
+                } else {
+                    I.check(mgh_flash_attn_f16kv(I.ctx, (const float*)I.dev(q), (const float*)I.dev(t->src[1]),
+                                                 (const float*)I.dev(t->src[2]), st, D, S, H, B, t->fparam[0],
+                                                 (float*)out, po));
+                }
                 break;
             }
             case Op::GetRows: {

@@ -168,6 +168,12 @@ int mgh_layernorm_affine(mgh_ctx* ctx, const float* d_x, const float* d_gamma, c
 int mgh_flash_attn_f16kv(mgh_ctx* ctx, const float* d_q, const float* d_k, const float* d_v,
                          const int64_t strides[4], int D, int S, int H, int B, float scale,
                          float* d_o, const int64_t o_strides[4]);
+/* the same attention with the output stored rounded to fp16 (the operand of the following
+ * dequantize-fused out-projection; no counterpart in the reference, whose FC rounds its fp32
+ * input to fp16 — the result is identical) */
+int mgh_flash_attn_f16kv_o16(mgh_ctx* ctx, const float* d_q, const float* d_k, const float* d_v,
+                             const int64_t strides[4], int D, int S, int H, int B, float scale,
+                             void* d_o16, const int64_t o_strides[4]);
 
 /* ---- fp32 GEMM with the fused epilogue (tied MLM head, F32 FC weights): replaces
  *      k_mul_mat_t and its dispatch (mg-opencl.cpp:60-94, 1429-1440).
@@ -203,6 +209,11 @@ int mgh_gemm_h16(mgh_ctx* ctx, const void* d_wp16, int N, int K, const void* d_x
                  const float* d_bias, int act, const float* d_resid, float* d_y);
 int mgh_gemm_h16_f32in(mgh_ctx* ctx, const void* d_wp16, int N, int K, const float* d_x, int M,
                        const float* d_bias, int act, const float* d_resid, float* d_y);
+/* the same product stored rounded to fp16 (d_y16 [M][N]): the operand of a following
+ * dequantize-fused FC (no counterpart in the reference, where the next FC rounds its fp32
+ * input; the result is identical) */
+int mgh_gemm_h16_y16(mgh_ctx* ctx, const void* d_wp16, int N, int K, const void* d_x16, int M,
+                     const float* d_bias, int act, const float* d_resid, void* d_y16);
 
 /* ---- iterative decoding on the device: one step of the reference's generate() loop,
  *      src/mg-generate.cpp:82-121, for B images whose logits [B][S][V] are already in HBM.

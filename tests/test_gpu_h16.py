@@ -158,6 +158,24 @@ def test_gemm_h16_f32in_equals_rounded_operand(ctx, M, N, K, act):
     assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
 
 
+@pytest.mark.parametrize("M,N,K,act", [(257, 3072, 768, 1), (1025, 768, 3072, 0)])
+def test_gemm_h16_y16_is_rounded_output(ctx, M, N, K, act):
+    """The fp16-output variant stores exactly the fp32 result rounded to nearest fp16."""
+    print(f"gemm_h16_y16 M={M} N={N} K={K} act={act}", flush=True)
+    rng = np.random.default_rng(M + N + 7 * K)
+    w16 = (rng.standard_normal((N, K)) * 0.02).astype(np.float16)
+    x16 = rng.standard_normal((M, K)).astype(np.float16)
+    bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+    dW, dX, dB = ctx.upload(w16), ctx.upload(x16), ctx.upload(bias)
+    dY, dH = ctx.alloc(M * N * 4), ctx.alloc(M * N * 2)
+    ctx.gemm_h16(dW, N, K, dX, M, dB, act, None, dY)
+    ctx.gemm_h16_y16(dW, N, K, dX, M, dB, act, None, dH)
+    y, h = ctx.download(dY, (M, N), np.float32), ctx.download(dH, (M, N), np.float16)
+    for t in (dW, dX, dB, dY, dH):
+        ctx.free(t)
+    assert np.array_equal(h.view(np.uint16), y.astype(np.float16).view(np.uint16))
+
+
 def test_gemm_h16_rejects_bad_args(ctx):
     buf = ctx.alloc(1 << 20)
     for (N, K) in [(6, 64), (8, 96), (0, 64)]:

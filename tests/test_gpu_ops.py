@@ -134,6 +134,25 @@ def test_flash_attn_vs_oracle(ctx, D, S, H, B):
     assert np.array_equal(om, oracle.merge_heads(o, D, S, H, B))
 
 
+@pytest.mark.parametrize("S", [257, 600])
+def test_flash_attn_o16_is_rounded_output(ctx, S):
+    """The fp16-output variant stores exactly the fp32 attention output rounded to fp16."""
+    D, H, B = 48, 4, 2
+    print(f"flash_attn_o16 S={S}", flush=True)
+    rng = np.random.default_rng(S)
+    q, k, v = _qkv(rng, D, S, H, B)
+    st, ost = (1, H * D, D, H * D * S), (1, H * D, D, H * D * S)
+    dq, dk, dv = ctx.upload(q), ctx.upload(k), ctx.upload(v)
+    do, dh = ctx.alloc(D * S * H * B * 4), ctx.alloc(D * S * H * B * 2)
+    ctx.flash_attn_f16kv(dq, dk, dv, st, D, S, H, B, 0.144, do, o_strides=ost)
+    ctx.flash_attn_f16kv_o16(dq, dk, dv, st, D, S, H, B, 0.144, dh, o_strides=ost)
+    o = ctx.download(do, (D * S * H * B,), np.float32)
+    h = ctx.download(dh, (D * S * H * B,), np.float16)
+    for t in (dq, dk, dv, do, dh):
+        ctx.free(t)
+    assert np.array_equal(h.view(np.uint16), o.astype(np.float16).view(np.uint16))
+
+
 def test_flash_attn_large_scores(ctx):
     """Peaked softmax (large logits): the running max rescaling must stay exact."""
     D, S, H, B = 48, 257, 2, 1
