@@ -44,11 +44,12 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 constexpr int NT = 256;
 constexpr int BN = 128;
 
-// XF32: the activation stage holds fp32 rows (16 chunks of 16 bytes) instead of fp16 ones
-template <int BM, bool XF32>
+// NS-deep ring of K stages. XF32: the activation stage holds fp32 rows (16 chunks of 16 bytes)
+// instead of fp16 ones
+template <int BM, bool XF32, int NS>
 struct HLds {
-    u32x4 w[2][BN * 8];                  // [stage][row][8 swizzled 16-byte chunks] fp16
-    u32x4 x[2][BM * (XF32 ? 16 : 8)];
+    u32x4 w[NS][BN * 8];                 // [stage][row][8 swizzled 16-byte chunks] fp16
+    u32x4 x[NS][BM * (XF32 ? 16 : 8)];
 };
 
 __device__ __forceinline__ void dma16(const void* g, void* lds) {
@@ -142,7 +143,7 @@ __global__ __launch_bounds__(256) void k_f32_to_f16(const f32x4* __restrict__ x,
 // split ks over its K range into ws. XF32: the activations arrive as fp32 (g.xf) and are
 // rounded to fp16 (nearest even, as k_f32_to_f16) when the MFMA fragments are read from LDS;
 // their stage rows are 256 bytes (16 chunks, swizzle chunk ^ (row & 15)).
-template <int ACT, int BM, bool PART, bool XF32>
+template <int ACT, int BM, bool PART, bool XF32, int NS>
 __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
     constexpr int J = BM / 32;                  // 16-row activation subtiles per wave
     constexpr int CW = BN / 32;                 // weight DMA instructions per wave and stage
@@ -150,7 +151,8 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
     constexpr int MID = 2 * J;                  // second-half MFMAs issued before the boundary
     constexpr int NR = 4 + (XF32 ? 2 : 1) * J;  // LDS reads per K half
     static_assert(NR <= 4 * J, "read/MFMA interleave");
-    __shared__ HLds<BM, XF32> L;
+    static_assert(NS >= 2 && (NS - 1) * (CW + CX) < 64, "ring depth");
+    __shared__ HLds<BM, XF32, NS> L;
 
     const int K = g.K, M = g.M, N = g.N;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
@@ -218,9 +220,14 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
         for (int j = 0; j < J; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     f16x8 a[2][4], b[2][J];
 
-    dma_stage(0, 0);
-    dma_stage(1, min(1, SL - 1));
-    wait_vm<CW + CX>();                         // stage 0 has landed (mine) ...
+    // Ring: stages 0..NS-1 requested up front; at the boundary of stage s, stage s+1 is
+    // awaited and stage s+NS goes into stage s's buffer (its fragments are in registers by
+    // then). Requests past the last stage re-load it into buffers that are never read, so
+    // every boundary issues the same DMA count and the vmcnt waits stay exact.
+    constexpr int NDMA = CW + CX;
+#pragma unroll
+    for (int k = 0; k < NS; k++) dma_stage(k, min(k, SL - 1));
+    wait_vm<(NS - 1) * NDMA>();                 // stage 0 has landed (mine) ...
     __syncthreads();                            // ... and everyone's
 #pragma unroll
     for (int i = 0; i < 4; i++) a[0][i] = frag(L.w[0], 64 * wn + 16 * i, 0);
@@ -229,7 +236,7 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
 
     int st = 0;
     for (int s = 0; s < SL; s++) {
-        const int stn = st ^ 1;
+        const int stn = st + 1 == NS ? 0 : st + 1;
         // K half 0: MFMAs on a/b[0] while the fragments of half 1 are read
 #pragma unroll
         for (int i = 0; i < 4; i++) a[1][i] = frag(L.w[st], 64 * wn + 16 * i, 1);
@@ -251,9 +258,10 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
         for (int q = 0; q < MID; q++)
             acc[q % 4][q / 4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1][q % 4], b[1][q / 4], acc[q % 4][q / 4], 0, 0, 0);
         if (s + 1 < SL) {
-            wait_vm0();                         // stage s+1 (requested one stage ago) landed
-            __syncthreads();                    // for every wave; stage s is no longer read
-            if (s + 2 < SL) dma_stage(st, s + 2);
+            wait_vm<(NS - 2) * NDMA>();         // stage s+1 has landed (mine) ...
+            __syncthreads();                    // ... and everyone's; stage s is no longer read
+            // (a 2-deep ring waits for everything, so it skips the re-loads past the end)
+            if (NS > 2 || s + NS < SL) dma_stage(st, min(s + NS, SL - 1));
 #pragma unroll
             for (int i = 0; i < 4; i++) a[0][i] = frag(L.w[stn], 64 * wn + 16 * i, 0);
 #pragma unroll
@@ -269,7 +277,7 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
     // epilogue: the tile leaves through LDS as whole rows, in two halves of BM/2 rows
     constexpr int P = BN + 4;                   // padded row pitch (floats)
     constexpr int HR = BM / 2;
-    static_assert(HR * P * 4 <= (int)sizeof(HLds<BM, XF32>), "transpose buffer fits the ring");
+    static_assert(HR * P * 4 <= (int)sizeof(HLds<BM, XF32, NS>), "transpose buffer fits the ring");
     float* T = (float*)&L;
     const int c = 4 * (tid & 31);               // this thread's 4 columns
     const int n = n0 + c;
@@ -342,13 +350,15 @@ __global__ __launch_bounds__(256) void k_gemm_h16_reduce(GemmH16Args g) {
         __builtin_nontemporal_store(v, (f32x4*)(g.y + o));
 }
 
-H16Plan gemm_h16_plan(int M, int N, int K) {
+H16Plan gemm_h16_plan(int M, int N, int K, bool xf32) {
     H16Plan p{};
+    p.ns = 2;
     const int tn = (N + BN - 1) / BN;
     const int t128 = ((M + 127) / 128) * tn;
     // 128-row activation tiles once there are about two per CU; below that the 64-row tile
     // (1.5x the operand traffic per flop, but twice the workgroups) measured faster
-    p.bm = t128 >= 512 ? 128 : 64;
+    // (with fp32 activations, 64-row tiles: their stage is as large as a 128-row fp16 stage)
+    p.bm = t128 >= 512 && !xf32 ? 128 : 64;
     const int tiles = ((M + p.bm - 1) / p.bm) * tn;
     const int S = K / 64;
     p.splits = 1;
@@ -382,30 +392,38 @@ hipError_t launch_f32_to_f16(const float* x, _Float16* h, int64_t n, hipStream_t
     return hipGetLastError();
 }
 
-template <int BMV, bool XF32>
+template <int BMV, bool XF32, int NSV>
 static hipError_t launch_h16_t(const GemmH16Args& a, hipStream_t s) {
     const int tiles = ((a.M + BMV - 1) / BMV) * ((a.N + BN - 1) / BN);
     const int splits = std::max(a.splits, 1);
     const dim3 block(NT);
     if (splits > 1) {
-        hipLaunchKernelGGL((k_gemm_h16<0, BMV, true, XF32>), dim3(tiles * splits), block, 0, s, a);
+        hipLaunchKernelGGL((k_gemm_h16<0, BMV, true, XF32, NSV>), dim3(tiles * splits), block, 0, s, a);
         const size_t n4 = (size_t)tiles * BMV * BN / 4;
         const dim3 rg((unsigned)((n4 + 255) / 256));
         if (a.act == 1) hipLaunchKernelGGL((k_gemm_h16_reduce<1, BMV>), rg, block, 0, s, a);
         else if (a.act == 2) hipLaunchKernelGGL((k_gemm_h16_reduce<2, BMV>), rg, block, 0, s, a);
         else hipLaunchKernelGGL((k_gemm_h16_reduce<0, BMV>), rg, block, 0, s, a);
     } else {
-        if (a.act == 1) hipLaunchKernelGGL((k_gemm_h16<1, BMV, false, XF32>), dim3(tiles), block, 0, s, a);
-        else if (a.act == 2) hipLaunchKernelGGL((k_gemm_h16<2, BMV, false, XF32>), dim3(tiles), block, 0, s, a);
-        else hipLaunchKernelGGL((k_gemm_h16<0, BMV, false, XF32>), dim3(tiles), block, 0, s, a);
+        if (a.act == 1) hipLaunchKernelGGL((k_gemm_h16<1, BMV, false, XF32, NSV>), dim3(tiles), block, 0, s, a);
+        else if (a.act == 2) hipLaunchKernelGGL((k_gemm_h16<2, BMV, false, XF32, NSV>), dim3(tiles), block, 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_h16<0, BMV, false, XF32, NSV>), dim3(tiles), block, 0, s, a);
     }
     return hipGetLastError();
 }
 
-hipError_t launch_gemm_h16(int bm, const GemmH16Args& a, hipStream_t s) {
+template <int BMV, bool XF32>
+static hipError_t launch_h16_ns(int ns, const GemmH16Args& a, hipStream_t s) {
+    if (ns == 2) return launch_h16_t<BMV, XF32, 2>(a, s);
+    if (ns == 3) return launch_h16_t<BMV, XF32, 3>(a, s);
+    if (ns == 4 && !(BMV == 128 && XF32)) return launch_h16_t<BMV, XF32, (BMV == 128 && XF32) ? 3 : 4>(a, s);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a, hipStream_t s) {
     const bool xf = a.xf != nullptr;
-    if (bm == 128) return xf ? launch_h16_t<128, true>(a, s) : launch_h16_t<128, false>(a, s);
-    if (bm == 64) return xf ? launch_h16_t<64, true>(a, s) : launch_h16_t<64, false>(a, s);
+    if (p.bm == 128) return xf ? launch_h16_ns<128, true>(p.ns, a, s) : launch_h16_ns<128, false>(p.ns, a, s);
+    if (p.bm == 64) return xf ? launch_h16_ns<64, true>(p.ns, a, s) : launch_h16_ns<64, false>(p.ns, a, s);
     return hipErrorInvalidValue;
 }
 

@@ -137,13 +137,13 @@ int run_gemm_qp(mgh_ctx* c, int wtype, mgh::GemmArgs a, bool dbg) {
 
 // The fp16 dequantize-fused GEMM with its split-K plan (workspace from the context).
 int run_gemm_h16(mgh_ctx* c, mgh::GemmH16Args a) {
-    const mgh::H16Plan p = mgh::gemm_h16_plan(a.M, a.N, a.K);
+    const mgh::H16Plan p = mgh::gemm_h16_plan(a.M, a.N, a.K, a.xf != nullptr);
     a.splits = p.splits;
     if (p.splits > 1) {
         if (int r = ensure_qp_ws(c, p.ws_bytes)) return r;
         a.ws = (float*)c->qp_ws;
     }
-    MGH_HIP(c, mgh::launch_gemm_h16(p.bm, a, c->stream), "k_gemm_h16");
+    MGH_HIP(c, mgh::launch_gemm_h16(p, a, c->stream), "k_gemm_h16");
     return MGH_OK;
 }
 
@@ -754,9 +754,20 @@ int mgh_gemm_h16_f32in(mgh_ctx* c, const void* wp16, int N, int K, const float* 
     if (M == 0) return MGH_OK;
     if (int r = set_dev(c)) return r;
     mgh::GemmH16Args a{};
-    a.xf = x; a.w = (const _Float16*)wp16;
+    a.w = (const _Float16*)wp16;
     a.bias = bias; a.resid = resid; a.y = y;
     a.M = M; a.N = N; a.K = K; a.act = act;
+    if (M < 2048) {
+        // few activation rows: round them while the GEMM reads them (one launch; the 64-row
+        // fp32 stage costs less than the separate rounding pass)
+        a.xf = x;
+    } else {
+        // many rows: a rounding pass, then the fp16-operand kernel with 128-row tiles (half the
+        // operand bytes per flop of the fp32-stage variant)
+        if (int r = ensure_scratch(c, round256((size_t)M * K * 2))) return r;
+        MGH_HIP(c, mgh::launch_f32_to_f16(x, (_Float16*)c->scratch, (int64_t)M * K, c->stream), "k_f32_to_f16");
+        a.x = (const _Float16*)c->scratch;
+    }
     return run_gemm_h16(c, a);
 }
 

@@ -142,13 +142,13 @@ struct GemmH16Args {
     int M, N, K, splits, act;
 };
 struct H16Plan {
-    int bm, splits;
+    int bm, splits, ns;    // activation tile rows, K splits, K-stage ring depth
     size_t ws_bytes;
 };
-H16Plan gemm_h16_plan(int M, int N, int K);
+H16Plan gemm_h16_plan(int M, int N, int K, bool xf32);
 size_t packed_weight_bytes_f16(int64_t N, int64_t K);
 hipError_t launch_pack_weights_f16(int wtype, const void* w, void* out, int N, int K, hipStream_t s);
 hipError_t launch_f32_to_f16(const float* x, _Float16* h, int64_t n, hipStream_t s);
-hipError_t launch_gemm_h16(int bm, const GemmH16Args& a, hipStream_t s);
+hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a, hipStream_t s);
 
 }  // namespace mgh
