@@ -28,7 +28,8 @@
 //    contracted on v_mfma_f32_16x16x32_bf16 (32 blocks per instruction, four cross terms,
 //    relative error ~2^-15 of the term).
 //  * Weights take the MFMA "A" role, so each lane ends with four consecutive output
-//    columns of one row: float4 bias/residual loads and output stores.
+//    columns of one row; the epilogue transposes the tile through LDS so it leaves as whole
+//    512-byte rows with streaming (non-temporal) stores.
 // Data movement: 128 weight rows x BM activation rows per 256-thread workgroup (2x2 waves,
 // 64 x BM/2 outputs each), K stage of 64 (two blocks), double-buffered. Every operand —
 // codes and scales — moves with global_load_lds (dwordx4 for codes, dword for scales)
@@ -371,66 +372,75 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_qp(GemmArgs g) {
         }
     }
 
-    if (splits > 1) {
-        // split-K: the partial tile goes to the workspace in [register][thread] order
-        // (coalesced 16-byte stores); k_gemm_qp_reduce sums the splits in split order — a
-        // fixed order, so results are deterministic — and applies the epilogue.
-        f32x4* part = (f32x4*)g.ws + ((size_t)lt * splits + ks) * (4 * J * NT);
+    // epilogue: the tile leaves through LDS as whole rows (512 bytes per 32 lanes), in two
+    // halves of BM/2 rows, with streaming stores; +bias -> act -> +resid (mg-opencl.cpp:485-491)
+    // on the way out, or (split-K) the raw partial tile row-major into the workspace, summed in
+    // split order by k_gemm_qp_reduce — a fixed order, so results are deterministic
+    constexpr int P = BN + 4;                   // padded row pitch (floats)
+    constexpr int HR = BM / 2;
+    static_assert(HR * P * 4 <= (int)sizeof(PLds<BM, NS>), "transpose buffer fits the ring");
+    float* Tt = (float*)&L;
+    const int c = 4 * (tid & 31);               // this thread's 4 columns
+    const int n = n0 + c;
+    f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+    if (splits == 1 && g.bias && n < N) bv = *(const f32x4*)(g.bias + n);
+    float* part = splits > 1 ? g.ws + ((size_t)lt * splits + ks) * (size_t)BM * BN : nullptr;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+    for (int h = 0; h < 2; h++) {
+        __syncthreads();                        // ring / previous half no longer read
+        if (wm == h) {
 #pragma unroll
-            for (int j = 0; j < J; j++) part[(size_t)(i * J + j) * NT + tid] = acc[i][j];
-        return;
-    }
-
-    // epilogue: lane holds y[m][n..n+3]; +bias -> act -> +resid (mg-opencl.cpp:485-491)
+            for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int n = n0 + 64 * wn + 16 * i + 4 * lq;
-        if (n >= N) continue;
-        const f32x4 bv = g.bias ? *(const f32x4*)(g.bias + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int j = 0; j < J; j++)
+                    *(f32x4*)&Tt[(16 * j + l16) * P + 64 * wn + 16 * i + 4 * lq] = acc[i][j];
+        }
+        __syncthreads();
 #pragma unroll
-        for (int j = 0; j < J; j++) {
-            const int m = m0 + (BM / 2) * wm + 16 * j + l16;
-            if (m >= M) continue;
+        for (int p = 0; p < HR / 8; p++) {
+            const int r = 8 * p + (tid >> 5);
+            const f32x4 v = *(const f32x4*)&Tt[r * P + c];
+            if (splits > 1) {
+                __builtin_nontemporal_store(v, (f32x4*)(part + (size_t)(HR * h + r) * BN + c));
+                continue;
+            }
+            const int m = m0 + HR * h + r;
+            if (m >= M || n >= N) continue;
+            f32x4 o = v + bv;
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = act_x<ACT>(o[e]);
             const size_t idx = (size_t)m * N + n;
-            f32x4 v = acc[i][j] + bv;
-#pragma unroll
-            for (int r = 0; r < 4; r++) v[r] = act_x<ACT>(v[r]);
-            if (g.resid) v += *(const f32x4*)(g.resid + idx);
-            *(f32x4*)(g.y + idx) = v;
+            if (g.resid) o += *(const f32x4*)(g.resid + idx);
+            __builtin_nontemporal_store(o, (f32x4*)(g.y + idx));
         }
     }
 }
 
-// Split-K epilogue: one thread per (tile, accumulator register, GEMM thread) float4, in the
-// GEMM's register layout; sums the splits in order, then +bias -> act -> +resid.
+// Split-K epilogue: one thread per output float4; sums the splits' row-major partial tiles in
+// split order, then +bias -> act -> +resid.
 template <int ACT, int BM>
 __global__ __launch_bounds__(256) void k_gemm_qp_reduce(GemmArgs g) {
-    constexpr int J = BM / 32;
     const int M = g.M, N = g.N, splits = g.splits;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const int tid = (int)(idx % NT);
-    const int q = (int)((idx / NT) % (4 * J));
-    const int lt = (int)(idx / ((size_t)NT * 4 * J));
+    const size_t idx4 = (size_t)blockIdx.x * 256 + threadIdx.x;
+    constexpr int Q = BM * BN / 4;              // float4s per tile
+    const int lt = (int)(idx4 / Q);
     if (lt >= tiles_m * tiles_n) return;
+    const int q = (int)(idx4 - (size_t)lt * Q);
+    const int r = q / (BN / 4), c = 4 * (q % (BN / 4));
     int m0, n0;
     tile_origin(lt, tiles_m, tiles_n, BM, m0, n0);
-    const int lane = tid & 63, wave = tid >> 6, wn = wave & 1, wm = wave >> 1;
-    const int i = q / J, j = q % J;
-    const int n = n0 + 64 * wn + 16 * i + 4 * (lane >> 4);
-    const int m = m0 + (BM / 2) * wm + 16 * j + (lane & 15);
-    if (n >= N || m >= M) return;
-    const f32x4* part = (const f32x4*)g.ws + (size_t)lt * splits * (4 * J * NT) + (size_t)q * NT + tid;
-    f32x4 v = part[0];
-    for (int k = 1; k < splits; k++) v += part[(size_t)k * 4 * J * NT];
+    const int m = m0 + r, n = n0 + c;
+    if (m >= M || n >= N) return;
+    const f32x4* part = (const f32x4*)(g.ws + (size_t)lt * splits * BM * BN) + q;
+    f32x4 v = __builtin_nontemporal_load(part);
+    for (int k = 1; k < splits; k++) v += __builtin_nontemporal_load(part + (size_t)k * Q);
     if (g.bias) v += *(const f32x4*)(g.bias + n);
 #pragma unroll
-    for (int r = 0; r < 4; r++) v[r] = act_x<ACT>(v[r]);
+    for (int e = 0; e < 4; e++) v[e] = act_x<ACT>(v[e]);
     const size_t o = (size_t)m * N + n;
     if (g.resid) v += *(const f32x4*)(g.resid + o);
-    *(f32x4*)(g.y + o) = v;
+    __builtin_nontemporal_store(v, (f32x4*)(g.y + o));
 }
 
 int gemm_qp_bm(int M, int N) {
