@@ -24,7 +24,7 @@ constexpr int LD = 36;     // LDS row stride (floats)
 
 template <int ACT>
 __device__ __forceinline__ float act_f(float v) {
-    if (ACT == 1) return 0.5f * v * (1.0f + erff(v * 0.70710678f));
+    if (ACT == 1) return gelu_erf(v);
     if (ACT == 2) return v / (1.0f + expf(-v));
     return v;
 }

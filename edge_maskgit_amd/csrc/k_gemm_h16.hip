@@ -41,12 +41,9 @@ namespace {
 typedef __attribute__((address_space(3))) void lds_void;
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
-constexpr int NT = 256;
-constexpr int BN = 128;
-
 // NS-deep ring of K stages. XF32: the activation stage holds fp32 rows (16 chunks of 16 bytes)
 // instead of fp16 ones
-template <int BM, bool XF32, int NS>
+template <int BM, int BN, bool XF32, int NS>
 struct HLds {
     u32x4 w[NS][BN * 8];                 // [stage][row][8 swizzled 16-byte chunks] fp16
     u32x4 x[NS][BM * (XF32 ? 16 : 8)];
@@ -64,17 +61,17 @@ __device__ __forceinline__ void wait_vm() {
 
 template <int ACT>
 __device__ __forceinline__ float act_h(float v) {
-    if (ACT == 1) return 0.5f * v * (1.0f + erff(v * 0.70710678f));
+    if (ACT == 1) return gelu_erf(v);
     if (ACT == 2) return v / (1.0f + expf(-v));
     return v;
 }
 
-__device__ __forceinline__ void tile_origin(int lt, int tiles_m, int tiles_n, int bm, int& m0, int& n0) {
+__device__ __forceinline__ void tile_origin(int lt, int tiles_m, int tiles_n, int bm, int bn, int& m0, int& n0) {
     const int panel = lt / (8 * tiles_n);
     const int pm = min(8, tiles_m - panel * 8);
     const int rem = lt - panel * 8 * tiles_n;
     m0 = (panel * 8 + rem % pm) * bm;
-    n0 = (rem / pm) * BN;
+    n0 = (rem / pm) * bn;
 }
 
 __device__ __forceinline__ uint32_t f16_bits(float v) {
@@ -143,16 +140,27 @@ __global__ __launch_bounds__(256) void k_f32_to_f16(const f32x4* __restrict__ x,
 // split ks over its K range into ws. XF32: the activations arrive as fp32 (g.xf) and are
 // rounded to fp16 (nearest even, as k_f32_to_f16) when the MFMA fragments are read from LDS;
 // their stage rows are 256 bytes (16 chunks, swizzle chunk ^ (row & 15)).
-template <int ACT, int BM, bool PART, bool XF32, int NS>
-__global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
-    constexpr int J = BM / 32;                  // 16-row activation subtiles per wave
-    constexpr int CW = BN / 32;                 // weight DMA instructions per wave and stage
-    constexpr int CX = XF32 ? BM / 16 : BM / 32;  // activation DMA instructions per wave and stage
-    constexpr int MID = 2 * J;                  // second-half MFMAs issued before the boundary
-    constexpr int NR = 4 + (XF32 ? 2 : 1) * J;  // LDS reads per K half
-    static_assert(NR <= 4 * J, "read/MFMA interleave");
+// Tile BN weight rows x BM activation rows on 2 x WMR waves, each BN/2 weight rows x BM/WMR
+// activation rows.
+template <int WMR, int BN>
+constexpr int kH16MinBlocks = (WMR == 2 && BN == 128) ? 2 : 1;
+
+template <int ACT, int BM, bool PART, bool XF32, int NS, int WMR, int BN>
+__global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h16(GemmH16Args g) {
+    constexpr int NW = 2 * WMR;                 // waves
+    constexpr int NTH = 64 * NW;                // threads
+    constexpr int RW = BM / WMR;                // activation rows per wave
+    constexpr int J = RW / 16;                  // 16-row activation subtiles per wave
+    constexpr int WN = BN / 2;                  // weight rows per wave
+    constexpr int I = WN / 16;                  // 16-row weight subtiles per wave
+    constexpr int CW = BN / 8 / NW;             // weight DMA instructions per wave and stage
+    constexpr int CX = XF32 ? BM / 4 / NW : BM / 8 / NW;  // activation DMA instructions per wave and stage
+    static_assert(CW >= 1 && CX >= 1 && RW % 16 == 0, "tile shape");
+    constexpr int MID = I * J / 2;              // second-half MFMAs issued before the boundary
+    constexpr int NR = I + (XF32 ? 2 : 1) * J;  // LDS reads per K half
+    static_assert(NR <= I * J, "read/MFMA interleave");
     static_assert(NS >= 2 && (NS - 1) * (CW + CX) < 64, "ring depth");
-    __shared__ HLds<BM, XF32, NS> L;
+    __shared__ HLds<BM, BN, XF32, NS> L;
 
     const int K = g.K, M = g.M, N = g.N;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
@@ -160,7 +168,7 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
     const int lfull = xcd_remap(blockIdx.x, tiles_m * tiles_n * splits);
     const int lt = lfull / splits, ks = lfull - lt * splits;
     int m0, n0;
-    tile_origin(lt, tiles_m, tiles_n, BM, m0, n0);
+    tile_origin(lt, tiles_m, tiles_n, BM, BN, m0, n0);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wn = wave & 1, wm = wave >> 1;
@@ -172,13 +180,13 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
     const uint8_t* srcx[CX];
 #pragma unroll
     for (int q = 0; q < CW; q++) {
-        const int c = wave + 4 * q;
+        const int c = wave + NW * q;
         const int n = min(n0 + 8 * c + (lane >> 3), N - 1);
         srcw[q] = (const uint8_t*)g.w + (size_t)n * K * 2 + ((lane & 7) ^ ((4 * c + (lane >> 4)) & 7)) * 16;
     }
 #pragma unroll
     for (int q = 0; q < CX; q++) {
-        const int c = wave + 4 * q;
+        const int c = wave + NW * q;
         if (XF32) {                             // 4 rows of 256 bytes per instruction
             const int r = 4 * c + (lane >> 4);
             const int m = min(m0 + r, M - 1);
@@ -196,9 +204,9 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
     auto dma_stage = [&](int st, int s) {
         const size_t ofs = (size_t)kst(s) * 128;
 #pragma unroll
-        for (int d = 0; d < CW; d++) dma16(srcw[d] + ofs, &L.w[st][(wave + 4 * d) * 64]);
+        for (int d = 0; d < CW; d++) dma16(srcw[d] + ofs, &L.w[st][(wave + NW * d) * 64]);
 #pragma unroll
-        for (int d = 0; d < CX; d++) dma16(srcx[d] + (XF32 ? 2 : 1) * ofs, &L.x[st][(wave + 4 * d) * 64]);
+        for (int d = 0; d < CX; d++) dma16(srcx[d] + (XF32 ? 2 : 1) * ofs, &L.x[st][(wave + NW * d) * 64]);
     };
     auto frag = [&](const u32x4* B, int r0, int kb) {
         return __builtin_bit_cast(f16x8, B[(r0 + l16) * 8 + ((4 * kb + lq) ^ ((l16 >> 1) & 7))]);
@@ -213,12 +221,12 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
                      (_Float16)v1[0], (_Float16)v1[1], (_Float16)v1[2], (_Float16)v1[3]};
     };
 
-    f32x4 acc[4][J];
+    f32x4 acc[I][J];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < I; i++)
 #pragma unroll
         for (int j = 0; j < J; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    f16x8 a[2][4], b[2][J];
+    f16x8 a[2][I], b[2][J];
 
     // Ring: stages 0..NS-1 requested up front; at the boundary of stage s, stage s+1 is
     // awaited and stage s+NS goes into stage s's buffer (its fragments are in registers by
@@ -230,74 +238,93 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
     wait_vm<(NS - 1) * NDMA>();                 // stage 0 has landed (mine) ...
     __syncthreads();                            // ... and everyone's
 #pragma unroll
-    for (int i = 0; i < 4; i++) a[0][i] = frag(L.w[0], 64 * wn + 16 * i, 0);
+    for (int i = 0; i < I; i++) a[0][i] = frag(L.w[0], WN * wn + 16 * i, 0);
 #pragma unroll
-    for (int j = 0; j < J; j++) b[0][j] = xfrag(L.x[0], (BM / 2) * wm + 16 * j, 0);
+    for (int j = 0; j < J; j++) b[0][j] = xfrag(L.x[0], RW * wm + 16 * j, 0);
 
     int st = 0;
     for (int s = 0; s < SL; s++) {
         const int stn = st + 1 == NS ? 0 : st + 1;
         // K half 0: MFMAs on a/b[0] while the fragments of half 1 are read
 #pragma unroll
-        for (int i = 0; i < 4; i++) a[1][i] = frag(L.w[st], 64 * wn + 16 * i, 1);
+        for (int i = 0; i < I; i++) a[1][i] = frag(L.w[st], WN * wn + 16 * i, 1);
 #pragma unroll
-        for (int j = 0; j < J; j++) b[1][j] = xfrag(L.x[st], (BM / 2) * wm + 16 * j, 1);
+        for (int j = 0; j < J; j++) b[1][j] = xfrag(L.x[st], RW * wm + 16 * j, 1);
 #pragma unroll
         for (int j = 0; j < J; j++)
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < I; i++)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0][i], b[0][j], acc[i][j], 0, 0, 0);
 #pragma unroll
         for (int t = 0; t < NR; t++) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 4 * J - NR, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, I * J - NR, 0);
         // K half 1: MID MFMAs, the stage boundary, the rest
 #pragma unroll
         for (int q = 0; q < MID; q++)
-            acc[q % 4][q / 4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1][q % 4], b[1][q / 4], acc[q % 4][q / 4], 0, 0, 0);
-        if (s + 1 < SL) {
-            wait_vm<(NS - 2) * NDMA>();         // stage s+1 has landed (mine) ...
-            __syncthreads();                    // ... and everyone's; stage s is no longer read
-            // (a 2-deep ring waits for everything, so it skips the re-loads past the end)
-            if (NS > 2 || s + NS < SL) dma_stage(st, min(s + NS, SL - 1));
+            acc[q % I][q / I] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1][q % I], b[1][q / I], acc[q % I][q / I], 0, 0, 0);
+        // The boundary runs on the last stage too (its fragment reads fetch an unused buffer):
+        // with no branch around the LDS reads, the compiler's wait before the remaining MFMAs
+        // covers only the reads those MFMAs consume, not the ones just issued.
+        wait_vm<(NS - 2) * NDMA>();             // stage s+1 has landed (mine) ...
+        __syncthreads();                        // ... and everyone's; stage s is no longer read
+        // (a 2-deep ring waits for everything, so it skips the re-loads past the end)
+        if (NS > 2 ? s + 1 < SL : s + NS < SL) dma_stage(st, min(s + NS, SL - 1));
 #pragma unroll
-            for (int i = 0; i < 4; i++) a[0][i] = frag(L.w[stn], 64 * wn + 16 * i, 0);
+        for (int i = 0; i < I; i++) a[0][i] = frag(L.w[stn], WN * wn + 16 * i, 0);
 #pragma unroll
-            for (int j = 0; j < J; j++) b[0][j] = xfrag(L.x[stn], (BM / 2) * wm + 16 * j, 0);
-        }
+        for (int j = 0; j < J; j++) b[0][j] = xfrag(L.x[stn], RW * wm + 16 * j, 0);
 #pragma unroll
-        for (int q = MID; q < 4 * J; q++)
-            acc[q % 4][q / 4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1][q % 4], b[1][q / 4], acc[q % 4][q / 4], 0, 0, 0);
+        for (int q = MID; q < I * J; q++)
+            acc[q % I][q / I] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1][q % I], b[1][q / I], acc[q % I][q / I], 0, 0, 0);
         st = stn;
     }
     wait_vm0();
 
-    // epilogue: the tile leaves through LDS as whole rows, in two halves of BM/2 rows
+    // bias and activation on the accumulators (lane column n0 + WN*wn + 16i + 4lq + e), where
+    // every value is independent of the others, before the transpose
+    if (!PART) {
+#pragma unroll
+        for (int i = 0; i < I; i++) {
+            const int nb = n0 + WN * wn + 16 * i + 4 * lq;
+            f32x4 bi = {0.f, 0.f, 0.f, 0.f};
+            if (g.bias && nb < N) bi = *(const f32x4*)(g.bias + nb);
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+                acc[i][j] += bi;
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[i][j][e] = act_h<ACT>(acc[i][j][e]);
+            }
+        }
+    }
+
+    // epilogue: the tile leaves through LDS as whole rows, HR rows (of one wave row) at a time
     constexpr int P = BN + 4;                   // padded row pitch (floats)
-    constexpr int HR = BM / 2;
-    static_assert(HR * P * 4 <= (int)sizeof(HLds<BM, XF32, NS>), "transpose buffer fits the ring");
+    constexpr int HR = RW < 64 ? RW : 64;
+    constexpr int HPW = RW / HR;                // passes per wave row
+    constexpr int JH = HR / 16;                 // activation subtiles per pass
+    static_assert(HR * P * 4 <= (int)sizeof(HLds<BM, BN, XF32, NS>), "transpose buffer fits the ring");
+    constexpr int TR = BN / 4;                  // threads per output row
     float* T = (float*)&L;
-    const int c = 4 * (tid & 31);               // this thread's 4 columns
+    const int c = 4 * (tid % TR);               // this thread's 4 columns
     const int n = n0 + c;
-    f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-    if (!PART && g.bias && n < N) bv = *(const f32x4*)(g.bias + n);
     float* part = PART ? g.ws + ((size_t)lt * splits + ks) * (size_t)BM * BN : nullptr;
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-        __syncthreads();                        // ring / previous half no longer read
-        if (wm == h) {
+    for (int h = 0; h < WMR * HPW; h++) {
+        __syncthreads();                        // ring / previous rows no longer read
+        if (wm == h / HPW) {
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < I; i++)
 #pragma unroll
-                for (int j = 0; j < J; j++)
-                    *(f32x4*)&T[(16 * j + l16) * P + 64 * wn + 16 * i + 4 * lq] = acc[i][j];
+                for (int j = 0; j < JH; j++)
+                    *(f32x4*)&T[(16 * j + l16) * P + WN * wn + 16 * i + 4 * lq] = acc[i][(h % HPW) * JH + j];
         }
         __syncthreads();
 #pragma unroll
-        for (int p = 0; p < HR / 8; p++) {
-            const int r = 8 * p + (tid >> 5);
+        for (int p = 0; p < HR / (NTH / TR); p++) {
+            const int r = (NTH / TR) * p + tid / TR;
             const f32x4 v = *(const f32x4*)&T[r * P + c];
             if (PART) {
                 __builtin_nontemporal_store(v, (f32x4*)(part + (size_t)(HR * h + r) * BN + c));
@@ -305,9 +332,7 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
             }
             const int m = m0 + HR * h + r;
             if (m >= M || n >= N) continue;
-            f32x4 o = v + bv;
-#pragma unroll
-            for (int e = 0; e < 4; e++) o[e] = act_h<ACT>(o[e]);
+            f32x4 o = v;
             const size_t idx = (size_t)m * N + n;
             if (g.resid) o += *(const f32x4*)(g.resid + idx);
             if (g.y16)
@@ -321,7 +346,7 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_h16(GemmH16Args g) {
 
 // Split-K epilogue: one thread per output float4; sums the splits' row-major partial tiles in
 // split order, then +bias -> act -> +resid.
-template <int ACT, int BM>
+template <int ACT, int BM, int BN>
 __global__ __launch_bounds__(256) void k_gemm_h16_reduce(GemmH16Args g) {
     const int M = g.M, N = g.N, splits = g.splits;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
@@ -332,7 +357,7 @@ __global__ __launch_bounds__(256) void k_gemm_h16_reduce(GemmH16Args g) {
     const int q = (int)(idx4 - (size_t)lt * Q);
     const int r = q / (BN / 4), c = 4 * (q % (BN / 4));
     int m0, n0;
-    tile_origin(lt, tiles_m, tiles_n, BM, m0, n0);
+    tile_origin(lt, tiles_m, tiles_n, BM, BN, m0, n0);
     const int m = m0 + r, n = n0 + c;
     if (m >= M || n >= N) return;
     const f32x4* part = (const f32x4*)(g.ws + (size_t)lt * splits * BM * BN) + q;
@@ -353,19 +378,28 @@ __global__ __launch_bounds__(256) void k_gemm_h16_reduce(GemmH16Args g) {
 H16Plan gemm_h16_plan(int M, int N, int K, bool xf32) {
     H16Plan p{};
     p.ns = 2;
-    const int tn = (N + BN - 1) / BN;
-    const int t128 = ((M + 127) / 128) * tn;
-    // 128-row activation tiles once there are about two per CU; below that the 64-row tile
-    // (1.5x the operand traffic per flop, but twice the workgroups) measured faster
-    // (with fp32 activations, 64-row tiles: their stage is as large as a 128-row fp16 stage)
-    p.bm = t128 >= 512 && !xf32 ? 128 : 64;
-    const int tiles = ((M + p.bm - 1) / p.bm) * tn;
+    p.bn = 128;
+    p.wmr = 2;
+    const int t128 = ((M + 127) / 128) * ((N + 127) / 128);
+    const int t256 = ((M + 255) / 256) * ((N + 255) / 256);
+    // Tile choice, from timings of the four FC shapes at M = 1025, 4112 and 16448 (fp16
+    // operands): 64-row tiles (three workgroups per CU) up to about four 128-row tiles per CU,
+    // 128-row tiles beyond; 256 x 256 tiles (8 waves, half the LDS and L2 operand traffic per
+    // flop of a 128 x 128 tile) for long-K shapes that still give most CUs a tile. With fp32
+    // activations, 64-row tiles: their stage is already as large as a 128-row fp16 stage.
+    p.bm = t128 >= 1024 && !xf32 ? 128 : 64;
+    if (!xf32 && K >= 2048 && t256 >= 192) {
+        p.bm = 256;
+        p.bn = 256;
+        p.wmr = 4;
+    }
+    const int tiles = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
     const int S = K / 64;
     p.splits = 1;
     // split K while there are fewer workgroups than about 1.5 per CU and each split keeps
     // >= 12 stages (K >= 768)
     while (tiles * p.splits * 2 <= 384 && S / (p.splits * 2) >= 12) p.splits *= 2;
-    p.ws_bytes = p.splits > 1 ? (size_t)tiles * p.splits * p.bm * BN * 4 : 0;
+    p.ws_bytes = p.splits > 1 ? (size_t)tiles * p.splits * p.bm * p.bn * 4 : 0;
     return p;
 }
 
@@ -392,38 +426,33 @@ hipError_t launch_f32_to_f16(const float* x, _Float16* h, int64_t n, hipStream_t
     return hipGetLastError();
 }
 
-template <int BMV, bool XF32, int NSV>
+template <int BM, bool XF32, int NS, int WMR, int BN>
 static hipError_t launch_h16_t(const GemmH16Args& a, hipStream_t s) {
-    const int tiles = ((a.M + BMV - 1) / BMV) * ((a.N + BN - 1) / BN);
+    const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     const int splits = std::max(a.splits, 1);
-    const dim3 block(NT);
+    const dim3 block(128 * WMR);
     if (splits > 1) {
-        hipLaunchKernelGGL((k_gemm_h16<0, BMV, true, XF32, NSV>), dim3(tiles * splits), block, 0, s, a);
-        const size_t n4 = (size_t)tiles * BMV * BN / 4;
-        const dim3 rg((unsigned)((n4 + 255) / 256));
-        if (a.act == 1) hipLaunchKernelGGL((k_gemm_h16_reduce<1, BMV>), rg, block, 0, s, a);
-        else if (a.act == 2) hipLaunchKernelGGL((k_gemm_h16_reduce<2, BMV>), rg, block, 0, s, a);
-        else hipLaunchKernelGGL((k_gemm_h16_reduce<0, BMV>), rg, block, 0, s, a);
+        hipLaunchKernelGGL((k_gemm_h16<0, BM, true, XF32, NS, WMR, BN>), dim3(tiles * splits), block, 0, s, a);
+        const size_t n4 = (size_t)tiles * BM * BN / 4;
+        const dim3 rg((unsigned)((n4 + 255) / 256)), rb(256);
+        if (a.act == 1) hipLaunchKernelGGL((k_gemm_h16_reduce<1, BM, BN>), rg, rb, 0, s, a);
+        else if (a.act == 2) hipLaunchKernelGGL((k_gemm_h16_reduce<2, BM, BN>), rg, rb, 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_h16_reduce<0, BM, BN>), rg, rb, 0, s, a);
     } else {
-        if (a.act == 1) hipLaunchKernelGGL((k_gemm_h16<1, BMV, false, XF32, NSV>), dim3(tiles), block, 0, s, a);
-        else if (a.act == 2) hipLaunchKernelGGL((k_gemm_h16<2, BMV, false, XF32, NSV>), dim3(tiles), block, 0, s, a);
-        else hipLaunchKernelGGL((k_gemm_h16<0, BMV, false, XF32, NSV>), dim3(tiles), block, 0, s, a);
+        if (a.act == 1) hipLaunchKernelGGL((k_gemm_h16<1, BM, false, XF32, NS, WMR, BN>), dim3(tiles), block, 0, s, a);
+        else if (a.act == 2) hipLaunchKernelGGL((k_gemm_h16<2, BM, false, XF32, NS, WMR, BN>), dim3(tiles), block, 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_h16<0, BM, false, XF32, NS, WMR, BN>), dim3(tiles), block, 0, s, a);
     }
     return hipGetLastError();
 }
 
-template <int BMV, bool XF32>
-static hipError_t launch_h16_ns(int ns, const GemmH16Args& a, hipStream_t s) {
-    if (ns == 2) return launch_h16_t<BMV, XF32, 2>(a, s);
-    if (ns == 3) return launch_h16_t<BMV, XF32, 3>(a, s);
-    if (ns == 4 && !(BMV == 128 && XF32)) return launch_h16_t<BMV, XF32, (BMV == 128 && XF32) ? 3 : 4>(a, s);
-    return hipErrorInvalidValue;
-}
-
 hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a, hipStream_t s) {
     const bool xf = a.xf != nullptr;
-    if (p.bm == 128) return xf ? launch_h16_ns<128, true>(p.ns, a, s) : launch_h16_ns<128, false>(p.ns, a, s);
-    if (p.bm == 64) return xf ? launch_h16_ns<64, true>(p.ns, a, s) : launch_h16_ns<64, false>(p.ns, a, s);
+    if (p.ns != 2) return hipErrorInvalidValue;
+    if (p.bn == 256 && p.bm == 256 && p.wmr == 4 && !xf) return launch_h16_t<256, false, 2, 4, 256>(a, s);
+    if (p.bn != 128 || p.wmr != 2) return hipErrorInvalidValue;
+    if (p.bm == 128) return xf ? launch_h16_t<128, true, 2, 2, 128>(a, s) : launch_h16_t<128, false, 2, 2, 128>(a, s);
+    if (p.bm == 64) return xf ? launch_h16_t<64, true, 2, 2, 128>(a, s) : launch_h16_t<64, false, 2, 2, 128>(a, s);
     return hipErrorInvalidValue;
 }
 

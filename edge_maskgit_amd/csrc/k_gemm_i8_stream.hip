@@ -175,7 +175,7 @@ __device__ __forceinline__ void unpack_step(SLds<WTYPE>& L, int tid) {
 
 template <int ACT>
 __device__ __forceinline__ float act_s(float v) {
-    if (ACT == 1) return 0.5f * v * (1.0f + erff(v * 0.70710678f));
+    if (ACT == 1) return gelu_erf(v);
     if (ACT == 2) return v / (1.0f + expf(-v));
     return v;
 }

@@ -210,7 +210,7 @@ __device__ __forceinline__ void unpack_step(XLds<WTYPE>& L, int t0, int tid) {
 
 template <int ACT>
 __device__ __forceinline__ float act_x(float v) {
-    if (ACT == 1) return 0.5f * v * (1.0f + erff(v * 0.70710678f));
+    if (ACT == 1) return gelu_erf(v);
     if (ACT == 2) return v / (1.0f + expf(-v));
     return v;
 }

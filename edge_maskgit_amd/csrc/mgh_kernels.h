@@ -142,7 +142,8 @@ struct GemmH16Args {
     int M, N, K, splits, act;
 };
 struct H16Plan {
-    int bm, splits, ns;    // activation tile rows, K splits, K-stage ring depth
+    int bm, bn, wmr;       // activation / weight tile rows, waves along the activation rows
+    int splits, ns;        // K splits, K-stage ring depth
     size_t ws_bytes;
 };
 H16Plan gemm_h16_plan(int M, int N, int K, bool xf32);

@@ -79,13 +79,14 @@ def test_f32_to_f16_rounding(ctx):
 
 
 SHAPES = [(1, 4, 64), (7, 132, 256), (65, 128, 768), (257, 3072, 768), (1025, 2304, 768),
-          (1025, 768, 768), (1025, 768, 3072), (300, 256, 3072), (4097, 768, 3072)]
+          (1025, 768, 768), (1025, 768, 3072), (300, 256, 3072), (4097, 768, 3072),
+          (4112, 3072, 768), (4500, 2304, 768), (6150, 2048, 2048)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
 @pytest.mark.parametrize("act,res", [(0, False), (1, False), (0, True), (2, True)])
 def test_gemm_h16_vs_float64(ctx, M, N, K, act, res):
-    if (M, N, K) == (4097, 768, 3072) and (act, res) != (0, True):
+    if M >= 4097 and (act, res) not in ((0, True), (1, False)):
         pytest.skip("one epilogue at the largest shape")
     print(f"gemm_h16 M={M} N={N} K={K} act={act} resid={res}", flush=True)
     rng = np.random.default_rng(M * 7 + N * 3 + K + act)
