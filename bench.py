@@ -18,8 +18,9 @@ weight once):
     kernels): per-32 int8 activation quantization (k_quantize_act_q8, codes as fp16), then
     k_gemm_qp on the packed codes with per-block scales applied in fp32.
 The other path is measured on the same workload and reported under extra.
-Each buffer set's step is captured once as a HIP graph and replayed (--no-graphs enqueues the
-kernels one by one instead). Buffers rotate over >= --rotate-gb of distinct sets so the 256 MB
+The step's kernels are enqueued one by one on the context's stream (--graphs instead captures
+each buffer set's step once as a HIP graph and replays it; for these few-kernel steps the
+graph launch measured slower). Buffers rotate over >= --rotate-gb of distinct sets so the 256 MB
 MALL and the L2s do not serve the timed reads. Synthetic data: x ~ N(0,1), W ~ N(0,0.02)
 quantized to Q8_0, biases ~ N(0,0.01), residuals ~ N(0,1), seeded.
 
@@ -57,6 +58,7 @@ LAYER = [  # name, N, K, act, residual
     ("up", 3072, 768, ema.ACT_GELU, False),
     ("down", 768, 3072, ema.ACT_NONE, True),
 ]
+CFG1 = [("cfg1", 3072, 768, ema.ACT_NONE, False)]   # configs[0]: one Q8_0 FC GEMM at M=257
 
 
 KERNEL = {"packed": "k_gemm_qp", "raw": "k_gemm_q_f16x", "h16": "k_gemm_h16"}
@@ -90,13 +92,13 @@ class LayerSet:
     rounded to fp16 inside the GEMM).
     path "raw": GGUF blocks as stored, per FC: quantizer + mgh_gemm_q_codes16."""
 
-    def __init__(self, ctx, host, M, wtype, path="packed"):
+    def __init__(self, ctx, host, M, wtype, path="packed", layer=LAYER):
         self.ctx = ctx
         self.M = M
         self.wtype = wtype
         self.path = path
         self.g = []
-        for (name, N, K, act, res), h in zip(LAYER, host):
+        for (name, N, K, act, res), h in zip(layer, host):
             nb = K // 32
             w = ctx.upload(h["wq"])
             if path == "h16":
@@ -178,11 +180,11 @@ def synth_q4_k(w):
     return out.reshape(N, -1)
 
 
-def host_layer(M, wtype, seed=0):
+def host_layer(M, wtype, seed=0, layer=LAYER):
     rng = np.random.default_rng(seed)
     out = []
     enc = synth_q8_0 if wtype == ema.WTYPE_Q8_0 else synth_q4_k
-    for name, N, K, act, res in LAYER:
+    for name, N, K, act, res in layer:
         w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
         out.append(dict(w=w, wq=enc(w),
                         x=rng.standard_normal((M, K)).astype(np.float32),
@@ -191,16 +193,16 @@ def host_layer(M, wtype, seed=0):
     return out
 
 
-def layer_ops(M):
-    return sum(2.0 * M * N * K for _, N, K, _, _ in LAYER)
+def layer_ops(M, layer=LAYER):
+    return sum(2.0 * M * N * K for _, N, K, _, _ in layer)
 
 
-def gemm_alg_bytes(M, wtype, path="h16"):
+def gemm_alg_bytes(M, wtype, path="h16", layer=LAYER):
     """Algorithmic HBM bytes of the four GEMM launches of one step: the quantized weights
     once, the fp16 activations (int8-dot path: fp16 codes + fp32 block scales (+ block sums for
     Q4_K)), the fp32 output, bias and residual."""
     tot = 0
-    for _, N, K, act, res in LAYER:
+    for _, N, K, act, res in layer:
         nb = K // 32
         if path == "h16":                  # fp32 activations read by the GEMM itself
             tot += N * row_bytes(wtype, K) + M * K * 4 + M * N * 4 + N * 4
@@ -212,11 +214,11 @@ def gemm_alg_bytes(M, wtype, path="h16"):
     return tot
 
 
-def step_alg_bytes(M, wtype):
+def step_alg_bytes(M, wtype, layer=LAYER):
     """Algorithmic bytes of the whole FC op: weights once, fp32 x once, fp32 y once, bias,
     residual once."""
     tot = 0
-    for _, N, K, act, res in LAYER:
+    for _, N, K, act, res in layer:
         tot += N * row_bytes(wtype, K) + M * K * 4 + M * N * 4 + N * 4 + (M * N * 4 if res else 0)
     return tot
 
@@ -230,14 +232,14 @@ def _capture(ctx, fn):
     return g
 
 
-def measure(ctx, M, wtype, steps, warmup, rotate_gb, use_graphs=True, path="packed"):
-    host = host_layer(M, wtype)
+def measure(ctx, M, wtype, steps, warmup, rotate_gb, use_graphs=True, path="packed", layer=LAYER):
+    host = host_layer(M, wtype, layer=layer)
     set_bytes = sum(h["wq"].nbytes + h["x"].nbytes + h["bias"].nbytes + M * len(h["bias"]) * 4 * 2
                     + (h["resid"].nbytes if h["resid"] is not None else 0) + h["x"].nbytes // 2
                     for h in host)
     nsets = max(2, int(np.ceil(rotate_gb * 1e9 / set_bytes)))
     log(f"[bench] M={M} wtype={wtype}: {nsets} buffer sets x {set_bytes/1e6:.1f} MB")
-    sets = [LayerSet(ctx, host, M, wtype, path) for _ in range(nsets)]
+    sets = [LayerSet(ctx, host, M, wtype, path, layer) for _ in range(nsets)]
     for s in sets:                      # first run outside any graph
         s.step()
     ctx.sync()
@@ -434,8 +436,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--rotate-gb", type=float, default=3.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-graphs", action="store_true",
-                    help="enqueue kernels one by one instead of replaying a captured HIP graph")
+    ap.add_argument("--graphs", action="store_true",
+                    help="replay a captured HIP graph per step instead of enqueuing the kernels one by one")
     ap.add_argument("--path", choices=["packed", "h16", "raw"], default="h16",
                     help="packed: int8-dot path on the device-native weight layout; h16: "
                          "dequantize-fused fp16 path; raw: int8-dot on GGUF blocks as stored")
@@ -466,7 +468,7 @@ def main():
         return
     M, wtype = 1025, ema.WTYPE_Q8_0
     ms_step, ms_gemms, host = measure(ctx, M, wtype, a.steps, a.warmup, a.rotate_gb,
-                                      use_graphs=not a.no_graphs, path=a.path)
+                                      use_graphs=a.graphs, path=a.path)
     ops = layer_ops(M)
     value = ops / (ms_step * 1e-3) / 1e12
     gb = gemm_alg_bytes(M, wtype, a.path)
@@ -479,14 +481,25 @@ def main():
                                                 / (ms_step * 1e-3), 4)}
     # the other production path on the same workload
     other = "packed" if a.path == "h16" else "h16"
-    so, go, _ = measure(ctx, M, wtype, a.steps, a.warmup, a.rotate_gb, use_graphs=not a.no_graphs, path=other)
+    so, go, _ = measure(ctx, M, wtype, a.steps, a.warmup, a.rotate_gb, use_graphs=a.graphs, path=other)
     extra[f"cfg2_{PATH_NAME[other]}"] = {
         "ms_per_step": round(so, 5), "tops": round(ops / (so * 1e-3) / 1e12, 2),
         "gemm_tops": round(ops / (go * 1e-3) / 1e12, 2), "kernel": KERNEL[other]}
+    # the single Q8_0 FC GEMM at M=257 (weight-streaming shape), both paths
+    extra["cfg1_m257"] = {}
+    ab1 = step_alg_bytes(257, wtype, CFG1)
+    for pth in (a.path, other):
+        s1, _, _ = measure(ctx, 257, wtype, a.steps, a.warmup, a.rotate_gb, use_graphs=a.graphs,
+                           path=pth, layer=CFG1)
+        extra["cfg1_m257"][PATH_NAME[pth]] = {
+            "us": round(s1 * 1e3, 2), "tops": round(layer_ops(257, CFG1) / (s1 * 1e-3) / 1e12, 2),
+            "alg_gbs": round(ab1 / (s1 * 1e-3) / 1e9, 1),
+            "frac_of_hbm_roofline": round(ab1 / (HBM_PEAK_GBS * 1e9) / (s1 * 1e-3), 4)}
+    extra["cfg1_m257"]["alg_bytes"] = ab1
     if a.extra:
         for (mm, wt) in ((4097, ema.WTYPE_Q8_0), (1025, ema.WTYPE_Q4_K), (4097, ema.WTYPE_Q4_K)):
             s, g, _ = measure(ctx, mm, wt, max(10, a.steps // 2), a.warmup, a.rotate_gb,
-                              use_graphs=not a.no_graphs, path=a.path)
+                              use_graphs=a.graphs, path=a.path)
             key = f"{'q8_0' if wt == ema.WTYPE_Q8_0 else 'q4_k'}_m{mm}"
             extra[key] = {"ms_per_step": round(s, 5), "tops": round(layer_ops(mm) / (s * 1e-3) / 1e12, 2),
                           "gemm_tops": round(layer_ops(mm) / (g * 1e-3) / 1e12, 2),
@@ -543,7 +556,7 @@ def main():
                                "M=1025, fp32 activations and outputs, " + WORKLOAD_PATH[a.path],
                    "path": PATH_NAME[a.path],
                    "M": M, "weights": "Q8_0", "rotate_gb": a.rotate_gb,
-                   "launch": "stream" if a.no_graphs else "hip_graph_per_step"},
+                   "launch": "hip_graph_per_step" if a.graphs else "stream"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": KERNEL[a.path], "bytes_per_step": gb},

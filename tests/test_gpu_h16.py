@@ -113,6 +113,33 @@ def test_gemm_h16_vs_float64(ctx, M, N, K, act, res):
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
 
 
+def test_gemm_h16_split_k_sequence(ctx):
+    """Split-K launches of different shapes back to back (4 splits, 2 splits, 4 again) share
+    the context's workspace: the repeated shape gives the same bits, and each result meets the
+    float64 bar."""
+    rng = np.random.default_rng(11)
+    shapes = [(257, 768, 3072, 1), (1025, 768, 3072, 0), (257, 768, 3072, 1)]
+    bufs, outs = {}, []
+    for M, N, K, act in shapes:
+        print(f"split-K sequence M={M} N={N} K={K} act={act}", flush=True)
+        if (M, N, K) not in bufs:
+            w16 = (rng.standard_normal((N, K)) * 0.02).astype(np.float16)
+            x16 = rng.standard_normal((M, K)).astype(np.float16)
+            bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+            bufs[(M, N, K)] = (w16, x16, bias, ctx.upload(w16), ctx.upload(x16), ctx.upload(bias),
+                               ctx.alloc(M * N * 4))
+        w16, x16, bias, dW, dX, dB, dY = bufs[(M, N, K)]
+        ctx.gemm_h16(dW, N, K, dX, M, dB, act, None, dY)
+        y = ctx.download(dY, (M, N), np.float32)
+        ref = _act64(x16.astype(np.float64) @ w16.astype(np.float64).T + bias, act)
+        assert _rel(y, ref) <= 1e-5
+        outs.append(y)
+    for v in bufs.values():
+        for t in v[3:]:
+            ctx.free(t)
+    assert np.array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32))
+
+
 @pytest.mark.parametrize("wtype", [ema.WTYPE_Q8_0, ema.WTYPE_Q4_K])
 @pytest.mark.parametrize("M,N,K,act,res", [(257, 768, 768, 0, True), (1025, 3072, 768, 1, False),
                                            (1025, 768, 3072, 0, True), (64, 2304, 768, 0, False)])
