@@ -442,6 +442,9 @@ def main():
                     help="packed: int8-dot path on the device-native weight layout; h16: "
                          "dequantize-fused fp16 path; raw: int8-dot on GGUF blocks as stored")
     ap.add_argument("--no-fwd", action="store_true", help="skip the transformer forward (cfg4)")
+    ap.add_argument("--only-main", action="store_true",
+                    help="measure only the cfg2 step of --path (no other path, no cfg1, no forward, "
+                         "no CPU baseline): the run a kernel profile wraps")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run 10 plain device copies of BYTES (k_copy4d), to calibrate the "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters, and exit")
@@ -479,23 +482,26 @@ def main():
              "step_hbm_roofline_us": round(step_alg_bytes(M, wtype) / (HBM_PEAK_GBS * 1e9) * 1e6, 2),
              "step_frac_of_hbm_roofline": round(step_alg_bytes(M, wtype) / (HBM_PEAK_GBS * 1e9)
                                                 / (ms_step * 1e-3), 4)}
-    # the other production path on the same workload
     other = "packed" if a.path == "h16" else "h16"
-    so, go, _ = measure(ctx, M, wtype, a.steps, a.warmup, a.rotate_gb, use_graphs=a.graphs, path=other)
-    extra[f"cfg2_{PATH_NAME[other]}"] = {
-        "ms_per_step": round(so, 5), "tops": round(ops / (so * 1e-3) / 1e12, 2),
-        "gemm_tops": round(ops / (go * 1e-3) / 1e12, 2), "kernel": KERNEL[other]}
-    # the single Q8_0 FC GEMM at M=257 (weight-streaming shape), both paths
-    extra["cfg1_m257"] = {}
-    ab1 = step_alg_bytes(257, wtype, CFG1)
-    for pth in (a.path, other):
-        s1, _, _ = measure(ctx, 257, wtype, a.steps, a.warmup, a.rotate_gb, use_graphs=a.graphs,
-                           path=pth, layer=CFG1)
-        extra["cfg1_m257"][PATH_NAME[pth]] = {
-            "us": round(s1 * 1e3, 2), "tops": round(layer_ops(257, CFG1) / (s1 * 1e-3) / 1e12, 2),
-            "alg_gbs": round(ab1 / (s1 * 1e-3) / 1e9, 1),
-            "frac_of_hbm_roofline": round(ab1 / (HBM_PEAK_GBS * 1e9) / (s1 * 1e-3), 4)}
-    extra["cfg1_m257"]["alg_bytes"] = ab1
+    if a.only_main:
+        a.no_fwd, a.no_cpu, a.extra = True, True, False
+    # the other production path on the same workload
+    if not a.only_main:
+        so, go, _ = measure(ctx, M, wtype, a.steps, a.warmup, a.rotate_gb, use_graphs=a.graphs, path=other)
+        extra[f"cfg2_{PATH_NAME[other]}"] = {
+            "ms_per_step": round(so, 5), "tops": round(ops / (so * 1e-3) / 1e12, 2),
+            "gemm_tops": round(ops / (go * 1e-3) / 1e12, 2), "kernel": KERNEL[other]}
+        # the single Q8_0 FC GEMM at M=257 (weight-streaming shape), both paths
+        extra["cfg1_m257"] = {}
+        ab1 = step_alg_bytes(257, wtype, CFG1)
+        for pth in (a.path, other):
+            s1, _, _ = measure(ctx, 257, wtype, a.steps, a.warmup, a.rotate_gb, use_graphs=a.graphs,
+                               path=pth, layer=CFG1)
+            extra["cfg1_m257"][PATH_NAME[pth]] = {
+                "us": round(s1 * 1e3, 2), "tops": round(layer_ops(257, CFG1) / (s1 * 1e-3) / 1e12, 2),
+                "alg_gbs": round(ab1 / (s1 * 1e-3) / 1e9, 1),
+                "frac_of_hbm_roofline": round(ab1 / (HBM_PEAK_GBS * 1e9) / (s1 * 1e-3), 4)}
+        extra["cfg1_m257"]["alg_bytes"] = ab1
     if a.extra:
         for (mm, wt) in ((4097, ema.WTYPE_Q8_0), (1025, ema.WTYPE_Q4_K), (4097, ema.WTYPE_Q4_K)):
             s, g, _ = measure(ctx, mm, wt, max(10, a.steps // 2), a.warmup, a.rotate_gb,

@@ -66,11 +66,14 @@ __device__ __forceinline__ float act_h(float v) {
     return v;
 }
 
-__device__ __forceinline__ void tile_origin(int lt, int tiles_m, int tiles_n, int bm, int bn, int& m0, int& n0) {
-    const int panel = lt / (8 * tiles_n);
-    const int pm = min(8, tiles_m - panel * 8);
-    const int rem = lt - panel * 8 * tiles_n;
-    m0 = (panel * 8 + rem % pm) * bm;
+// Logical tile lt -> origin: panels of PH activation-row tiles spanning all weight-row tiles,
+// activation rows fastest inside a panel.
+__device__ __forceinline__ void tile_origin(int lt, int tiles_m, int tiles_n, int bm, int bn, int ph,
+                                            int& m0, int& n0) {
+    const int panel = lt / (ph * tiles_n);
+    const int pm = min(ph, tiles_m - panel * ph);
+    const int rem = lt - panel * ph * tiles_n;
+    m0 = (panel * ph + rem % pm) * bm;
     n0 = (rem / pm) * bn;
 }
 
@@ -168,7 +171,7 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
     const int lfull = xcd_remap(blockIdx.x, tiles_m * tiles_n * splits);
     const int lt = lfull / splits, ks = lfull - lt * splits;
     int m0, n0;
-    tile_origin(lt, tiles_m, tiles_n, BM, BN, m0, n0);
+    tile_origin(lt, tiles_m, tiles_n, BM, BN, g.ph, m0, n0);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wn = wave & 1, wm = wave >> 1;
@@ -357,7 +360,7 @@ __global__ __launch_bounds__(256) void k_gemm_h16_reduce(GemmH16Args g) {
     const int q = (int)(idx4 - (size_t)lt * Q);
     const int r = q / (BN / 4), c = 4 * (q % (BN / 4));
     int m0, n0;
-    tile_origin(lt, tiles_m, tiles_n, BM, BN, m0, n0);
+    tile_origin(lt, tiles_m, tiles_n, BM, BN, g.ph, m0, n0);
     const int m = m0 + r, n = n0 + c;
     if (m >= M || n >= N) return;
     const f32x4* part = (const f32x4*)(g.ws + (size_t)lt * splits * BM * BN) + q;
@@ -400,6 +403,11 @@ H16Plan gemm_h16_plan(int M, int N, int K, bool xf32) {
     // >= 12 stages (K >= 768)
     while (tiles * p.splits * 2 <= 384 && S / (p.splits * 2) >= 12) p.splits *= 2;
     p.ws_bytes = p.splits > 1 ? (size_t)tiles * p.splits * p.bm * p.bn * 4 : 0;
+    // tile order: with few activation-row tiles (M ~ 1000) consecutive tiles walk the weight
+    // rows of one activation tile (its fp32 rows are the larger operand); with many, panels of
+    // 8 activation tiles keep both operands of an XCD's tiles in its L2 (measured)
+    const int tm = (M + p.bm - 1) / p.bm;
+    p.ph = tm <= 32 ? 1 : 8;
     return p;
 }
 
@@ -446,7 +454,9 @@ static hipError_t launch_h16_t(const GemmH16Args& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a, hipStream_t s) {
+hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a0, hipStream_t s) {
+    GemmH16Args a = a0;
+    a.ph = p.ph;
     const bool xf = a.xf != nullptr;
     if (p.ns != 2) return hipErrorInvalidValue;
     if (p.bn == 256 && p.bm == 256 && p.wmr == 4 && !xf) return launch_h16_t<256, false, 2, 4, 256>(a, s);

@@ -140,10 +140,12 @@ struct GemmH16Args {
     _Float16* y16;         // [M][N] fp16 output instead of y when set
     float* ws;             // split-K partial tiles (H16Plan::ws_bytes)
     int M, N, K, splits, act;
+    int ph;                // tile order: panels of ph activation-row tiles (set from the plan)
 };
 struct H16Plan {
     int bm, bn, wmr;       // activation / weight tile rows, waves along the activation rows
     int splits, ns;        // K splits, K-stage ring depth
+    int ph;                // tile order: panel height in activation-row tiles
     size_t ws_bytes;
 };
 H16Plan gemm_h16_plan(int M, int N, int K, bool xf32);
