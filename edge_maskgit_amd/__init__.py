@@ -37,7 +37,7 @@ MGH_SYMBOLS = [
     "mgh_layernorm_affine", "mgh_flash_attn_f16kv", "mgh_gemm_f32", "mgh_get_rows", "mgh_add",
     "mgh_copy_strided", "mgh_decode_state_bytes", "mgh_decode_work_bytes", "mgh_decode_init",
     "mgh_decode_step", "mgh_packed_weight_bytes_f16", "mgh_pack_weights_f16", "mgh_f32_to_f16",
-    "mgh_gemm_h16", "mgh_gemm_h16_f32in", "mgh_gemm_h16_y16", "mgh_flash_attn_f16kv_o16",
+    "mgh_gemm_h16", "mgh_gemm_h16_f32in", "mgh_gemm_h16_y16", "mgh_flash_attn_f16kv_o16", "mgh_flash_attn_f16in",
 ]
 
 _lib = None
@@ -103,6 +103,7 @@ def lib():
         L.mgh_gemm_h16_f32in.argtypes = [P, P, I, I, P, I, P, I, P, P]
         L.mgh_gemm_h16_y16.argtypes = [P, P, I, I, P, I, P, I, P, P]
         L.mgh_flash_attn_f16kv_o16.argtypes = [P, P, P, P, P, I, I, I, I, ctypes.c_float, P, P]
+        L.mgh_flash_attn_f16in.argtypes = [P, P, P, P, P, I, I, I, I, ctypes.c_float, P, P, P]
         L.mgh_decode_state_bytes.argtypes = [I]
         L.mgh_decode_state_bytes.restype = SZ
         L.mgh_decode_work_bytes.argtypes = [I, I]
@@ -313,6 +314,15 @@ class Context:
         st = (ctypes.c_int64 * 4)(*strides)
         ost = None if o_strides is None else (ctypes.c_int64 * 4)(*o_strides)
         self._check(lib().mgh_flash_attn_f16kv_o16(self.h, P(q), P(k), P(v), st, D, S, H, B, scale, P(o16), ost))
+
+    def flash_attn_f16in(self, q16, k16, v16, strides, D, S, H, B, scale, o=None, o16=None, o_strides=None):
+        """Attention on fp16 q/k/v (element strides as for flash_attn_f16kv); exactly one of
+        o (fp32) and o16 (fp16) is given."""
+        P = self._ptr
+        st = (ctypes.c_int64 * 4)(*strides)
+        ost = None if o_strides is None else (ctypes.c_int64 * 4)(*o_strides)
+        self._check(lib().mgh_flash_attn_f16in(self.h, P(q16), P(k16), P(v16), st, D, S, H, B, scale,
+                                               P(o), P(o16), ost))
 
     def gemm_h16_f32in(self, wp16, N, K, x, M, bias, act, resid, y):
         P = self._ptr

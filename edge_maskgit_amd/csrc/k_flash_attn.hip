@@ -174,7 +174,16 @@ __global__ __launch_bounds__(256) void k_flash_attn_f16kv(FaArgs a) {
 template <int KT>
 constexpr int kHeadWaves = KT <= 17 ? (KT + 1) / 2 : 8;
 
-template <int DC, int KT>
+// 4 consecutive elements of q/k/v as fp16: rounded from fp32 (RNE) or, with I16, loaded as
+// stored (the producer rounded them the same way)
+template <bool I16>
+__device__ __forceinline__ f16x4 load_h4(const float* p32, const _Float16* p16, int64_t e) {
+    if (I16) return *(const f16x4*)(p16 + e);
+    const f32x4 v = *(const f32x4*)(p32 + e);
+    return f16x4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+}
+
+template <int DC, int KT, bool I16>
 __global__ __launch_bounds__(64 * kHeadWaves<KT>) void k_attn_head(FaArgs a) {
     constexpr int D = 16 * DC;
     constexpr int KLD = D + 8;         // K row stride (halves)
@@ -191,24 +200,48 @@ __global__ __launch_bounds__(64 * kHeadWaves<KT>) void k_attn_head(FaArgs a) {
 
     // K row-major: one float4 of a key row per task. V transposed: a task loads a 4-key x
     // 4-d block and stores it as four 8-byte rows of V^T.
-    for (int idx = tid; idx < SP * (D / 4); idx += blockDim.x) {
-        const int t = idx / (D / 4), d = 4 * (idx - t * (D / 4));
-        f32x4 kv = {0.f, 0.f, 0.f, 0.f};
-        if (t < S) kv = *(const f32x4*)(a.k + base + (int64_t)t * a.st[1] + d);
-        *(f16x4*)&Ks[t * KLD + d] = f16x4{(_Float16)kv[0], (_Float16)kv[1], (_Float16)kv[2], (_Float16)kv[3]};
-    }
-    for (int idx = tid; idx < (SP / 4) * (D / 4); idx += blockDim.x) {
-        const int kg = idx / (D / 4), d = 4 * (idx - kg * (D / 4));
-        f32x4 vv[4];
+    // The staging is latency-bound (one workgroup per CU at typical shapes): each thread
+    // issues UK (K) or 4 x UV (V) loads before it stores any, so a few round trips fill LDS.
+    constexpr int KTASK = SP * (D / 4), VTASK = (SP / 4) * (D / 4);
+    constexpr int UK = 8, UV = 2;
+    for (int i0 = tid; i0 < KTASK; i0 += UK * blockDim.x) {
+        f16x4 kv[UK];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = 4 * kg + i;
-            vv[i] = t < S ? *(const f32x4*)(a.v + base + (int64_t)t * a.st[1] + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int u = 0; u < UK; u++) {
+            const int idx = i0 + u * blockDim.x;
+            const int t = idx / (D / 4), d = 4 * (idx - t * (D / 4));
+            kv[u] = f16x4{0, 0, 0, 0};
+            if (idx < KTASK && t < S) kv[u] = load_h4<I16>(a.k, a.k16, base + (int64_t)t * a.st[1] + d);
         }
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            *(f16x4*)&Vt[(d + j) * VT + 4 * kg] =
-                f16x4{(_Float16)vv[0][j], (_Float16)vv[1][j], (_Float16)vv[2][j], (_Float16)vv[3][j]};
+        for (int u = 0; u < UK; u++) {
+            const int idx = i0 + u * blockDim.x;
+            const int t = idx / (D / 4), d = 4 * (idx - t * (D / 4));
+            if (idx < KTASK) *(f16x4*)&Ks[t * KLD + d] = kv[u];
+        }
+    }
+    for (int i0 = tid; i0 < VTASK; i0 += UV * blockDim.x) {
+        f16x4 vv[UV][4];
+#pragma unroll
+        for (int u = 0; u < UV; u++) {
+            const int idx = i0 + u * blockDim.x;
+            const int kg = idx / (D / 4), d = 4 * (idx - kg * (D / 4));
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = 4 * kg + i;
+                vv[u][i] = f16x4{0, 0, 0, 0};
+                if (idx < VTASK && t < S) vv[u][i] = load_h4<I16>(a.v, a.v16, base + (int64_t)t * a.st[1] + d);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < UV; u++) {
+            const int idx = i0 + u * blockDim.x;
+            const int kg = idx / (D / 4), d = 4 * (idx - kg * (D / 4));
+            if (idx >= VTASK) continue;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                *(f16x4*)&Vt[(d + j) * VT + 4 * kg] = f16x4{vv[u][0][j], vv[u][1][j], vv[u][2][j], vv[u][3][j]};
+        }
     }
     __syncthreads();
 
@@ -222,12 +255,9 @@ __global__ __launch_bounds__(64 * kHeadWaves<KT>) void k_attn_head(FaArgs a) {
         f16x4 qf[DC];
         {
             const int qi = min(q0 + l16, S - 1);
-            const float* qrow = a.q + base + (int64_t)qi * a.st[1];
+            const int64_t qrow = base + (int64_t)qi * a.st[1];
 #pragma unroll
-            for (int c = 0; c < DC; c++) {
-                const f32x4 v = *(const f32x4*)(qrow + 16 * c + 4 * lg);
-                qf[c] = f16x4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-            }
+            for (int c = 0; c < DC; c++) qf[c] = load_h4<I16>(a.q, a.q16, qrow + 16 * c + 4 * lg);
         }
         // scores: register r of key tile t holds key 16t + 4lg + r of query q0 + l16
         f32x4 sc[KT];
@@ -301,8 +331,12 @@ template <int DC, int KT>
 void launch_head_t(const FaArgs& a, hipStream_t s) {
     const int nqt = (a.S + 15) / 16;
     const int nw = std::min(kHeadWaves<KT>, std::max(1, (nqt + 1) / 2));  // ~2 query tiles per wave
-    hipLaunchKernelGGL((k_attn_head<DC, KT>), dim3((unsigned)a.H, (unsigned)a.B), dim3((unsigned)(64 * nw)),
-                       0, s, a);
+    if (a.q16)
+        hipLaunchKernelGGL((k_attn_head<DC, KT, true>), dim3((unsigned)a.H, (unsigned)a.B),
+                           dim3((unsigned)(64 * nw)), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_attn_head<DC, KT, false>), dim3((unsigned)a.H, (unsigned)a.B),
+                           dim3((unsigned)(64 * nw)), 0, s, a);
 }
 
 template <int DC>
@@ -318,14 +352,16 @@ hipError_t launch_head(const FaArgs& a, hipStream_t s) {
 
 bool head_ok(const FaArgs& a, int D) {
     auto al = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+    const bool ptrs = a.q16 ? al(a.q16) && al(a.k16) && al(a.v16) : al(a.q) && al(a.k) && al(a.v);
     return a.S <= 512 && a.st[0] == 1 && a.st[1] % 4 == 0 && a.st[2] % 4 == 0 && a.st[3] % 4 == 0 &&
-           D % 16 == 0 && al(a.q) && al(a.k) && al(a.v) && a.H <= 65535 && a.B <= 65535;
+           D % 16 == 0 && ptrs && a.H <= 65535 && a.B <= 65535;
 }
 
 }  // namespace
 
 hipError_t launch_flash_attn_f16kv(const FaArgs& a, int D, hipStream_t s) {
     if (a.S <= 0 || a.H <= 0 || a.B <= 0) return hipSuccess;
+    if (a.q16 && !head_ok(a, D)) return hipErrorInvalidValue;   // fp16 inputs: whole-head kernel only
     if (head_ok(a, D)) {
         switch (D) {
             case 16: return launch_head<1>(a, s);

@@ -563,18 +563,29 @@ int mgh_layernorm_affine(mgh_ctx* c, const float* x, const float* g, const float
 
 namespace {
 
-int flash_attn(mgh_ctx* c, const float* q, const float* k, const float* v, const int64_t st[4], int D, int S,
-               int H, int B, float scale, float* o, _Float16* o16, const int64_t ost[4]) {
+int flash_attn(mgh_ctx* c, const void* q, const void* k, const void* v, bool in16, const int64_t st[4], int D,
+               int S, int H, int B, float scale, float* o, _Float16* o16, const int64_t ost[4]) {
     if (!c) return MGH_ERR_ARG;
     if (S < 0 || H < 0 || B < 0) return fail(c, MGH_ERR_ARG, "flash_attn: negative shape");
     if (D != 16 && D != 32 && D != 48 && D != 64)
         return fail(c, MGH_ERR_UNSUPPORTED, "flash_attn: D must be 16, 32, 48 or 64");
     if (S == 0 || H == 0 || B == 0) return MGH_OK;
-    if (!q || !k || !v || (!o && !o16) || !st) return fail(c, MGH_ERR_ARG, "flash_attn: null pointer");
+    if (!q || !k || !v || (!o && !o16) || (o && o16) || !st) return fail(c, MGH_ERR_ARG, "flash_attn: null pointer");
     if (H > 65535 || B > 65535) return fail(c, MGH_ERR_UNSUPPORTED, "flash_attn: H and B must be <= 65535");
+    if (in16) {
+        auto al = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+        if (S > 512 || st[0] != 1 || st[1] % 4 || st[2] % 4 || st[3] % 4 || !al(q) || !al(k) || !al(v))
+            return fail(c, MGH_ERR_UNSUPPORTED, "flash_attn_f16in: needs S <= 512, unit d stride, other strides "
+                                                "multiples of 4 and 16-byte aligned q/k/v");
+    }
     if (int r = set_dev(c)) return r;
     mgh::FaArgs a{};
-    a.q = q; a.k = k; a.v = v; a.o = o; a.o16 = o16;
+    if (in16) {
+        a.q16 = (const _Float16*)q; a.k16 = (const _Float16*)k; a.v16 = (const _Float16*)v;
+    } else {
+        a.q = (const float*)q; a.k = (const float*)k; a.v = (const float*)v;
+    }
+    a.o = o; a.o16 = o16;
     for (int i = 0; i < 4; i++) a.st[i] = st[i];
     if (ost) {
         for (int i = 0; i < 4; i++) a.os[i] = ost[i];
@@ -593,13 +604,19 @@ extern "C" {
 int mgh_flash_attn_f16kv(mgh_ctx* c, const float* q, const float* k, const float* v,
                          const int64_t st[4], int D, int S, int H, int B, float scale, float* o,
                          const int64_t ost[4]) {
-    return flash_attn(c, q, k, v, st, D, S, H, B, scale, o, nullptr, ost);
+    return flash_attn(c, q, k, v, false, st, D, S, H, B, scale, o, nullptr, ost);
 }
 
 int mgh_flash_attn_f16kv_o16(mgh_ctx* c, const float* q, const float* k, const float* v,
                              const int64_t st[4], int D, int S, int H, int B, float scale, void* o16,
                              const int64_t ost[4]) {
-    return flash_attn(c, q, k, v, st, D, S, H, B, scale, nullptr, (_Float16*)o16, ost);
+    return flash_attn(c, q, k, v, false, st, D, S, H, B, scale, nullptr, (_Float16*)o16, ost);
+}
+
+int mgh_flash_attn_f16in(mgh_ctx* c, const void* q16, const void* k16, const void* v16,
+                         const int64_t st[4], int D, int S, int H, int B, float scale, float* o, void* o16,
+                         const int64_t ost[4]) {
+    return flash_attn(c, q16, k16, v16, true, st, D, S, H, B, scale, o, (_Float16*)o16, ost);
 }
 
 int mgh_gemm_f32(mgh_ctx* c, const float* w, int N, int K, const float* x, int M, const float* bias,

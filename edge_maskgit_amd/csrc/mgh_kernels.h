@@ -62,6 +62,9 @@ struct FaArgs {
     const float* q;
     const float* k;
     const float* v;
+    const _Float16* q16;   // fp16 q/k/v instead of q/k/v when set (whole-head kernel only)
+    const _Float16* k16;
+    const _Float16* v16;
     float* o;
     _Float16* o16;         // fp16 output instead of o when set
     int64_t st[4];         // q/k/v element strides for d, s, h, b

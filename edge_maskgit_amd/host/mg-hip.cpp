@@ -352,6 +352,8 @@ const void* HipRuntime::run(Graph& g, bool readback) {
     // through its strides
     std::vector<std::vector<Tensor*>> groups;
     std::unordered_map<const Tensor*, int> grp_of;
+    std::unordered_set<int> grp16;                       // groups stored as fp16
+    std::unordered_set<const Tensor*> h16_store;         // nodes whose device data is fp16
     I.pitch.clear();
     I.owner.clear();
     if (I.algo == MGH_ALGO_DEQ_F16) {
@@ -384,6 +386,32 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                 grp_of[m] = (int)gi;
                 last[lead] = std::max(last[lead], last.count(m) ? last[m] : 0);
             }
+        }
+        // a group whose attentions can all read fp16 q/k/v (the whole-head kernel: S <= 512,
+        // unit d stride, strides and column offsets in multiples of 8 halves) stores its wide
+        // output as fp16; the attention would round q/k/v to fp16 on load (same result)
+        for (size_t gi = 0; gi < groups.size(); gi++) {
+            if (groups[gi].size() < 2) continue;
+            bool ok = true;
+            int64_t Nt = 0, off = 0;
+            for (const Tensor* m : groups[gi]) Nt += m->src[0]->ne[1];
+            for (const Tensor* m : groups[gi]) {
+                ok = ok && off % 8 == 0;
+                off += m->src[0]->ne[1];
+                for (const Tensor* c : cons[m]) {
+                    const int D = (int)c->src[0]->ne[0], S = (int)c->src[0]->ne[1];
+                    ok = ok && S <= 512 && (D == 16 || D == 32 || D == 48 || D == 64);
+                    for (int j = 0; j < 3 && ok; j++) {
+                        int64_t st[4];
+                        Impl::elem_strides(c->src[j], st);
+                        const int64_t rowlen = I.root(c->src[j])->ne[0];
+                        for (int i = 0; i < 4; i++)
+                            if (st[i] >= rowlen && st[i] % rowlen == 0) st[i] = st[i] / rowlen * Nt;
+                        ok = ok && st[0] == 1 && st[1] % 8 == 0 && st[2] % 8 == 0 && st[3] % 8 == 0;
+                    }
+                }
+            }
+            if (ok) grp16.insert((int)gi);
         }
     }
 
@@ -454,20 +482,24 @@ const void* HipRuntime::run(Graph& g, bool readback) {
             const int M = (int)(x->nelements() / K);
             int64_t Nt = 0;
             for (const Tensor* m : grp) Nt += m->src[0]->ne[1];
-            out = I.take((size_t)M * Nt * 4);
             void* wp = I.fused_weight(grp, K, Nt);
             const float* bias = (const float*)I.fused_bias(grp, Nt);
             const auto c = I.codes.find(I.root(x));
-            if (c != I.codes.end())
+            const bool h16 = c != I.codes.end() && grp16.count(grp_of.at(t));
+            out = I.take((size_t)M * Nt * (h16 ? 2 : 4));
+            if (h16)
+                I.check(mgh_gemm_h16_y16(I.ctx, wp, (int)Nt, K, c->second.q, M, bias, t->iparam[0], nullptr, out));
+            else if (c != I.codes.end())
                 I.check(mgh_gemm_h16(I.ctx, wp, (int)Nt, K, c->second.q, M, bias, t->iparam[0], nullptr, (float*)out));
             else
                 I.check(mgh_gemm_h16_f32in(I.ctx, wp, (int)Nt, K, (const float*)I.dev(x), M, bias, t->iparam[0],
                                            nullptr, (float*)out));
             int64_t off = 0;
             for (const Tensor* m : grp) {
-                I.addr[m] = (float*)out + off;
+                I.addr[m] = (char*)out + off * (h16 ? 2 : 4);
                 I.pitch[m] = Nt;
                 I.owner[m] = grp[0];
+                if (h16) h16_store.insert(m);
                 off += m->src[0]->ne[1];
             }
         } else if (t->op == Op::Cont && fa_into.count(t)) {
@@ -576,7 +608,16 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                     ost[0] = 1; ost[1] = (int64_t)D * H; ost[2] = D; ost[3] = (int64_t)D * H * S;
                     po = ost;
                 }
-                if (po && emit16.count(fa_target.at(t))) {
+                const bool in16 = h16_store.count(I.root(q)) && h16_store.count(I.root(t->src[1])) &&
+                                  h16_store.count(I.root(t->src[2]));
+                if (in16) {
+                    const bool o16 = po && emit16.count(fa_target.at(t));
+                    Impl::Codes cd;
+                    if (o16) cd.q = I.take((size_t)D * S * H * B * 2);
+                    I.check(mgh_flash_attn_f16in(I.ctx, I.dev(q), I.dev(t->src[1]), I.dev(t->src[2]), st, D, S, H, B,
+                                                 t->fparam[0], o16 ? nullptr : (float*)out, o16 ? cd.q : nullptr, po));
+                    if (o16) I.codes[fa_target.at(t)] = cd;
+                } else if (po && emit16.count(fa_target.at(t))) {
                     Impl::Codes cd;
                     cd.q = I.take((size_t)D * S * H * B * 2);
                     I.check(mgh_flash_attn_f16kv_o16(I.ctx, (const float*)I.dev(q), (const float*)I.dev(t->src[1]),

@@ -153,6 +153,42 @@ def test_flash_attn_o16_is_rounded_output(ctx, S):
     assert np.array_equal(h.view(np.uint16), o.astype(np.float16).view(np.uint16))
 
 
+@pytest.mark.parametrize("D,S,H,B", [(48, 257, 16, 2), (48, 1, 2, 1), (64, 130, 4, 1), (32, 512, 2, 1)])
+def test_flash_attn_f16in_equals_rounded_inputs(ctx, D, S, H, B):
+    """The fp16-input variant on q/k/v rounded to fp16 gives the same bits as the fp32-input
+    attention (which rounds its inputs to fp16 on load), for both output types, with q/k/v
+    read through the strides of one wide [S*B][3*H*D] buffer (the fused QKV output)."""
+    print(f"flash_attn_f16in D={D} S={S} H={H} B={B}", flush=True)
+    rng = np.random.default_rng(7 * D + S)
+    E = H * D
+    wide = rng.standard_normal((B * S, 3 * E)).astype(np.float16)
+    st = (1, 3 * E, D, 3 * E * S)
+    ost = (1, E, D, E * S)
+    d32 = ctx.upload(wide.astype(np.float32))
+    d16 = ctx.upload(wide)
+    n = D * S * H * B
+    o_ref, o_32, o_16 = ctx.alloc(n * 4), ctx.alloc(n * 4), ctx.alloc(n * 2)
+    ctx.flash_attn_f16kv(d32.ptr, d32.ptr + 4 * E, d32.ptr + 8 * E, st, D, S, H, B, 0.144, o_ref, o_strides=ost)
+    ctx.flash_attn_f16in(d16.ptr, d16.ptr + 2 * E, d16.ptr + 4 * E, st, D, S, H, B, 0.144, o=o_32, o_strides=ost)
+    ctx.flash_attn_f16in(d16.ptr, d16.ptr + 2 * E, d16.ptr + 4 * E, st, D, S, H, B, 0.144, o16=o_16, o_strides=ost)
+    ref = ctx.download(o_ref, (n,), np.float32)
+    a = ctx.download(o_32, (n,), np.float32)
+    h = ctx.download(o_16, (n,), np.float16)
+    for t in (d32, d16, o_ref, o_32, o_16):
+        ctx.free(t)
+    assert np.array_equal(a.view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(h.view(np.uint16), ref.astype(np.float16).view(np.uint16))
+
+
+def test_flash_attn_f16in_rejects_long_sequences(ctx):
+    buf = ctx.alloc(1 << 20)
+    with pytest.raises(ema.MghError):
+        ctx.flash_attn_f16in(buf, buf, buf, (1, 48, 48, 48 * 600), 48, 600, 1, 1, 0.1, o=buf)
+    with pytest.raises(ema.MghError):
+        ctx.flash_attn_f16in(buf, buf, buf, (1, 48, 48, 48 * 4), 48, 4, 1, 1, 0.1, o=buf, o16=buf)
+    ctx.free(buf)
+
+
 def test_flash_attn_large_scores(ctx):
     """Peaked softmax (large logits): the running max rescaling must stay exact."""
     D, S, H, B = 48, 257, 2, 1
