@@ -11,7 +11,8 @@
 //
 // gfx950 mapping (one workgroup = 4 waves = 64 queries of one (b, h); keys in chunks of 64
 // staged once per workgroup in LDS as fp16):
-//  * Scores as S^T = K . Q^T on v_mfma_f32_16x16x16_f16: fp16 products are exact in fp32, so
+//  * Scores as S^T = K . Q^T on v_mfma_f32_16x16x32_f16 (two 16-wide d chunks per
+//    instruction, an odd last chunk paired with zeros): fp16 products are exact in fp32, so
 //    only the summation order differs from the reference. The S^T accumulator layout (lane
 //    = query, registers = 4 consecutive keys) is exactly the A-operand layout of the next
 //    product, so P . V needs no data exchange between lanes.
@@ -31,6 +32,11 @@ namespace mgh {
 namespace {
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f16x8 cat8(f16x4 a, f16x4 b) {
+    return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
 
 constexpr int KT = 64;             // keys per LDS chunk
 constexpr int VLD = KT + 8;        // V^T row stride (halves)
@@ -86,11 +92,18 @@ __global__ __launch_bounds__(256) void k_flash_attn_f16kv(FaArgs a) {
         f32x4 sc[KT / 16];
 #pragma unroll
         for (int t = 0; t < KT / 16; t++) {
+            // pairs of 16-wide d chunks on the 32-deep MFMA (k = 8lg + j: d = 16(c + j/4) + 4lg +
+            // j%4 in both operands); an odd last chunk is paired with zeros (the 16-deep MFMA
+            // takes as long, and a 16-deep MFMA accumulating right after a 32-deep one into
+            // the same registers gave wrong sums)
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            const _Float16* krow = &Ks[(16 * t + l16) * KLD + 4 * lg];
 #pragma unroll
-            for (int c = 0; c < DC; c++) {
-                const f16x4 kf = *(const f16x4*)&Ks[(16 * t + l16) * KLD + 16 * c + 4 * lg];
-                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kf, qf[c], acc, 0, 0, 0);
+            for (int c = 0; c < DC; c += 2) {
+                const f16x4 k1 = c + 1 < DC ? *(const f16x4*)(krow + 16 * c + 16) : f16x4{0, 0, 0, 0};
+                const f16x4 q1 = c + 1 < DC ? qf[c + 1] : f16x4{0, 0, 0, 0};
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(cat8(*(const f16x4*)(krow + 16 * c), k1),
+                                                             cat8(qf[c], q1), acc, 0, 0, 0);
             }
 #pragma unroll
             for (int r = 0; r < 4; r++) {
@@ -166,9 +179,13 @@ __global__ __launch_bounds__(256) void k_flash_attn_f16kv(FaArgs a) {
 // and V (transposed) once in LDS as fp16, then each wave takes 16-query tiles and computes all
 // scores of a tile in registers, a plain (not online) max-subtracted softmax over the row —
 // the order of the reference CPU kernel — and P . V. K/V are read once per head instead of
-// once per query tile, with 16-byte loads (needs unit d stride and 16-byte aligned rows). The
-// exponentials use the hardware exp2 on log2(e)-scaled scores (relative error ~1e-7, far
-// inside the attention tolerance).
+// once per query tile (needs unit d stride and 16-byte aligned rows; q/k/v either fp32,
+// rounded to fp16 on load, or already fp16). The exponentials use the hardware exp2 on
+// log2(e)-scaled scores (relative error ~1e-7, far inside the attention tolerance), with the
+// scale folded into one fma. Both products run on v_mfma_f32_16x16x32_f16 (the 16-deep
+// instruction takes as many cycles on gfx950): scores over pairs of d chunks, P . V over pairs
+// of key tiles (k = 8lg + j maps to key 16(t + j/4) + 4lg + j%4 in both operands, so the score
+// registers are the P operand as they stand).
 // at most NW waves (a workgroup takes min(NW, ~half the query tiles) waves), so the score
 // registers (4 * KT per lane) fit without spilling
 template <int KT>
@@ -183,7 +200,8 @@ __device__ __forceinline__ f16x4 load_h4(const float* p32, const _Float16* p16, 
     return f16x4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
 }
 
-template <int DC, int KT, bool I16>
+// TAIL: S > 16 (KT - 1), so every key tile but the last is full (no masking there)
+template <int DC, int KT, bool I16, bool TAIL>
 __global__ __launch_bounds__(64 * kHeadWaves<KT>) void k_attn_head(FaArgs a) {
     constexpr int D = 16 * DC;
     constexpr int KLD = D + 8;         // K row stride (halves)
@@ -264,51 +282,87 @@ __global__ __launch_bounds__(64 * kHeadWaves<KT>) void k_attn_head(FaArgs a) {
         float mx = -INFINITY;
 #pragma unroll
         for (int t = 0; t < KT; t++) {
+            // pairs of 16-wide d chunks on the 32-deep MFMA (k = 8lg + j: d = 16(c + j/4) + 4lg +
+            // j%4 in both operands); an odd last chunk is paired with zeros (the 16-deep MFMA
+            // takes as long, and a 16-deep MFMA accumulating right after a 32-deep one into
+            // the same registers gave wrong sums)
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            const _Float16* krow = &Ks[(16 * t + l16) * KLD + 4 * lg];
 #pragma unroll
-            for (int c = 0; c < DC; c++) {
-                const f16x4 kf = *(const f16x4*)&Ks[(16 * t + l16) * KLD + 16 * c + 4 * lg];
-                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kf, qf[c], acc, 0, 0, 0);
+            for (int c = 0; c < DC; c += 2) {
+                const f16x4 k1 = c + 1 < DC ? *(const f16x4*)(krow + 16 * c + 16) : f16x4{0, 0, 0, 0};
+                const f16x4 q1 = c + 1 < DC ? qf[c + 1] : f16x4{0, 0, 0, 0};
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(cat8(*(const f16x4*)(krow + 16 * c), k1),
+                                                             cat8(qf[c], q1), acc, 0, 0, 0);
             }
+            // raw scores; keys past S are -inf (with TAIL only the last tile holds such keys)
+            if (TAIL && t < KT - 1) {
+                sc[t] = acc;
+            } else {
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                sc[t][r] = 16 * t + 4 * lg + r < S ? acc[r] * scale2 : -INFINITY;
-                mx = fmaxf(mx, sc[t][r]);
+                for (int r = 0; r < 4; r++) sc[t][r] = 16 * t + 4 * lg + r < S ? acc[r] : -INFINITY;
             }
+            mx = fmaxf(fmaxf(mx, sc[t][0]), sc[t][1]);
+            mx = fmaxf(fmaxf(mx, sc[t][2]), sc[t][3]);
             __builtin_amdgcn_sched_barrier(0);  // keep the K fragment loads per key tile
         }
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // scale2 > 0 (checked at launch), so the max of the scaled scores is the scaled max;
+        // p = exp2(s * scale2 - max) as one fma, and exp2(-inf) = 0 for the masked keys
+        const float mxs = mx * scale2;
         float ps = 0.f;
 #pragma unroll
         for (int t = 0; t < KT; t++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const float p = sc[t][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sc[t][r] - mx);
+                const float p = __builtin_amdgcn_exp2f(fmaf(sc[t][r], scale2, -mxs));
                 sc[t][r] = p;
                 ps += p;
             }
         ps += __shfl_xor(ps, 16);
         ps += __shfl_xor(ps, 32);
-        // O += P . V, P = hi + lo in fp16 (A operand: query l16, keys 16t + 4lg + j)
+        // O += P . V, P = hi + lo in fp16 (A operand: query l16, keys 16t + 4lg + j): hi is P
+        // rounded toward zero, lo the exact remainder rounded toward zero (|P - hi - lo| <=
+        // 2^-20 P)
         f32x4 O[DC];
 #pragma unroll
         for (int c = 0; c < DC; c++) O[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        auto split = [&](int t, f16x4& ph, f16x4& pl) {
+            const auto h01 = __builtin_amdgcn_cvt_pkrtz(sc[t][0], sc[t][1]);
+            const auto h23 = __builtin_amdgcn_cvt_pkrtz(sc[t][2], sc[t][3]);
+            const auto l01 = __builtin_amdgcn_cvt_pkrtz(sc[t][0] - (float)h01[0], sc[t][1] - (float)h01[1]);
+            const auto l23 = __builtin_amdgcn_cvt_pkrtz(sc[t][2] - (float)h23[0], sc[t][3] - (float)h23[1]);
+            ph = __builtin_bit_cast(f16x4, u32x2{__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)});
+            pl = __builtin_bit_cast(f16x4, u32x2{__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)});
+        };
+        // pairs of key tiles on the 32-deep MFMA (k = 8lg + j: key 16(t + j/4) + 4lg + j%4 in
+        // both operands), an odd last tile on the 16-deep one
 #pragma unroll
-        for (int t = 0; t < KT; t++) {
-            f16x4 ph, pl;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                ph[j] = (_Float16)sc[t][j];
-                pl[j] = (_Float16)(sc[t][j] - (float)ph[j]);
-            }
+        for (int t = 0; t + 1 < KT; t += 2) {
+            f16x4 ph0, pl0, ph1, pl1;
+            split(t, ph0, pl0);
+            split(t + 1, ph1, pl1);
+            const f16x8 ph = cat8(ph0, ph1), pl = cat8(pl0, pl1);
 #pragma unroll
             for (int c = 0; c < DC; c++) {
-                const f16x4 vf = *(const f16x4*)&Vt[(16 * c + l16) * VT + 16 * t + 4 * lg];
-                O[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vf, O[c], 0, 0, 0);
-                O[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vf, O[c], 0, 0, 0);
+                const _Float16* vrow = &Vt[(16 * c + l16) * VT + 16 * t + 4 * lg];
+                const f16x8 vf = cat8(*(const f16x4*)vrow, *(const f16x4*)(vrow + 16));
+                O[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vf, O[c], 0, 0, 0);
+                O[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vf, O[c], 0, 0, 0);
             }
-            __builtin_amdgcn_sched_barrier(0);  // keep the V fragment loads per key tile (registers)
+            __builtin_amdgcn_sched_barrier(0);  // keep the V fragment loads per key tile pair (registers)
+        }
+        if (KT % 2) {                          // the odd last tile, paired with zeros
+            f16x4 ph, pl;
+            split(KT - 1, ph, pl);
+            const f16x4 z = {0, 0, 0, 0};
+#pragma unroll
+            for (int c = 0; c < DC; c++) {
+                const f16x8 vf = cat8(*(const f16x4*)&Vt[(16 * c + l16) * VT + 16 * (KT - 1) + 4 * lg], z);
+                O[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cat8(ph, z), vf, O[c], 0, 0, 0);
+                O[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cat8(pl, z), vf, O[c], 0, 0, 0);
+            }
         }
         // O register r: query q0 + 4lg + r, d = 16c + l16; its row sum sits in lane 4lg + r
 #pragma unroll
@@ -331,12 +385,15 @@ template <int DC, int KT>
 void launch_head_t(const FaArgs& a, hipStream_t s) {
     const int nqt = (a.S + 15) / 16;
     const int nw = std::min(kHeadWaves<KT>, std::max(1, (nqt + 1) / 2));  // ~2 query tiles per wave
-    if (a.q16)
-        hipLaunchKernelGGL((k_attn_head<DC, KT, true>), dim3((unsigned)a.H, (unsigned)a.B),
-                           dim3((unsigned)(64 * nw)), 0, s, a);
-    else
-        hipLaunchKernelGGL((k_attn_head<DC, KT, false>), dim3((unsigned)a.H, (unsigned)a.B),
-                           dim3((unsigned)(64 * nw)), 0, s, a);
+    const dim3 grid((unsigned)a.H, (unsigned)a.B), block((unsigned)(64 * nw));
+    const bool tail = a.S > 16 * (KT - 1);
+    if (a.q16) {
+        if (tail) hipLaunchKernelGGL((k_attn_head<DC, KT, true, true>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((k_attn_head<DC, KT, true, false>), grid, block, 0, s, a);
+    } else {
+        if (tail) hipLaunchKernelGGL((k_attn_head<DC, KT, false, true>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((k_attn_head<DC, KT, false, false>), grid, block, 0, s, a);
+    }
 }
 
 template <int DC>
@@ -354,7 +411,7 @@ bool head_ok(const FaArgs& a, int D) {
     auto al = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
     const bool ptrs = a.q16 ? al(a.q16) && al(a.k16) && al(a.v16) : al(a.q) && al(a.k) && al(a.v);
     return a.S <= 512 && a.st[0] == 1 && a.st[1] % 4 == 0 && a.st[2] % 4 == 0 && a.st[3] % 4 == 0 &&
-           D % 16 == 0 && ptrs && a.H <= 65535 && a.B <= 65535;
+           D % 16 == 0 && ptrs && a.H <= 65535 && a.B <= 65535 && a.scale > 0.f;
 }
 
 }  // namespace

@@ -574,9 +574,10 @@ int flash_attn(mgh_ctx* c, const void* q, const void* k, const void* v, bool in1
     if (H > 65535 || B > 65535) return fail(c, MGH_ERR_UNSUPPORTED, "flash_attn: H and B must be <= 65535");
     if (in16) {
         auto al = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
-        if (S > 512 || st[0] != 1 || st[1] % 4 || st[2] % 4 || st[3] % 4 || !al(q) || !al(k) || !al(v))
+        if (S > 512 || st[0] != 1 || st[1] % 4 || st[2] % 4 || st[3] % 4 || !al(q) || !al(k) || !al(v) ||
+            !(scale > 0.f))
             return fail(c, MGH_ERR_UNSUPPORTED, "flash_attn_f16in: needs S <= 512, unit d stride, other strides "
-                                                "multiples of 4 and 16-byte aligned q/k/v");
+                                                "multiples of 4, 16-byte aligned q/k/v and scale > 0");
     }
     if (int r = set_dev(c)) return r;
     mgh::FaArgs a{};

@@ -388,7 +388,7 @@ const void* HipRuntime::run(Graph& g, bool readback) {
             }
         }
         // a group whose attentions can all read fp16 q/k/v (the whole-head kernel: S <= 512,
-        // unit d stride, strides and column offsets in multiples of 8 halves) stores its wide
+        // scale > 0, unit d stride, strides and column offsets in multiples of 8 halves) stores its wide
         // output as fp16; the attention would round q/k/v to fp16 on load (same result)
         for (size_t gi = 0; gi < groups.size(); gi++) {
             if (groups[gi].size() < 2) continue;
@@ -400,7 +400,7 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                 off += m->src[0]->ne[1];
                 for (const Tensor* c : cons[m]) {
                     const int D = (int)c->src[0]->ne[0], S = (int)c->src[0]->ne[1];
-                    ok = ok && S <= 512 && (D == 16 || D == 32 || D == 48 || D == 64);
+                    ok = ok && S <= 512 && (D == 16 || D == 32 || D == 48 || D == 64) && c->fparam[0] > 0.f;
                     for (int j = 0; j < 3 && ok; j++) {
                         int64_t st[4];
                         Impl::elem_strides(c->src[j], st);

@@ -177,8 +177,8 @@ int mgh_flash_attn_f16kv_o16(mgh_ctx* ctx, const float* d_q, const float* d_k, c
 /* the same attention on q/k/v already stored as fp16 (the fused QKV FC's fp16 output; no
  * counterpart in the reference, whose k_flash_attention_h rounds its fp32 q/k/v to fp16 on
  * load, mg-opencl.cpp:859-937 — the result is identical). Exactly one of d_o (fp32) and d_o16
- * (fp16) is non-NULL. Needs S <= 512, strides[0] == 1, the other strides multiples of 4 and
- * 16-byte aligned q/k/v (MGH_ERR_UNSUPPORTED otherwise). */
+ * (fp16) is non-NULL. Needs S <= 512, strides[0] == 1, the other strides multiples of 4,
+ * 16-byte aligned q/k/v and scale > 0 (MGH_ERR_UNSUPPORTED otherwise). */
 int mgh_flash_attn_f16in(mgh_ctx* ctx, const void* d_q16, const void* d_k16, const void* d_v16,
                          const int64_t strides[4], int D, int S, int H, int B, float scale,
                          float* d_o, void* d_o16, const int64_t o_strides[4]);
