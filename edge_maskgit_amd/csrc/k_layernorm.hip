@@ -90,7 +90,7 @@ __global__ __launch_bounds__(256) void k_layernorm_affine(const float* __restric
 #pragma unroll
         for (int e = 0; e < 4; e++)
             o[e] = (float)((double)v[c][e] - mean) * inv * g[e] + b[e];
-        *(f32x4*)(yr + k) = o;
+        __builtin_nontemporal_store(o, (f32x4*)(yr + k));   // streamed: read again layers later
         if (EMIT == 1) {
             // k_quantize_act_q8 on the 32-element block of lanes 8j..8j+7
             float a = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
@@ -118,10 +118,10 @@ __global__ __launch_bounds__(256) void k_layernorm_affine(const float* __restric
             su += __shfl_xor(su, 1);
             su += __shfl_xor(su, 2);
             su += __shfl_xor(su, 4);
-            *(f16x4*)((_Float16*)codes + (size_t)row * D + k) = h;
+            __builtin_nontemporal_store(h, (f16x4*)((_Float16*)codes + (size_t)row * D + k));
             if ((lane & 7) == 0) {
                 const size_t blk = (size_t)row * (D / 32) + (k >> 5);
-                dx[blk] = 1.0f;
+                if (dx) dx[blk] = 1.0f;
                 if (s4) ((float*)s4)[blk] = su;
             }
         }

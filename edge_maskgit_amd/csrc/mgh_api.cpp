@@ -548,8 +548,8 @@ int mgh_layernorm_affine(mgh_ctx* c, const float* x, const float* g, const float
     if (emit < 0 || emit > 2) return fail(c, MGH_ERR_ARG, "layernorm_affine: emit must be 0, 1 or 2");
     if (rows == 0) return MGH_OK;
     if (!x || !g || !b || !y) return fail(c, MGH_ERR_ARG, "layernorm_affine: null pointer");
-    if (emit && (!codes || !dx || (emit == 1 && !s4)))
-        return fail(c, MGH_ERR_ARG, "layernorm_affine: emit needs d_codes, d_dx (and d_s4 for INT8)");
+    if (emit && (!codes || (emit == 1 && (!dx || !s4))))
+        return fail(c, MGH_ERR_ARG, "layernorm_affine: emit needs d_codes (and d_dx, d_s4 for INT8)");
     if (!aligned16(x) || !aligned16(y) || !aligned16(g) || !aligned16(b) || !aligned16(codes) ||
         ((uintptr_t)dx & 3u) || ((uintptr_t)s4 & 3u))
         return fail(c, MGH_ERR_ARG, "layernorm_affine: x/y/gamma/beta/codes must be 16-byte aligned");

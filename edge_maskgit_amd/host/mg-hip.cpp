@@ -580,8 +580,10 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                     emit = I.algo == MGH_ALGO_INT8 ? MGH_EMIT_INT8 : MGH_EMIT_DEQ_F16;
                     const size_t T = (size_t)D / 32;
                     cd.q = I.take((size_t)rows * D * 2);
-                    cd.dx = I.take((size_t)rows * T * 4);
-                    cd.sx = I.take((size_t)rows * T * 4);
+                    if (emit == MGH_EMIT_INT8) {       // the dequant-fused GEMM reads only the fp16 y
+                        cd.dx = I.take((size_t)rows * T * 4);
+                        cd.sx = I.take((size_t)rows * T * 4);
+                    }
                 }
                 I.check(mgh_layernorm_affine(I.ctx, (const float*)I.dev(x), gm, bt, rows, D, t->fparam[0],
                                              (float*)out, emit, cd.q, (float*)cd.dx, cd.sx));

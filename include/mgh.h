@@ -154,8 +154,8 @@ enum { MGH_EMIT_NONE = 0, MGH_EMIT_INT8 = 1, MGH_EMIT_DEQ_F16 = 2 };
  *      aligned x/y/gamma/beta/codes. Statistics in double, as the reference CPU executor.
  *      emit = MGH_EMIT_INT8 also writes the next GEMM's operand for y (as
  *      mgh_quantize_act_q8_codes16): d_codes fp16 codes [rows][D], d_dx fp32 and d_s4 int32
- *      [rows][D/32]; MGH_EMIT_DEQ_F16 writes fp16-rounded y, unit d_dx and fp32 block sums
- *      in d_s4 (nullable). No reference counterpart for the fused operand (the reference
+ *      [rows][D/32]; MGH_EMIT_DEQ_F16 writes fp16-rounded y, and (each nullable) unit d_dx
+ *      and fp32 block sums in d_s4. No reference counterpart for the fused operand (the reference
  *      quantizes in a separate k_quantize_q8 dispatch, mg-opencl.cpp:1381-1389). ---- */
 int mgh_layernorm_affine(mgh_ctx* ctx, const float* d_x, const float* d_gamma, const float* d_beta,
                          int rows, int D, float eps, float* d_y, int emit, void* d_codes,

@@ -93,8 +93,15 @@ def test_layernorm_emit_deq_operand(ctx):
     h = ctx.download(dC, (rows, D), np.float16)
     dx = ctx.download(dD, (rows, D // 32), np.float32)
     ux = ctx.download(dS, (rows, D // 32), np.float32)
-    for t in (dX, dG, dB, dY, dC, dD, dS):
+    # the block scales and sums are optional: the fp16 operand alone, bit-identical
+    dC2, dY2 = ctx.alloc(rows * D * 2), ctx.alloc(x.nbytes)
+    ctx.layernorm_affine(dX, dG, dB, rows, D, 1e-12, dY2, ema.EMIT_DEQ_F16, dC2, None, None)
+    y2 = ctx.download(dY2, x.shape, np.float32)
+    h2 = ctx.download(dC2, (rows, D), np.float16)
+    for t in (dX, dG, dB, dY, dC, dD, dS, dC2, dY2):
         ctx.free(t)
+    assert np.array_equal(h2.view(np.uint16), h.view(np.uint16))
+    assert np.array_equal(y2.view(np.uint32), y.view(np.uint32))
     assert np.array_equal(h, y.astype(np.float16))
     assert np.all(dx == 1.0)
     blk = h.astype(np.float64).reshape(rows, D // 32, 32).sum(-1)
