@@ -314,8 +314,18 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
     const int c = 4 * (tid % TR);               // this thread's 4 columns
     const int n = n0 + c;
     float* part = PART ? g.ws + ((size_t)lt * splits + ks) * (size_t)BM * BN : nullptr;
+    constexpr int NP = HR / (NTH / TR);         // output rows per thread and pass
 #pragma unroll
     for (int h = 0; h < WMR * HPW; h++) {
+        // the pass's residual loads go out before the transpose, all at once (one HBM
+        // round trip per pass, overlapped with the LDS work)
+        f32x4 rv[NP];
+#pragma unroll
+        for (int p = 0; p < NP; p++) {
+            const int m = m0 + HR * h + (NTH / TR) * p + tid / TR;
+            rv[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (!PART && g.resid && m < M && n < N) rv[p] = *(const f32x4*)(g.resid + (size_t)m * N + n);
+        }
         __syncthreads();                        // ring / previous rows no longer read
         if (wm == h / HPW) {
 #pragma unroll
@@ -326,7 +336,7 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
         }
         __syncthreads();
 #pragma unroll
-        for (int p = 0; p < HR / (NTH / TR); p++) {
+        for (int p = 0; p < NP; p++) {
             const int r = (NTH / TR) * p + tid / TR;
             const f32x4 v = *(const f32x4*)&T[r * P + c];
             if (PART) {
@@ -337,7 +347,7 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
             if (m >= M || n >= N) continue;
             f32x4 o = v;
             const size_t idx = (size_t)m * N + n;
-            if (g.resid) o += *(const f32x4*)(g.resid + idx);
+            if (g.resid) o += rv[p];
             if (g.y16)
                 __builtin_nontemporal_store(f16x4{(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]},
                                             (f16x4*)(g.y16 + idx));

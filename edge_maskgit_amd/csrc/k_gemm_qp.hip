@@ -387,6 +387,17 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_qp(GemmArgs g) {
     float* part = splits > 1 ? g.ws + ((size_t)lt * splits + ks) * (size_t)BM * BN : nullptr;
 #pragma unroll
     for (int h = 0; h < 2; h++) {
+        // with 64-row tiles (the shapes that carry a residual) the half's residual loads go out
+        // before the transpose, all at once (one HBM round trip per half, overlapped with the
+        // LDS work); 128-row tiles load them in the store loop (no registers to spare)
+        constexpr bool PRE = BM == 64;
+        f32x4 rv[PRE ? HR / 8 : 1];
+#pragma unroll
+        for (int p = 0; p < (PRE ? HR / 8 : 0); p++) {
+            const int m = m0 + HR * h + 8 * p + (tid >> 5);
+            rv[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (splits == 1 && g.resid && m < M && n < N) rv[p] = *(const f32x4*)(g.resid + (size_t)m * N + n);
+        }
         __syncthreads();                        // ring / previous half no longer read
         if (wm == h) {
 #pragma unroll
@@ -410,7 +421,7 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_qp(GemmArgs g) {
 #pragma unroll
             for (int e = 0; e < 4; e++) o[e] = act_x<ACT>(o[e]);
             const size_t idx = (size_t)m * N + n;
-            if (g.resid) o += *(const f32x4*)(g.resid + idx);
+            if (g.resid) o += PRE ? rv[PRE ? p : 0] : *(const f32x4*)(g.resid + idx);
             __builtin_nontemporal_store(o, (f32x4*)(g.y + idx));
         }
     }
