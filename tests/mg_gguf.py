@@ -76,9 +76,9 @@ def encode(tensors: dict, quant: str) -> list:
     return out
 
 
-def write_model(path: str, n_layer: int = 2, quant: str = "f32", seed: int = 0) -> dict:
+def write_model(path: str, n_layer: int = 2, quant: str = "f32", seed: int = 0, n_pos: int = 257) -> dict:
     """Write a synthetic model; returns the float tensors (pre-quantization)."""
-    meta, t = synthetic_model(n_layer, quant, seed)
+    meta, t = synthetic_model(n_layer, quant, seed, n_pos=n_pos)
     write_gguf(path, meta, encode(t, quant))
     return t
 

@@ -82,6 +82,23 @@ def test_forward_deq_f16_vs_dequant_f32(models):
     assert err <= 1e-3
 
 
+def test_forward_deq_f16_long_sequence(tmp_path):
+    """S = 600 > 512: the attention takes the chunked online-softmax kernel, so the runtime
+    keeps the fused QKV output in fp32 (the fp16 q/k/v form needs the whole-head kernel); the
+    forward still meets the dequantize-then-F32 bar."""
+    path = str(tmp_path / "m_long.gguf")
+    t = mg_gguf.write_model(path, n_layer=1, quant="q8_0", seed=4, n_pos=601)
+    rng = np.random.default_rng(14)
+    tok = mg_gguf.tokens(rng, 600, 1)
+    print("forward q8_0 dequant-fp16 S=600 B=1", flush=True)
+    with rt.TransformerRuntime(path, algo=2) as m:
+        got = m.forward(tok)
+    want = ofwd.transformer_forward(t, 1, 16, tok, quant="q8_0", algo="deq", f16kv=True)
+    err = _rel(got, want)
+    print(f"  rel err {err:.2e}")
+    assert err <= 1e-3
+
+
 def test_forward_f32(models):
     path, t = models["f32"]
     rng = np.random.default_rng(12)
