@@ -409,9 +409,11 @@ H16Plan gemm_h16_plan(int M, int N, int K, bool xf32) {
     const int tiles = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
     const int S = K / 64;
     p.splits = 1;
-    // split K while there are fewer workgroups than about 1.5 per CU and each split keeps
-    // >= 12 stages (K >= 768)
-    while (tiles * p.splits * 2 <= 384 && S / (p.splits * 2) >= 12) p.splits *= 2;
+    // split K while there are at most two workgroups per CU and each split keeps >= 12
+    // stages (>= 6 with at most half a tile per CU); measured at M = 1025: the down-proj (102
+    // tiles, 48 stages) fastest at 4 splits, the out-proj (102 tiles, 12 stages) at 2
+    const int min_stages = tiles <= 128 ? 6 : 12;
+    while (tiles * p.splits * 2 <= 512 && S / (p.splits * 2) >= min_stages) p.splits *= 2;
     p.ws_bytes = p.splits > 1 ? (size_t)tiles * p.splits * p.bm * p.bn * 4 : 0;
     // tile order: with few activation-row tiles (M ~ 1000) consecutive tiles walk the weight
     // rows of one activation tile (its fp32 rows are the larger operand); with many, panels of
