@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X Q8_0 / Q4_K FC hot path (one JSON line on stdout).
 
-Workload (the metric's configuration): one MaskGIT transformer
+Workload (the headline configuration, cfg2): one MaskGIT transformer
 layer's four Q8_0 FC GEMMs at M = 1025 tokens (32x32 grid + class token), fp32 activations:
     QKV   768 -> 2304  (+bias)            (q/k/v stacked: Q8_0 blocks are row-local)
     out   768 -> 768   (+bias +residual)
@@ -278,7 +278,7 @@ def measure(ctx, M, wtype, steps, warmup, rotate_gb, use_graphs=True, path="pack
 
 
 def write_synthetic_model(path, n_layer, wtype, seed=0):
-    """Random-init MaskGIT transformer GGUF (BASELINE cfg4/cfg5 recipe): FC weights ~N(0,0.02)
+    """Random-init MaskGIT transformer GGUF (the cfg4/cfg5 recipe): FC weights ~N(0,0.02)
     in Q8_0 / Q4_K blocks (bench-local encoders), embeddings ~N(0,0.02), biases ~N(0,0.01),
     LN gamma ~1+N(0,0.02), beta ~N(0,0.01); hidden 768, 16 heads, MLP 3072, vocab 2025."""
     from edge_maskgit_amd.gguf import GGML_F32, GGML_Q4_K, GGML_Q8_0, write_gguf

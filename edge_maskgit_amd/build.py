@@ -22,7 +22,9 @@ OBJ = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "lib")
 
 ARCH = "gfx950"
-# Packed fp32 VALU ops are disabled for all device code; see DESIGN.md ("build flags").
+# Packed fp32 VALU ops (v_pk_*_f32) are disabled for all device code: forms of them have given
+# silently wrong results on this hardware, and the compiler would otherwise emit them from plain
+# fp32 code.
 HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wno-unused-command-line-argument"]

@@ -5,7 +5,7 @@ Writes the layout the reference's converter produces (tools/convert_to_gguf.py:1
 F32 / Q8_0 / Q4_K blocks (quantized by the oracle's encoders, which are pinned to the
 reference encoder's bytes), everything else F32, 32-byte aligned data.
 
-Synthetic weights follow BASELINE's random-init recipe: FC weights ~N(0, 0.02), biases
+Synthetic weights follow the benchmark's random-init recipe: FC weights ~N(0, 0.02), biases
 ~N(0, 0.01), embeddings ~N(0, 0.02), LayerNorm gamma ~ 1 + N(0, 0.02), beta ~N(0, 0.01).
 """
 from __future__ import annotations

@@ -1,6 +1,6 @@
 """GPU parity: activation quantizer, MFMA block dots and quantized FC GEMMs vs the oracle.
 
-Bars:
+Bars (the path's acceptance bars):
   * qx / dx / sx of the quantizer: bit-exact.
   * int32 block dot products of the production GEMM's MFMA path: bit-exact.
   * fp32 GEMM outputs: max|y - y_oracle| <= 1e-3 * max|y_oracle| against the int8-dot oracle
@@ -143,7 +143,7 @@ def test_gemm_int8_deviation_from_dequant_f32(ctx, wtype):
                                          (ema.WTYPE_Q4_K, 4097, 2304, 768),
                                          (ema.WTYPE_Q4_K, 4112, 768, 3072)])
 def test_gemm_full_size_row_sample(ctx, wtype, M, N, K):
-    """BASELINE-size GEMMs: rows are independent, so check a random row sample of the full
+    """Full-size GEMMs (M = 4097): rows are independent, so check a random row sample of the full
     GPU result against the oracle evaluated on those rows only."""
     print(f"gemm_full wtype={wtype} M={M} N={N} K={K}", flush=True)
     rng = np.random.default_rng(M + N)

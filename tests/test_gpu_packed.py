@@ -1,6 +1,6 @@
 """GPU parity of the packed-weight production path: mgh_pack_weights + mgh_gemm_q_packed.
 
-Bars:
+Bars (the path's acceptance bars):
   * packed weights: codes * scale - min reproduces the oracle's dequantization bit-exactly
     (the fp32 products d*sc_j, dmin*m_j are formed once at pack time, as the reference forms
     them per use, mg-opencl.cpp:546-547);
@@ -218,7 +218,7 @@ def test_packed_f32in_int8_vs_oracle(ctx, wtype):
 
 @pytest.mark.parametrize("wtype", [ema.WTYPE_Q8_0, ema.WTYPE_Q4_K])
 def test_packed_full_size_rows(ctx, wtype):
-    """M=4097 (BASELINE cfg 3 size): check a sample of rows against the oracle."""
+    """M=4097 (cfg3 size): check a sample of rows against the oracle."""
     M, N, K = 4097, 768, 3072
     print(f"packed full-size wtype={wtype} M={M} N={N} K={K}", flush=True)
     rng = np.random.default_rng(4097 + wtype)
