@@ -442,6 +442,10 @@ def main():
                     help="packed: int8-dot path on the device-native weight layout; h16: "
                          "dequantize-fused fp16 path; raw: int8-dot on GGUF blocks as stored")
     ap.add_argument("--no-fwd", action="store_true", help="skip the transformer forward (cfg4)")
+    ap.add_argument("--only-config", choices=["cfg1", "m4097"], default=None,
+                    help="measure only this workload of --path (cfg1: one Q8_0 FC at M=257; m4097: "
+                         "the four Q8_0 FCs at M=4097) and print its timing: the run a kernel "
+                         "profile of that workload wraps")
     ap.add_argument("--only-main", action="store_true",
                     help="measure only the cfg2 step of --path (no other path, no cfg1, no forward, "
                          "no CPU baseline): the run a kernel profile wraps")
@@ -467,6 +471,16 @@ def main():
             ctx.copy_strided(src, (n, 1, 1, 1), (1, n, n, n), dst)
         ctx.sync()
         print(json.dumps({"copy_probe_bytes": n * 4, "launches": 10}), flush=True)
+        ctx.close()
+        return
+    if a.only_config:
+        M1, lay = (257, CFG1) if a.only_config == "cfg1" else (4097, LAYER)
+        s1, g1, _ = measure(ctx, M1, ema.WTYPE_Q8_0, a.steps, a.warmup, a.rotate_gb, use_graphs=a.graphs,
+                            path=a.path, layer=lay)
+        ab = step_alg_bytes(M1, ema.WTYPE_Q8_0, lay)
+        print(json.dumps({"config": a.only_config, "path": PATH_NAME[a.path], "M": M1, "ms_per_step": round(s1, 5),
+                          "tops": round(layer_ops(M1, lay) / (s1 * 1e-3) / 1e12, 2),
+                          "alg_bytes_per_step": ab, "alg_gbs": round(ab / (s1 * 1e-3) / 1e9, 1)}), flush=True)
         ctx.close()
         return
     M, wtype = 1025, ema.WTYPE_Q8_0

@@ -415,11 +415,12 @@ H16Plan gemm_h16_plan(int M, int N, int K, bool xf32) {
     const int min_stages = tiles <= 128 ? 6 : 12;
     while (tiles * p.splits * 2 <= 512 && S / (p.splits * 2) >= min_stages) p.splits *= 2;
     p.ws_bytes = p.splits > 1 ? (size_t)tiles * p.splits * p.bm * p.bn * 4 : 0;
-    // tile order: with few activation-row tiles (M ~ 1000) consecutive tiles walk the weight
-    // rows of one activation tile (its fp32 rows are the larger operand); with many, panels of
-    // 8 activation tiles keep both operands of an XCD's tiles in its L2 (measured)
+    // tile order: with few activation-row tiles and activations at least half the weight bytes
+    // (M ~ 1000, fp32 rows) consecutive tiles walk the weight rows of one activation tile; else
+    // panels of 8 activation tiles, which keep an XCD's weight tiles in its L2 (measured: the
+    // former wins 3-9% on the four FCs at M = 1025, the latter 6% on one FC at M = 257)
     const int tm = (M + p.bm - 1) / p.bm;
-    p.ph = tm <= 32 ? 1 : 8;
+    p.ph = tm <= 32 && (int64_t)M * (xf32 ? 4 : 2) * 2 >= (int64_t)N * 2 ? 1 : 8;
     return p;
 }
 
