@@ -417,16 +417,24 @@ def cpu_baseline(host, M, wtype, budget_s=15.0):
         return {"value": round(ops / dt / 1e12, 6), "unit": "TOPS", "cores": 1, "kind": "reference",
                 "sample": f"reference mg-cpu k_mul_mat (F32, dequantized Q8_0 weights), the same four "
                           f"GEMMs on rows 0..{rows_done - 1} of M={M} ({ops/1e9:.2f} Gop in {dt:.1f} s)"}
-    nth = os.cpu_count() or 1
+    return cpu_oracle_int8(host, M, wtype)
+
+
+def cpu_oracle_int8(host, M, wtype, rows=None):
+    """The C oracle's int8-dot path (the reference's int8 kernel semantics, OpenMP over all
+    host threads, scalar C) over the same four GEMMs (all rows unless a sample is given)."""
+    import oracle
+    rows = M if rows is None else rows
+    nth = int(os.environ.get("OMP_NUM_THREADS", 0)) or os.cpu_count() or 1
     ops = 0.0
     t0 = time.perf_counter()
     for (name, N, K, act, res), h in zip(LAYER, host):
-        qx, dx, _ = oracle.quantize_act_q8(h["x"][:256])
+        qx, dx, _ = oracle.quantize_act_q8(h["x"][:rows])
         oracle.gemm_q_i8(wtype, h["wq"], N, K, qx, dx, bias=h["bias"], act=act)
-        ops += 2.0 * 256 * N * K
+        ops += 2.0 * rows * N * K
     dt = time.perf_counter() - t0
     return {"value": round(ops / dt / 1e12, 6), "unit": "TOPS", "cores": nth, "kind": "port",
-            "sample": f"C oracle int8 path (OpenMP), four GEMMs on 256 of {M} rows"}
+            "sample": f"C oracle int8-dot path (OpenMP), four GEMMs on {rows} of {M} rows ({ops/1e9:.2f} Gop in {dt:.1f} s)"}
 
 
 def main():
@@ -554,6 +562,8 @@ def main():
                     "workload": f"64 images x 257 tokens, 8 steps, Q4_K 24 layers, {PATH_NAME[a.path]}; "
                                 "forward + on-device sampling per step, grids read back once"}
     cpu = None if a.no_cpu else cpu_baseline(host, M, wtype)
+    if not a.no_cpu and cpu is not None and cpu.get("kind") == "reference":
+        extra["cpu_oracle_int8_omp"] = cpu_oracle_int8(host, M, wtype)   # a multi-core CPU point
     traffic = None
     tf = os.path.join(ROOT, "profiles", f"traffic_{KERNEL[a.path]}_cfg2_q8_m1025.json")
     if os.path.exists(tf):
