@@ -394,18 +394,15 @@ H16Plan gemm_h16_plan(int M, int N, int K, bool xf32) {
     p.bn = 128;
     p.wmr = 2;
     const int t128 = ((M + 127) / 128) * ((N + 127) / 128);
-    const int t256 = ((M + 255) / 256) * ((N + 255) / 256);
-    // Tile choice, from timings of the four FC shapes at M = 1025, 4112 and 16448 (fp16
-    // operands): 64-row tiles (three workgroups per CU) up to about four 128-row tiles per CU,
-    // 128-row tiles beyond; 256 x 256 tiles (8 waves, half the LDS and L2 operand traffic per
-    // flop of a 128 x 128 tile) for long-K shapes that still give most CUs a tile. With fp32
+    // Tile choice, from timings of the four FC shapes at M = 1025, 4112 and 16448 on fp16
+    // operands with cold weights and activations (buffers rotated over 1 GB): 64-row tiles
+    // (three workgroups per CU) up to about four 128-row tiles per CU, 128-row tiles beyond;
+    // for narrow outputs (N <= 1024, where the activations are the larger operand) 128-row
+    // tiles from about one tile per CU (M = 4112 down-proj: 40.5 against 43.7 us). Larger
+    // tiles (128 x 256 on 4 waves, 256 x 256 on 8) measured slower on every shape. With fp32
     // activations, 64-row tiles: their stage is already as large as a 128-row fp16 stage.
-    p.bm = t128 >= 1024 && !xf32 ? 128 : 64;
-    if (!xf32 && K >= 2048 && t256 >= 192) {
-        p.bm = 256;
-        p.bn = 256;
-        p.wmr = 4;
-    }
+    const bool wide128 = t128 >= 1024 || (N <= 1024 && t128 >= 192);
+    p.bm = wide128 && !xf32 ? 128 : 64;
     const int tiles = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
     const int S = K / 64;
     p.splits = 1;
@@ -472,7 +469,6 @@ hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a0, hipStream_t 
     a.ph = p.ph;
     const bool xf = a.xf != nullptr;
     if (p.ns != 2) return hipErrorInvalidValue;
-    if (p.bn == 256 && p.bm == 256 && p.wmr == 4 && !xf) return launch_h16_t<256, false, 2, 4, 256>(a, s);
     if (p.bn != 128 || p.wmr != 2) return hipErrorInvalidValue;
     if (p.bm == 128) return xf ? launch_h16_t<128, true, 2, 2, 128>(a, s) : launch_h16_t<128, false, 2, 2, 128>(a, s);
     if (p.bm == 64) return xf ? launch_h16_t<64, true, 2, 2, 128>(a, s) : launch_h16_t<64, false, 2, 2, 128>(a, s);
