@@ -41,12 +41,22 @@ namespace {
 typedef __attribute__((address_space(3))) void lds_void;
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
-// NS-deep ring of K stages. XF32: the activation stage holds fp32 rows (16 chunks of 16 bytes)
-// instead of fp16 ones
+// Stage geometry: a stage is 64 K values; one row's stage segment is CPR 16-byte chunks (fp16
+// rows: 8, fp32 rows: 16), whole 128-byte lines. Chunk j of row r sits in slot j ^ swz(r): a
+// fragment read (16 consecutive rows, one chunk) then touches 16 distinct 16-byte bank groups
+// of the 256-byte bank row, and one DMA instruction (64 lanes x 16 bytes) fills 64 / CPR whole
+// row segments. (32-deep stages with a deeper ring measured slower on every FC shape: their
+// fp16 row segments are half lines, and the stage boundaries double.)
+template <bool F32>
+constexpr int kCpr = F32 ? 16 : 8;
+template <int CPR>
+__device__ __forceinline__ int swz(int r) { return (r / (16 / CPR)) & (CPR - 1); }
+
+// NS-deep ring of K stages
 template <int BM, int BN, bool XF32, int NS>
 struct HLds {
-    u32x4 w[NS][BN * 8];                 // [stage][row][8 swizzled 16-byte chunks] fp16
-    u32x4 x[NS][BM * (XF32 ? 16 : 8)];
+    u32x4 w[NS][BN * kCpr<false>];      // [stage][row][swizzled 16-byte chunks] fp16
+    u32x4 x[NS][BM * kCpr<XF32>];
 };
 
 __device__ __forceinline__ void dma16(const void* g, void* lds) {
@@ -57,6 +67,20 @@ template <int N>
 __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Stage hand-over: this wave's DMA up to the newest N instructions has landed and its LDS
+// reads are done, then the workgroup barrier. __syncthreads() is not used here: its
+// workgroup fence makes the compiler wait for every outstanding LDS DMA (vmcnt(0)), which
+// drains the prefetched stages of the ring. The empty asm statements keep the compiler from
+// moving memory accesses across the barrier.
+template <int N>
+__device__ __forceinline__ void stage_sync() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));   // vmcnt(N) lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 template <int ACT>
@@ -141,10 +165,9 @@ __global__ __launch_bounds__(256) void k_f32_to_f16(const f32x4* __restrict__ x,
 
 // y[M][N] = act(x16[M][K] . w16[N][K]^T + bias) + resid, or (PART) the raw partial tile of
 // split ks over its K range into ws. XF32: the activations arrive as fp32 (g.xf) and are
-// rounded to fp16 (nearest even, as k_f32_to_f16) when the MFMA fragments are read from LDS;
-// their stage rows are 256 bytes (16 chunks, swizzle chunk ^ (row & 15)).
+// rounded to fp16 (nearest even, as k_f32_to_f16) when the MFMA fragments are read from LDS.
 // Tile BN weight rows x BM activation rows on 2 x WMR waves, each BN/2 weight rows x BM/WMR
-// activation rows.
+// activation rows; K stages of 64 values in an NS-deep ring.
 template <int WMR, int BN>
 constexpr int kH16MinBlocks = (WMR == 2 && BN == 128) ? 2 : 1;
 
@@ -156,10 +179,11 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
     constexpr int J = RW / 16;                  // 16-row activation subtiles per wave
     constexpr int WN = BN / 2;                  // weight rows per wave
     constexpr int I = WN / 16;                  // 16-row weight subtiles per wave
-    constexpr int CW = BN / 8 / NW;             // weight DMA instructions per wave and stage
-    constexpr int CX = XF32 ? BM / 4 / NW : BM / 8 / NW;  // activation DMA instructions per wave and stage
+    constexpr int CPW = kCpr<false>, CPX = kCpr<XF32>;  // chunks per stage row
+    constexpr int CW = BN * CPW / 64 / NW;      // weight DMA instructions per wave and stage
+    constexpr int CX = BM * CPX / 64 / NW;      // activation DMA instructions per wave and stage
     static_assert(CW >= 1 && CX >= 1 && RW % 16 == 0, "tile shape");
-    constexpr int MID = I * J / 2;              // second-half MFMAs issued before the boundary
+    constexpr int MID = I * J / 2;              // MFMAs issued before a stage boundary
     constexpr int NR = I + (XF32 ? 2 : 1) * J;  // LDS reads per K half
     static_assert(NR <= I * J, "read/MFMA interleave");
     static_assert(NS >= 2 && (NS - 1) * (CW + CX) < 64, "ring depth");
@@ -177,27 +201,22 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
     const int wn = wave & 1, wm = wave >> 1;
     const int l16 = lane & 15, lq = lane >> 4;
 
-    // row r's 128-byte stage segment lives at LDS slots r*8 + (chunk ^ ((r >> 1) & 7)); one
-    // DMA instruction moves rows 8c .. 8c+7 (lane l: row 8c + l/8, chunk (l & 7) ^ swizzle)
+    // DMA instruction c of an operand moves rows (64/CPR)*c + lane/CPR, slot lane % CPR, which
+    // holds that row's chunk slot ^ swz(row)
     const uint8_t* srcw[CW];
     const uint8_t* srcx[CX];
 #pragma unroll
     for (int q = 0; q < CW; q++) {
-        const int c = wave + NW * q;
-        const int n = min(n0 + 8 * c + (lane >> 3), N - 1);
-        srcw[q] = (const uint8_t*)g.w + (size_t)n * K * 2 + ((lane & 7) ^ ((4 * c + (lane >> 4)) & 7)) * 16;
+        const int r = (64 / CPW) * (wave + NW * q) + lane / CPW;
+        const int n = min(n0 + r, N - 1);
+        srcw[q] = (const uint8_t*)g.w + (size_t)n * K * 2 + ((lane % CPW) ^ swz<CPW>(r)) * 16;
     }
 #pragma unroll
     for (int q = 0; q < CX; q++) {
-        const int c = wave + NW * q;
-        if (XF32) {                             // 4 rows of 256 bytes per instruction
-            const int r = 4 * c + (lane >> 4);
-            const int m = min(m0 + r, M - 1);
-            srcx[q] = (const uint8_t*)g.xf + (size_t)m * K * 4 + ((lane & 15) ^ (r & 15)) * 16;
-        } else {
-            const int m = min(m0 + 8 * c + (lane >> 3), M - 1);
-            srcx[q] = (const uint8_t*)g.x + (size_t)m * K * 2 + ((lane & 7) ^ ((4 * c + (lane >> 4)) & 7)) * 16;
-        }
+        const int r = (64 / CPX) * (wave + NW * q) + lane / CPX;
+        const int m = min(m0 + r, M - 1);
+        const uint8_t* base = XF32 ? (const uint8_t*)g.xf + (size_t)m * K * 4 : (const uint8_t*)g.x + (size_t)m * K * 2;
+        srcx[q] = base + ((lane % CPX) ^ swz<CPX>(r)) * 16;
     }
     const int S = K / 64;
     const int s_beg = (int)((int64_t)ks * S / splits), s_end = (int)((int64_t)(ks + 1) * S / splits);
@@ -205,21 +224,22 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
     const int s0 = ((m0 / BM) + 4 * (n0 / BN)) % SL;          // K rotation
     auto kst = [&](int s) { int v = s + s0; return s_beg + (v >= SL ? v - SL : v); };
     auto dma_stage = [&](int st, int s) {
-        const size_t ofs = (size_t)kst(s) * 128;
+        const size_t ofs = (size_t)kst(s) * 16;
 #pragma unroll
-        for (int d = 0; d < CW; d++) dma16(srcw[d] + ofs, &L.w[st][(wave + NW * d) * 64]);
+        for (int d = 0; d < CW; d++) dma16(srcw[d] + ofs * CPW, &L.w[st][(wave + NW * d) * 64]);
 #pragma unroll
-        for (int d = 0; d < CX; d++) dma16(srcx[d] + (XF32 ? 2 : 1) * ofs, &L.x[st][(wave + NW * d) * 64]);
+        for (int d = 0; d < CX; d++) dma16(srcx[d] + ofs * CPX, &L.x[st][(wave + NW * d) * 64]);
     };
+    // fragment of 16 rows from r0 (r0 % 16 == 0), K half kb: lane (l16, lq) takes 8 values
     auto frag = [&](const u32x4* B, int r0, int kb) {
-        return __builtin_bit_cast(f16x8, B[(r0 + l16) * 8 + ((4 * kb + lq) ^ ((l16 >> 1) & 7))]);
+        return __builtin_bit_cast(f16x8, B[(r0 + l16) * CPW + ((4 * kb + lq) ^ swz<CPW>(l16))]);
     };
     // activation fragment: fp16 rows as stored, or fp32 rows rounded to fp16 on the way in
     auto xfrag = [&](const u32x4* B, int r0, int kb) {
         if (!XF32) return frag(B, r0, kb);
-        const int r = r0 + l16, c = 8 * kb + 2 * lq;  // r0 % 16 == 0, so r & 15 == l16
-        const f32x4 v0 = __builtin_bit_cast(f32x4, B[r * 16 + (c ^ l16)]);
-        const f32x4 v1 = __builtin_bit_cast(f32x4, B[r * 16 + ((c + 1) ^ l16)]);
+        const int r = r0 + l16, c = 8 * kb + 2 * lq;
+        const f32x4 v0 = __builtin_bit_cast(f32x4, B[r * CPX + (c ^ swz<CPX>(l16))]);
+        const f32x4 v1 = __builtin_bit_cast(f32x4, B[r * CPX + ((c + 1) ^ swz<CPX>(l16))]);
         return f16x8{(_Float16)v0[0], (_Float16)v0[1], (_Float16)v0[2], (_Float16)v0[3],
                      (_Float16)v1[0], (_Float16)v1[1], (_Float16)v1[2], (_Float16)v1[3]};
     };
@@ -238,50 +258,55 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
     constexpr int NDMA = CW + CX;
 #pragma unroll
     for (int k = 0; k < NS; k++) dma_stage(k, min(k, SL - 1));
-    wait_vm<(NS - 1) * NDMA>();                 // stage 0 has landed (mine) ...
-    __syncthreads();                            // ... and everyone's
+    stage_sync<(NS - 1) * NDMA>();              // stage 0 has landed (mine, then everyone's)
 #pragma unroll
     for (int i = 0; i < I; i++) a[0][i] = frag(L.w[0], WN * wn + 16 * i, 0);
 #pragma unroll
     for (int j = 0; j < J; j++) b[0][j] = xfrag(L.x[0], RW * wm + 16 * j, 0);
 
-    int st = 0;
-    for (int s = 0; s < SL; s++) {
-        const int stn = st + 1 == NS ? 0 : st + 1;
-        // K half 0: MFMAs on a/b[0] while the fragments of half 1 are read
+    // MFMAs of one K half on (ca, cb) while the next half's fragments go into (na, nb): read
+    // from half 1 of the same stage (no boundary), or, at the stage boundary (half 1 of stage
+    // s), from half 0 of stage s+1 after MID of the MFMAs
+    auto mfma_all = [&](const f16x8 (&ca)[I], const f16x8 (&cb)[J], int q0, int q1) {
 #pragma unroll
-        for (int i = 0; i < I; i++) a[1][i] = frag(L.w[st], WN * wn + 16 * i, 1);
+        for (int q = q0; q < q1; q++)
+            acc[q % I][q / I] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ca[q % I], cb[q / I], acc[q % I][q / I], 0, 0, 0);
+    };
+    auto half_inner = [&](const f16x8 (&ca)[I], const f16x8 (&cb)[J], f16x8 (&na)[I], f16x8 (&nb)[J], int st) {
 #pragma unroll
-        for (int j = 0; j < J; j++) b[1][j] = xfrag(L.x[st], RW * wm + 16 * j, 1);
+        for (int i = 0; i < I; i++) na[i] = frag(L.w[st], WN * wn + 16 * i, 1);
 #pragma unroll
-        for (int j = 0; j < J; j++)
-#pragma unroll
-            for (int i = 0; i < I; i++)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0][i], b[0][j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < J; j++) nb[j] = xfrag(L.x[st], RW * wm + 16 * j, 1);
+        mfma_all(ca, cb, 0, I * J);
 #pragma unroll
         for (int t = 0; t < NR; t++) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
         }
         __builtin_amdgcn_sched_group_barrier(0x008, I * J - NR, 0);
-        // K half 1: MID MFMAs, the stage boundary, the rest
-#pragma unroll
-        for (int q = 0; q < MID; q++)
-            acc[q % I][q / I] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1][q % I], b[1][q / I], acc[q % I][q / I], 0, 0, 0);
+    };
+    auto half_boundary = [&](const f16x8 (&ca)[I], const f16x8 (&cb)[J], f16x8 (&na)[I], f16x8 (&nb)[J],
+                             int s, int st, int stn) {
+        mfma_all(ca, cb, 0, MID);
         // The boundary runs on the last stage too (its fragment reads fetch an unused buffer):
         // with no branch around the LDS reads, the compiler's wait before the remaining MFMAs
         // covers only the reads those MFMAs consume, not the ones just issued.
-        wait_vm<(NS - 2) * NDMA>();             // stage s+1 has landed (mine) ...
-        __syncthreads();                        // ... and everyone's; stage s is no longer read
+        stage_sync<(NS - 2) * NDMA>();          // stage s+1 has landed (mine, then everyone's);
+                                                // stage s is no longer read
         // (a 2-deep ring waits for everything, so it skips the re-loads past the end)
         if (NS > 2 ? s + 1 < SL : s + NS < SL) dma_stage(st, min(s + NS, SL - 1));
 #pragma unroll
-        for (int i = 0; i < I; i++) a[0][i] = frag(L.w[stn], WN * wn + 16 * i, 0);
+        for (int i = 0; i < I; i++) na[i] = frag(L.w[stn], WN * wn + 16 * i, 0);
 #pragma unroll
-        for (int j = 0; j < J; j++) b[0][j] = xfrag(L.x[stn], RW * wm + 16 * j, 0);
-#pragma unroll
-        for (int q = MID; q < I * J; q++)
-            acc[q % I][q / I] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1][q % I], b[1][q / I], acc[q % I][q / I], 0, 0, 0);
+        for (int j = 0; j < J; j++) nb[j] = xfrag(L.x[stn], RW * wm + 16 * j, 0);
+        mfma_all(ca, cb, MID, I * J);
+    };
+
+    int st = 0;
+    for (int s = 0; s < SL; s++) {
+        const int stn = st + 1 == NS ? 0 : st + 1;
+        half_inner(a[0], b[0], a[1], b[1], st);
+        half_boundary(a[1], b[1], a[0], b[0], s, st, stn);
         st = stn;
     }
     wait_vm0();
@@ -406,6 +431,17 @@ H16Plan gemm_h16_plan(int M, int N, int K, bool xf32) {
     const int tiles = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
     const int S = K / 64;
     p.splits = 1;
+    // long-K narrow outputs on fp16 operands with one to three 64-row tiles per CU: 64-row
+    // tiles on a 3-deep ring (72 KB, two workgroups per CU) and no split (M = 4112 down-proj:
+    // 38.5 against 42.8 us for 128-row tiles in 2 splits; at M = 16448 the 128-row tiles win)
+    const int t64 = ((M + 63) / 64) * ((N + 127) / 128);
+    if (!xf32 && N <= 1024 && K >= 2048 && t64 >= 256 && t64 <= 768) {
+        p.bm = 64;
+        p.ns = 3;
+        p.ws_bytes = 0;
+        p.ph = 8;
+        return p;
+    }
     // split K while there are at most two workgroups per CU and each split keeps >= 12
     // stages (>= 6 with at most half a tile per CU); measured at M = 1025: the down-proj (102
     // tiles, 48 stages) fastest at 4 splits, the out-proj (102 tiles, 12 stages) at 2
@@ -468,10 +504,12 @@ hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a0, hipStream_t 
     GemmH16Args a = a0;
     a.ph = p.ph;
     const bool xf = a.xf != nullptr;
-    if (p.ns != 2) return hipErrorInvalidValue;
     if (p.bn != 128 || p.wmr != 2) return hipErrorInvalidValue;
-    if (p.bm == 128) return xf ? launch_h16_t<128, true, 2, 2, 128>(a, s) : launch_h16_t<128, false, 2, 2, 128>(a, s);
-    if (p.bm == 64) return xf ? launch_h16_t<64, true, 2, 2, 128>(a, s) : launch_h16_t<64, false, 2, 2, 128>(a, s);
+    if (p.ns == 2) {
+        if (p.bm == 128) return xf ? launch_h16_t<128, true, 2, 2, 128>(a, s) : launch_h16_t<128, false, 2, 2, 128>(a, s);
+        if (p.bm == 64) return xf ? launch_h16_t<64, true, 2, 2, 128>(a, s) : launch_h16_t<64, false, 2, 2, 128>(a, s);
+    }
+    if (p.ns == 3 && p.bm == 64 && !xf) return launch_h16_t<64, false, 3, 2, 128>(a, s);
     return hipErrorInvalidValue;
 }
 

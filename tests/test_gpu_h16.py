@@ -80,7 +80,7 @@ def test_f32_to_f16_rounding(ctx):
 
 SHAPES = [(1, 4, 64), (7, 132, 256), (65, 128, 768), (257, 3072, 768), (1025, 2304, 768),
           (1025, 768, 768), (1025, 768, 3072), (300, 256, 3072), (4097, 768, 3072),
-          (4112, 3072, 768), (4500, 2304, 768), (6150, 2048, 2048)]
+          (4112, 3072, 768), (4500, 2304, 768), (6150, 2048, 2048), (2731, 1024, 2048)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
