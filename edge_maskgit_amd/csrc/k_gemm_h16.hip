@@ -185,7 +185,7 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
     static_assert(CW >= 1 && CX >= 1 && RW % 16 == 0, "tile shape");
     constexpr int MID = I * J / 2;              // MFMAs issued before a stage boundary
     constexpr int NR = I + (XF32 ? 2 : 1) * J;  // LDS reads per K half
-    static_assert(NR <= I * J, "read/MFMA interleave");
+    constexpr int NI = NR < I * J ? NR : I * J;  // MFMA : LDS-read pairs in the interleave
     static_assert(NS >= 2 && (NS - 1) * (CW + CX) < 64, "ring depth");
     __shared__ HLds<BM, BN, XF32, NS> L;
 
@@ -279,11 +279,11 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
         for (int j = 0; j < J; j++) nb[j] = xfrag(L.x[st], RW * wm + 16 * j, 1);
         mfma_all(ca, cb, 0, I * J);
 #pragma unroll
-        for (int t = 0; t < NR; t++) {
+        for (int t = 0; t < NI; t++) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, I * J - NR, 0);
+        if (I * J > NI) __builtin_amdgcn_sched_group_barrier(0x008, I * J - NI, 0);
     };
     auto half_boundary = [&](const f16x8 (&ca)[I], const f16x8 (&cb)[J], f16x8 (&na)[I], f16x8 (&nb)[J],
                              int s, int st, int stn) {
@@ -431,6 +431,29 @@ H16Plan gemm_h16_plan(int M, int N, int K, bool xf32) {
     const int tiles = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
     const int S = K / 64;
     p.splits = 1;
+    // Few tiles: 64 x 64 tiles on a 3-deep ring (72 KB per workgroup with fp32 activation
+    // rows, 48 KB with fp16: two resp. three workgroups per CU) when every tile is resident at
+    // once, for short K or at most half a tile per CU; 32-row tiles below half a tile per CU
+    // for short K; split K while every split keeps >= 12 stages and stays resident. Measured on
+    // the four FC shapes at M = 257 and 1025 against the 64 x 128 2-deep plan (split-K and
+    // reduce included), fp32 / fp16 activations: M = 257 QKV 8.7 / 7.0 against 11.0 / 10.4 us,
+    // up 9.4 / 7.8 against 12.1 / 10.9, out 6.7 / 6.5 against 9.7 / 9.2, down 13.8 / 12.3
+    // against 17.3 / 16.3; M = 1025 out 9.8 / 8.2 against 12.8 / 11.9, QKV (fp16) 11.9 against
+    // 12.8. Long-K shapes with more tiles (M = 1025 down-proj on fp32 rows: 23.8 against 22.1)
+    // keep the 64 x 128 split-K plan.
+    const int t6464 = ((M + 63) / 64) * ((N + 63) / 64);
+    const int slots = xf32 ? 512 : 768;
+    if ((K <= 1024 || t6464 <= 128) && t6464 <= slots) {
+        p.ns = 3;
+        p.bn = 64;
+        p.bm = K <= 1024 && t6464 < 128 ? 32 : 64;
+        const int ts = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
+        while (ts * p.splits * 2 <= slots && S / (p.splits * 2) >= 12) p.splits *= 2;
+        p.ws_bytes = p.splits > 1 ? (size_t)ts * p.splits * p.bm * p.bn * 4 : 0;
+        const int tm = (M + p.bm - 1) / p.bm;
+        p.ph = tm <= 32 && (int64_t)M * (xf32 ? 4 : 2) * 2 >= (int64_t)N * 2 ? 1 : 8;
+        return p;
+    }
     // long-K narrow outputs on fp16 operands with one to three 64-row tiles per CU: 64-row
     // tiles on a 3-deep ring (72 KB, two workgroups per CU) and no split (M = 4112 down-proj:
     // 38.5 against 42.8 us for 128-row tiles in 2 splits; at M = 16448 the 128-row tiles win)
@@ -504,12 +527,16 @@ hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a0, hipStream_t 
     GemmH16Args a = a0;
     a.ph = p.ph;
     const bool xf = a.xf != nullptr;
-    if (p.bn != 128 || p.wmr != 2) return hipErrorInvalidValue;
-    if (p.ns == 2) {
-        if (p.bm == 128) return xf ? launch_h16_t<128, true, 2, 2, 128>(a, s) : launch_h16_t<128, false, 2, 2, 128>(a, s);
+    if (p.wmr != 2) return hipErrorInvalidValue;
+    if (p.bn == 128 && p.ns == 2) {
+        if (p.bm == 128 && !xf) return launch_h16_t<128, false, 2, 2, 128>(a, s);
         if (p.bm == 64) return xf ? launch_h16_t<64, true, 2, 2, 128>(a, s) : launch_h16_t<64, false, 2, 2, 128>(a, s);
     }
-    if (p.ns == 3 && p.bm == 64 && !xf) return launch_h16_t<64, false, 3, 2, 128>(a, s);
+    if (p.bn == 128 && p.ns == 3 && p.bm == 64 && !xf) return launch_h16_t<64, false, 3, 2, 128>(a, s);
+    if (p.bn == 64 && p.ns == 3) {
+        if (p.bm == 64) return xf ? launch_h16_t<64, true, 3, 2, 64>(a, s) : launch_h16_t<64, false, 3, 2, 64>(a, s);
+        if (p.bm == 32) return xf ? launch_h16_t<32, true, 3, 2, 64>(a, s) : launch_h16_t<32, false, 3, 2, 64>(a, s);
+    }
     return hipErrorInvalidValue;
 }
 

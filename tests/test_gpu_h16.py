@@ -165,11 +165,15 @@ def test_gemm_h16_f32in_vs_dequant_f32(ctx, wtype, M, N, K, act, res):
     assert err <= 1e-3
 
 
-@pytest.mark.parametrize("M,N,K,act", [(65, 128, 768, 0), (1025, 2304, 768, 1), (1025, 768, 3072, 0),
-                                       (4097, 3072, 768, 2)])
-def test_gemm_h16_f32in_equals_rounded_operand(ctx, M, N, K, act):
+@pytest.mark.parametrize("M,N,K,act,exact", [(65, 128, 768, 0, True), (1025, 3072, 768, 1, True),
+                                             (1025, 768, 3072, 0, True), (4097, 3072, 768, 2, True),
+                                             (1025, 2304, 768, 1, False)])
+def test_gemm_h16_f32in_equals_rounded_operand(ctx, M, N, K, act, exact):
     """The in-kernel fp32 -> fp16 rounding (XF32 variant) gives the same bits as rounding with
-    mgh_f32_to_f16 first and running the fp16-operand kernel."""
+    mgh_f32_to_f16 first and running the fp16-operand kernel, where the tile plan is the same
+    for both operand forms. At (1025, 2304, 768) the fp16 operand fits all its 64 x 64 tiles on
+    the GPU at once and takes them, the fp32 one keeps 64 x 128 tiles: the same products summed
+    in another order, so the bar there is fp32 summation-order agreement."""
     print(f"gemm_h16 f32in == f32_to_f16 + gemm_h16: M={M} N={N} K={K}", flush=True)
     rng = np.random.default_rng(M + 3 * N + K)
     w16 = (rng.standard_normal((N, K)) * 0.02).astype(np.float16)
@@ -183,7 +187,10 @@ def test_gemm_h16_f32in_equals_rounded_operand(ctx, M, N, K, act):
     y1, y2 = ctx.download(dY1, (M, N), np.float32), ctx.download(dY2, (M, N), np.float32)
     for t in (dW, dX, dB, dH, dY1, dY2):
         ctx.free(t)
-    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    if exact:
+        assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    else:
+        assert np.abs(y1 - y2).max() <= 2e-6 * np.abs(y2).max()
 
 
 @pytest.mark.parametrize("M,N,K,act", [(257, 3072, 768, 1), (1025, 768, 3072, 0)])
