@@ -426,7 +426,10 @@ H16Plan gemm_h16_plan(int M, int N, int K, bool xf32) {
     // tiles from about one tile per CU (M = 4112 down-proj: 40.5 against 43.7 us). Larger
     // tiles (128 x 256 on 4 waves, 256 x 256 on 8) measured slower on every shape. With fp32
     // activations, 64-row tiles: their stage is already as large as a 128-row fp16 stage.
-    const bool wide128 = t128 >= 1024 || (N <= 1024 && t128 >= 192);
+    // 3072-wide outputs (the MLP up-proj) take 128-row tiles from about 1.5 tiles per CU
+    // (M = 4112: 43.6 against 46.2 us; M = 2056: 23.8 against 27.2 us; at M = 1025 the 64-row
+    // tiles win, 15.2 against 17.2 us)
+    const bool wide128 = t128 >= 1024 || (N <= 1024 && t128 >= 192) || (N >= 3072 && t128 >= 384);
     p.bm = wide128 && !xf32 ? 128 : 64;
     const int tiles = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
     const int S = K / 64;
@@ -454,11 +457,12 @@ H16Plan gemm_h16_plan(int M, int N, int K, bool xf32) {
         p.ph = tm <= 32 && (int64_t)M * (xf32 ? 4 : 2) * 2 >= (int64_t)N * 2 ? 1 : 8;
         return p;
     }
-    // long-K narrow outputs on fp16 operands with one to three 64-row tiles per CU: 64-row
+    // long-K narrow outputs on fp16 operands with 0.75 to three 64-row tiles per CU: 64-row
     // tiles on a 3-deep ring (72 KB, two workgroups per CU) and no split (M = 4112 down-proj:
-    // 38.5 against 42.8 us for 128-row tiles in 2 splits; at M = 16448 the 128-row tiles win)
+    // 38.5 against 42.8 us for 128-row tiles in 2 splits; M = 2056: 26.4 against 28.9 us for
+    // 2 splits; at M = 16448 the 128-row tiles win)
     const int t64 = ((M + 63) / 64) * ((N + 127) / 128);
-    if (!xf32 && N <= 1024 && K >= 2048 && t64 >= 256 && t64 <= 768) {
+    if (!xf32 && N <= 1024 && K >= 2048 && t64 >= 192 && t64 <= 768) {
         p.bm = 64;
         p.ns = 3;
         p.ws_bytes = 0;
