@@ -472,7 +472,9 @@ const void* HipRuntime::run(Graph& g, bool readback) {
             release_after(i, t);
             continue;
         }
-        if (I.profiling) I.check(mgh_timer_start(I.ctx));
+        // a cont written by its attention launches nothing: not timed
+        const bool timed = I.profiling && !(t->op == Op::Cont && fa_into.count(t));
+        if (timed) I.check(mgh_timer_start(I.ctx));
 
         void* out = nullptr;
         if (grp_of.count(t)) {
@@ -663,7 +665,7 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                 throw std::runtime_error(std::string("HipRuntime: unsupported op ") + std::to_string((int)t->op));
         }
 
-        if (I.profiling) {
+        if (timed) {
             float ms = 0.f;
             I.check(mgh_timer_stop(I.ctx, &ms));
             auto& e = I.prof[op_name(t)];
