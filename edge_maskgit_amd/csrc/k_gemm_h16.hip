@@ -69,20 +69,6 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// Stage hand-over: this wave's DMA up to the newest N instructions has landed and its LDS
-// reads are done, then the workgroup barrier. __syncthreads() is not used here: its
-// workgroup fence makes the compiler wait for every outstanding LDS DMA (vmcnt(0)), which
-// drains the prefetched stages of the ring. The empty asm statements keep the compiler from
-// moving memory accesses across the barrier.
-template <int N>
-__device__ __forceinline__ void stage_sync() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));   // vmcnt(N) lgkmcnt(0)
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
 template <int ACT>
 __device__ __forceinline__ float act_h(float v) {
     if (ACT == 1) return gelu_erf(v);

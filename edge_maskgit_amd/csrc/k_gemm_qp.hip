@@ -53,13 +53,13 @@ constexpr int NT = 256;
 constexpr int BN = 128;            // weight rows (output columns) per workgroup
 constexpr int KB = 2;              // blocks per stage
 #ifndef MGH_QP_NS128
-#define MGH_QP_NS128 2             // ring depth with 128-row activation tiles (68 KB LDS, 2 per CU)
+#define MGH_QP_NS128 3             // ring depth with 128-row activation tiles (102 KB LDS, 1 per CU)
 #endif
 #ifndef MGH_QP_SPLIT_TARGET
 #define MGH_QP_SPLIT_TARGET 400    // split-K aims at about this many workgroups
 #endif
 #ifndef MGH_QP_NS64
-#define MGH_QP_NS64 2              // ring depth with 64-row activation tiles (51 KB LDS, 3 per CU)
+#define MGH_QP_NS64 3              // ring depth with 64-row activation tiles (77 KB LDS, 2 per CU)
 #endif
 
 template <int BM, int NS>
@@ -211,9 +211,10 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_qp(GemmArgs g) {
     int bn = NS - 1;                        // buffer receiving stage s + NS - 1
     for (int s = s_beg; s < s_end; s++) {
         const int sn = min(s + NS - 1, s_end - 1);
-        if (DEBUG) wait_vm0();              // the dot stores also count in vmcnt
-        else wait_vm<(NS - 2) * NDMA>();    // my loads of stage s have landed
-        __syncthreads();                    // ... everyone's; and stage s-1 is consumed
+        // my loads of stage s have landed, then everyone's; and stage s-1 is consumed (the
+        // debug variant's dot stores also count in vmcnt, so it waits for all)
+        if (DEBUG) stage_sync<0>();
+        else stage_sync<(NS - 2) * NDMA>();
 
         const u32x4* W = L.w[st];
         const u32x4* X = L.x[st];

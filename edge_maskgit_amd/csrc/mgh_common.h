@@ -55,6 +55,20 @@ __device__ __forceinline__ int swz_slot(int j, int r, int rows) {
     return j * rows + (r ^ (j & 7));
 }
 
+// Stage hand-over: this wave's DMA up to the newest N instructions has landed and its LDS
+// reads are done, then the workgroup barrier. __syncthreads() is not used here: its
+// workgroup fence makes the compiler wait for every outstanding LDS DMA (vmcnt(0)), which
+// drains the prefetched stages of the ring. The empty asm statements keep the compiler from
+// moving memory accesses across the barrier.
+template <int N>
+__device__ __forceinline__ void stage_sync() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));   // vmcnt(N) lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // XCD-aware workgroup remap: the dispatcher sends workgroup i to XCD i % 8. Give each XCD
 // a contiguous range of logical tiles so tiles that share operand rows share an L2.
 __device__ __forceinline__ int xcd_remap(int bid, int G) {
