@@ -53,8 +53,8 @@ constexpr int NT = 256;
 constexpr int BN = 128;            // weight rows (output columns) per workgroup
 constexpr int KB = 2;              // blocks per stage
 #ifndef MGH_QP_NS128
-#define MGH_QP_NS128 3             // ring depth with 128-row activation tiles (102 KB LDS, 1 per CU)
-#endif
+#define MGH_QP_NS128 3             // ring depth with 128-row activation tiles when every workgroup
+#endif                             // has a CU (102 KB LDS, 1 per CU); 2 beyond (68 KB, 2 per CU)
 #ifndef MGH_QP_SPLIT_TARGET
 #define MGH_QP_SPLIT_TARGET 400    // split-K aims at about this many workgroups
 #endif
@@ -506,7 +506,13 @@ hipError_t launch_gemm_qp_t(int wtype, const GemmArgs& a, bool dbg, hipStream_t 
 
 // a.splits > 1 needs a.ws sized by gemm_qp_plan (the caller's plan for this shape).
 hipError_t launch_gemm_qp(int wtype, const GemmArgs& a, bool dbg, hipStream_t s) {
-    if (gemm_qp_bm(a.M, a.N) == 128) return launch_gemm_qp_t<128, MGH_QP_NS128>(wtype, a, dbg, s);
+    if (gemm_qp_bm(a.M, a.N) == 128) {
+        // the 3-deep ring halves the workgroups per CU: only where they all run at once
+        // (cfg2 up-proj, 216 tiles: 24.2 -> 21.1 us; at M = 4112 it slowed the int8 forward)
+        const int wgs = ((a.M + 127) / 128) * ((a.N + BN - 1) / BN) * (dbg ? 1 : std::max(a.splits, 1));
+        if (wgs <= 256) return launch_gemm_qp_t<128, MGH_QP_NS128>(wtype, a, dbg, s);
+        return launch_gemm_qp_t<128, 2>(wtype, a, dbg, s);
+    }
     return launch_gemm_qp_t<64, MGH_QP_NS64>(wtype, a, dbg, s);
 }
 
