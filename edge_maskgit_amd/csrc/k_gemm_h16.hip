@@ -10,11 +10,14 @@
 // fp16 storage of the two operands and the fp32 summation.
 //
 // gfx950 mapping
-//  * y tile 128 weight rows x BM activation rows per 256-thread workgroup (2 x 2 waves, each
-//    64 x BM/2 outputs as 4 x BM/32 v_mfma_f32_16x16x32_f16 tiles); K stage 64.
-//  * Operands move with global_load_lds (16 bytes per lane) straight into a double-buffered
-//    LDS ring: one instruction moves 8 whole 128-byte row segments, XOR-swizzled so the MFMA
-//    fragment reads are bank-conflict free (the layout of k_gemm_qp.hip).
+//  * y tile BN (128 or 64) weight rows x BM (128, 64 or 32) activation rows per 256-thread
+//    workgroup (2 x 2 waves, each BN/2 x BM/2 outputs as v_mfma_f32_16x16x32_f16 tiles); K
+//    stage 64. gemm_h16_plan picks the tile, the ring depth and the K split per shape.
+//  * Operands move with global_load_lds (16 bytes per lane) straight into a 2- or 3-deep LDS
+//    ring: one instruction moves whole 128-byte row segments, XOR-swizzled so the MFMA
+//    fragment reads are bank-conflict free (the layout of k_gemm_qp.hip). The stage
+//    hand-over is an explicit vmcnt/lgkmcnt wait and s_barrier (stage_sync), which keeps the
+//    prefetched stages in flight.
 //  * Software pipeline: the fragments of the next K half are read from LDS while the current
 //    half's MFMAs issue; the stage boundary (vmcnt wait, barrier, next DMA, first fragment
 //    reads of the new stage) sits between two halves of the second K half's MFMAs, so the MFMA

@@ -142,7 +142,8 @@ def test_gemm_h16_split_k_sequence(ctx):
 
 @pytest.mark.parametrize("wtype", [ema.WTYPE_Q8_0, ema.WTYPE_Q4_K])
 @pytest.mark.parametrize("M,N,K,act,res", [(257, 768, 768, 0, True), (1025, 3072, 768, 1, False),
-                                           (1025, 768, 3072, 0, True), (64, 2304, 768, 0, False)])
+                                           (1025, 768, 3072, 0, True), (64, 2304, 768, 0, False),
+                                           (257, 768, 3072, 0, True)])
 def test_gemm_h16_f32in_vs_dequant_f32(ctx, wtype, M, N, K, act, res):
     print(f"gemm_h16_f32in wtype={wtype} M={M} N={N} K={K}", flush=True)
     rng = np.random.default_rng(M + N + K + wtype)
