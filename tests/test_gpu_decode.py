@@ -165,3 +165,31 @@ def test_generate_matches_host_loop(q4_model, algo):
     assert np.array_equal(got, again)
     assert not np.array_equal(got, other)
     assert got.min() >= 0 and got.max() < 1024
+
+
+def test_generate_full_cfg5(tmp_path):
+    """cfg5 at full size: 24 Q4_K layers, 64 images x 257 tokens, 8 steps from all-masked,
+    dequant-fp16 path. The device-resident generate equals the same loop run from the host
+    (the runtime's forward read back, then the oracle step) token for token, repeats
+    bit-identically, and ends with every position a codebook id."""
+    path = str(tmp_path / "cfg5.gguf")
+    mg_gguf.write_model(path, n_layer=24, quant="q4_k", seed=9)
+    B, steps = 64, 8
+    rng = np.random.default_rng(5)
+    classes = [int(c) for c in rng.integers(0, 1000, B)]
+    seeds = [int(s) for s in rng.integers(0, 2**62, B)]
+    print("generate cfg5 full size: 24 layers q4_k, B=64, 8 steps", flush=True)
+    with rt.TransformerRuntime(path, algo=2) as m:
+        got = m.generate(classes, seeds, steps)
+        again = m.generate(classes, seeds, steps)
+        S = m.hparams["n_tokens"] + 1
+        tok = np.full((B, S), MASK, np.int32)
+        tok[:, 0] = np.asarray(classes) + 1024
+        for step in range(steps):
+            logits = m.forward(tok)
+            tok, res = oracle.decode_step(logits, tok, step, steps, seeds, 2 * S * step,
+                                          choice_temp=4.5)
+    print(f"  mismatches {int((got != res[:, 1:]).sum())}", flush=True)
+    assert np.array_equal(got, res[:, 1:])
+    assert np.array_equal(got, again)
+    assert got.min() >= 0 and got.max() < 1024
