@@ -544,13 +544,18 @@ def main():
         extra["cfg1_m257"]["alg_bytes"] = ab1
     if a.extra:
         for (mm, wt) in ((4097, ema.WTYPE_Q8_0), (1025, ema.WTYPE_Q4_K), (4097, ema.WTYPE_Q4_K)):
-            s, g, _ = measure(ctx, mm, wt, max(10, a.steps // 2), a.warmup, a.rotate_gb,
-                              use_graphs=a.graphs, path=a.path)
             key = f"{'q8_0' if wt == ema.WTYPE_Q8_0 else 'q4_k'}_m{mm}"
-            extra[key] = {"ms_per_step": round(s, 5), "tops": round(layer_ops(mm) / (s * 1e-3) / 1e12, 2),
-                          "gemm_tops": round(layer_ops(mm) / (g * 1e-3) / 1e12, 2),
-                          "frac_of_hbm_roofline": round(step_alg_bytes(mm, wt) / (HBM_PEAK_GBS * 1e9)
-                                                        / (s * 1e-3), 4)}
+            for pth in (a.path, other):        # the production path, then the other one
+                s, g, _ = measure(ctx, mm, wt, max(10, a.steps // 2), a.warmup, a.rotate_gb,
+                                  use_graphs=a.graphs, path=pth)
+                r = {"ms_per_step": round(s, 5), "tops": round(layer_ops(mm) / (s * 1e-3) / 1e12, 2),
+                     "gemm_tops": round(layer_ops(mm) / (g * 1e-3) / 1e12, 2),
+                     "frac_of_hbm_roofline": round(step_alg_bytes(mm, wt) / (HBM_PEAK_GBS * 1e9)
+                                                   / (s * 1e-3), 4)}
+                if pth == a.path:
+                    extra[key] = r
+                else:
+                    extra[key][PATH_NAME[pth]] = r
     if not a.no_fwd:
         import tempfile
         with tempfile.TemporaryDirectory() as d:
