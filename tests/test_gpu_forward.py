@@ -179,8 +179,9 @@ def test_forward_full_cfg4_properties(tmp_path, algo):
             assert dmax < 1.0 and err <= 2.5 * noise   # measured 1.2-1.3x (two draws: ~sqrt 2)
 
 
-def test_forward_24_layers_vs_oracle(tmp_path):
-    """Full depth against the oracle, one image (24 Q8_0 layers, S = 257): the dequant-fp16
+@pytest.mark.parametrize("quant", ["q8_0", "q4_k"])
+def test_forward_24_layers_vs_oracle(tmp_path, quant):
+    """Full depth against the oracle, one image (24 Q8_0 / Q4_K layers, S = 257): the dequant-fp16
     path against dequantize-then-F32 with fp16 K/V, and the int8-dot path against the oracle's
     int8-dot forward (the reference's k_quantize_q8 + k_mul_mat_q8_i8 semantics). The two
     int8 forwards sum in different orders, so codes flip and later layers decorrelate at the
@@ -188,19 +189,19 @@ def test_forward_24_layers_vs_oracle(tmp_path):
     (its int8 forward against its dequantize-then-F32 forward), with the reference's
     max|d| < 1.0 (tools/verify-opencl-transformer.cpp:98-101)."""
     path = str(tmp_path / "m24.gguf")
-    t = mg_gguf.write_model(path, n_layer=24, quant="q8_0", seed=5)
+    t = mg_gguf.write_model(path, n_layer=24, quant=quant, seed=5)
     tok = mg_gguf.tokens(np.random.default_rng(21), 257, 1)
-    print("forward 24 layers q8_0 B=1 vs oracle (both paths)", flush=True)
+    print(f"forward 24 layers {quant} B=1 vs oracle (both paths)", flush=True)
     with rt.TransformerRuntime(path, algo=2) as m:
         g16 = m.forward(tok)
     with rt.TransformerRuntime(path, algo=1) as m:
         g8 = m.forward(tok)
-    deq = ofwd.transformer_forward(t, 24, 16, tok, quant="q8_0", algo="deq", f16kv=True)
-    i8 = ofwd.transformer_forward(t, 24, 16, tok, quant="q8_0", algo="int8", f16kv=True)
+    deq = ofwd.transformer_forward(t, 24, 16, tok, quant=quant, algo="deq", f16kv=True)
+    i8 = ofwd.transformer_forward(t, 24, 16, tok, quant=quant, algo="int8", f16kv=True)
     e16, noise, e8 = _rel(g16, deq), _rel(i8, deq), _rel(g8, i8)
     print(f"  dequant-fp16 vs dequantize-then-F32: rel {e16:.2e}  cos {_cos(g16, deq):.7f}", flush=True)
     print(f"  oracle int8 vs oracle dequantize-then-F32 (quantization noise): rel {noise:.2e}", flush=True)
     print(f"  int8-dot vs oracle int8: rel {e8:.2e}  cos {_cos(g8, i8):.7f}  "
           f"max|d| {np.abs(g8 - i8).max():.3e}", flush=True)
-    assert e16 <= 2e-3                     # measured 8.6e-4 (cos 0.9999996)
+    assert e16 <= 2e-3                     # measured 8.6e-4 (q8_0), 8.5e-4 (q4_k)
     assert e8 <= 2.5 * noise and np.abs(g8 - i8).max() < 1.0   # measured 1.2x the noise
