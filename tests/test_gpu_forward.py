@@ -117,6 +117,26 @@ def test_forward_f32(models):
         assert c >= 0.9999
 
 
+def test_forward_f32_short_sequence(models):
+    """S = 16 (one query and key tile, the sequence length of the reference's own GPU test,
+    tools/test-opencl.cpp:36-38: K = 768, S = 16, F = 3072), F32 weights, two images: against
+    the oracle with fp16 K/V, and the first image against the reference CPU executor."""
+    path, t = models["f32"]
+    tok = mg_gguf.tokens(np.random.default_rng(16), 16, 2)
+    print("forward f32 S=16 B=2", flush=True)
+    with rt.TransformerRuntime(path) as m:
+        got = m.forward(tok)
+    want = ofwd.transformer_forward(t, L, 16, tok, quant="f32", f16kv=True)
+    err = _rel(got, want)
+    print(f"  rel err vs oracle (fp16 K/V) {err:.2e}")
+    assert err <= 1e-3
+    if ref.available():
+        cpu = ref.transformer_forward(path, tok[:1], 2025)
+        c = _cos(got[:1], cpu)
+        print(f"  vs reference CPU (F32 attention): rel {_rel(got[:1], cpu):.2e} cos {c:.8f}")
+        assert c >= 0.9999
+
+
 def test_forward_batch_rows_match_single(models):
     """M = S*B flattening: image b of a batch equals that image run alone (dequant-fp16 path).
     Batch sizes change the GEMM plan (tiles, K splits), hence fp32 summation order, and an

@@ -116,7 +116,7 @@ def _qkv(rng, D, S, H, B):
 
 # S <= 512 runs the whole-head kernel (K/V of a head resident in LDS), longer sequences the
 # chunked online-softmax kernel
-@pytest.mark.parametrize("D,S,H,B", [(48, 1, 2, 1), (48, 17, 2, 1), (48, 64, 3, 2), (48, 65, 2, 1),
+@pytest.mark.parametrize("D,S,H,B", [(48, 1, 2, 1), (48, 16, 2, 1), (48, 17, 2, 1), (48, 64, 3, 2), (48, 65, 2, 1),
                                      (48, 257, 16, 2), (64, 130, 4, 1), (16, 40, 1, 1), (32, 300, 2, 1),
                                      (48, 512, 2, 1), (64, 512, 1, 1), (48, 513, 2, 1), (48, 1025, 1, 1)])
 def test_flash_attn_vs_oracle(ctx, D, S, H, B):
