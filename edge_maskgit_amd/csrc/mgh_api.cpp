@@ -780,9 +780,9 @@ int mgh_gemm_h16_f32in(mgh_ctx* c, const void* wp16, int N, int K, const float* 
         // fp32 stage costs less than the separate rounding pass)
         a.xf = x;
     } else {
-        // many rows: a rounding pass, then the fp16-operand kernel (its smaller stages fit
-        // three workgroups per CU; measured 2-7% faster per four-FC step at M = 4097 than
-        // rounding inside the GEMM)
+        // many rows: a rounding pass, then the fp16-operand kernel and its tile plans (128-row
+        // and 3-deep tiles exist for fp16 operands only); per four-FC step at M = 4097 this
+        // measured equal to rounding inside the GEMM (377.7 against 376.4 TOPS)
         if (int r = ensure_scratch(c, round256((size_t)M * K * 2))) return r;
         MGH_HIP(c, mgh::launch_f32_to_f16(x, (_Float16*)c->scratch, (int64_t)M * K, c->stream), "k_f32_to_f16");
         a.x = (const _Float16*)c->scratch;
