@@ -38,6 +38,7 @@ MGH_SYMBOLS = [
     "mgh_copy_strided", "mgh_decode_state_bytes", "mgh_decode_work_bytes", "mgh_decode_init",
     "mgh_decode_step", "mgh_packed_weight_bytes_f16", "mgh_pack_weights_f16", "mgh_f32_to_f16",
     "mgh_gemm_h16", "mgh_gemm_h16_f32in", "mgh_gemm_h16_y16", "mgh_flash_attn_f16kv_o16", "mgh_flash_attn_f16in",
+    "mgh_softmax", "mgh_binary", "mgh_scale", "mgh_unary", "mgh_gemm_f32_batched",
 ]
 
 _lib = None
@@ -110,6 +111,11 @@ def lib():
         L.mgh_decode_work_bytes.restype = SZ
         L.mgh_decode_init.argtypes = [P, I, P, P]
         L.mgh_decode_step.argtypes = [P, P, P, P, I, I, I, I, I, I, I, I, ctypes.c_float, P, P]
+        L.mgh_softmax.argtypes = [P, P, I64, I, ctypes.c_float, P]
+        L.mgh_binary.argtypes = [P, I, P, P, P, P, P, P, P]
+        L.mgh_scale.argtypes = [P, P, I64, ctypes.c_float, P]
+        L.mgh_unary.argtypes = [P, I, P, I64, P]
+        L.mgh_gemm_f32_batched.argtypes = [P, P, P, P, P, P, P, P, I, P, P]
         L.mgh_graph_begin.argtypes = [P]
         L.mgh_graph_end.argtypes = [P, ctypes.POINTER(P)]
         L.mgh_graph_launch.argtypes = [P, P]
@@ -353,6 +359,24 @@ class Context:
         P = self._ptr
         self._check(lib().mgh_gemm_q_f32in(self.h, algo, wtype, P(w), N, K, P(x), M,
                                            P(bias), act, P(resid), P(y)))
+
+    def softmax(self, x, rows, D, scale, y):
+        self._check(lib().mgh_softmax(self.h, self._ptr(x), rows, D, scale, self._ptr(y)))
+
+    def binary(self, op, a, a_strides, b, b_ne, b_strides, ne, out):
+        P, A = self._ptr, (lambda v: (ctypes.c_int64 * 4)(*v))
+        self._check(lib().mgh_binary(self.h, op, P(a), A(a_strides), P(b), A(b_ne), A(b_strides), A(ne), P(out)))
+
+    def scale(self, x, n, s, y):
+        self._check(lib().mgh_scale(self.h, self._ptr(x), n, s, self._ptr(y)))
+
+    def unary(self, act, x, n, y):
+        self._check(lib().mgh_unary(self.h, act, self._ptr(x), n, self._ptr(y)))
+
+    def gemm_f32_batched(self, w, w_ne, w_strides, x, x_ne, x_strides, bias, act, resid, y):
+        P, A = self._ptr, (lambda v: (ctypes.c_int64 * 4)(*v))
+        self._check(lib().mgh_gemm_f32_batched(self.h, P(w), A(w_ne), A(w_strides), P(x), A(x_ne), A(x_strides),
+                                               P(bias), act, P(resid), P(y)))
 
     # ---- graphs ----
     def graph_begin(self):

@@ -488,6 +488,7 @@ int mgh_gemm_q_packed_f32in(mgh_ctx* c, int algo, int wtype, const void* wp, int
         return fail(c, MGH_ERR_ARG, "algo must be MGH_ALGO_AUTO, _INT8 or _DEQ_F16");
     if (act < 0 || act > 2) return fail(c, MGH_ERR_ARG, "act must be 0 (none), 1 (gelu) or 2 (silu)");
     // the activation operands are built in aligned context scratch
+    if (algo == MGH_ALGO_AUTO) algo = MGH_ALGO_DEQ_F16;
     if (int r = check_packed_w(c, "gemm_q_packed_f32in", wtype, wp, N, K, M, bias, resid, y, true)) return r;
     if (M == 0) return MGH_OK;
     if (!x) return fail(c, MGH_ERR_ARG, "gemm_q_packed_f32in: null pointer");
@@ -504,6 +505,7 @@ int mgh_gemm_q_f32in(mgh_ctx* c, int algo, int wtype, const void* w, int N, int 
     if (algo != MGH_ALGO_AUTO && algo != MGH_ALGO_INT8 && algo != MGH_ALGO_DEQ_F16)
         return fail(c, MGH_ERR_ARG, "algo must be MGH_ALGO_AUTO, _INT8 or _DEQ_F16");
     if (act < 0 || act > 2) return fail(c, MGH_ERR_ARG, "act must be 0 (none), 1 (gelu) or 2 (silu)");
+    if (algo == MGH_ALGO_AUTO) algo = MGH_ALGO_DEQ_F16;
     if (M == 0) return MGH_OK;
     if (!x || !w || !y) return fail(c, MGH_ERR_ARG, "gemm_q_f32in: null pointer");
     if (int r = set_dev(c)) return r;
@@ -670,6 +672,81 @@ int mgh_copy_strided(mgh_ctx* c, const float* a, const int64_t ne[4], const int6
     if (!a || !out) return fail(c, MGH_ERR_ARG, "copy_strided: null pointer");
     if (int r = set_dev(c)) return r;
     MGH_HIP(c, mgh::launch_copy4d(a, ca, out, c->stream), "k_copy4d");
+    return MGH_OK;
+}
+
+int mgh_softmax(mgh_ctx* c, const float* x, int64_t rows, int D, float scale, float* y) {
+    if (!c) return MGH_ERR_ARG;
+    if (rows < 0 || D < 0) return fail(c, MGH_ERR_ARG, "softmax: need rows >= 0, D >= 0");
+    if (rows == 0 || D == 0) return MGH_OK;
+    if (!x || !y) return fail(c, MGH_ERR_ARG, "softmax: null pointer");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_softmax_rows(x, rows, D, scale, y, c->stream), "k_softmax_rows");
+    return MGH_OK;
+}
+
+int mgh_binary(mgh_ctx* c, int op, const float* a, const int64_t as[4], const float* b, const int64_t bne[4],
+               const int64_t bs[4], const int64_t ne[4], float* out) {
+    if (!c) return MGH_ERR_ARG;
+    if (op != 0 && op != 1) return fail(c, MGH_ERR_ARG, "binary: op must be 0 (add) or 1 (mul)");
+    if (!as || !bne || !bs || !ne) return fail(c, MGH_ERR_ARG, "binary: null shape");
+    mgh::BinaryArgs p{};
+    for (int i = 0; i < 4; i++) {
+        if (ne[i] <= 0) return fail(c, MGH_ERR_ARG, "binary: shape must be positive");
+        if (bne[i] != ne[i] && bne[i] != 1) return fail(c, MGH_ERR_ARG, "binary: b dims must equal the output's or be 1");
+        p.ne[i] = ne[i];
+        p.as[i] = as[i];
+        p.bne[i] = bne[i];
+        p.bs[i] = bs[i];
+    }
+    if (!a || !b || !out) return fail(c, MGH_ERR_ARG, "binary: null pointer");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_binary(op, a, b, p, out, c->stream), "k_binary");
+    return MGH_OK;
+}
+
+int mgh_scale(mgh_ctx* c, const float* x, int64_t n, float s, float* y) {
+    if (!c) return MGH_ERR_ARG;
+    if (n < 0) return fail(c, MGH_ERR_ARG, "scale: need n >= 0");
+    if (n == 0) return MGH_OK;
+    if (!x || !y) return fail(c, MGH_ERR_ARG, "scale: null pointer");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_unary(0, x, n, s, y, c->stream), "k_unary");
+    return MGH_OK;
+}
+
+int mgh_unary(mgh_ctx* c, int act, const float* x, int64_t n, float* y) {
+    if (!c) return MGH_ERR_ARG;
+    if (act != MGH_ACT_GELU && act != MGH_ACT_SILU) return fail(c, MGH_ERR_ARG, "unary: act must be GELU (1) or SiLU (2)");
+    if (n < 0) return fail(c, MGH_ERR_ARG, "unary: need n >= 0");
+    if (n == 0) return MGH_OK;
+    if (!x || !y) return fail(c, MGH_ERR_ARG, "unary: null pointer");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_unary(act, x, n, 0.0f, y, c->stream), "k_unary");
+    return MGH_OK;
+}
+
+int mgh_gemm_f32_batched(mgh_ctx* c, const float* w, const int64_t wne[4], const int64_t ws[4], const float* x,
+                         const int64_t xne[4], const int64_t xs[4], const float* bias, int act, const float* resid,
+                         float* y) {
+    if (!c) return MGH_ERR_ARG;
+    if (!wne || !ws || !xne || !xs) return fail(c, MGH_ERR_ARG, "gemm_f32_batched: null shape");
+    if (act < 0 || act > 2) return fail(c, MGH_ERR_ARG, "gemm_f32_batched: act must be 0, 1 or 2");
+    for (int i = 0; i < 4; i++)
+        if (wne[i] <= 0 || xne[i] <= 0) return fail(c, MGH_ERR_ARG, "gemm_f32_batched: shapes must be positive");
+    if (wne[0] != xne[0]) return fail(c, MGH_ERR_ARG, "gemm_f32_batched: w and x must share K (ne[0])");
+    if ((wne[2] != 1 && wne[2] != xne[2]) || (wne[3] != 1 && wne[3] != xne[3]))
+        return fail(c, MGH_ERR_ARG, "gemm_f32_batched: w batch dims must equal x's or be 1");
+    if (xne[2] * xne[3] > 65535) return fail(c, MGH_ERR_UNSUPPORTED, "gemm_f32_batched: at most 65535 batches");
+    if (!w || !x || !y) return fail(c, MGH_ERR_ARG, "gemm_f32_batched: null pointer");
+    mgh::BatchedGemmArgs a{};
+    a.w = w; a.x = x; a.bias = bias; a.resid = resid; a.y = y;
+    a.K = wne[0]; a.N = wne[1]; a.M = xne[1]; a.B2 = xne[2]; a.B3 = xne[3];
+    a.wne2 = wne[2]; a.wne3 = wne[3];
+    for (int i = 0; i < 4; i++) { a.ws[i] = ws[i]; a.xs[i] = xs[i]; }
+    a.act = act;
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_gemm_f32_batched(a, c->stream), "k_gemm_f32_batched");
     return MGH_OK;
 }
 

@@ -96,6 +96,29 @@ hipError_t launch_get_rows(const float* a, int64_t E, int64_t R, const int32_t* 
 hipError_t launch_add_bcast(const float* a, const float* b, int64_t nb, float* out, int64_t n,
                             hipStream_t s);
 hipError_t launch_copy4d(const float* a, const CopyArgs& c, float* out, hipStream_t s);
+// Remaining F32 graph ops (k_ops.hip). Element strides throughout; out is contiguous.
+struct BinaryArgs {
+    int64_t ne[4];         // output shape
+    int64_t as[4];         // a strides
+    int64_t bne[4];        // b shape (each dim equal to ne or 1: broadcast)
+    int64_t bs[4];         // b strides
+};
+struct BatchedGemmArgs {
+    const float* w;        // {K, N, wne2, wne3} with strides ws
+    const float* x;        // {K, M, B2, B3} with strides xs
+    const float* bias;     // [N] or null
+    const float* resid;    // [B3][B2][M][N] or null
+    float* y;              // [B3][B2][M][N]
+    int64_t K, N, M, B2, B3, wne2, wne3;
+    int64_t ws[4], xs[4];
+    int act;
+};
+hipError_t launch_softmax_rows(const float* x, int64_t rows, int D, float scale, float* y, hipStream_t s);
+hipError_t launch_binary(int op, const float* a, const float* b, const BinaryArgs& p, float* out, hipStream_t s);
+// op 0: y = x * sc; 1: GELU (erf); 2: SiLU
+hipError_t launch_unary(int op, const float* x, int64_t n, float sc, float* y, hipStream_t s);
+hipError_t launch_gemm_f32_batched(const BatchedGemmArgs& a, hipStream_t s);
+
 // Weight repack (k_pack_w.hip): raw Q8_0/Q4_K -> fp16 codes [N][K] | fp32 scale [K/32][N]
 // (| fp32 min [N][K/32] for Q4_K).
 size_t packed_weight_bytes(int wtype, int64_t N, int64_t K);

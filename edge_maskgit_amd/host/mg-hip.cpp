@@ -16,8 +16,10 @@
 //     decode step) and returns without waiting.
 // Leaves are uploaded once per (host address, byte size) and kept; quantized weights are
 // packed on upload (mgh_pack_weights for the int8-dot path, mgh_pack_weights_f16 for the
-// dequantize-fused path). Supported ops: MulMat (Q8_0, Q4_K, F32 weights),
-// Norm (plain or affine), FlashAttention, GetRows, Add, Cont, Reshape, View, Permute.
+// dequantize-fused path). Supported ops: MulMat (Q8_0, Q4_K; F32 weights, batched and
+// strided), Norm (plain or affine), SoftMax, FlashAttention, GetRows, Add, Mul, Scale, Gelu,
+// Silu, Cont, Reshape, View, Permute — the ops of the reference's GPU runtime outside the
+// VQGAN decoder (mg-opencl.cpp:1367-1534). Any other op throws (:1600-1601).
 #include "mg-hip.hpp"
 
 #include <algorithm>
@@ -41,9 +43,14 @@ const char* op_name(const Tensor* t) {
         case Op::MulMat:
             return (t->src[0]->type == Type::Q8_0 || t->src[0]->type == Type::Q4_K) ? "MulMat(q)" : "MulMat(f32)";
         case Op::Norm: return "Norm";
+        case Op::SoftMax: return "SoftMax";
         case Op::FlashAttention: return "FlashAttention";
         case Op::GetRows: return "GetRows";
         case Op::Add: return "Add";
+        case Op::Mul: return "Mul";
+        case Op::Scale: return "Scale";
+        case Op::Gelu: return "Gelu";
+        case Op::Silu: return "Silu";
         case Op::Cont: return "Cont";
         default: return "Other";
     }
@@ -54,7 +61,9 @@ const char* op_name(const Tensor* t) {
 struct HipRuntime::Impl {
     mgh_ctx* ctx = nullptr;
     std::string name;
-    int algo = MGH_ALGO_INT8;
+    // the reference's choice on a device without cl_arm_integer_dot_product (any non-Mali
+    // GPU): the dequant-fused path (mg-opencl.cpp:1237-1238, 1400-1423)
+    int algo = MGH_ALGO_DEQ_F16;
     bool profiling = false;
     std::map<std::string, std::pair<int, double>> prof;
 
@@ -340,7 +349,12 @@ const void* HipRuntime::run(Graph& g, bool readback) {
             const Tensor* p = t->src[0];
             if (p->op != Op::Permute || !p->src[0] || p->src[0]->op != Op::FlashAttention) continue;
             const Tensor* fa = p->src[0];
-            if (uses[fa] == 1 && uses[p] == 1 && fa->type == Type::F32) fa_into[t] = fa;
+            // only the head merge permute(0, 2, 1, 3): the attention then writes its output
+            // straight into the merged layout; any other view goes through the strided copy
+            const bool merge = p->ne[0] == fa->ne[0] && p->ne[1] == fa->ne[2] && p->ne[2] == fa->ne[1] &&
+                               p->ne[3] == fa->ne[3] && p->nb[0] == fa->nb[0] && p->nb[1] == fa->nb[2] &&
+                               p->nb[2] == fa->nb[1] && p->nb[3] == fa->nb[3] && fa->is_contiguous();
+            if (merge && uses[fa] == 1 && uses[p] == 1 && fa->type == Type::F32) fa_into[t] = fa;
         }
     }
     std::unordered_map<const Tensor*, const Tensor*> fa_target;  // FA -> cont it writes
@@ -455,9 +469,12 @@ const void* HipRuntime::run(Graph& g, bool readback) {
             const bool fc_out = t->op == Op::MulMat && quant(t->src[0]);
             if (!fa_out && !fc_out) continue;
             bool ok = !cons[t].empty();
+            // every consumer reads t only as its activations (not as weight, bias or residual)
             for (const Tensor* c : cons[t])
                 ok = ok && c->op == Op::MulMat && quant(c->src[0]) && I.root(c->src[1]) == t &&
-                     I.root(c->src[0]) != t;
+                     I.root(c->src[0]) != t && (!c->src[2] || I.root(c->src[2]) != t) &&
+                     (!c->src[3] || I.root(c->src[3]) != t) && c->src[1]->type == Type::F32 &&
+                     c->src[1]->is_contiguous();
             if (ok) emit16.insert(t);
         }
     }
@@ -480,6 +497,8 @@ const void* HipRuntime::run(Graph& g, bool readback) {
         if (grp_of.count(t)) {
             const std::vector<Tensor*>& grp = groups[grp_of.at(t)];
             const Tensor* x = t->src[1];
+            if (x->type != Type::F32 || !x->is_contiguous())
+                throw std::runtime_error("HipRuntime: MulMat needs a contiguous F32 input");
             const int K = (int)t->src[0]->ne[0];
             const int M = (int)(x->nelements() / K);
             int64_t Nt = 0;
@@ -508,8 +527,12 @@ const void* HipRuntime::run(Graph& g, bool readback) {
             out = I.dev(fa_into.at(t));                         // written by the attention
             I.addr[t] = out;
         } else if (t->op == Op::FlashAttention && fa_target.count(t)) {
-            out = I.take(fa_target.at(t)->nbytes());
+            // an fp16-only merged output (emit16) needs no fp32 buffer
+            out = emit16.count(fa_target.at(t)) ? nullptr : I.take(fa_target.at(t)->nbytes());
             I.addr[fa_target.at(t)] = out;
+            I.addr[t] = out;
+        } else if (t->op == Op::MulMat && emit16.count(t) && I.codes.count(I.root(t->src[1]))) {
+            out = nullptr;                                      // stored as fp16 only (below)
             I.addr[t] = out;
         } else {
             out = I.take(t->nbytes());
@@ -522,7 +545,30 @@ const void* HipRuntime::run(Graph& g, bool readback) {
             case Op::MulMat: {
                 const Tensor* w = t->src[0];
                 const Tensor* x = t->src[1];
-                if (x->type != Type::F32 || !x->is_contiguous())
+                if (x->type != Type::F32)
+                    throw std::runtime_error("HipRuntime: MulMat needs an F32 input");
+                // F32 weights: strided or batched operands (the unfused attention chain), and
+                // every product up to 2^28 multiply-adds, take the order-exact kernel (each
+                // output sums k in order with separate multiply and add, as the reference CPU
+                // executor, so the reference's absolute gates hold: tools/test-opencl.cpp:50);
+                // larger contiguous products (the tied MLM head) take the fp32 MFMA GEMM
+                const bool f32_exact = w->type == Type::F32 &&
+                                       (!x->is_contiguous() || !w->is_contiguous() || w->ne[2] != 1 ||
+                                        w->ne[3] != 1 || (double)w->ne[0] * w->ne[1] * (x->nelements() / x->ne[0]) <=
+                                                             (double)(1 << 28));
+                if (f32_exact) {
+                    // the reference's k_mul_mat_t contract (mg-opencl.cpp:60-94, 1429-1440)
+                    if (t->src[3] && !t->src[3]->is_contiguous())
+                        throw std::runtime_error("HipRuntime: MulMat residual must be contiguous");
+                    int64_t wst[4], xst[4];
+                    Impl::elem_strides(w, wst);
+                    Impl::elem_strides(x, xst);
+                    I.check(mgh_gemm_f32_batched(I.ctx, (const float*)I.dev(w), w->ne, wst, (const float*)I.dev(x), x->ne,
+                                                 xst, (const float*)I.dev(t->src[2]), t->iparam[0],
+                                                 (const float*)I.dev(t->src[3]), (float*)out));
+                    break;
+                }
+                if (!x->is_contiguous())
                     throw std::runtime_error("HipRuntime: MulMat needs a contiguous F32 input");
                 const int K = (int)w->ne[0], N = (int)w->ne[1];
                 const int M = (int)(x->nelements() / K);     // batch flattened into M
@@ -644,13 +690,52 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                                      (const int32_t*)I.dev(ids), ids->nelements(), (float*)out));
                 break;
             }
-            case Op::Add: {
+            case Op::Add:
+            case Op::Mul: {
+                // b broadcast over its size-1 dimensions (mg-cpu.cpp:27-38, k_add / k_mul
+                // mg-opencl.cpp:947-960)
                 const Tensor* a = t->src[0];
                 const Tensor* b = t->src[1];
-                if (!a->is_contiguous() || !b->is_contiguous() || a->nelements() % b->nelements())
-                    throw std::runtime_error("HipRuntime: Add needs contiguous operands with a repeating second one");
-                I.check(mgh_add(I.ctx, (const float*)I.dev(a), (const float*)I.dev(b), b->nelements(), (float*)out,
-                                a->nelements()));
+                if (a->type != Type::F32 || b->type != Type::F32)
+                    throw std::runtime_error("HipRuntime: Add/Mul need F32 operands");
+                bool prefix = a->is_contiguous() && b->is_contiguous(), ones = false;
+                for (int d = 0; d < 4; d++) {
+                    if (b->ne[d] != t->ne[d] && b->ne[d] != 1)
+                        throw std::runtime_error("HipRuntime: Add/Mul operand dims must match or be 1");
+                    if (ones) prefix = prefix && b->ne[d] == 1;
+                    else if (b->ne[d] != t->ne[d]) ones = true;
+                }
+                if (t->op == Op::Add && prefix) {   // b repeats as a whole (bias row, position table)
+                    I.check(mgh_add(I.ctx, (const float*)I.dev(a), (const float*)I.dev(b), b->nelements(),
+                                    (float*)out, a->nelements()));
+                } else {
+                    int64_t ast[4], bst[4];
+                    Impl::elem_strides(a, ast);
+                    Impl::elem_strides(b, bst);
+                    I.check(mgh_binary(I.ctx, t->op == Op::Mul ? 1 : 0, (const float*)I.dev(a), ast,
+                                       (const float*)I.dev(b), b->ne, bst, t->ne, (float*)out));
+                }
+                break;
+            }
+            case Op::SoftMax: {
+                const Tensor* x = t->src[0];
+                if (x->type != Type::F32 || !x->is_contiguous())
+                    throw std::runtime_error("HipRuntime: SoftMax needs a contiguous F32 input");
+                const int D = (int)t->ne[0];
+                I.check(mgh_softmax(I.ctx, (const float*)I.dev(x), t->nelements() / D, D, t->fparam[0], (float*)out));
+                break;
+            }
+            case Op::Scale:
+            case Op::Gelu:
+            case Op::Silu: {
+                const Tensor* x = t->src[0];
+                if (x->type != Type::F32 || !x->is_contiguous())
+                    throw std::runtime_error("HipRuntime: Scale/Gelu/Silu need a contiguous F32 input");
+                if (t->op == Op::Scale)
+                    I.check(mgh_scale(I.ctx, (const float*)I.dev(x), t->nelements(), t->fparam[0], (float*)out));
+                else
+                    I.check(mgh_unary(I.ctx, t->op == Op::Gelu ? MGH_ACT_GELU : MGH_ACT_SILU, (const float*)I.dev(x),
+                                      t->nelements(), (float*)out));
                 break;
             }
             case Op::Cont: {

@@ -176,6 +176,9 @@ std::unique_ptr<Model> Model::load(const std::string& path, Context& ctx) {
     if (r.get<uint32_t>() != 3) throw std::runtime_error("gguf: only version 3 is supported");
     const uint64_t n_tensors = r.get<uint64_t>();
     const uint64_t n_kv = r.get<uint64_t>();
+    // every tensor record takes at least 8 (name length) + 4 (rank) + 8 (one dim) + 4 (type) +
+    // 8 (offset) bytes: a count the file cannot hold is rejected before anything is sized by it
+    if (n_tensors > size / 32) throw std::runtime_error("gguf: tensor count larger than the file allows");
     uint32_t alignment = 32;
     for (uint64_t i = 0; i < n_kv; i++) GgufReader::kv(r, m->hp_, alignment);
 
@@ -192,7 +195,11 @@ std::unique_ptr<Model> Model::load(const std::string& path, Context& ctx) {
         in.n_dims = (int)r.get<uint32_t>();
         if (in.n_dims < 1 || in.n_dims > MAX_DIMS) throw std::runtime_error("gguf: bad rank for " + in.name);
         for (int d = 0; d < MAX_DIMS; d++) in.ne[d] = 1;
-        for (int d = 0; d < in.n_dims; d++) in.ne[d] = (int64_t)r.get<uint64_t>();
+        for (int d = 0; d < in.n_dims; d++) {
+            const uint64_t v = r.get<uint64_t>();
+            if (v == 0 || v > ((uint64_t)1 << 40)) throw std::runtime_error("gguf: bad dimension for " + in.name);
+            in.ne[d] = (int64_t)v;
+        }
         in.type = r.get<uint32_t>();
         in.offset = r.get<uint64_t>();
     }
@@ -207,8 +214,15 @@ std::unique_ptr<Model> Model::load(const std::string& path, Context& ctx) {
             case G_I4: t = Type::I4; break;
             default: throw std::runtime_error("gguf: unsupported tensor type for " + in.name);
         }
-        Tensor* x = ctx.external(t, in.n_dims, in.ne, const_cast<uint8_t*>(b) + data0 + in.offset);
-        if (data0 + in.offset + x->nbytes() > size) throw std::runtime_error("gguf: tensor past EOF: " + in.name);
+        // bounds without overflow: the data section starts inside the file, the offset lies
+        // in it, and the tensor's bytes fit after the offset; the pointer is formed only then
+        double elems = 1.0;
+        for (int d = 0; d < MAX_DIMS; d++) elems *= (double)in.ne[d];
+        if (elems > 1e15) throw std::runtime_error("gguf: tensor too large: " + in.name);
+        if (data0 > size || in.offset > size - data0) throw std::runtime_error("gguf: tensor past EOF: " + in.name);
+        Tensor* x = ctx.external(t, in.n_dims, in.ne, nullptr);
+        if (x->nbytes() > size - data0 - in.offset) throw std::runtime_error("gguf: tensor past EOF: " + in.name);
+        x->data = const_cast<uint8_t*>(b) + data0 + in.offset;
         x->name = in.name;
         m->tensors_[in.name] = x;
     }

@@ -55,11 +55,13 @@ size_t Tensor::nbytes() const {
     }
 }
 
+// Contiguous means every stride equals the packed stride, size-1 dimensions included
+// (reference src/mg-tensor.cpp:36-43).
 bool Tensor::is_contiguous() const {
     size_t s = type_size(type);
     for (int i = 0; i < MAX_DIMS; i++) {
         if (ne[i] == 0) return true;
-        if (ne[i] != 1 && nb[i] != s) return false;
+        if (nb[i] != s) return false;
         s *= (size_t)ne[i];
     }
     return true;
@@ -269,8 +271,11 @@ void visit(std::vector<Tensor*>& order, std::vector<const Tensor*>& seen, Tensor
 }
 }  // namespace
 
+// A graph holds the nodes of one output: building it again starts from an empty list
+// (reference src/mg-tensor.cpp:241).
 void Graph::build_forward(Tensor* out) {
-    std::vector<const Tensor*> seen(nodes.begin(), nodes.end());
+    nodes.clear();
+    std::vector<const Tensor*> seen;
     visit(nodes, seen, out);
 }
 

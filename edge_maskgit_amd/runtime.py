@@ -75,9 +75,10 @@ def graph_stats(path: str, S: int, B: int) -> tuple:
 
 
 class TransformerRuntime:
-    """A GGUF model on one GPU. algo: 1 = int8-dot FC layers, 2 = dequant-fp16."""
+    """A GGUF model on one GPU. algo: 2 = dequant-fp16 FC layers (default, the reference's
+    choice on a device without cl_arm_integer_dot_product), 1 = int8-dot."""
 
-    def __init__(self, path: str, device: int = 0, algo: int = 1):
+    def __init__(self, path: str, device: int = 0, algo: int = 2):
         h = ctypes.c_void_p()
         _check(lib().mgr_load(path.encode(), device, algo, ctypes.byref(h)))
         self.h = h

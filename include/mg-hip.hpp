@@ -49,8 +49,10 @@ public:
     void profile_reset();
     std::vector<OpProfile> profile_report() const;
 
-    // Algorithm for quantized FC weights: 1 = int8-dot (the reference's int8 path, default),
-    // 2 = dequantized weights x fp16 activations (its dequant-fused path).
+    // Algorithm for quantized FC weights: 2 = dequantized weights x fp16 activations (the
+    // default: the reference's dequant-fused path, which it takes on every device without
+    // cl_arm_integer_dot_product, mg-opencl.cpp:1237-1238, 1400-1423), 1 = int8-dot (its Mali
+    // int8 path, :1381-1398).
     void set_quant_algo(int algo);
 
     // ---- device-resident decoding: additions with no counterpart in OpenCLRuntime ----

@@ -35,7 +35,7 @@ inline constexpr int Q4_K_BYTES = 144;    // fp16 d, dmin + 12 B scales/mins + 1
 
 enum class Op {
     None = 0,
-    Add,             // src1 same shape, or a prefix repeating over the leading dims
+    Add,             // src1 broadcast over its size-1 dims (same shape, bias row, ...)
     Mul,
     Scale,           // fparam[0]
     MulMat,          // src[2] bias {N}, src[3] residual (shape of the output), iparam[0] act

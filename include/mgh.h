@@ -46,7 +46,9 @@ enum { MGH_ACT_NONE = 0, MGH_ACT_GELU = 1, MGH_ACT_SILU = 2 };
 /* GEMM algorithm for quantized weights. INT8 = per-32 int8 activation codes, exact block
  * dots (the reference's int8-dot path, mg-opencl.cpp:1381-1398); DEQ_F16 = fp16-rounded
  * activations against the dequantized weights, fp32 accumulation (the reference's
- * dequant-fused fp16-slab path, mg-opencl.cpp:1400-1423). AUTO = INT8. */
+ * dequant-fused fp16-slab path, mg-opencl.cpp:1400-1423). AUTO = DEQ_F16, the reference's
+ * choice on any device without cl_arm_integer_dot_product (mg-opencl.cpp:1237-1238), which
+ * includes this one. */
 enum { MGH_ALGO_AUTO = 0, MGH_ALGO_INT8 = 1, MGH_ALGO_DEQ_F16 = 2 };
 
 /* ---- context: replaces OpenCLRuntime::OpenCLRuntime / ~OpenCLRuntime / device_name
@@ -127,8 +129,8 @@ int mgh_gemm_q_packed(mgh_ctx* ctx, int wtype, const void* d_wp, int N, int K,
                       const float* d_bias, int act, const float* d_resid, float* d_y);
 
 /* ---- the whole MulMat(q) node on packed weights and fp32 activations (replaces the node
- *      dispatch mg-opencl.cpp:1367-1428): ALGO_AUTO/INT8 = per-32 int8 activation codes +
- *      mgh_gemm_q_packed; ALGO_DEQ_F16 = activations rounded to fp16 against the dequantized
+ *      dispatch mg-opencl.cpp:1367-1428): ALGO_INT8 = per-32 int8 activation codes +
+ *      mgh_gemm_q_packed; ALGO_AUTO/DEQ_F16 = activations rounded to fp16 against the dequantized
  *      weights (the reference's fp16-slab path k_mul_mat_*_t2_h, mg-opencl.cpp:320-411),
  *      same kernel. Activation operands live in context scratch (grown on demand, not during
  *      graph capture). Shape/alignment rules of mgh_gemm_q_packed; d_x 16-byte aligned. ---- */
@@ -199,6 +201,30 @@ int mgh_get_rows(mgh_ctx* ctx, const float* d_a, int64_t E, int64_t R, const int
 int mgh_add(mgh_ctx* ctx, const float* d_a, const float* d_b, int64_t nb, float* d_out, int64_t n);
 int mgh_copy_strided(mgh_ctx* ctx, const float* d_a, const int64_t ne[4], const int64_t strides[4],
                      float* d_out);
+
+/* ---- the remaining F32 graph ops of the reference's GPU runtime
+ *      (mg-opencl.cpp:1450-1534; CPU semantics mg-cpu.cpp:27-38, 40-45, 88-103, 150-163).
+ *      Strides are in elements; outputs are contiguous.
+ *      mgh_softmax: SoftMax over rows of D contiguous values, y = softmax(x * scale)
+ *        (k_soft_max :732-751); x and y may alias.
+ *      mgh_binary: out = a + b (op 0, Add) or a * b (op 1, Mul) over shape ne, a read with
+ *        a_strides, b of shape b_ne broadcast over its size-1 dimensions (k_add/k_mul
+ *        :947-960; the reference needs each b_ne[i] to be ne[i] or 1, so does this).
+ *      mgh_scale: y = x * s (Scale, k_scale :961-963).
+ *      mgh_unary: y = GELU(x) (act MGH_ACT_GELU, exact erf, k_gelu :964-967) or SiLU
+ *        (MGH_ACT_SILU, k_silu :968-971).
+ *      mgh_gemm_f32_batched: the stride-aware batched F32 MulMat (k_mul_mat_t :60-94, dispatch
+ *        :1429-1440): w {K, N, w_ne[2], w_ne[3]}, x {K, M, B2, B3}; w broadcasts over batch
+ *        dimensions of size 1; y [B3][B2][M][N] = act(w . x + bias) + resid. Each output sums
+ *        over k in order with separate multiply and add, as the reference CPU executor. ---- */
+int mgh_softmax(mgh_ctx* ctx, const float* d_x, int64_t rows, int D, float scale, float* d_y);
+int mgh_binary(mgh_ctx* ctx, int op, const float* d_a, const int64_t a_strides[4], const float* d_b,
+               const int64_t b_ne[4], const int64_t b_strides[4], const int64_t ne[4], float* d_out);
+int mgh_scale(mgh_ctx* ctx, const float* d_x, int64_t n, float s, float* d_y);
+int mgh_unary(mgh_ctx* ctx, int act, const float* d_x, int64_t n, float* d_y);
+int mgh_gemm_f32_batched(mgh_ctx* ctx, const float* d_w, const int64_t w_ne[4], const int64_t w_strides[4],
+                         const float* d_x, const int64_t x_ne[4], const int64_t x_strides[4],
+                         const float* d_bias, int act, const float* d_resid, float* d_y);
 
 /* ---- dequantize-fused fp16 FC path: the reference's fp16-slab dequant GEMMs
  *      k_mul_mat_q8_0_t2_h / k_mul_mat_q4k_t2_h (src/mg-opencl/mg-opencl.cpp:320-411).

@@ -17,7 +17,8 @@ extern "C" {
 
 typedef struct mgr_model mgr_model;
 
-/* algo: 1 = int8-dot FC (default), 2 = dequantized weights x fp16 activations */
+/* algo: 0 = default (2), 1 = int8-dot FC, 2 = dequantized weights x fp16 activations (the
+ * reference's choice on a device without cl_arm_integer_dot_product, mg-opencl.cpp:1237-1238) */
 int mgr_load(const char* gguf_path, int device, int algo, mgr_model** out);
 void mgr_free(mgr_model* m);
 const char* mgr_last_error(void);

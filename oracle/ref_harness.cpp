@@ -9,6 +9,8 @@
 #include "mg-tensor.hpp"
 #include "mg-transformer.hpp"
 
+#include "graph_cases.h"
+
 #include <cstdint>
 #include <cstring>
 #include <exception>
@@ -96,6 +98,19 @@ int mgref_transformer_forward(const char* gguf_path, const int32_t* tokens, int6
         if (out->nelements() != logits_len) { g_err = "logits size mismatch"; return -2; }
         Graph g; g.build_forward(out); compute(ctx, g);
         std::memcpy(logits, out->data, (size_t)logits_len * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) { g_err = e.what(); return -1; }
+}
+
+// The graphs of graph_cases.h on the reference CPU executor (the same source HipRuntime runs
+// in tests/graph_harness.cpp). which 0: ffn(K=a, S=b, F=c); 1: ops(D=a, H=b, S=c, B=d).
+int mgref_graph_case(int which, int64_t a, int64_t b, int64_t c, int64_t d, float* out, int64_t out_len) {
+    try {
+        Context ctx((size_t)512 << 20);
+        Tensor* o = which == 0 ? graph_cases::ffn(ctx, a, b, c) : graph_cases::ops(ctx, a, b, c, d);
+        if (o->nelements() != out_len) { g_err = "output size mismatch"; return -2; }
+        Graph g; g.build_forward(o); compute(ctx, g);
+        std::memcpy(out, o->data, (size_t)out_len * sizeof(float));
         return 0;
     } catch (const std::exception& e) { g_err = e.what(); return -1; }
 }

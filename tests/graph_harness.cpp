@@ -1,0 +1,67 @@
+// graph_harness.cpp — runs the graphs of oracle/graph_cases.h through mg::HipRuntime
+// (TEST INFRASTRUCTURE ONLY). The same graph source runs on the reference CPU executor in
+// oracle/ref_harness.cpp; tests/test_gpu_graph.py compares the two. Built by
+// __graft_entry__.build() into tests/_build/libgraph_harness.so.
+#include "mg-hip.hpp"
+#include "mg-tensor.hpp"
+
+#include "graph_cases.h"
+
+#include <cstdint>
+#include <cstring>
+#include <exception>
+#include <string>
+
+namespace {
+std::string g_err;
+}
+
+extern "C" {
+
+const char* gh_last_error() { return g_err.c_str(); }
+
+// which 0: ffn(K=a, S=b, F=c); 1: ops(D=a, H=b, S=c, B=d). out receives the final node.
+int gh_graph_case(int which, int64_t a, int64_t b, int64_t c, int64_t d, float* out, int64_t out_len) {
+    try {
+        mg::Context ctx((size_t)512 << 20);
+        mg::Tensor* o = which == 0 ? graph_cases::ffn(ctx, a, b, c) : graph_cases::ops(ctx, a, b, c, d);
+        if (o->nelements() != out_len) { g_err = "output size mismatch"; return -2; }
+        mg::Graph g;
+        g.build_forward(o);
+        mg::HipRuntime rt;
+        rt.compute(g);
+        std::memcpy(out, o->data, (size_t)out_len * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
+// Host-only checks of the graph API semantics (no device): returns 0 or the first failed check.
+//  1: build_forward starts from an empty node list (reference src/mg-tensor.cpp:241)
+//  2: a view whose size-1 dimension carries a non-packed stride is not contiguous
+//     (reference src/mg-tensor.cpp:36-43)
+//  3: a contiguous tensor and a reshape of it are contiguous; quantized tensors (all strides 0)
+//     are contiguous
+int gh_api_checks() {
+    mg::Context c(1 << 20);
+    mg::Tensor* a = c.tensor2d(mg::Type::F32, 8, 4);
+    mg::Tensor* b = c.tensor2d(mg::Type::F32, 8, 4);
+    mg::Tensor* s1 = mg::add(c, a, b);
+    mg::Tensor* s2 = mg::gelu(c, mg::scale(c, a, 2.0f));
+    mg::Graph g;
+    g.build_forward(s1);
+    g.build_forward(s2);
+    if (g.nodes.size() != 2 || g.nodes[0]->op != mg::Op::Scale || g.nodes[1] != s2) return 1;
+    mg::Tensor* t = c.tensor3d(mg::Type::F32, 8, 1, 4);
+    mg::Tensor* p = mg::permute(c, t, 0, 2, 1, 3);      // {8, 4, 1}: dim 2 has stride 32 B
+    if (p->ne[2] != 1 || p->is_contiguous()) return 2;
+    if (!t->is_contiguous() || !mg::reshape(c, t, {32})->is_contiguous()) return 3;
+    const int64_t qne[4] = {256, 2, 1, 1};
+    mg::Tensor* q = c.external(mg::Type::Q8_0, 2, qne, nullptr);
+    if (!q->is_contiguous()) return 3;
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,258 @@
+"""GPU parity of the F32 graph ops HipRuntime runs besides the FC path — SoftMax, Add/Mul with
+broadcasting, Scale, Gelu, Silu and the batched, strided F32 MulMat (the reference's
+OpenCLRuntime::compute, src/mg-opencl/mg-opencl.cpp:1429-1534) — first through the C ABI
+against numpy restatements of the reference CPU executor (src/mg-cpu/mg-cpu.cpp), then as
+whole graphs through mg::HipRuntime against the reference CPU executor itself
+(oracle/_ref, the same graph source oracle/graph_cases.h compiled against the reference's
+headers).
+
+Bars:
+  * Scale, Add, Mul, and the raw sums of the batched F32 MulMat: bit-exact (the kernels round
+    every product and sum as the scalar CPU loop does, k in order).
+  * SoftMax: within 1e-6 of float64 per element (from the fp32 x * scale the reference forms;
+    the row sum is a tree, not a loop).
+  * Gelu / Silu: within 1e-6 * max(1, |y|) of float64 (library erf / exp; near GELU's
+    negative tail 1 + erf(x) in fp32 carries the rounding of erf(x)).
+  * Graphs: the reference's own acceptance gates — the FFN graph of its GPU harness
+    (tools/test-opencl.cpp:50: max|d| < 1e-3, cos > 0.999999) and, for the transformer with the
+    unfused attention chain (MG_NO_FLASH_ATTN, src/mg-transformer.cpp:55, 75-81), its F32
+    transformer gate (tools/verify-opencl-transformer.cpp:98-101: max|d| < 2e-2,
+    cos > 0.99999).
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+import edge_maskgit_amd as ema
+from oracle import forward as ofwd
+from oracle import ref
+from tests import mg_gguf
+from edge_maskgit_amd import runtime as rt
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HARNESS = os.path.join(ROOT, "tests", "_build", "libgraph_harness.so")
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = ema.Context(0)
+    yield c
+    c.close()
+
+
+def _cos(a, b):
+    a, b = a.ravel().astype(np.float64), b.ravel().astype(np.float64)
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def _span(ne, st):
+    """one past the largest element index a view {ne} with element strides st touches"""
+    return 1 + sum((n - 1) * s for n, s in zip(ne, st))
+
+
+def _view(base, ne, st):
+    """numpy view of flat `base` with mg shape ne (innermost first) and element strides st"""
+    assert _span(ne, st) <= base.size
+    return np.lib.stride_tricks.as_strided(base, shape=tuple(reversed(ne)),
+                                           strides=tuple(4 * s for s in reversed(st)))
+
+
+# ---- kernels through the C ABI ---------------------------------------------------------
+@pytest.mark.parametrize("rows,D,scale", [(1, 1, 1.0), (37, 257, 0.1443), (5, 1024, 1.0), (64, 63, 3.0)])
+def test_softmax(ctx, rows, D, scale):
+    print(f"softmax rows={rows} D={D}", flush=True)
+    x = (np.random.default_rng(D).standard_normal((rows, D)) * 4).astype(np.float32)
+    dX, dY = ctx.upload(x), ctx.alloc(x.nbytes)
+    ctx.softmax(dX, rows, D, scale, dY)
+    y = ctx.download(dY, x.shape, np.float32)
+    t = (x * np.float32(scale)).astype(np.float64)
+    e = np.exp(t - t.max(axis=1, keepdims=True))
+    want = e / e.sum(axis=1, keepdims=True)
+    print(f"  max|d| {np.abs(y - want).max():.2e}")
+    assert np.abs(y - want).max() <= 1e-6
+    ctx.softmax(dX, rows, D, scale, dX)            # in place
+    assert np.array_equal(ctx.download(dX, x.shape, np.float32), y)
+
+
+@pytest.mark.parametrize("op", [0, 1])
+def test_binary_broadcast(ctx, op):
+    """out {8,6,5,3} = a (op) b: a is a transposed view, b broadcasts over dims 0 and 2."""
+    print(f"binary op={op}", flush=True)
+    rng = np.random.default_rng(op)
+    ne = (8, 6, 5, 3)
+    base = rng.standard_normal(8 * 6 * 5 * 3).astype(np.float32)
+    ast = (6, 1, 48, 240)                         # dims 0 and 1 swapped
+    bne = (1, 6, 1, 3)
+    b = rng.standard_normal(18).astype(np.float32)
+    bst = (1, 1, 6, 6)
+    av = _view(base, ne, ast)
+    bv = _view(b, bne, bst)
+    want = (av * bv if op else av + bv).astype(np.float32)
+    dA, dB, dO = ctx.upload(base), ctx.upload(b), ctx.alloc(want.nbytes)
+    ctx.binary(op, dA, ast, dB, bne, bst, ne, dO)
+    got = ctx.download(dO, want.shape, np.float32)
+    assert np.array_equal(got, want)
+
+
+def test_scale_gelu_silu(ctx):
+    print("scale / gelu / silu", flush=True)
+    x = np.concatenate([np.linspace(-12, 12, 4001, dtype=np.float32),
+                        (np.random.default_rng(3).standard_normal(999) * 3).astype(np.float32)])
+    n = x.size
+    dX, dY = ctx.upload(x), ctx.alloc(x.nbytes)
+    ctx.scale(dX, n, 0.75, dY)
+    assert np.array_equal(ctx.download(dY, x.shape, np.float32), x * np.float32(0.75))
+    from math import erf
+    xd = x.astype(np.float64)
+    for act, want in ((ema.ACT_GELU, 0.5 * xd * (1 + np.array([erf(v / np.sqrt(2)) for v in xd]))),
+                      (ema.ACT_SILU, xd / (1 + np.exp(-xd)))):
+        ctx.unary(act, dX, n, dY)
+        y = ctx.download(dY, x.shape, np.float32)
+        err = float((np.abs(y - want) / np.maximum(1.0, np.abs(want))).max())
+        print(f"  act {act}: max rel {err:.2e}")
+        assert err <= 1e-6
+
+
+def _mul_mat_seq(wv, xv, bias=None, resid=None):
+    """the CPU executor's k loop: acc += w[k] * x[k] in float32, in order (mg-cpu.cpp:48-72).
+    wv: (W3, W2, N, K), xv: (B3, B2, M, K) -> (B3, B2, M, N)"""
+    K = wv.shape[-1]
+    w = np.broadcast_to(wv, xv.shape[:2] + wv.shape[2:])
+    acc = np.zeros(xv.shape[:2] + (xv.shape[2], w.shape[2]), np.float32)
+    for k in range(K):
+        acc = acc + (xv[..., :, k][..., :, None] * w[..., :, k][..., None, :])
+    if bias is not None:
+        acc = acc + bias
+    if resid is not None:
+        acc = acc + resid
+    return acc
+
+
+@pytest.mark.parametrize("case", ["attn_scores", "attn_values", "w_broadcast", "epilogue"])
+def test_gemm_f32_batched(ctx, case):
+    """the unfused attention products on strided head views, a weight broadcast over the batch,
+    and the bias + residual epilogue; raw sums bit-exact against the sequential CPU loop"""
+    print(f"gemm_f32_batched {case}", flush=True)
+    rng = np.random.default_rng(len(case))
+    D, H, S, B = 48, 3, 37, 2
+    bias = resid = None
+    if case in ("attn_scores", "attn_values"):
+        kq = rng.standard_normal(D * H * S * B).astype(np.float32)    # [B][S][H*D] linear output
+        hs = (1, D * H, D, D * H * S)                                 # {D,S,H,B} head view strides
+        if case == "attn_scores":                                     # mul_mat(k, q)
+            wne, wst, xne, xst = (D, S, H, B), hs, (D, S, H, B), hs
+            wbase = xbase = kq
+        else:                                                         # mul_mat(permute(v,1,0,2,3), s)
+            wne, wst = (S, D, H, B), (D * H, 1, D, D * H * S)
+            wbase = kq
+            xbase = rng.standard_normal(S * S * H * B).astype(np.float32)
+            xne, xst = (S, S, H, B), (1, S, S * S, S * S * H)
+    elif case == "w_broadcast":
+        K, N, M = 67, 19, 23
+        wbase = rng.standard_normal(K * N * 3).astype(np.float32)
+        wne, wst = (K, N, 3, 1), (1, K, K * N, K * N * 3)
+        xbase = rng.standard_normal(K * M * 3 * 2).astype(np.float32)
+        xne, xst = (K, M, 3, 2), (1, K, K * M, K * M * 3)
+    else:
+        K, N, M = 130, 70, 66
+        wbase = rng.standard_normal(K * N).astype(np.float32)
+        wne, wst = (K, N, 1, 1), (N, 1, K * N, K * N)                 # transposed weight view
+        xbase = rng.standard_normal(K * M * 2).astype(np.float32)
+        xne, xst = (K, M, 2, 1), (1, K, K * M, K * M * 2)
+        bias = rng.standard_normal(N).astype(np.float32)
+        resid = rng.standard_normal((1, 2, M, N)).astype(np.float32)
+    wv = _view(wbase, wne, wst)       # (W3, W2, N, K)
+    xv = _view(xbase, xne, xst)       # (B3, B2, M, K)
+    want = _mul_mat_seq(wv, xv, bias, resid)
+    dW, dX, dY = ctx.upload(wbase), ctx.upload(xbase), ctx.alloc(want.nbytes)
+    dB = ctx.upload(bias) if bias is not None else None
+    dR = ctx.upload(resid) if resid is not None else None
+    ctx.gemm_f32_batched(dW, wne, wst, dX, xne, xst, dB, 0, dR, dY)
+    got = ctx.download(dY, want.shape, np.float32)
+    assert np.array_equal(got, want)
+    if case == "epilogue":                          # GELU between bias and residual
+        ctx.gemm_f32_batched(dW, wne, wst, dX, xne, xst, dB, ema.ACT_GELU, dR, dY)
+        got = ctx.download(dY, want.shape, np.float32)
+        from math import erf
+        v = (want - resid).astype(np.float64)
+        g = 0.5 * v * (1 + np.vectorize(erf)(v / np.sqrt(2))) + resid
+        assert float(np.abs(got - g).max() / np.abs(g).max()) <= 1e-6
+
+
+# ---- whole graphs through HipRuntime vs the reference CPU executor ------------------------
+def _harness():
+    if not os.path.exists(HARNESS):
+        pytest.fail(f"{HARNESS} missing: run __graft_entry__.build()")
+    L = ctypes.CDLL(HARNESS)
+    L.gh_graph_case.argtypes = [ctypes.c_int] + [ctypes.c_int64] * 4 + [ctypes.c_void_p, ctypes.c_int64]
+    L.gh_last_error.restype = ctypes.c_char_p
+    return L
+
+
+def _ref_case(which, dims, n):
+    L = ref.lib()
+    L.mgref_graph_case.argtypes = [ctypes.c_int] + [ctypes.c_int64] * 4 + [ctypes.c_void_p, ctypes.c_int64]
+    out = np.empty(n, np.float32)
+    rc = L.mgref_graph_case(which, *dims, out.ctypes.data_as(ctypes.c_void_p), n)
+    assert rc == 0, L.mgref_last_error().decode()
+    return out
+
+
+@pytest.mark.parametrize("which,dims,n", [(0, (768, 16, 3072, 0), 768 * 16),
+                                          (1, (48, 4, 37, 2), 48 * 37 * 4 * 2)])
+def test_graph_vs_reference_cpu(which, dims, n):
+    """0: the FFN graph of the reference's GPU harness (mul_mat -> add_bias -> gelu -> mul_mat
+    -> add_bias, K=768, S=16, F=3072); 1: strided batched products, SoftMax, broadcast Mul,
+    Scale, Silu, Gelu and Add in one graph"""
+    if not ref.available():
+        pytest.skip("oracle/_ref (the reference CPU build) is not present")
+    print(f"graph case {which} dims={dims}", flush=True)
+    L = _harness()
+    got = np.empty(n, np.float32)
+    rc = L.gh_graph_case(which, *dims, got.ctypes.data_as(ctypes.c_void_p), n)
+    assert rc == 0, L.gh_last_error().decode()
+    want = _ref_case(which, dims, n)
+    d, c = float(np.abs(got - want).max()), _cos(got, want)
+    print(f"  max|d| {d:.3e} cos {c:.9f}")
+    assert d < 1e-3 and c > 0.999999
+
+
+@pytest.fixture
+def no_flash_attn(monkeypatch):
+    monkeypatch.setenv("MG_NO_FLASH_ATTN", "1")
+
+
+def test_forward_unfused_attention_f32(tmp_path, no_flash_attn):
+    """MG_NO_FLASH_ATTN: mul_mat(k, q) -> soft_max -> mul_mat(v^T, s) per layer, F32 weights,
+    against the reference CPU executor building the same graph under the same environment"""
+    if not ref.available():
+        pytest.skip("oracle/_ref (the reference CPU build) is not present")
+    path = str(tmp_path / "m_f32.gguf")
+    mg_gguf.write_model(path, n_layer=2, quant="f32", seed=5)
+    tok = mg_gguf.tokens(np.random.default_rng(21), 257, 1)
+    print("forward f32 unfused attention S=257 B=1", flush=True)
+    with rt.TransformerRuntime(path) as m:
+        got = m.forward(tok)
+    want = ref.transformer_forward(path, tok, 2025)
+    d, c = float(np.abs(got - want).max()), _cos(got, want)
+    print(f"  max|d| {d:.3e} cos {c:.9f}")
+    assert d < 2e-2 and c > 0.99999
+
+
+def test_forward_unfused_attention_q8_0(tmp_path, no_flash_attn):
+    """the same chain with Q8_0 FC weights on the dequantize-fused path: within 1e-3 of
+    dequantize-then-F32 with fp32 attention (the oracle forward)"""
+    path = str(tmp_path / "m_q8.gguf")
+    t = mg_gguf.write_model(path, n_layer=2, quant="q8_0", seed=6)
+    tok = mg_gguf.tokens(np.random.default_rng(22), 257, 2)
+    print("forward q8_0 unfused attention S=257 B=2", flush=True)
+    with rt.TransformerRuntime(path, algo=2) as m:
+        got = m.forward(tok)
+    want = ofwd.transformer_forward(t, 2, 16, tok, quant="q8_0", algo="deq", f16kv=False)
+    err = float(np.abs(got - want).max() / np.abs(want).max())
+    print(f"  rel err {err:.2e}")
+    assert err <= 1e-3

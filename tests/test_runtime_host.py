@@ -56,6 +56,56 @@ def test_forward_graph_structure(f32_model):
     assert n == int(c.sum())
 
 
+def test_forward_graph_structure_unfused_attention(f32_model, monkeypatch):
+    """MG_NO_FLASH_ATTN (mg-transformer.cpp:55, 75-81): per layer the attention is
+    mul_mat(k, q) -> soft_max -> mul_mat(permute(v), scores), no FlashAttention node."""
+    path, _ = f32_model
+    monkeypatch.setenv("MG_NO_FLASH_ATTN", "1")
+    n, c = rt.graph_stats(path, 257, 1)
+    OP = dict(MulMat=4, SoftMax=6, FlashAttention=13, Permute=16, Cont=17)
+    L = 2
+    assert c[OP["MulMat"]] == 8 * L + 2
+    assert c[OP["SoftMax"]] == L and c[OP["FlashAttention"]] == 0
+    assert c[OP["Permute"]] == 5 * L and c[OP["Cont"]] == L
+    assert n == int(c.sum())
+
+
+def test_sequence_longer_than_position_table_rejected(f32_model):
+    """the position table is viewed as its first S rows: S beyond its 257 rows is an error, not
+    a read past the tensor"""
+    path, _ = f32_model
+    rt.graph_stats(path, 257, 1)
+    with pytest.raises(Exception, match="position table"):
+        rt.graph_stats(path, 258, 1)
+
+
+def test_gguf_rejects_malformed_files(f32_model, tmp_path):
+    """truncated data, an impossible tensor count and a zero dimension are reported, never
+    mapped past the end of the file"""
+    import struct
+    from edge_maskgit_amd import MghError
+    path, _ = f32_model
+    raw = open(path, "rb").read()
+    cut = tmp_path / "cut.gguf"
+    cut.write_bytes(raw[: len(raw) - 4096])
+    with pytest.raises(MghError, match="past EOF"):
+        rt.gguf_info(str(cut))
+    many = tmp_path / "many.gguf"
+    many.write_bytes(raw[:8] + struct.pack("<Q", 1 << 60) + raw[16:])
+    with pytest.raises(MghError, match="tensor count"):
+        rt.gguf_info(str(many))
+
+
+def test_graph_api_semantics():
+    """build_forward restarts the node list, contiguity is strict on size-1 dimensions, as the
+    reference's graph core (checks in tests/graph_harness.cpp, host only)"""
+    import ctypes
+    lib = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_build", "libgraph_harness.so")
+    if not os.path.exists(lib):
+        pytest.fail(f"{lib} missing: run __graft_entry__.build()")
+    assert ctypes.CDLL(lib).gh_api_checks() == 0
+
+
 @pytest.mark.skipif(not ref.available(), reason="oracle/_ref/libmgref.so not built (needs /root/reference)")
 def test_oracle_forward_matches_reference_cpu(f32_model):
     """The oracle forward (F32 weights, F32 attention) against the reference's own CPU
