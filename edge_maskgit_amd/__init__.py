@@ -39,6 +39,7 @@ MGH_SYMBOLS = [
     "mgh_decode_step", "mgh_packed_weight_bytes_f16", "mgh_pack_weights_f16", "mgh_f32_to_f16",
     "mgh_gemm_h16", "mgh_gemm_h16_f32in", "mgh_gemm_h16_y16", "mgh_flash_attn_f16kv_o16", "mgh_flash_attn_f16in",
     "mgh_softmax", "mgh_binary", "mgh_scale", "mgh_unary", "mgh_gemm_f32_batched",
+    "mgh_gemm_h16_f32in_noalloc",
 ]
 
 _lib = None
@@ -103,6 +104,7 @@ def lib():
         L.mgh_gemm_h16.argtypes = [P, P, I, I, P, I, P, I, P, P]
         L.mgh_gemm_h16_f32in.argtypes = [P, P, I, I, P, I, P, I, P, P]
         L.mgh_gemm_h16_y16.argtypes = [P, P, I, I, P, I, P, I, P, P]
+        L.mgh_gemm_h16_f32in_noalloc.argtypes = [P, P, I, I, P, I, P, I, P, P]
         L.mgh_flash_attn_f16kv_o16.argtypes = [P, P, P, P, P, I, I, I, I, ctypes.c_float, P, P]
         L.mgh_flash_attn_f16in.argtypes = [P, P, P, P, P, I, I, I, I, ctypes.c_float, P, P, P]
         L.mgh_decode_state_bytes.argtypes = [I]
@@ -333,6 +335,12 @@ class Context:
     def gemm_h16_f32in(self, wp16, N, K, x, M, bias, act, resid, y):
         P = self._ptr
         self._check(lib().mgh_gemm_h16_f32in(self.h, P(wp16), N, K, P(x), M, P(bias), act, P(resid), P(y)))
+
+    def gemm_h16_f32in_noalloc(self, wp16, N, K, x, M, bias, act, resid, y):
+        """mgh_gemm_h16_f32in with its scratch in the library's fixed per-GPU array."""
+        P = self._ptr
+        self._check(lib().mgh_gemm_h16_f32in_noalloc(self.h, P(wp16), N, K, P(x), M, P(bias), act, P(resid),
+                                                     P(y)))
 
     def decode_init(self, seeds, state):
         """seeds: host sequence of B uint64 seeds; state: mgh_decode_state_bytes(B) bytes."""

@@ -867,6 +867,40 @@ int mgh_gemm_h16_f32in(mgh_ctx* c, const void* wp16, int N, int K, const float* 
     return run_gemm_h16(c, a);
 }
 
+int mgh_gemm_h16_f32in_noalloc(mgh_ctx* c, const void* wp16, int N, int K, const float* x, int M,
+                               const float* bias, int act, const float* resid, float* y) {
+    if (!c) return MGH_ERR_ARG;
+    if (int r = check_h16(c, "gemm_h16_f32in_noalloc", wp16, N, K, x, M, bias, act, resid, y)) return r;
+    if (M == 0) return MGH_OK;
+    // the same launches as mgh_gemm_h16_f32in, with the rounded activations (M >= 2048) and the
+    // split-K partials placed in the fixed scratch array instead of context buffers
+    mgh::GemmH16Args a{};
+    a.w = (const _Float16*)wp16;
+    a.bias = bias; a.resid = resid; a.y = y;
+    a.M = M; a.N = N; a.K = K; a.act = act;
+    const bool round_pass = M >= 2048;
+    const size_t x16_b = round_pass ? round256((size_t)M * K * 2) : 0;
+    const mgh::H16Plan p = mgh::gemm_h16_plan(M, N, K, !round_pass);
+    const size_t need = x16_b + (p.splits > 1 ? round256(p.ws_bytes) : 0);
+    const size_t cap = mgh::noalloc_scratch_bytes();
+    if (need > cap)
+        return fail(c, MGH_ERR_UNSUPPORTED, "gemm_h16_f32in_noalloc: this shape needs " + std::to_string(need) +
+                                                " bytes of scratch, the maximum is " + std::to_string(cap));
+    if (int r = set_dev(c)) return r;
+    void* base = nullptr;
+    MGH_HIP(c, mgh::noalloc_scratch(c->device, &base), "hipGetSymbolAddress(scratch)");
+    if (round_pass) {
+        MGH_HIP(c, mgh::launch_f32_to_f16(x, (_Float16*)base, (int64_t)M * K, c->stream), "k_f32_to_f16");
+        a.x = (const _Float16*)base;
+    } else {
+        a.xf = x;
+    }
+    a.splits = p.splits;
+    if (p.splits > 1) a.ws = (float*)((char*)base + x16_b);
+    MGH_HIP(c, mgh::launch_gemm_h16(p, a, c->stream), "k_gemm_h16");
+    return MGH_OK;
+}
+
 int mgh_debug_block_dots(mgh_ctx* c, int wtype, const void* w, int N, int K, const int8_t* qx,
                          int M, int32_t* out) {
     if (!c) return MGH_ERR_ARG;

@@ -180,4 +180,9 @@ hipError_t launch_pack_weights_f16(int wtype, const void* w, void* out, int N, i
 hipError_t launch_f32_to_f16(const float* x, _Float16* h, int64_t n, hipStream_t s);
 hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a, hipStream_t s);
 
+// Scratch of the no-allocation entry point (noalloc.hip): the device address of this device's
+// copy of a fixed-size file-scope array, looked up once per device.
+size_t noalloc_scratch_bytes();
+hipError_t noalloc_scratch(int device, void** out);
+
 }  // namespace mgh

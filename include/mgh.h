@@ -243,6 +243,15 @@ int mgh_gemm_h16(mgh_ctx* ctx, const void* d_wp16, int N, int K, const void* d_x
                  const float* d_bias, int act, const float* d_resid, float* d_y);
 int mgh_gemm_h16_f32in(mgh_ctx* ctx, const void* d_wp16, int N, int K, const float* d_x, int M,
                        const float* d_bias, int act, const float* d_resid, float* d_y);
+/* mgh_gemm_h16_f32in for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): identical launches and
+ * results, with the rounded activations and split-K partials in a fixed 64 MiB scratch array
+ * the library holds on each GPU it runs on (no hipMalloc/hipFree, no context buffer growth).
+ * Shapes whose scratch exceeds 64 MiB return MGH_ERR_UNSUPPORTED before anything runs. All
+ * calls on one GPU share that array: calls that overlap on one GPU race. No counterpart in the
+ * reference (its runtime grows scratch buffers on demand, mg-opencl.cpp:1130-1134). */
+int mgh_gemm_h16_f32in_noalloc(mgh_ctx* ctx, const void* d_wp16, int N, int K, const float* d_x, int M,
+                               const float* d_bias, int act, const float* d_resid, float* d_y);
 /* the same product stored rounded to fp16 (d_y16 [M][N]): the operand of a following
  * dequantize-fused FC (no counterpart in the reference, where the next FC rounds its fp32
  * input; the result is identical) */
