@@ -32,6 +32,8 @@ def lib():
         L.mgref_norm_affine.argtypes = [P, I64, I64, P, P, ctypes.c_float, P]
         L.mgref_attention.argtypes = [P, P, P, I64, I64, I64, I64, ctypes.c_float, P]
         L.mgref_transformer_forward.argtypes = [ctypes.c_char_p, P, I64, I64, P, I64]
+        L.mgref_generate.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_uint64, ctypes.c_int,
+                                     ctypes.c_float, P, P, P]
         _lib = L
     return _lib
 
@@ -80,3 +82,15 @@ def transformer_forward(gguf_path: str, tokens, vocab: int):
     out = np.empty((B, S, vocab), np.float32)
     _check(lib().mgref_transformer_forward(gguf_path.encode(), _p(tokens), S, B, _p(out), out.size))
     return out
+
+
+def generate(gguf_path: str, class_id: int, seed: int, steps: int, temperature: float, logits):
+    """The reference's generate() loop with the caller's logits per step ([steps][S][vocab]):
+    returns (tokens fed to each step's forward [steps][S], final grid [S-1])."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    S = logits.shape[1]
+    toks = np.empty((steps, S), np.int32)
+    grid = np.empty(S - 1, np.int32)
+    _check(lib().mgref_generate(gguf_path.encode(), class_id, seed, steps, temperature, _p(logits),
+                                _p(toks), _p(grid)))
+    return toks, grid

@@ -5,6 +5,7 @@
 // tests and bench.py's cpu_baseline leg load it. Each function builds the same graph the
 // reference builds and runs the reference's mg::compute (src/mg-cpu/mg-cpu.cpp:296-298),
 // so its results are the reference's F32 CPU semantics, not a restatement.
+#include "mg-generate.hpp"
 #include "mg-model.hpp"
 #include "mg-tensor.hpp"
 #include "mg-transformer.hpp"
@@ -15,7 +16,9 @@
 #include <cstring>
 #include <exception>
 #include <memory>
+#include <stdexcept>
 #include <string>
+#include <vector>
 
 using namespace mg;
 
@@ -111,6 +114,41 @@ int mgref_graph_case(int which, int64_t a, int64_t b, int64_t c, int64_t d, floa
         if (o->nelements() != out_len) { g_err = "output size mismatch"; return -2; }
         Graph g; g.build_forward(o); compute(ctx, g);
         std::memcpy(out, o->data, (size_t)out_len * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) { g_err = e.what(); return -1; }
+}
+
+// The reference's own decoding loop, generate() (src/mg-generate.cpp:39-123), on a GGUF
+// model's hyper-parameters, driven through its two hooks: the TransformerFwd hook records the
+// tokens of each step's forward (tokens_out [steps][S]) and answers with the caller's logits for
+// that step (logits [steps][S][vocab]); the VqganFwd hook captures the final token grid
+// (grid_out [n_tokens]) and returns a blank image, so neither the transformer nor the VQGAN runs.
+int mgref_generate(const char* gguf_path, int class_id, uint64_t seed, int steps, float temperature,
+                   const float* logits, int32_t* tokens_out, int32_t* grid_out) {
+    try {
+        Context wctx(64 << 20);
+        auto model = Model::load(gguf_path, wctx);
+        const auto& h = model->hparams();
+        const int S = h.n_tokens + 1;
+        const size_t per = (size_t)S * h.vocab_size;
+        int step = 0;
+        TransformerFwd fwd = [&](const int32_t* tok, float* out) {
+            if (step >= steps) throw std::runtime_error("more forwards than steps");
+            std::memcpy(tokens_out + (size_t)step * S, tok, (size_t)S * sizeof(int32_t));
+            std::memcpy(out, logits + (size_t)step * per, per * sizeof(float));
+            step++;
+        };
+        VqganFwd vq = [&](const int32_t* grid, float* img) {
+            std::memcpy(grid_out, grid, (size_t)h.n_tokens * sizeof(int32_t));
+            std::memset(img, 0, (size_t)h.resolution * h.resolution * 3 * sizeof(float));
+        };
+        GenConfig cfg;
+        cfg.class_id = class_id;
+        cfg.steps = steps;
+        cfg.seed = seed;
+        cfg.temperature = temperature;
+        generate(*model, cfg, false, fwd, vq);
+        if (step != steps) { g_err = "fewer forwards than steps"; return -2; }
         return 0;
     } catch (const std::exception& e) { g_err = e.what(); return -1; }
 }

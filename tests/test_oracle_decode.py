@@ -18,7 +18,11 @@ term, known tokens treated as unknown):
   * cosine schedule counts over 8 steps: 251, 236, 212, 181, 142, 97, 49 positions masked, and
     at the last step (zero temperature, all confidences tied) none;
   * known tokens keep their value and are never re-masked; one unknown left is re-masked (the
-    cutoff is then +inf), none left changes nothing.
+    cutoff is then +inf), none left changes nothing;
+  * the reference's own generate() (src/mg-generate.cpp:39-123, compiled from its source into
+    oracle/_ref) driven through its TransformerFwd / VqganFwd hooks with the same logits: the
+    oracle loop feeds every step's forward the same tokens and ends on the same grid, over
+    several seeds, class ids and choice temperatures.
 """
 import math
 
@@ -26,6 +30,7 @@ import numpy as np
 import pytest
 
 import oracle
+from oracle import ref
 
 S, V, CB, MASK, NT = 257, 2025, 1024, 2024, 256
 
@@ -151,3 +156,30 @@ def test_one_or_no_unknown_left():
     keep[17] = False
     assert np.array_equal(tok[0][keep], tok0[0][keep])
     assert np.array_equal(tok[1], tok0[1]) and np.array_equal(res[1], tok0[1])
+
+
+@pytest.fixture(scope="module")
+def gen_model(tmp_path_factory):
+    from tests import mg_gguf
+    p = str(tmp_path_factory.mktemp("gen") / "gen.gguf")
+    mg_gguf.write_model(p, n_layer=1, quant="f32", seed=9)
+    return p
+
+
+@pytest.mark.skipif(not ref.available(), reason="oracle/_ref/libmgref.so not built (needs /root/reference)")
+@pytest.mark.parametrize("seed,cls,temp,scale", [(42, 207, 4.5, 3.0), (7, 0, 1.0, 3.0), (2024, 999, -1.0, 1.0),
+                                                 (1, 512, 0.0, 6.0), (123456789, 88, 4.5, 0.3)])
+def test_decode_loop_equals_reference_generate(gen_model, seed, cls, temp, scale):
+    """8 steps of the oracle step against the reference's generate() on the same per-step
+    logits: identical tokens into every forward and the identical final grid (a negative
+    temperature selects the model's 4.5, as the reference does)"""
+    steps = 8
+    rng = np.random.default_rng(seed % 1000)
+    logits = (rng.standard_normal((steps, S, V)) * scale).astype(np.float32)
+    ref_tok, ref_grid = ref.generate(gen_model, cls, seed, steps, temp, logits)
+    tok = _start(1, cls=[cls])
+    ct = 4.5 if temp < 0 else temp
+    for step in range(steps):
+        assert np.array_equal(tok[0], ref_tok[step]), f"tokens into step {step}"
+        tok, res = oracle.decode_step(logits[step][None], tok, step, steps, [seed], 2 * S * step, choice_temp=ct)
+    assert np.array_equal(res[0, 1:], ref_grid)
