@@ -12,6 +12,8 @@
 //  2. Run the nodes in order; device buffers of computed roots come from a size-bucketed
 //     pool and return to it after their last consumer.
 //  3. Copy the final node to its host data and wait (the reference's readback, :1622-1642);
+//     with MG_DUMP_NAMED set in the environment, every named computed node is also copied to
+//     its host data (:1627-1641) — right after it runs, before its buffer can be reused;
 //     compute_device() instead keeps the result in HBM for device-side consumers (the
 //     decode step) and returns without waiting.
 // Leaves are uploaded once per (host address, byte size) and kept; quantized weights are
@@ -23,6 +25,7 @@
 #include "mg-hip.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <stdexcept>
@@ -479,6 +482,10 @@ const void* HipRuntime::run(Graph& g, bool readback) {
         }
     }
 
+    // MG_DUMP_NAMED: named computed nodes are read back to their host data (mg-opencl.cpp
+    // :1627-1641), each right after its kernel, while its buffer is still its own
+    const bool dump_named = std::getenv("MG_DUMP_NAMED") != nullptr;
+
     // ---- run ----
     for (int i = 0; i < n; i++) {
         Tensor* t = g.nodes[i];
@@ -756,6 +763,11 @@ const void* HipRuntime::run(Graph& g, bool readback) {
             auto& e = I.prof[op_name(t)];
             e.first++;
             e.second += ms;
+        }
+        if (dump_named && !t->name.empty() && t->data) {
+            const auto a = I.addr.find(t);
+            if (a != I.addr.end() && a->second && !h16_store.count(t) && !I.pitch.count(t))
+                I.check(mgh_d2h(I.ctx, t->data, a->second, t->nbytes()));
         }
         release_after(i, t);
     }

@@ -36,6 +36,9 @@ struct mgr_model {
     void* d_state = nullptr;
     void* d_work = nullptr;
     size_t cap_tok = 0, cap_res = 0, cap_state = 0, cap_work = 0;
+    // named nodes of the last forward's graph (their host data holds the values after a
+    // forward run with MG_DUMP_NAMED set)
+    std::vector<const mg::Tensor*> named;
 
     ~mgr_model() {
         if (!rt) return;
@@ -135,6 +138,9 @@ int mgr_forward(mgr_model* m, const int32_t* tokens, int S, int B, float* logits
         mg::Tensor* out = mg::build_transformer(*m->gctx, *m->model, tok);
         mg::Graph g;
         g.build_forward(out);
+        m->named.clear();
+        for (const mg::Tensor* t : g.nodes)
+            if (!t->name.empty()) m->named.push_back(t);
         m->rt->invalidate(tok);               // new token ids at a reused host address
         // the logits go straight from HBM to the caller's buffer (or stay on the device)
         const void* d = m->rt->compute_device(g);
@@ -144,6 +150,31 @@ int mgr_forward(mgr_model* m, const int32_t* tokens, int S, int B, float* logits
     } catch (const std::exception& e) {
         return fail(e);
     }
+}
+
+int mgr_named(const mgr_model* m, const char* name, float* out, int64_t capacity) {
+    if (!m || !name) {
+        g_err = "mgr_named: null argument";
+        return -1;
+    }
+    for (const mg::Tensor* t : m->named) {
+        if (t->name != name) continue;
+        const int64_t n = t->nelements();
+        if (t->type != mg::Type::F32 || !t->data) {
+            g_err = std::string("mgr_named: '") + name + "' has no F32 host data";
+            return -1;
+        }
+        if (out) {
+            if (capacity < n) {
+                g_err = "mgr_named: output too small";
+                return -1;
+            }
+            std::memcpy(out, t->data, (size_t)n * sizeof(float));
+        }
+        return (int)n;
+    }
+    g_err = std::string("mgr_named: no node named '") + name + "' in the last forward";
+    return -1;
 }
 
 int mgr_generate(mgr_model* m, const int32_t* class_ids, const uint64_t* seeds, int B, int steps,

@@ -16,7 +16,7 @@ from . import LIB_DIR, MghError
 
 MGR_SYMBOLS = ["mgr_load", "mgr_free", "mgr_last_error", "mgr_hparams", "mgr_device_name",
                "mgr_forward", "mgr_profile_enable", "mgr_profile_report", "mgr_gguf_info",
-               "mgr_graph_stats", "mgr_decode_params", "mgr_generate"]
+               "mgr_graph_stats", "mgr_decode_params", "mgr_generate", "mgr_named"]
 
 _lib = None
 
@@ -43,6 +43,7 @@ def lib():
         L.mgr_graph_stats.argtypes = [ctypes.c_char_p, I, I, P]
         L.mgr_decode_params.argtypes = [P, P, P, P]
         L.mgr_generate.argtypes = [P, P, P, I, I, ctypes.c_float, P]
+        L.mgr_named.argtypes = [P, ctypes.c_char_p, P, ctypes.c_int64]
         _lib = L
     return _lib
 
@@ -126,6 +127,14 @@ class TransformerRuntime:
         _check(lib().mgr_generate(self.h, cls.ctypes.data_as(ctypes.c_void_p),
                                   sd.ctypes.data_as(ctypes.c_void_p), cls.size, steps, temperature,
                                   out.ctypes.data_as(ctypes.c_void_p)))
+        return out
+
+    def named(self, name: str) -> np.ndarray:
+        """A named node of the last forward (its values are current only if that forward ran
+        with MG_DUMP_NAMED set in the environment), flat float32."""
+        n = _check(lib().mgr_named(self.h, name.encode(), None, 0))
+        out = np.empty(n, np.float32)
+        _check(lib().mgr_named(self.h, name.encode(), out.ctypes.data_as(ctypes.c_void_p), n))
         return out
 
     def profile(self, on: bool = True):

@@ -33,6 +33,14 @@ int mgr_decode_params(const mgr_model* m, int32_t* n_tokens, int32_t* codebook, 
  * forward then runs without the final readback. */
 int mgr_forward(mgr_model* m, const int32_t* tokens, int S, int B, float* logits);
 
+/* A named node of the last mgr_forward graph (embd_post_norm, blk.<l>.attn_post,
+ * blk.<l>.ffn_post, output_norm, output_logits: src/mg-transformer.cpp:47, 91, 98, 106, 109),
+ * as the reference's verification tools read them: its values are current only if that
+ * forward ran with MG_DUMP_NAMED set in the environment, which makes the runtime read every
+ * named node back (mg-opencl.cpp:1627-1641). Copies up to `capacity` floats into out (NULL:
+ * size query); returns the element count, or < 0. */
+int mgr_named(const mgr_model* m, const char* name, float* out, int64_t capacity);
+
 /* Iterative decoding of B images on the device: the reference's generate() loop
  * (src/mg-generate.cpp:39-121) without the VQGAN decode. Image b starts from class token
  * class_ids[b] + codebook and all n_tokens positions masked, draws from

@@ -12,6 +12,7 @@ Each FC node uses the semantics of the reference kernel that runs it:
   * "deq"  — Q8_0/Q4_K weights, dequantize-then-F32 (mg-opencl.cpp:320-411;
              oracle.gemm_q_deq_f32).
 Attention is the fp16-K/V variant (mg-opencl.cpp:859-937) when f16kv, else the F32 CPU one.
+`Layers` exposes the pieces separately, so each can be applied to given input activations.
 """
 from __future__ import annotations
 
@@ -23,41 +24,70 @@ from . import (WTYPE_Q4_K, WTYPE_Q8_0, attention, gemm_f32, gemm_q_deq_f32, gemm
 FC = ("attn_q", "attn_k", "attn_v", "attn_o", "ffn_up", "ffn_down")
 
 
+class Layers:
+    """The forward's pieces, each a function of its input activations (so a test can feed each
+    piece the GPU's own input): embed, attention sublayer, MLP sublayer, head (LN output and
+    logits). t: float tensors by GGUF name (FC weights before quantization)."""
+
+    def __init__(self, t: dict, n_head: int, B: int, S: int, quant: str = "f32", algo: str = "int8",
+                 f16kv: bool = True, eps: float = 1e-12):
+        self.t, self.H, self.B, self.S = t, n_head, B, S
+        self.E = t["token_embd.weight"].shape[1]
+        self.D = self.E // n_head
+        self.wt = {"q8_0": WTYPE_Q8_0, "q4_k": WTYPE_Q4_K}.get(quant)
+        self.algo, self.f16kv, self.eps = algo, f16kv, eps
+        self._wq = {}
+
+    def fc(self, name, x, act=0, resid=None):
+        t = self.t
+        w, b = t[name + ".weight"], t[name + ".bias"]
+        N, K = w.shape
+        if self.wt is None:
+            return gemm_f32(w, x, bias=b, act=act, resid=resid)
+        if name not in self._wq:
+            self._wq[name] = quantize(self.wt, w)
+        wq = self._wq[name]
+        if self.algo == "int8":
+            qx, dx, _ = quantize_act_q8(x)
+            return gemm_q_i8(self.wt, wq, N, K, qx, dx, bias=b, act=act, resid=resid)
+        return gemm_q_deq_f32(self.wt, wq, N, K, x, bias=b, act=act, resid=resid)
+
+    def ln(self, name, x):
+        return layernorm_affine(x, self.t[name + ".weight"], self.t[name + ".bias"], self.eps)
+
+    def embed(self, tokens):                                  # :41-48
+        B, S, E = self.B, self.S, self.E
+        x = get_rows(self.t["token_embd.weight"], tokens.reshape(-1))
+        x = (x.reshape(B, S, E) + self.t["pos_embd.weight"][:S][None]).reshape(B * S, E).astype(np.float32)
+        return self.ln("token_embd_norm", x)
+
+    def attn(self, l, x):                                     # :59-92
+        p = f"blk.{l}."
+        B, S, E, D, H = self.B, self.S, self.E, self.D, self.H
+        q, k, v = (self.fc(p + n, x) for n in ("attn_q", "attn_k", "attn_v"))
+        scale = np.float32(1.0) / np.sqrt(np.float32(D))
+        a = attention(q, k, v, (1, E, D, E * S), D, S, H, B, float(scale), self.f16kv)
+        a = merge_heads(a, D, S, H, B).reshape(B * S, E)
+        return self.ln(p + "attn_norm", self.fc(p + "attn_o", a, resid=x))
+
+    def mlp(self, l, x):                                      # :94-99
+        p = f"blk.{l}."
+        f = self.fc(p + "ffn_up", x, act=1)
+        return self.ln(p + "ffn_norm", self.fc(p + "ffn_down", f, resid=x))
+
+    def head_norm(self, x):                                   # :102-106
+        return self.ln("output_norm", self.fc("output_proj", x, act=1))
+
+    def logits(self, h):                                      # :107-109
+        return gemm_f32(self.t["token_embd.weight"], h, bias=self.t["output.bias"])
+
+
 def transformer_forward(t: dict, n_layer: int, n_head: int, tokens: np.ndarray, quant: str = "f32",
                         algo: str = "int8", f16kv: bool = True, eps: float = 1e-12) -> np.ndarray:
     """t: float tensors by GGUF name (FC weights before quantization); tokens [B][S]."""
     B, S = tokens.shape
-    E = t["token_embd.weight"].shape[1]
-    D = E // n_head
-    wt = {"q8_0": WTYPE_Q8_0, "q4_k": WTYPE_Q4_K}.get(quant)
-
-    def fc(name, x, act=0, resid=None):
-        w, b = t[name + ".weight"], t[name + ".bias"]
-        N, K = w.shape
-        if wt is None:
-            return gemm_f32(w, x, bias=b, act=act, resid=resid)
-        wq = quantize(wt, w)
-        if algo == "int8":
-            qx, dx, _ = quantize_act_q8(x)
-            return gemm_q_i8(wt, wq, N, K, qx, dx, bias=b, act=act, resid=resid)
-        return gemm_q_deq_f32(wt, wq, N, K, x, bias=b, act=act, resid=resid)
-
-    def ln(name, x):
-        return layernorm_affine(x, t[name + ".weight"], t[name + ".bias"], eps)
-
-    x = get_rows(t["token_embd.weight"], tokens.reshape(-1))
-    x = (x.reshape(B, S, E) + t["pos_embd.weight"][:S][None]).reshape(B * S, E).astype(np.float32)
-    x = ln("token_embd_norm", x)
-    scale = np.float32(1.0) / np.sqrt(np.float32(D))
-    st = (1, E, D, E * S)
+    L = Layers(t, n_head, B, S, quant, algo, f16kv, eps)
+    x = L.embed(tokens)
     for l in range(n_layer):
-        p = f"blk.{l}."
-        q, k, v = (fc(p + n, x) for n in ("attn_q", "attn_k", "attn_v"))
-        a = attention(q, k, v, st, D, S, n_head, B, float(scale), f16kv)
-        a = merge_heads(a, D, S, n_head, B).reshape(B * S, E)
-        x = ln(p + "attn_norm", fc(p + "attn_o", a, resid=x))
-        f = fc(p + "ffn_up", x, act=1)
-        x = ln(p + "ffn_norm", fc(p + "ffn_down", f, resid=x))
-    h = ln("output_norm", fc("output_proj", x, act=1))
-    logits = gemm_f32(t["token_embd.weight"], h, bias=t["output.bias"])
-    return logits.reshape(B, S, -1)
+        x = L.mlp(l, L.attn(l, x))
+    return L.logits(L.head_norm(x)).reshape(B, S, -1)

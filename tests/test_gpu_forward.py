@@ -7,13 +7,14 @@ Bars:
   * Q8_0 / Q4_K, int8-dot path, against the oracle forward with the same per-layer activation
     quantization and fp16 K/V attention: the reference's own gate for its quantized GPU path,
     cos > 0.9999 and max|d logits| < 1.0 (tools/verify-opencl-transformer.cpp:98-101), plus
-    max|d| <= 2e-2 * max|logits|. A full int8 forward cannot be compared tighter: any 1-ulp
-    difference in summation order (split-K, MFMA order) eventually moves an activation across
-    a code's rounding boundary, and from there every later layer re-quantizes with
-    decorrelated noise of the per-GEMM quantization level (~5e-3 of ||y||, the int8 path's
-    deviation from dequantize-then-F32). The same happens between one image run alone and in
-    a batch. The per-GEMM kernels are checked tightly (bit-exact dots, <= 1e-3 outputs) in
-    test_gpu_packed.py;
+    max|d| <= 2e-2 * max|logits| at 2 layers. End to end a full int8 forward cannot be compared
+    tighter: any 1-ulp difference in summation order (split-K, MFMA order) eventually moves an
+    activation across a code's rounding boundary, and from there every later layer
+    re-quantizes with decorrelated noise of the per-GEMM quantization level (~5e-3 of ||y||).
+    At 24 layers every sublayer is instead checked against the oracle applied to the GPU's own
+    input for it (named intermediates, MG_DUMP_NAMED): within 1e-3 of max|x| per sublayer,
+    both FC paths. The per-GEMM kernels are checked tightly (bit-exact dots, <= 1e-3 outputs)
+    in test_gpu_packed.py;
   * Q8_0, dequant-fp16 path: within 1e-3 * max|logits| of dequantize-then-F32 (oracle, fp16 K/V);
   * F32 weights: within 1e-3 of the oracle (fp16 K/V attention, as the reference GPU kernel),
     and cos >= 0.9999 against the reference CPU executor (its F32 attention) — the reference's
@@ -164,10 +165,10 @@ def test_forward_full_cfg4_properties(tmp_path, algo):
     2) a value can cross an fp16 rounding boundary, which over 24 post-LN layers stays at the
     fp16 level, while a flattening or indexing error would be O(1). On the int8-dot path (algo
     1) a crossing flips an int8 code and decorrelates the later layers at the quantization
-    level: the bar is the path's own quantization noise at this depth (its distance from the
-    dequant-fp16 path on the same image, ~1.6e-2 of max|logits|, cos 0.99988 at 24 layers),
-    which two independent draws exceed by about sqrt 2, plus the reference's max|d| < 1.0
-    (tools/verify-opencl-transformer.cpp:98-101)."""
+    level (reported beside the path's own quantization noise, its distance from the
+    dequant-fp16 path on the same image); the gate is the reference's max|d| < 1.0
+    (tools/verify-opencl-transformer.cpp:98-101); the int8 path's parity at depth is checked
+    per sublayer on the GPU's own inputs (test_forward_24_layers_per_sublayer_vs_oracle)."""
     path = str(tmp_path / "cfg4.gguf")
     mg_gguf.write_model(path, n_layer=24, quant="q8_0", seed=5)
     rng = np.random.default_rng(21)
@@ -196,7 +197,47 @@ def test_forward_full_cfg4_properties(tmp_path, algo):
             noise = _rel(one, ref16[b])
             print(f"    int8 vs dequant-fp16 path (quantization noise): rel {noise:.2e}, "
                   f"cos {_cos(one, ref16[b]):.7f}", flush=True)
-            assert dmax < 1.0 and err <= 2.5 * noise   # measured 1.2-1.3x (two draws: ~sqrt 2)
+            assert dmax < 1.0
+
+
+@pytest.mark.parametrize("quant,algo", [("q8_0", 1), ("q4_k", 1), ("q8_0", 2), ("q4_k", 2)])
+def test_forward_24_layers_per_sublayer_vs_oracle(tmp_path, monkeypatch, quant, algo):
+    """Every piece of the 24-layer forward against the oracle applied to the GPU's own input for
+    that piece: with MG_DUMP_NAMED set the runtime reads back the named nodes the reference's
+    verification tools compare (embd_post_norm, blk.<l>.attn_post / ffn_post, output_norm;
+    mg-opencl.cpp:1627-1641, src/mg-transformer.cpp:47-109), so the attention sublayer of layer
+    l is checked on the GPU's output of layer l-1, and so on. A fixed bar per piece, independent
+    of depth: within 1e-3 of max|x| (the north star's per-FC bar, here over a whole sublayer;
+    measured 2.0e-4 .. 3.7e-4), and the logits within 1e-3 (measured 3e-7). On identical
+    inputs the int8 path quantizes the named activations to the
+    same codes as the oracle; only codes of internal operands (attention output, GELU output)
+    can flip, by one step."""
+    path = str(tmp_path / "m24.gguf")
+    t = mg_gguf.write_model(path, n_layer=24, quant=quant, seed=5)
+    tok = mg_gguf.tokens(np.random.default_rng(21), 257, 1)
+    print(f"forward 24 layers {quant} algo {algo}: per-sublayer parity", flush=True)
+    monkeypatch.setenv("MG_DUMP_NAMED", "1")
+    with rt.TransformerRuntime(path, algo=algo) as m:
+        logits = m.forward(tok)
+        got = {n: m.named(n).reshape(257, 768) for n in
+               ["embd_post_norm", "output_norm"] + [f"blk.{l}.{k}" for l in range(24) for k in ("attn_post", "ffn_post")]}
+    L = ofwd.Layers(t, 16, 1, 257, quant=quant, algo="int8" if algo == 1 else "deq", f16kv=True)
+    worst = 0.0
+    checks = [("embd_post_norm", L.embed(tok), got["embd_post_norm"])]
+    prev = got["embd_post_norm"]
+    for l in range(24):
+        a = got[f"blk.{l}.attn_post"]
+        checks.append((f"blk.{l}.attn_post", L.attn(l, prev), a))
+        prev = got[f"blk.{l}.ffn_post"]
+        checks.append((f"blk.{l}.ffn_post", L.mlp(l, a), prev))
+    checks.append(("output_norm", L.head_norm(prev), got["output_norm"]))
+    for name, want, have in checks:
+        e = _rel(have, want)
+        worst = max(worst, e)
+        assert e <= 1e-3, f"{name}: rel {e:.2e}"
+    el = _rel(logits.reshape(257, -1), L.logits(got["output_norm"]))
+    print(f"  worst piece rel {worst:.2e}; logits from the GPU's output_norm: rel {el:.2e}", flush=True)
+    assert el <= 1e-3
 
 
 @pytest.mark.parametrize("quant", ["q8_0", "q4_k"])
@@ -205,9 +246,10 @@ def test_forward_24_layers_vs_oracle(tmp_path, quant):
     path against dequantize-then-F32 with fp16 K/V, and the int8-dot path against the oracle's
     int8-dot forward (the reference's k_quantize_q8 + k_mul_mat_q8_i8 semantics). The two
     int8 forwards sum in different orders, so codes flip and later layers decorrelate at the
-    int8 path's quantization level; the bar is that level as the oracle itself measures it
-    (its int8 forward against its dequantize-then-F32 forward), with the reference's
-    max|d| < 1.0 (tools/verify-opencl-transformer.cpp:98-101)."""
+    int8 path's quantization level (reported next to that level as the oracle itself measures
+    it, its int8 forward against its dequantize-then-F32 forward); the gate is the reference's
+    max|d| < 1.0 (tools/verify-opencl-transformer.cpp:98-101). Parity proper of the int8 path
+    at this depth is the per-sublayer test above."""
     path = str(tmp_path / "m24.gguf")
     t = mg_gguf.write_model(path, n_layer=24, quant=quant, seed=5)
     tok = mg_gguf.tokens(np.random.default_rng(21), 257, 1)
@@ -224,4 +266,4 @@ def test_forward_24_layers_vs_oracle(tmp_path, quant):
     print(f"  int8-dot vs oracle int8: rel {e8:.2e}  cos {_cos(g8, i8):.7f}  "
           f"max|d| {np.abs(g8 - i8).max():.3e}", flush=True)
     assert e16 <= 2e-3                     # measured 8.6e-4 (q8_0), 8.5e-4 (q4_k)
-    assert e8 <= 2.5 * noise and np.abs(g8 - i8).max() < 1.0   # measured 1.2x the noise
+    assert np.abs(g8 - i8).max() < 1.0
