@@ -63,7 +63,7 @@ LAYER = [  # name, N, K, act, residual
 CFG1 = [("cfg1", 3072, 768, ema.ACT_NONE, False)]   # configs[0]: one Q8_0 FC GEMM at M=257
 
 
-KERNEL = {"packed": "k_gemm_qp", "raw": "k_gemm_q_f16x", "h16": "k_gemm_h16"}
+KERNEL = {"packed": "k_gemm_qp", "raw": "k_gemm_q_i8", "h16": "k_gemm_h16"}
 PATH_NAME = {"packed": "int8_dot", "raw": "int8_dot_raw", "h16": "dequant_f16"}
 WORKLOAD_PATH = {
     "h16": "dequantize-fused path (weights dequantized once to fp16 at upload; per FC one GEMM "
@@ -92,7 +92,8 @@ class LayerSet:
     path "h16" (dequantize-fused production path): weights dequantized once at upload into
     fp16 (mgh_pack_weights_f16), then per FC one mgh_gemm_h16_f32in (the fp32 activations are
     rounded to fp16 inside the GEMM).
-    path "raw": GGUF blocks as stored, per FC: quantizer + mgh_gemm_q_codes16."""
+    path "raw": GGUF blocks as stored, per FC: int8 quantizer + mgh_gemm_q (the int8-MFMA
+    raw-block kernel)."""
 
     def __init__(self, ctx, host, M, wtype, path="packed", layer=LAYER):
         self.ctx = ctx
@@ -126,7 +127,7 @@ class LayerSet:
         if self.path == "h16":
             c.gemm_h16(d["w"], d["N"], d["K"], d["qx"], self.M, d["b"], d["act"], d["r"], d["y"])
             return
-        f = c.gemm_q_packed if self.path == "packed" else c.gemm_q_codes16
+        f = c.gemm_q_packed if self.path == "packed" else c.gemm_q
         f(self.wtype, d["w"], d["N"], d["K"], d["qx"], d["dx"], d["sx"], self.M,
           d["b"], d["act"], d["r"], d["y"])
 
@@ -136,7 +137,10 @@ class LayerSet:
             if self.path == "h16":         # fp32 activations rounded to fp16 inside the GEMM
                 c.gemm_h16_f32in(d["w"], d["N"], d["K"], d["x"], self.M, d["b"], d["act"], d["r"], d["y"])
                 continue
-            c.quantize_act_q8_codes16(d["x"], self.M, d["K"], d["qx"], d["dx"], d["sx"])
+            if self.path == "packed":
+                c.quantize_act_q8_codes16(d["x"], self.M, d["K"], d["qx"], d["dx"], d["sx"])
+            else:
+                c.quantize_act_q8(d["x"], self.M, d["K"], d["qx"], d["dx"], d["sx"])
             self._gemm(d)
 
     def gemms_only(self):

@@ -31,7 +31,7 @@ MGH_SYMBOLS = [
     "mgh_timer_start", "mgh_timer_stop",
     "mgh_quantize_act_q8", "mgh_gemm_q", "mgh_gemm_q_f32in", "mgh_debug_block_dots",
     "mgh_graph_begin", "mgh_graph_end", "mgh_graph_launch", "mgh_graph_destroy",
-    "mgh_quantize_act_q8_codes16", "mgh_gemm_q_codes16",
+    "mgh_quantize_act_q8_codes16",
     "mgh_packed_weight_bytes", "mgh_pack_weights", "mgh_gemm_q_packed", "mgh_debug_block_dots_packed",
     "mgh_gemm_q_packed_f32in",
     "mgh_layernorm_affine", "mgh_flash_attn_f16kv", "mgh_gemm_f32", "mgh_get_rows", "mgh_add",
@@ -83,7 +83,6 @@ def lib():
         L.mgh_gemm_q_f32in.argtypes = [P, I, I, P, I, I, P, I, P, I, P, P]
         L.mgh_debug_block_dots.argtypes = [P, I, P, I, I, P, I, P]
         L.mgh_quantize_act_q8_codes16.argtypes = [P, P, I, I, P, P, P]
-        L.mgh_gemm_q_codes16.argtypes = [P, I, P, I, I, P, P, P, I, P, I, P, P]
         L.mgh_packed_weight_bytes.argtypes = [I, I, I]
         L.mgh_packed_weight_bytes.restype = SZ
         L.mgh_pack_weights.argtypes = [P, I, P, I, I, P]
@@ -259,11 +258,6 @@ class Context:
     def quantize_act_q8_codes16(self, x, M, K, qx16, dx, sx=None):
         P = self._ptr
         self._check(lib().mgh_quantize_act_q8_codes16(self.h, P(x), M, K, P(qx16), P(dx), P(sx)))
-
-    def gemm_q_codes16(self, wtype, w, N, K, qx16, dx, sx, M, bias, act, resid, y):
-        P = self._ptr
-        self._check(lib().mgh_gemm_q_codes16(self.h, wtype, P(w), N, K, P(qx16), P(dx), P(sx), M,
-                                             P(bias), act, P(resid), P(y)))
 
     def pack_weights(self, wtype, w, N, K, wp):
         P = self._ptr

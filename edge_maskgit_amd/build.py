@@ -29,14 +29,12 @@ HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wno-unused-command-line-argument"]
 
-KERNEL_SOURCES = ["k_quant_act.hip", "k_gemm_i8.hip", "k_gemm_i8_stream.hip", "k_gemm_q_f16x.hip",
+KERNEL_SOURCES = ["k_quant_act.hip", "k_gemm_i8.hip",
                   "k_pack_w.hip", "k_gemm_qp.hip", "k_layernorm.hip", "k_flash_attn.hip",
                   "k_gemm_f32.hip", "k_glue.hip", "k_ops.hip", "noalloc.hip", "k_decode.hip", "k_gemm_h16.hip", "mgh_api.cpp"]
 # Per-source extra flags. The int8 GEMM keeps MFMA results in VGPRs so the per-block
 # scale FMAs read them without v_accvgpr_read copies.
 EXTRA_FLAGS = {"k_gemm_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-               "k_gemm_i8_stream.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-               "k_gemm_q_f16x.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
                "k_gemm_qp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 # C++ host runtime (graph API mirror, GGUF loader, transformer builder, HipRuntime, mgr C ABI):
 # plain host code over the libmgh C ABI, compiled with g++ into lib/libmg_hip.so.

@@ -16,7 +16,7 @@
 namespace mgh {
 
 // F16 = false: qx is int8 (the reference layout). F16 = true: the same codes are written as
-// fp16 values (exact for |q| <= 127), the operand format of k_gemm_q_f16x.
+// fp16 values (exact for |q| <= 127), the operand format of k_gemm_qp.
 template <bool F16>
 __global__ __launch_bounds__(256) void k_quantize_act_q8(const float* __restrict__ x,
                                                          void* __restrict__ qx,
@@ -115,23 +115,6 @@ hipError_t launch_round_act_f16(const float* x, _Float16* x16, float* ones, floa
     const int64_t grid = (nblocks * 8 + 255) / 256;
     hipLaunchKernelGGL(k_round_act_f16, dim3((unsigned)grid), dim3(256), 0, s, x, x16, ones, ux,
                        nblocks);
-    return hipGetLastError();
-}
-
-// int8 codes -> fp16 codes (exact); lets the debug entry point feed given int8 activations
-// to the fp16-operand GEMM.
-__global__ __launch_bounds__(256) void k_i8_to_f16(const int8_t* __restrict__ q,
-                                                   _Float16* __restrict__ h, size_t n) {
-    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const size_t stride = (size_t)gridDim.x * 256;
-    for (; i < n; i += stride) h[i] = (_Float16)q[i];
-}
-
-hipError_t launch_i8_to_f16(const int8_t* q, _Float16* h, size_t n, hipStream_t s) {
-    if (n == 0) return hipSuccess;
-    size_t grid = (n + 255) / 256;
-    if (grid > 65536) grid = 65536;
-    hipLaunchKernelGGL(k_i8_to_f16, dim3((unsigned)grid), dim3(256), 0, s, q, h, n);
     return hipGetLastError();
 }
 

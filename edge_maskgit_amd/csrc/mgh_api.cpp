@@ -82,10 +82,6 @@ mgh::TileCfg pick_tile(int M, int N) {
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // fp16-code production kernel: K % 256 == 0, N % 4 == 0, 16-byte aligned w/bias/resid/y.
-bool f16x_ok(int K, int N, const void* w, const void* bias, const void* resid, const void* y) {
-    return K % 256 == 0 && N % 4 == 0 && aligned16(w) && aligned16(bias) && aligned16(resid) &&
-           aligned16(y);
-}
 
 size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 
@@ -161,12 +157,8 @@ int check_h16(mgh_ctx* c, const char* fn, const void* wp, int N, int K, const vo
 }
 
 
-// Streamed kernel when K is a multiple of 256 and every streamed operand is 16-byte aligned
-// (its 16-byte direct-to-LDS loads and vector scale loads need both); general kernel otherwise.
+// The raw-block int8-dot GEMM (GGUF blocks as stored, int8 activation codes)
 hipError_t launch_gemm(int wtype, const mgh::GemmArgs& a, bool dbg, hipStream_t s) {
-    if (a.K % 256 == 0 && aligned16(a.w) && aligned16(a.qx) && (dbg || aligned16(a.dx)) &&
-        (dbg || wtype != MGH_WTYPE_Q4_K || aligned16(a.sx)))
-        return mgh::launch_gemm_q_i8_s256(wtype, a, dbg, s);
     return mgh::launch_gemm_q_i8(wtype, a, pick_tile(a.M, a.N), dbg, s);
 }
 
@@ -385,27 +377,6 @@ int mgh_quantize_act_q8_codes16(mgh_ctx* c, const float* x, int M, int K, uint16
     return MGH_OK;
 }
 
-int mgh_gemm_q_codes16(mgh_ctx* c, int wtype, const void* w, int N, int K, const uint16_t* qx16,
-                       const float* dx, const int32_t* sx, int M, const float* bias, int act,
-                       const float* resid, float* y) {
-    if (!c) return MGH_ERR_ARG;
-    if (int r = check_quant_shape(c, wtype, N, K, M)) return r;
-    if (act < 0 || act > 2) return fail(c, MGH_ERR_ARG, "act must be 0 (none), 1 (gelu) or 2 (silu)");
-    if (M == 0) return MGH_OK;
-    if (!w || !qx16 || !dx || !y) return fail(c, MGH_ERR_ARG, "gemm_q_codes16: null pointer");
-    if (wtype == MGH_WTYPE_Q4_K && !sx) return fail(c, MGH_ERR_ARG, "gemm_q_codes16: Q4_K needs block sums sx");
-    if (!f16x_ok(K, N, w, bias, resid, y) || !aligned16(qx16) || !aligned16(dx) || !aligned16(sx))
-        return fail(c, MGH_ERR_UNSUPPORTED, "gemm_q_codes16 needs K % 256 == 0, N % 4 == 0 and "
-                                            "16-byte aligned operands");
-    if (int r = set_dev(c)) return r;
-    mgh::GemmArgs a{};
-    a.w = (const uint8_t*)w; a.qx16 = qx16; a.dx = dx; a.sx = sx;
-    a.bias = bias; a.resid = resid; a.y = y;
-    a.M = M; a.N = N; a.K = K; a.act = act;
-    MGH_HIP(c, mgh::launch_gemm_q_f16x(wtype, a, false, c->stream), "k_gemm_q_f16x");
-    return MGH_OK;
-}
-
 size_t mgh_packed_weight_bytes(int wtype, int N, int K) {
     if ((wtype != MGH_WTYPE_Q8_0 && wtype != MGH_WTYPE_Q4_K) || N <= 0 || K <= 0 || K % 32) return 0;
     if (wtype == MGH_WTYPE_Q4_K && K % 256) return 0;
@@ -521,25 +492,14 @@ int mgh_gemm_q_f32in(mgh_ctx* c, int algo, int wtype, const void* w, int N, int 
                             (char*)c->scratch + wb);
     }
     const size_t nb = (size_t)K / 32;
-    const bool fast = f16x_ok(K, N, w, bias, resid, y);
-    const size_t q_b = round256((size_t)M * K * (fast ? 2 : 1));
+    const size_t q_b = round256((size_t)M * K);
     const size_t d_b = round256((size_t)M * nb * 4);
     if (int r = ensure_scratch(c, q_b + 2 * d_b)) return r;
-    void* q = c->scratch;
+    int8_t* q = (int8_t*)c->scratch;
     float* dx = (float*)((char*)c->scratch + q_b);
     int32_t* sx = (int32_t*)((char*)c->scratch + q_b + d_b);
-    if (!fast) {
-        if (int r = mgh_quantize_act_q8(c, x, M, K, (int8_t*)q, dx, sx)) return r;
-        return mgh_gemm_q(c, wtype, w, N, K, (const int8_t*)q, dx, sx, M, bias, act, resid, y);
-    }
-    MGH_HIP(c, mgh::launch_quantize_act_q8_f16(x, (_Float16*)q, dx, sx, M, K, c->stream),
-            "k_quantize_act_q8<f16>");
-    mgh::GemmArgs a{};
-    a.w = (const uint8_t*)w; a.qx16 = q; a.dx = dx; a.sx = sx;
-    a.bias = bias; a.resid = resid; a.y = y;
-    a.M = M; a.N = N; a.K = K; a.act = act;
-    MGH_HIP(c, mgh::launch_gemm_q_f16x(wtype, a, false, c->stream), "k_gemm_q_f16x");
-    return MGH_OK;
+    if (int r = mgh_quantize_act_q8(c, x, M, K, q, dx, sx)) return r;
+    return mgh_gemm_q(c, wtype, w, N, K, q, dx, sx, M, bias, act, resid, y);
 }
 
 int mgh_layernorm_affine(mgh_ctx* c, const float* x, const float* g, const float* b, int rows, int D,
@@ -911,15 +871,6 @@ int mgh_debug_block_dots(mgh_ctx* c, int wtype, const void* w, int N, int K, con
     mgh::GemmArgs a{};
     a.w = (const uint8_t*)w; a.qx = qx; a.dots = out;
     a.M = M; a.N = N; a.K = K;
-    if (f16x_ok(K, N, w, nullptr, nullptr, nullptr)) {
-        // the kernel mgh_gemm_q_f32in runs for this shape: feed it the codes as fp16
-        const size_t n = (size_t)M * K;
-        if (int r = ensure_scratch(c, round256(n * 2))) return r;
-        MGH_HIP(c, mgh::launch_i8_to_f16(qx, (_Float16*)c->scratch, n, c->stream), "k_i8_to_f16");
-        a.qx16 = c->scratch;
-        MGH_HIP(c, mgh::launch_gemm_q_f16x(wtype, a, true, c->stream), "k_gemm_q_f16x(debug)");
-        return MGH_OK;
-    }
     MGH_HIP(c, launch_gemm(wtype, a, true, c->stream), "k_gemm_q_i8(debug)");
     return MGH_OK;
 }

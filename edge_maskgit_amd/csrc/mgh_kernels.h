@@ -15,7 +15,7 @@ struct GemmArgs {
     const int8_t* qx;
     const float* dx;
     const int32_t* sx;
-    const void* qx16;      // activation codes as fp16 [M][K] (k_gemm_q_f16x operand)
+    const void* qx16;      // activation codes as fp16 [M][K] (k_gemm_qp operand)
     const float* x;        // fp32 activations (dequant-f16 path)
     const float* ux;       // Q4_K min-term activation factor [M][K/32] in fp32 (dequant-f16
                            // path: block sums of the fp16 activations); null: dx * sx
@@ -40,14 +40,8 @@ hipError_t launch_quantize_act_q8_f16(const float* x, _Float16* qx16, float* dx,
                                       int64_t M, int64_t K, hipStream_t s);
 hipError_t launch_round_act_f16(const float* x, _Float16* x16, float* ones, float* ux,
                                 int64_t M, int64_t K, hipStream_t s);
-hipError_t launch_i8_to_f16(const int8_t* q, _Float16* h, size_t n, hipStream_t s);
 hipError_t launch_gemm_q_i8(int wtype, const GemmArgs& a, TileCfg t, bool debug_dots,
                             hipStream_t s);
-// Production kernel for K % 256 == 0, N % 4 == 0, 16-byte aligned operands: fp16-code
-// activations (qx16), 16x16x32 fp16 MFMA block dots.
-hipError_t launch_gemm_q_f16x(int wtype, const GemmArgs& a, bool debug_dots, hipStream_t s);
-// Streamed variant for K % 256 == 0 with 16-byte aligned qx/dx/sx/w (64x64 tiles).
-hipError_t launch_gemm_q_i8_s256(int wtype, const GemmArgs& a, bool debug_dots, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t s);
 
 // LayerNorm + affine over rows of D (D % 256 == 0, D <= 2048); emit 0: y only, 1: also the

@@ -97,17 +97,10 @@ int mgh_gemm_q(mgh_ctx* ctx, int wtype, const void* d_w, int N, int K,
                const int8_t* d_qx, const float* d_dx, const int32_t* d_sx, int M,
                const float* d_bias, int act, const float* d_resid, float* d_y);
 
-/* ---- the two kernels mgh_gemm_q_f32in runs when K % 256 == 0, N % 4 == 0 and d_w,
- *      d_bias, d_resid, d_y are 16-byte aligned: the quantizer of mgh_quantize_act_q8
- *      writing its int8 codes as fp16 values (uint16 bit patterns, exact for |q| <= 127),
- *      and the GEMM consuming them (fp16 MFMA block dots, exact). Same semantics as
- *      mgh_quantize_act_q8 + mgh_gemm_q; mgh_gemm_q_codes16 returns MGH_ERR_UNSUPPORTED
- *      outside those shape/alignment conditions. ---- */
+/* ---- the quantizer of mgh_quantize_act_q8 writing its int8 codes as fp16 values (uint16
+ *      bit patterns, exact for |q| <= 127): the activation operand of mgh_gemm_q_packed. ---- */
 int mgh_quantize_act_q8_codes16(mgh_ctx* ctx, const float* d_x, int M, int K,
                                 uint16_t* d_qx16, float* d_dx, int32_t* d_sx);
-int mgh_gemm_q_codes16(mgh_ctx* ctx, int wtype, const void* d_w, int N, int K,
-                       const uint16_t* d_qx16, const float* d_dx, const int32_t* d_sx, int M,
-                       const float* d_bias, int act, const float* d_resid, float* d_y);
 
 /* ---- device-native weight layout. The reference's OpenCL runtime uploads each weight
  *      tensor once into a device buffer it caches for the model's lifetime
@@ -139,10 +132,10 @@ int mgh_gemm_q_packed_f32in(mgh_ctx* ctx, int algo, int wtype, const void* d_wp,
                             const float* d_resid, float* d_y);
 
 /* ---- quantized FC GEMM on fp32 activations: replaces the whole MulMat(q) node
- *      dispatch (mg-opencl.cpp:1367-1428): quantize + GEMM for ALGO_INT8 (activation
- *      scratch owned by the context and grown on demand, like the reference's
- *      qx_buf/dx_buf, mg-opencl.cpp:1125-1134), or one dequant-fp16 GEMM for
- *      ALGO_DEQ_F16. Output semantics as mgh_gemm_q. ---- */
+ *      dispatch (mg-opencl.cpp:1367-1428): mgh_quantize_act_q8 + mgh_gemm_q for ALGO_INT8
+ *      (activation scratch owned by the context and grown on demand, like the reference's
+ *      qx_buf/dx_buf, mg-opencl.cpp:1125-1134), or the weights packed into scratch and one
+ *      dequant-fp16 GEMM for ALGO_AUTO/DEQ_F16. Output semantics as mgh_gemm_q. ---- */
 int mgh_gemm_q_f32in(mgh_ctx* ctx, int algo, int wtype, const void* d_w, int N, int K,
                      const float* d_x, int M, const float* d_bias, int act,
                      const float* d_resid, float* d_y);
