@@ -402,6 +402,110 @@ __global__ __launch_bounds__(256) void k_gemm_h16_reduce(GemmH16Args g) {
         __builtin_nontemporal_store(v, (f32x4*)(g.y + o));
 }
 
+// Skinny-M FC (M <= 16 * MT, decode- and GEMV-shaped calls): one workgroup per 16 weight rows,
+// its KS waves split K (wave w takes the 32-deep K steps w, w + KS, ...), each lane streams 16
+// bytes of its weight row per step straight into registers (no LDS staging: every weight is
+// read once) and multiplies on v_mfma_f32_16x16x32_f16 against the activation rows, taken as MT
+// 16-row MFMA tiles (rows past M are zero). The KS partial tiles are summed in LDS in wave order
+// (deterministic) and the epilogue is the one of k_gemm_h16: +bias -> act -> +resid, fp32 or
+// fp16 out. Same operand rounding as k_gemm_h16 (fp32 activations rounded to fp16, nearest
+// even), so the two differ only in the fp32 summation order.
+template <int ACT, bool XF32, int MT, int KS>
+__global__ __launch_bounds__(64 * KS) void k_gemv_h16(GemmH16Args g) {
+    constexpr int U = 4;                        // K steps in flight per wave
+    __shared__ f32x4 part[KS][MT][64];
+    const int K = g.K, M = g.M, N = g.N;
+    const int T = K / 32;
+    const int n0 = blockIdx.x * 16;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r16 = lane & 15, g4 = lane >> 4;
+    const _Float16* wrow = g.w + (size_t)min(n0 + r16, N - 1) * K + 8 * g4;
+    size_t xofs[MT];
+    bool xin[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        const int m = 16 * mt + r16;
+        xin[mt] = m < M;
+        xofs[mt] = (size_t)min(m, M - 1) * K + 8 * g4;
+    }
+    auto xfrag = [&](int mt, int t) {
+        if (!xin[mt]) return f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (!XF32) return *(const f16x8*)(g.x + xofs[mt] + 32 * t);
+        const f32x4* p = (const f32x4*)(g.xf + xofs[mt] + 32 * t);
+        const f32x4 v0 = p[0], v1 = p[1];
+        return f16x8{(_Float16)v0[0], (_Float16)v0[1], (_Float16)v0[2], (_Float16)v0[3],
+                     (_Float16)v1[0], (_Float16)v1[1], (_Float16)v1[2], (_Float16)v1[3]};
+    };
+    f32x4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    int t = wave;
+    for (; t + (U - 1) * KS < T; t += U * KS) {
+        f16x8 a[U], b[U][MT];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            a[u] = *(const f16x8*)(wrow + 32 * (t + u * KS));
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) b[u][mt] = xfrag(mt, t + u * KS);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], b[u][mt], acc[mt], 0, 0, 0);
+    }
+    for (; t < T; t += KS) {
+        const f16x8 a = *(const f16x8*)(wrow + 32 * t);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xfrag(mt, t), acc[mt], 0, 0, 0);
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) part[wave][mt][lane] = acc[mt];
+    __syncthreads();
+    if (tid >= MT * 64) return;
+    // thread (mt, l) owns the outputs lane l of every wave holds for tile mt:
+    // rows m = 16 mt + l % 16, columns n .. n + 3 with n = n0 + 4 (l / 16)
+    const int mt = tid >> 6, l = tid & 63;
+    f32x4 v = part[0][mt][l];
+#pragma unroll
+    for (int w = 1; w < KS; w++) v += part[w][mt][l];
+    const int m = 16 * mt + (l & 15), n = n0 + 4 * (l >> 4);
+    if (m >= M || n >= N) return;
+    if (g.bias) v += *(const f32x4*)(g.bias + n);
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = act_h<ACT>(v[e]);
+    const size_t o = (size_t)m * N + n;
+    if (g.resid) v += *(const f32x4*)(g.resid + o);
+    if (g.y16)
+        *(f16x4*)(g.y16 + o) = f16x4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+    else
+        *(f32x4*)(g.y + o) = v;
+}
+
+template <bool XF32, int MT>
+static hipError_t launch_gemv_t(const GemmH16Args& a, hipStream_t s) {
+    constexpr int KS = 8;
+    const dim3 grid((unsigned)((a.N + 15) / 16)), block(64 * KS);
+    if (a.act == 1) hipLaunchKernelGGL((k_gemv_h16<1, XF32, MT, KS>), grid, block, 0, s, a);
+    else if (a.act == 2) hipLaunchKernelGGL((k_gemv_h16<2, XF32, MT, KS>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_gemv_h16<0, XF32, MT, KS>), grid, block, 0, s, a);
+    return hipGetLastError();
+}
+
+// Skinny-M kernel or tiled plan: measured on the four FC shapes with cold operands (fp32
+// activations, buffers rotated over 24 sets): the skinny kernel is faster up to 16 rows on
+// every shape (M = 1: 3.5-3.9 against 5.8-6.4 us for K = 768, 6.8 against 11.0 us for the
+// K = 3072 down-proj; M = 16: 4.5-4.7 against 6.0-6.3 us, 10.4 against 11.4 us) and up to 32
+// rows for K <= 1024 (M = 32: 5.9-6.1 against 6.2-6.5 us); above, the tiled plan wins.
+bool use_gemv_h16(int M, int K) { return M >= 1 && (M <= 16 || (M <= 32 && K <= 1024)); }
+
+hipError_t launch_gemv_h16(const GemmH16Args& a, hipStream_t s) {
+    const bool xf = a.xf != nullptr;
+    if (a.M < 1 || a.M > kGemvMaxRows) return hipErrorInvalidValue;
+    if (a.M <= 16) return xf ? launch_gemv_t<true, 1>(a, s) : launch_gemv_t<false, 1>(a, s);
+    return xf ? launch_gemv_t<true, 2>(a, s) : launch_gemv_t<false, 2>(a, s);
+}
+
 H16Plan gemm_h16_plan(int M, int N, int K, bool xf32) {
     H16Plan p{};
     p.ns = 2;

@@ -133,6 +133,10 @@ int run_gemm_qp(mgh_ctx* c, int wtype, mgh::GemmArgs a, bool dbg) {
 
 // The fp16 dequantize-fused GEMM with its split-K plan (workspace from the context).
 int run_gemm_h16(mgh_ctx* c, mgh::GemmH16Args a) {
+    if (mgh::use_gemv_h16(a.M, a.K)) {
+        MGH_HIP(c, mgh::launch_gemv_h16(a, c->stream), "k_gemv_h16");
+        return MGH_OK;
+    }
     const mgh::H16Plan p = mgh::gemm_h16_plan(a.M, a.N, a.K, a.xf != nullptr);
     a.splits = p.splits;
     if (p.splits > 1) {
@@ -838,6 +842,12 @@ int mgh_gemm_h16_f32in_noalloc(mgh_ctx* c, const void* wp16, int N, int K, const
     a.w = (const _Float16*)wp16;
     a.bias = bias; a.resid = resid; a.y = y;
     a.M = M; a.N = N; a.K = K; a.act = act;
+    if (mgh::use_gemv_h16(M, K)) {               // skinny-M kernel: no scratch at all
+        if (int r = set_dev(c)) return r;
+        a.xf = x;
+        MGH_HIP(c, mgh::launch_gemv_h16(a, c->stream), "k_gemv_h16");
+        return MGH_OK;
+    }
     const bool round_pass = M >= 2048;
     const size_t x16_b = round_pass ? round256((size_t)M * K * 2) : 0;
     const mgh::H16Plan p = mgh::gemm_h16_plan(M, N, K, !round_pass);

@@ -173,6 +173,11 @@ size_t packed_weight_bytes_f16(int64_t N, int64_t K);
 hipError_t launch_pack_weights_f16(int wtype, const void* w, void* out, int N, int K, hipStream_t s);
 hipError_t launch_f32_to_f16(const float* x, _Float16* h, int64_t n, hipStream_t s);
 hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a, hipStream_t s);
+// skinny-M form of the same product (1 <= M <= kGemvMaxRows; no workspace), and the rule that
+// picks it over the tiled plan
+constexpr int kGemvMaxRows = 32;
+bool use_gemv_h16(int M, int K);
+hipError_t launch_gemv_h16(const GemmH16Args& a, hipStream_t s);
 
 // Scratch of the no-allocation entry point (noalloc.hip): the device address of this device's
 // copy of a fixed-size file-scope array, looked up once per device.

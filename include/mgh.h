@@ -227,7 +227,10 @@ int mgh_gemm_f32_batched(mgh_ctx* ctx, const float* d_w, const int64_t w_ne[4], 
  *      y[M][N] = act(x16[M][K] . w16^T + bias) + resid with fp16 activations (for example
  *      from mgh_layernorm_affine with MGH_EMIT_DEQ_F16 or mgh_f32_to_f16) and fp32
  *      accumulation; mgh_gemm_h16_f32in rounds fp32 activations to fp16 first (context
- *      scratch). K % 64 == 0, N % 4 == 0, 16-byte aligned operands. ---- */
+ *      scratch). A few activation rows (M <= 16, or M <= 32 with K <= 1024: decode- and
+ *      GEMV-shaped calls) take a skinny-M kernel that streams each weight row once and sums
+ *      K slices across waves, the rest the tiled kernel; the same product and rounding.
+ *      K % 64 == 0, N % 4 == 0, 16-byte aligned operands. ---- */
 size_t mgh_packed_weight_bytes_f16(int N, int K);
 int mgh_pack_weights_f16(mgh_ctx* ctx, int wtype, const void* d_w, int N, int K, void* d_wp16);
 /* x -> fp16 (round to nearest even); n % 8 == 0 */

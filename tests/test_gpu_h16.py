@@ -1,5 +1,6 @@
 """GPU parity of the dequantize-fused fp16 FC path: mgh_pack_weights_f16, mgh_f32_to_f16,
-mgh_gemm_h16 / mgh_gemm_h16_f32in (k_gemm_h16.hip).
+mgh_gemm_h16 / mgh_gemm_h16_f32in (k_gemm_h16.hip: the tiled kernel and, for a few activation
+rows, the skinny-M kernel).
 
 Bars:
   * packed weights: the oracle's dequantization (pinned to the reference decoder) rounded to
@@ -78,7 +79,12 @@ def test_f32_to_f16_rounding(ctx):
     assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
 
 
-SHAPES = [(1, 4, 64), (7, 132, 256), (65, 128, 768), (257, 3072, 768), (1025, 2304, 768),
+# the first eight run the skinny-M kernel (k_gemv_h16: M <= 16, or M <= 32 with K <= 1024),
+# the rest the tiled plans; the pairs (16 | 17, 32 | 33) sit on both sides of the switch and N = 132
+# ends in a partial 16-row weight group
+SHAPES = [(1, 4, 64), (7, 132, 256), (1, 2304, 768), (16, 3072, 768), (17, 2304, 768),
+          (32, 768, 768), (16, 768, 3072), (24, 132, 768), (33, 768, 768), (17, 768, 3072),
+          (65, 128, 768), (257, 3072, 768), (1025, 2304, 768),
           (1025, 768, 768), (1025, 768, 3072), (300, 256, 3072), (4097, 768, 3072),
           (4112, 3072, 768), (4500, 2304, 768), (6150, 2048, 2048), (2731, 1024, 2048)]
 
@@ -143,7 +149,8 @@ def test_gemm_h16_split_k_sequence(ctx):
 @pytest.mark.parametrize("wtype", [ema.WTYPE_Q8_0, ema.WTYPE_Q4_K])
 @pytest.mark.parametrize("M,N,K,act,res", [(257, 768, 768, 0, True), (1025, 3072, 768, 1, False),
                                            (1025, 768, 3072, 0, True), (64, 2304, 768, 0, False),
-                                           (257, 768, 3072, 0, True)])
+                                           (257, 768, 3072, 0, True), (3, 3072, 768, 1, False),
+                                           (9, 768, 3072, 0, True)])
 def test_gemm_h16_f32in_vs_dequant_f32(ctx, wtype, M, N, K, act, res):
     print(f"gemm_h16_f32in wtype={wtype} M={M} N={N} K={K}", flush=True)
     rng = np.random.default_rng(M + N + K + wtype)
@@ -166,7 +173,8 @@ def test_gemm_h16_f32in_vs_dequant_f32(ctx, wtype, M, N, K, act, res):
     assert err <= 1e-3
 
 
-@pytest.mark.parametrize("M,N,K,act,exact", [(65, 128, 768, 0, True), (1025, 3072, 768, 1, True),
+@pytest.mark.parametrize("M,N,K,act,exact", [(5, 768, 3072, 1, True), (20, 2304, 768, 0, True),
+                                             (65, 128, 768, 0, True), (1025, 3072, 768, 1, True),
                                              (1025, 768, 3072, 0, True), (4097, 3072, 768, 2, True),
                                              (1025, 2304, 768, 1, False)])
 def test_gemm_h16_f32in_equals_rounded_operand(ctx, M, N, K, act, exact):
@@ -194,7 +202,7 @@ def test_gemm_h16_f32in_equals_rounded_operand(ctx, M, N, K, act, exact):
         assert np.abs(y1 - y2).max() <= 2e-6 * np.abs(y2).max()
 
 
-@pytest.mark.parametrize("M,N,K,act", [(257, 3072, 768, 1), (1025, 768, 3072, 0)])
+@pytest.mark.parametrize("M,N,K,act", [(9, 3072, 768, 1), (257, 3072, 768, 1), (1025, 768, 3072, 0)])
 def test_gemm_h16_y16_is_rounded_output(ctx, M, N, K, act):
     """The fp16-output variant stores exactly the fp32 result rounded to nearest fp16."""
     print(f"gemm_h16_y16 M={M} N={N} K={K} act={act}", flush=True)

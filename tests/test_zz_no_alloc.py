@@ -1,7 +1,8 @@
 """The entry point that allocates nothing: mgh_gemm_h16_f32in_noalloc (scratch in the library's
 fixed per-GPU array) against mgh_gemm_h16_f32in (context scratch) on the same inputs, bit for
 bit, over consecutive calls that reuse the array with different shapes — a rounding pass plus
-the fp16-operand plan, then a smaller call on the split-K plan, then a tiny one — and the
+the fp16-operand plan, then a smaller call on the split-K plan, then a tiny one, then one on the
+skinny-M kernel (no scratch) — and the
 rejection of a shape whose scratch exceeds the array, before anything runs."""
 import numpy as np
 import pytest
@@ -34,9 +35,11 @@ def _case(ctx, rng, M, N, K, act, resid):
 def test_noalloc_equals_allocating_entry_point():
     rng = np.random.default_rng(77)
     with ema.Context(0) as ctx:
-        # rounding pass into the array (M >= 2048), then a smaller split-K call, then a tiny one
+        # rounding pass into the array (M >= 2048), then a smaller split-K call, then a tiny one,
+        # then a skinny-M call
         for M, N, K, act, resid in ((2500, 768, 3072, 0, True), (1025, 768, 3072, 0, True),
-                                    (37, 96, 512, ema.ACT_GELU, False)):
+                                    (37, 96, 512, ema.ACT_GELU, False),
+                                    (12, 768, 768, ema.ACT_GELU, True)):
             print(f"noalloc M={M} N={N} K={K}", flush=True)
             y0, y1 = _case(ctx, rng, M, N, K, act, resid)
             assert np.isfinite(y0).all()
