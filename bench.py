@@ -31,7 +31,9 @@ roofline = the dominant kernel (k_gemm_h16, resp. k_gemm_qp), HBM-bound: algorit
 its launches (quantized weights once + fp16 activations (+ block scales on the int8 path) +
 fp32 output + bias + residual) divided by its average launch duration, timed with HIP events
 on the stream it runs on; traffic = the measured HBM bytes of those launches (rocprofv3
-FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy), from profiles/.
+FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy), from profiles/traffic_*.json, reported only
+when that file was measured on the same kernel sources (SHA-256 of edge_maskgit_amd/csrc, also
+in config.csrc_sha256_16), else null with the reason in roofline.traffic_source.
 cpu_baseline = the reference's own CPU executor (mg-cpu k_mul_mat, single thread, built
 from the reference sources into oracle/_ref) on the dequantized weights, timed on this
 host over the same four GEMMs; if that library is absent, the C oracle's int8 path.
@@ -149,6 +151,38 @@ class LayerSet:
             return
         for d in self.g:
             self._gemm(d)
+
+
+def csrc_digest():
+    """First 16 hex digits of the SHA-256 of the kernel library's sources (edge_maskgit_amd/csrc,
+    file names and contents in name order): the key that ties a committed rocprofv3 traffic file
+    to the kernels it was measured on."""
+    import hashlib
+    h = hashlib.sha256()
+    d = os.path.join(ROOT, "edge_maskgit_amd", "csrc")
+    for f in sorted(os.listdir(d)):
+        if f.endswith((".hip", ".cpp", ".h")):
+            h.update(f.encode())
+            with open(os.path.join(d, f), "rb") as fh:
+                h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(path, digest):
+    """HBM bytes per step of the headline launches from a committed rocprofv3 summary (FETCH_SIZE +
+    WRITE_SIZE, scaled on a plain copy): (bytes, provenance) when the file was measured on kernel
+    sources with this digest, (None, provenance with the reason) when it was not, (None, None)
+    when there is no file."""
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        tj = json.load(f)
+    src = {"file": os.path.relpath(path, ROOT), "git_head": tj.get("git_head"),
+           "csrc_sha256_16": tj.get("csrc_sha256_16"), "command": tj.get("command")}
+    if tj.get("csrc_sha256_16") == digest:
+        return tj.get("traffic_bytes_per_step"), src
+    src["stale"] = f"measured on kernel sources {tj.get('csrc_sha256_16')}, this run's are {digest}: not used"
+    return None, src
 
 
 def synth_q8_0(w):
@@ -598,10 +632,9 @@ def main():
     cpu = None if a.no_cpu else cpu_baseline(host, M, wtype)
     if not a.no_cpu and cpu is not None and cpu.get("kind") == "reference":
         extra["cpu_oracle_int8_omp"] = cpu_oracle_int8(host, M, wtype)   # a multi-core CPU point
-    traffic = None
-    tf = os.path.join(ROOT, "profiles", f"traffic_{KERNEL[a.path]}_cfg2_q8_m1025.json")
-    if os.path.exists(tf):
-        traffic = json.load(open(tf)).get("traffic_bytes_per_step")   # rocprofv3 --pmc, scaled
+    digest = csrc_digest()
+    traffic, traffic_src = measured_traffic(
+        os.path.join(ROOT, "profiles", f"traffic_{KERNEL[a.path]}_cfg2_q8_m1025.json"), digest)
     line = {
         "metric": "Q8_0/Q4_K GEMM TOPS + % roofline at M=1025/4097; transformer fwd ms",
         "value": round(value, 3),
@@ -620,10 +653,11 @@ def main():
                                "M=1025, fp32 activations and outputs, " + WORKLOAD_PATH[a.path],
                    "path": PATH_NAME[a.path],
                    "M": M, "weights": "Q8_0", "rotate_gb": a.rotate_gb,
-                   "launch": "hip_graph_per_step" if a.graphs else "stream"},
+                   "launch": "hip_graph_per_step" if a.graphs else "stream",
+                   "csrc_sha256_16": digest},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": KERNEL[a.path], "bytes_per_step": gb},
+                     "kernel": KERNEL[a.path], "bytes_per_step": gb, "traffic_source": traffic_src},
         "cpu_baseline": cpu,
         "extra": extra,
     }
