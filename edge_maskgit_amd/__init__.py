@@ -39,7 +39,7 @@ MGH_SYMBOLS = [
     "mgh_decode_step", "mgh_packed_weight_bytes_f16", "mgh_pack_weights_f16", "mgh_f32_to_f16",
     "mgh_gemm_h16", "mgh_gemm_h16_f32in", "mgh_gemm_h16_y16", "mgh_flash_attn_f16kv_o16", "mgh_flash_attn_f16in",
     "mgh_softmax", "mgh_binary", "mgh_scale", "mgh_unary", "mgh_gemm_f32_batched",
-    "mgh_gemm_h16_f32in_noalloc",
+    "mgh_gemm_h16_f32in_noalloc", "mgh_conv2d", "mgh_group_norm", "mgh_upscale",
 ]
 
 _lib = None
@@ -117,6 +117,9 @@ def lib():
         L.mgh_scale.argtypes = [P, P, I64, ctypes.c_float, P]
         L.mgh_unary.argtypes = [P, I, P, I64, P]
         L.mgh_gemm_f32_batched.argtypes = [P, P, P, P, P, P, P, P, I, P, P]
+        L.mgh_conv2d.argtypes = [P, P, I, I, I, I, P, I, I, I, I, I, P]
+        L.mgh_group_norm.argtypes = [P, P, I, I, I, I, I, ctypes.c_float, P, P, P]
+        L.mgh_upscale.argtypes = [P, P, I, I, I, I, I, P]
         L.mgh_graph_begin.argtypes = [P]
         L.mgh_graph_end.argtypes = [P, ctypes.POINTER(P)]
         L.mgh_graph_launch.argtypes = [P, P]
@@ -379,6 +382,18 @@ class Context:
         P, A = self._ptr, (lambda v: (ctypes.c_int64 * 4)(*v))
         self._check(lib().mgh_gemm_f32_batched(self.h, P(w), A(w_ne), A(w_strides), P(x), A(x_ne), A(x_strides),
                                                P(bias), act, P(resid), P(y)))
+
+    # ---- VQGAN decoder ops, layout {W, H, C, N} ----
+    def conv2d(self, x, IW, IH, IC, N, ker, KW, KH, OC, stride, pad, y):
+        P = self._ptr
+        self._check(lib().mgh_conv2d(self.h, P(x), IW, IH, IC, N, P(ker), KW, KH, OC, stride, pad, P(y)))
+
+    def group_norm(self, x, W, H, C, N, groups, eps, gamma, beta, y):
+        P = self._ptr
+        self._check(lib().mgh_group_norm(self.h, P(x), W, H, C, N, groups, eps, P(gamma), P(beta), P(y)))
+
+    def upscale(self, x, W, H, C, N, factor, y):
+        self._check(lib().mgh_upscale(self.h, self._ptr(x), W, H, C, N, factor, self._ptr(y)))
 
     # ---- graphs ----
     def graph_begin(self):

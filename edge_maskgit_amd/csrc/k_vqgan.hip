@@ -1,0 +1,267 @@
+// k_vqgan.hip — the VQGAN decoder's ops on gfx950: 2-D convolution as an implicit GEMM on
+// fp32 MFMA, GroupNorm (+ per-channel affine + SiLU), nearest-neighbour upscale.
+//
+// Semantics (layout ne = {W, H, C, N}, W innermost, every tensor contiguous):
+//  * Conv2D: out[n][oc][oh][ow] = sum over (ic, kh, kw) of ker[oc][ic][kh][kw] *
+//    in[n][ic][oh*stride - pad + kh][ow*stride - pad + kw] (zero outside), fp32 products and
+//    fp32 accumulation — the reference's CPU executor k_conv_2d (src/mg-cpu/mg-cpu.cpp:165-190)
+//    and its non-Mali GPU kernel k_conv2d_t (src/mg-opencl/mg-opencl.cpp:985-1025); only the
+//    summation order differs.
+//  * GroupNorm over each (n, group of C/G channels): mean and variance in double (two passes,
+//    as mg-cpu.cpp:123-147), inv = 1 / sqrt((float)var + eps) with the fp32 sqrt and divide
+//    correctly rounded, y = (float)(x - mean) * inv; with the fused affine + SiLU
+//    (mg-cpu.cpp:262-276, GPU k_group_norm_affine_silu mg-opencl.cpp:1059-1095): xn = y *
+//    gamma[c] + beta[c] (two roundings), out = xn / (1 + exp(-xn)).
+//  * Upscale by f: out[n][c][oh][ow] = in[n][c][oh / f][ow / f] (mg-cpu.cpp:192-198).
+//
+// gfx950 mapping
+//  * Conv2D: a workgroup computes 64 output pixels (flattened p = ow + OW*oh) x 64 output
+//    channels; K = IC*KH*KW in slabs of 16 (the weights' own order: kw fastest, then kh, then
+//    ic). Each thread gathers 4 im2col values (one pixel, four k) and 4 weights per slab into
+//    registers one slab ahead, then writes them to a double-buffered LDS tile; four waves of
+//    2 x 2 v_mfma_f32_16x16x4_f32 tiles read 1-float fragments (bank-conflict free: a row of
+//    16 consecutive pixels or channels). A lane ends with four consecutive pixels of one
+//    channel: one 16-byte store.
+//  * GroupNorm: the statistics of one (n, group) are split over chunks of 4096 elements, one
+//    workgroup each (the reference's one workgroup per group leaves all but 32 CUs idle at
+//    the largest resolution); pass 1 writes per-chunk sums, pass 2 per-chunk sums of squared
+//    deviations from the mean (each workgroup adds the pass-1 partials in chunk order, so every
+//    chunk sees the same mean), and the apply pass derives mean and variance the same way.
+//    Partials are summed in a fixed order: results do not depend on scheduling.
+#include "mgh_common.h"
+#include "mgh_kernels.h"
+
+namespace mgh {
+
+namespace {
+
+constexpr int CBM = 64, CBN = 64, CBK = 16, CPAD = 4;
+
+// KSZ > 0: KW = KH = KSZ known at compile time (the index arithmetic then divides by a
+// constant); 0: any kernel size
+template <int KSZ>
+__global__ __launch_bounds__(256) void k_conv2d_f32(ConvArgs a) {
+    __shared__ float As[2][CBK][CBM + CPAD];    // im2col tile: [k][pixel]
+    __shared__ float Bs[2][CBK][CBN + CPAD];    // weights: [k][channel]
+    const int KW = KSZ ? KSZ : a.KW, KH = KSZ ? KSZ : a.KH;
+    const int IW = a.IW, IH = a.IH, OC = a.OC;
+    const int M = a.OW * a.OH, K = a.IC * KW * KH;
+    const int n = blockIdx.z;
+    const int m0 = blockIdx.x * CBM, n0 = blockIdx.y * CBN;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int r16 = lane & 15, g = lane >> 4;
+
+    // gather roles: im2col values (pixel am, k = ak0 + 4i), weights (k = bk, channel bn0 + 16i)
+    const int am = tid & 63, ak0 = tid >> 6;
+    const int p = m0 + am;
+    const bool pv = p < M;
+    const int ow = pv ? p % a.OW : 0, oh = pv ? p / a.OW : 0;
+    const int iw0 = ow * a.stride - a.pad, ih0 = oh * a.stride - a.pad;
+    const float* inb = a.in + (size_t)n * a.IC * IH * IW;
+    const int bk = tid & 15, bn0 = tid >> 4;
+    float ra[4], rb[4];
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int k = k0 + ak0 + 4 * i;
+            float v = 0.f;
+            if (pv && k < K) {
+                const int kw = k % KW, t = k / KW, kh = t % KH, ic = t / KH;
+                const int iw = iw0 + kw, ih = ih0 + kh;
+                if (iw >= 0 && iw < IW && ih >= 0 && ih < IH) v = inb[iw + (size_t)IW * (ih + (size_t)IH * ic)];
+            }
+            ra[i] = v;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int oc = n0 + bn0 + 16 * i, k = k0 + bk;
+            rb[i] = oc < OC && k < K ? a.ker[(size_t)oc * K + k] : 0.f;
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) As[buf][ak0 + 4 * i][am] = ra[i];
+#pragma unroll
+        for (int i = 0; i < 4; i++) Bs[buf][bk][bn0 + 16 * i] = rb[i];
+    };
+
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int nk = (K + CBK - 1) / CBK;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int t = 0; t < nk; t++) {
+        const int cur = t & 1;
+        if (t + 1 < nk) load((t + 1) * CBK);
+#pragma unroll
+        for (int kk = 0; kk < CBK; kk += 4) {
+            float av[2], bv[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) av[i] = As[cur][kk + g][32 * wm + 16 * i + r16];
+#pragma unroll
+            for (int j = 0; j < 2; j++) bv[j] = Bs[cur][kk + g][32 * wn + 16 * j + r16];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+        }
+        // the other buffer was last read before the previous barrier
+        if (t + 1 < nk) store(cur ^ 1);
+        __syncthreads();
+    }
+    // register e of tile (i, j): pixel m0 + 32wm + 16i + 4g + e, channel n0 + 32wn + 16j + r16
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int oc = n0 + 32 * wn + 16 * j + r16;
+        if (oc >= OC) continue;
+        float* o = a.out + ((size_t)n * OC + oc) * M;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int pp = m0 + 32 * wm + 16 * i + 4 * g;
+            if (pp + 3 < M && (M & 3) == 0) {
+                *(f32x4*)(o + pp) = acc[i][j];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (pp + e < M) o[pp + e] = acc[i][j][e];
+            }
+        }
+    }
+}
+
+constexpr int GN_CHUNK = 4096;
+
+__device__ __forceinline__ double block_sum_d(double v, double* red) {
+    // fixed-order reduction: wave butterflies, then the 4 wave sums in wave order
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)u, o);
+        const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(u >> 32), o);
+        v += __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+// mean of group ng from the pass-1 partials, summed in chunk order
+__device__ __forceinline__ double gn_mean(const double* part, int ng, int chunks, int64_t cnt) {
+    double s = 0.0;
+    for (int c = 0; c < chunks; c++) s += part[(size_t)ng * chunks + c];
+    return s / (double)cnt;
+}
+
+// PASS 0: partial sums of x; PASS 1: partial sums of (x - mean)^2
+template <int PASS>
+__global__ __launch_bounds__(256) void k_gn_stats(const float* __restrict__ x, double* __restrict__ part,
+                                                  double* __restrict__ part2, int64_t cnt, int chunks) {
+    __shared__ double red[4];
+    const int chunk = blockIdx.x, ng = blockIdx.y;
+    const float* xg = x + (size_t)ng * cnt;
+    const int64_t b = (int64_t)chunk * GN_CHUNK, e = min(cnt, b + GN_CHUNK);
+    const double mean = PASS ? gn_mean(part, ng, chunks, cnt) : 0.0;
+    double s = 0.0;
+    for (int64_t i = b + threadIdx.x; i < e; i += 256) {
+        const double d = (double)xg[i] - mean;
+        s += PASS ? d * d : d;
+    }
+    s = block_sum_d(s, red);
+    if (threadIdx.x == 0) (PASS ? part2 : part)[(size_t)ng * chunks + chunk] = s;
+}
+
+template <bool AFFINE_SILU>
+__global__ __launch_bounds__(256) void k_gn_apply(const float* __restrict__ x, const double* __restrict__ part,
+                                                  const double* __restrict__ part2,
+                                                  const float* __restrict__ gamma, const float* __restrict__ beta,
+                                                  float* __restrict__ y, int64_t cnt, int64_t plane, int cpg,
+                                                  int G, int chunks, float eps) {
+#pragma clang fp contract(off)   // xn = y*gamma + beta rounds twice, as in the reference
+    const int chunk = blockIdx.x, ng = blockIdx.y;
+    const double mean = gn_mean(part, ng, chunks, cnt);
+    double q = 0.0;
+    for (int c = 0; c < chunks; c++) q += part2[(size_t)ng * chunks + c];
+    const double var = q / (double)cnt;
+    // fp32 sqrt and divide, each correctly rounded (evaluated in double, rounded once)
+    const float sq = (float)sqrt((double)__fadd_rn((float)var, eps));
+    const float inv = (float)(1.0 / (double)sq);
+    const float* xg = x + (size_t)ng * cnt;
+    float* yg = y + (size_t)ng * cnt;
+    const int c0 = (ng % G) * cpg;
+    const int64_t b = (int64_t)chunk * GN_CHUNK, e = min(cnt, b + GN_CHUNK);
+    for (int64_t i = b + threadIdx.x; i < e; i += 256) {
+        float v = (float)((double)xg[i] - mean) * inv;
+        if (AFFINE_SILU) {
+            const int c = c0 + (int)(i / plane);
+            v = v * gamma[c] + beta[c];
+            v = v / (1.0f + expf(-v));
+        }
+        yg[i] = v;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_upscale(const float* __restrict__ x, float* __restrict__ y, int IW,
+                                                 int IH, int f, int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const int OW = IW * f, OH = IH * f;
+    const int ow = (int)(i % OW);
+    const int64_t r = i / OW;
+    const int oh = (int)(r % OH);
+    const int64_t cn = r / OH;
+    y[i] = x[(cn * IH + oh / f) * IW + ow / f];
+}
+
+}  // namespace
+
+hipError_t launch_conv2d_f32(const ConvArgs& a, hipStream_t s) {
+    const int M = a.OW * a.OH;
+    if (M == 0 || a.OC == 0 || a.N == 0) return hipSuccess;
+    const dim3 grid((unsigned)((M + CBM - 1) / CBM), (unsigned)((a.OC + CBN - 1) / CBN), (unsigned)a.N), block(256);
+    if (a.KW == 3 && a.KH == 3) hipLaunchKernelGGL(k_conv2d_f32<3>, grid, block, 0, s, a);
+    else if (a.KW == 1 && a.KH == 1) hipLaunchKernelGGL(k_conv2d_f32<1>, grid, block, 0, s, a);
+    else hipLaunchKernelGGL(k_conv2d_f32<0>, grid, block, 0, s, a);
+    return hipGetLastError();
+}
+
+size_t group_norm_ws_bytes(int64_t W, int64_t H, int C, int N, int G) {
+    const int64_t cnt = W * H * (C / G);
+    const int64_t chunks = (cnt + GN_CHUNK - 1) / GN_CHUNK;
+    return (size_t)(2 * chunks * G * N) * sizeof(double);
+}
+
+hipError_t launch_group_norm(const float* x, int64_t W, int64_t H, int C, int N, int G, float eps,
+                             const float* gamma, const float* beta, float* y, void* ws, hipStream_t s) {
+    const int cpg = C / G;
+    const int64_t plane = W * H, cnt = plane * cpg;
+    if (cnt == 0 || N == 0) return hipSuccess;
+    const int chunks = (int)((cnt + GN_CHUNK - 1) / GN_CHUNK);
+    double* part = (double*)ws;
+    double* part2 = part + (size_t)chunks * G * N;
+    const dim3 grid((unsigned)chunks, (unsigned)(G * N)), block(256);
+    hipLaunchKernelGGL(k_gn_stats<0>, grid, block, 0, s, x, part, part2, cnt, chunks);
+    hipLaunchKernelGGL(k_gn_stats<1>, grid, block, 0, s, x, part, part2, cnt, chunks);
+    if (gamma)
+        hipLaunchKernelGGL(k_gn_apply<true>, grid, block, 0, s, x, part, part2, gamma, beta, y, cnt, plane, cpg, G,
+                           chunks, eps);
+    else
+        hipLaunchKernelGGL(k_gn_apply<false>, grid, block, 0, s, x, part, part2, gamma, beta, y, cnt, plane, cpg, G,
+                           chunks, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_upscale(const float* x, int IW, int IH, int64_t CN, int f, float* y, hipStream_t s) {
+    const int64_t total = (int64_t)IW * f * IH * f * CN;
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_upscale, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, x, y, IW, IH, f, total);
+    return hipGetLastError();
+}
+
+}  // namespace mgh

@@ -690,6 +690,60 @@ int mgh_unary(mgh_ctx* c, int act, const float* x, int64_t n, float* y) {
     return MGH_OK;
 }
 
+int mgh_conv2d(mgh_ctx* c, const float* in, int IW, int IH, int IC, int N, const float* ker, int KW, int KH,
+               int OC, int stride, int pad, float* out) {
+    if (!c) return MGH_ERR_ARG;
+    if (IW <= 0 || IH <= 0 || IC <= 0 || N < 0 || KW <= 0 || KH <= 0 || OC <= 0 || stride <= 0 || pad < 0)
+        return fail(c, MGH_ERR_ARG, "conv2d: need positive sizes, stride >= 1, pad >= 0");
+    const int64_t OW = ((int64_t)IW + 2 * pad - KW) / stride + 1, OH = ((int64_t)IH + 2 * pad - KH) / stride + 1;
+    if (IW + 2 * (int64_t)pad < KW || IH + 2 * (int64_t)pad < KH || OW <= 0 || OH <= 0)
+        return fail(c, MGH_ERR_ARG, "conv2d: kernel larger than the padded input");
+    // grid: x = ceil(OW*OH / 64) workgroups of 256 threads (at most 2^32 work-items), z = N
+    if ((int64_t)IW * IH > INT32_MAX || OW * OH > ((int64_t)1 << 30) || (int64_t)IC * KW * KH > INT32_MAX ||
+        (int64_t)N > 65535)
+        return fail(c, MGH_ERR_UNSUPPORTED, "conv2d: shape too large");
+    if (N == 0) return MGH_OK;
+    if (!in || !ker || !out) return fail(c, MGH_ERR_ARG, "conv2d: null pointer");
+    if (!aligned16(out)) return fail(c, MGH_ERR_ARG, "conv2d: d_out must be 16-byte aligned");
+    if (int r = set_dev(c)) return r;
+    mgh::ConvArgs a{in, ker, out, IW, IH, IC, (int)OW, (int)OH, OC, KW, KH, stride, pad, N};
+    MGH_HIP(c, mgh::launch_conv2d_f32(a, c->stream), "k_conv2d_f32");
+    return MGH_OK;
+}
+
+int mgh_group_norm(mgh_ctx* c, const float* x, int W, int H, int C, int N, int groups, float eps,
+                   const float* gamma, const float* beta, float* y) {
+    if (!c) return MGH_ERR_ARG;
+    if (W <= 0 || H <= 0 || C <= 0 || N < 0 || groups <= 0 || C % groups)
+        return fail(c, MGH_ERR_ARG, "group_norm: need positive sizes and C % groups == 0");
+    if (!(eps >= 0.0f)) return fail(c, MGH_ERR_ARG, "group_norm: eps must be >= 0");
+    if ((gamma == nullptr) != (beta == nullptr))
+        return fail(c, MGH_ERR_ARG, "group_norm: gamma and beta go together (affine + SiLU) or not at all");
+    // grid: x = one workgroup of 256 per 4096-element chunk of a group, y = groups * N
+    if ((int64_t)groups * N > 65535 || (int64_t)W * H * (C / groups) > ((int64_t)1 << 32))
+        return fail(c, MGH_ERR_UNSUPPORTED, "group_norm: shape too large");
+    if (N == 0) return MGH_OK;
+    if (!x || !y) return fail(c, MGH_ERR_ARG, "group_norm: null pointer");
+    if (int r = set_dev(c)) return r;
+    if (int r = ensure_scratch(c, mgh::group_norm_ws_bytes(W, H, C, N, groups))) return r;
+    MGH_HIP(c, mgh::launch_group_norm(x, W, H, C, N, groups, eps, gamma, beta, y, c->scratch, c->stream),
+            "k_group_norm");
+    return MGH_OK;
+}
+
+int mgh_upscale(mgh_ctx* c, const float* x, int W, int H, int C, int N, int factor, float* y) {
+    if (!c) return MGH_ERR_ARG;
+    if (W <= 0 || H <= 0 || C <= 0 || N < 0 || factor <= 0) return fail(c, MGH_ERR_ARG, "upscale: need positive sizes");
+    if ((int64_t)W * factor > INT32_MAX || (int64_t)H * factor > INT32_MAX ||
+        (double)W * H * factor * factor * C * N > (double)((int64_t)1 << 31))
+        return fail(c, MGH_ERR_UNSUPPORTED, "upscale: shape too large");
+    if (N == 0) return MGH_OK;
+    if (!x || !y) return fail(c, MGH_ERR_ARG, "upscale: null pointer");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_upscale(x, W, H, (int64_t)C * N, factor, y, c->stream), "k_upscale");
+    return MGH_OK;
+}
+
 int mgh_gemm_f32_batched(mgh_ctx* c, const float* w, const int64_t wne[4], const int64_t ws[4], const float* x,
                          const int64_t xne[4], const int64_t xs[4], const float* bias, int act, const float* resid,
                          float* y) {

@@ -181,6 +181,19 @@ hipError_t launch_gemv_h16(const GemmH16Args& a, hipStream_t s);
 
 // Scratch of the no-allocation entry point (noalloc.hip): the device address of this device's
 // copy of a fixed-size file-scope array, looked up once per device.
+// VQGAN decoder ops (k_vqgan.hip); layouts {W, H, C, N}, W innermost, contiguous
+struct ConvArgs {
+    const float* in;       // {IW, IH, IC, N}
+    const float* ker;      // {KW, KH, IC, OC}
+    float* out;            // {OW, OH, OC, N}
+    int IW, IH, IC, OW, OH, OC, KW, KH, stride, pad, N;
+};
+hipError_t launch_conv2d_f32(const ConvArgs& a, hipStream_t s);
+size_t group_norm_ws_bytes(int64_t W, int64_t H, int C, int N, int G);
+hipError_t launch_group_norm(const float* x, int64_t W, int64_t H, int C, int N, int G, float eps,
+                             const float* gamma, const float* beta, float* y, void* ws, hipStream_t s);
+hipError_t launch_upscale(const float* x, int IW, int IH, int64_t CN, int f, float* y, hipStream_t s);
+
 size_t noalloc_scratch_bytes();
 hipError_t noalloc_scratch(int device, void** out);
 

@@ -219,6 +219,21 @@ int mgh_gemm_f32_batched(mgh_ctx* ctx, const float* d_w, const int64_t w_ne[4], 
                          const float* d_x, const int64_t x_ne[4], const int64_t x_strides[4],
                          const float* d_bias, int act, const float* d_resid, float* d_y);
 
+/* ---- VQGAN decoder ops, layout ne = {W, H, C, N} (W innermost), fp32, contiguous.
+ *      mgh_conv2d: the Conv2D node (CPU mg-cpu.cpp:165-190; GPU k_conv2d_t,
+ *      mg-opencl.cpp:985-1025, 1535-1566): ker {KW, KH, IC, OC}, out {OW, OH, OC, N} with
+ *      OW = (IW + 2 pad - KW) / stride + 1; fp32 products and accumulation; d_out 16-byte aligned.
+ *      mgh_group_norm: the GroupNorm node (mg-cpu.cpp:123-147, 262-276; mg-opencl.cpp:1027-1095,
+ *      1568-1590): statistics per (n, group) in double, y = (x - mean) / sqrt(var + eps); with
+ *      d_gamma and d_beta [C] also the fused per-channel affine and SiLU (both null: plain).
+ *      Scratch from the context. mgh_upscale: nearest-neighbour upscale by factor
+ *      (mg-cpu.cpp:192-198, mg-opencl.cpp:1096-1103, 1591-1599). ---- */
+int mgh_conv2d(mgh_ctx* ctx, const float* d_in, int IW, int IH, int IC, int N, const float* d_ker,
+               int KW, int KH, int OC, int stride, int pad, float* d_out);
+int mgh_group_norm(mgh_ctx* ctx, const float* d_x, int W, int H, int C, int N, int groups, float eps,
+                   const float* d_gamma, const float* d_beta, float* d_y);
+int mgh_upscale(mgh_ctx* ctx, const float* d_x, int W, int H, int C, int N, int factor, float* d_y);
+
 /* ---- dequantize-fused fp16 FC path: the reference's fp16-slab dequant GEMMs
  *      k_mul_mat_q8_0_t2_h / k_mul_mat_q4k_t2_h (src/mg-opencl/mg-opencl.cpp:320-411).
  *      mgh_pack_weights_f16 expands raw Q8_0 / Q4_K blocks once into fp16 [N][K]
