@@ -38,7 +38,7 @@ EXTRA_FLAGS = {"k_gemm_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
                "k_gemm_qp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 # C++ host runtime (graph API mirror, GGUF loader, transformer builder, HipRuntime, mgr C ABI):
 # plain host code over the libmgh C ABI, compiled with g++ into lib/libmg_hip.so.
-HOST_SOURCES = ["mg-tensor.cpp", "mg-model.cpp", "mg-transformer.cpp", "mg-hip.cpp", "mgr_api.cpp"]
+HOST_SOURCES = ["mg-tensor.cpp", "mg-model.cpp", "mg-transformer.cpp", "mg-vqgan.cpp", "mg-hip.cpp", "mgr_api.cpp"]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-parameter"]
 
 

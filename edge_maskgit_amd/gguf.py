@@ -10,7 +10,7 @@ from __future__ import annotations
 import struct
 
 GGML_F32, GGML_Q8_0, GGML_Q4_K = 0, 8, 12
-_U32, _I32, _F32, _STR = 4, 5, 6, 8
+_U32, _I32, _F32, _STR, _ARRAY = 4, 5, 6, 8, 9
 ALIGN = 32
 
 def _s(b: bytearray, text: str):
@@ -19,7 +19,7 @@ def _s(b: bytearray, text: str):
 
 
 def write_gguf(path: str, meta: list, tensors: list) -> None:
-    """meta: [(key, kind, value)] with kind in {"u32", "i32", "f32", "str"};
+    """meta: [(key, kind, value)] with kind in {"u32", "i32", "f32", "str", "i32_array"};
     tensors: [(name, numpy shape, ggml type, raw bytes)]."""
     kv = bytearray()
     for key, kind, val in meta:
@@ -30,6 +30,8 @@ def write_gguf(path: str, meta: list, tensors: list) -> None:
             kv += struct.pack("<Ii", _I32, val)
         elif kind == "f32":
             kv += struct.pack("<If", _F32, val)
+        elif kind == "i32_array":       # array type, element type, count, elements
+            kv += struct.pack("<IIQ", _ARRAY, _I32, len(val)) + struct.pack(f"<{len(val)}i", *val)
         else:
             kv += struct.pack("<I", _STR)
             _s(kv, val)

@@ -55,6 +55,9 @@ const char* op_name(const Tensor* t) {
         case Op::Gelu: return "Gelu";
         case Op::Silu: return "Silu";
         case Op::Cont: return "Cont";
+        case Op::GroupNorm: return "GroupNorm";
+        case Op::Conv2D: return "Conv2D";
+        case Op::Upscale: return "Upscale";
         default: return "Other";
     }
 }
@@ -751,6 +754,52 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                 Impl::elem_strides(t->src[0], st);
                 const int64_t ne[4] = {t->ne[0], t->ne[1], t->ne[2], t->ne[3]};
                 I.check(mgh_copy_strided(I.ctx, (const float*)I.dev(t->src[0]), ne, st, (float*)out));
+                break;
+            }
+            case Op::Conv2D: {
+                // src[0] kernel {KW, KH, IC, OC}, src[1] input {IW, IH, IC, N}; iparam[0] stride,
+                // iparam[1] pad (mg-tensor.cpp:167-177, dispatch mg-opencl.cpp:1535-1566)
+                const Tensor* k = t->src[0];
+                const Tensor* x = t->src[1];
+                if (k->type != Type::F32 || x->type != Type::F32 || !k->is_contiguous() || !x->is_contiguous())
+                    throw std::runtime_error("HipRuntime: Conv2D needs contiguous F32 kernel and input");
+                if (k->ne[2] != x->ne[2] || t->ne[2] != k->ne[3] || t->ne[3] != x->ne[3])
+                    throw std::runtime_error("HipRuntime: Conv2D kernel channels must match the input's");
+                const int64_t dims[] = {x->ne[0], x->ne[1], x->ne[2], x->ne[3], k->ne[0], k->ne[1], k->ne[3]};
+                for (int64_t d : dims)
+                    if (d > INT32_MAX) throw std::runtime_error("HipRuntime: Conv2D dimension too large");
+                I.check(mgh_conv2d(I.ctx, (const float*)I.dev(x), (int)x->ne[0], (int)x->ne[1], (int)x->ne[2],
+                                   (int)x->ne[3], (const float*)I.dev(k), (int)k->ne[0], (int)k->ne[1],
+                                   (int)k->ne[3], t->iparam[0], t->iparam[1], (float*)out));
+                break;
+            }
+            case Op::GroupNorm: {
+                // iparam[0] groups, fparam[1] eps; affine + SiLU when iparam[1] == 1 with gamma and
+                // beta in src[1], src[2] (mg-opencl.cpp:1568-1590)
+                const Tensor* x = t->src[0];
+                if (x->type != Type::F32 || !x->is_contiguous())
+                    throw std::runtime_error("HipRuntime: GroupNorm needs a contiguous F32 input");
+                const bool fused = t->src[1] && t->src[2] && t->iparam[1] == 1;
+                if (fused)
+                    for (const Tensor* p : {t->src[1], t->src[2]})
+                        if (p->type != Type::F32 || !p->is_contiguous() || p->nelements() != t->ne[2])
+                            throw std::runtime_error("HipRuntime: GroupNorm gamma/beta must be F32 [C]");
+                for (int d = 0; d < 4; d++)
+                    if (t->ne[d] > INT32_MAX) throw std::runtime_error("HipRuntime: GroupNorm dimension too large");
+                I.check(mgh_group_norm(I.ctx, (const float*)I.dev(x), (int)t->ne[0], (int)t->ne[1], (int)t->ne[2],
+                                       (int)t->ne[3], t->iparam[0], t->fparam[1],
+                                       fused ? (const float*)I.dev(t->src[1]) : nullptr,
+                                       fused ? (const float*)I.dev(t->src[2]) : nullptr, (float*)out));
+                break;
+            }
+            case Op::Upscale: {
+                const Tensor* x = t->src[0];
+                if (x->type != Type::F32 || !x->is_contiguous())
+                    throw std::runtime_error("HipRuntime: Upscale needs a contiguous F32 input");
+                for (int d = 0; d < 4; d++)
+                    if (x->ne[d] > INT32_MAX) throw std::runtime_error("HipRuntime: Upscale dimension too large");
+                I.check(mgh_upscale(I.ctx, (const float*)I.dev(x), (int)x->ne[0], (int)x->ne[1], (int)x->ne[2],
+                                    (int)x->ne[3], t->iparam[0], (float*)out));
                 break;
             }
             default:

@@ -1,6 +1,7 @@
 // mgr_api.cpp — C entry points (include/mgr.h) over Model + build_transformer + HipRuntime.
 #include "mgr.h"
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <exception>
@@ -13,6 +14,7 @@
 #include "mgh.h"
 #include "mg-model.hpp"
 #include "mg-transformer.hpp"
+#include "mg-vqgan.hpp"
 
 namespace {
 thread_local std::string g_err;
@@ -67,6 +69,33 @@ struct mgr_model {
 };
 
 namespace {
+
+// host bytes the VQGAN decoder graph's nodes reserve for B images (each node keeps host
+// storage, the reference's Context semantics; the arena is not zero-filled, so only the
+// ids and the image pages are ever touched): the nodes of build_vqgan_decoder level by
+// level — a res block at most 6 nodes of its wider width, an up-sampling 3 nodes at twice
+// the side — plus alignment slack
+size_t vqgan_graph_bytes(const mg::HParams& h, int B) {
+    int64_t L = 1;
+    while (L * L < h.n_tokens) L++;
+    const std::vector<int>& mult = h.vq_channel_mult;
+    if (mult.empty()) return 64u << 20;
+    const int R = h.vq_num_res_blocks;
+    int64_t side = L, width = (int64_t)h.vq_filters * mult.back();
+    int64_t el = 2 * (int64_t)h.vq_embedding_dim * L * L + 2 * L * L * width + 6 * R * L * L * width;
+    for (int i = (int)mult.size() - 1; i >= 0; i--) {
+        const int64_t out = (int64_t)h.vq_filters * mult[i];
+        el += 6 * R * side * side * std::max(width, out);
+        if (R > 0) width = out;
+        if (i > 0) {
+            side *= 2;
+            el += 3 * side * side * width;
+        }
+    }
+    el += side * side * (width + 6);
+    const size_t nodes = 64 + 16 * (size_t)(R + 2) * mult.size();
+    return (size_t)el * B * 4 + nodes * 64 + (64u << 20);
+}
 
 void grow(mgh_ctx* c, void** p, size_t* cap, size_t need) {
     if (*cap >= need) return;
@@ -146,6 +175,48 @@ int mgr_forward(mgr_model* m, const int32_t* tokens, int S, int B, float* logits
         const void* d = m->rt->compute_device(g);
         mgh_ctx* c = m->rt->context();
         check(c, logits ? mgh_d2h(c, logits, d, out->nbytes()) : mgh_sync(c));
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e);
+    }
+}
+
+int mgr_image_side(const mgr_model* m) {
+    if (!m) return -1;
+    const mg::HParams& h = m->model->hparams();
+    if (h.n_tokens <= 0 || h.vq_channel_mult.empty()) return 0;
+    int64_t L = 1;
+    while (L * L < h.n_tokens) L++;
+    return (int)(L << (h.vq_channel_mult.size() - 1));   // one 2x up-sampling per level but the last
+}
+
+int mgr_decode_images(mgr_model* m, const int32_t* grids, int B, float* images) {
+    if (!m || !grids || B <= 0) {
+        g_err = "mgr_decode_images: bad argument";
+        return -1;
+    }
+    try {
+        const mg::HParams& h = m->model->hparams();
+        if (h.n_tokens <= 0 || h.vq_embedding_dim <= 0) throw std::runtime_error("mgr_decode_images: no VQGAN in the model");
+        const size_t need = vqgan_graph_bytes(h, B);
+        if (!m->gctx || m->gctx_bytes < need) {
+            m->gctx.reset(new mg::Context(need));
+            m->gctx_bytes = need;
+        }
+        m->gctx->reset();
+        mg::Tensor* ids = m->gctx->tensor2d(mg::Type::I32, h.n_tokens, B);
+        std::memcpy(ids->data, grids, (size_t)h.n_tokens * B * sizeof(int32_t));
+        for (int64_t i = 0; i < (int64_t)h.n_tokens * B; i++)
+            if (grids[i] < 0 || grids[i] >= h.vq_codebook_size)
+                throw std::runtime_error("mgr_decode_images: code id outside the codebook");
+        mg::Tensor* out = mg::build_vqgan_decoder(*m->gctx, *m->model, ids);
+        mg::Graph g;
+        g.build_forward(out);
+        m->named.clear();
+        m->rt->invalidate(ids);               // new ids at a reused host address
+        const void* d = m->rt->compute_device(g);
+        mgh_ctx* c = m->rt->context();
+        check(c, images ? mgh_d2h(c, images, d, out->nbytes()) : mgh_sync(c));
         return 0;
     } catch (const std::exception& e) {
         return fail(e);

@@ -16,7 +16,8 @@ from . import LIB_DIR, MghError
 
 MGR_SYMBOLS = ["mgr_load", "mgr_free", "mgr_last_error", "mgr_hparams", "mgr_device_name",
                "mgr_forward", "mgr_profile_enable", "mgr_profile_report", "mgr_gguf_info",
-               "mgr_graph_stats", "mgr_decode_params", "mgr_generate", "mgr_named"]
+               "mgr_graph_stats", "mgr_decode_params", "mgr_generate", "mgr_named", "mgr_decode_images",
+               "mgr_image_side"]
 
 _lib = None
 
@@ -44,6 +45,8 @@ def lib():
         L.mgr_decode_params.argtypes = [P, P, P, P]
         L.mgr_generate.argtypes = [P, P, P, I, I, ctypes.c_float, P]
         L.mgr_named.argtypes = [P, ctypes.c_char_p, P, ctypes.c_int64]
+        L.mgr_decode_images.argtypes = [P, P, I, P]
+        L.mgr_image_side.argtypes = [P]
         _lib = L
     return _lib
 
@@ -127,6 +130,20 @@ class TransformerRuntime:
         _check(lib().mgr_generate(self.h, cls.ctypes.data_as(ctypes.c_void_p),
                                   sd.ctypes.data_as(ctypes.c_void_p), cls.size, steps, temperature,
                                   out.ctypes.data_as(ctypes.c_void_p)))
+        return out
+
+    def decode_images(self, grids, readback: bool = True):
+        """VQGAN decode (mgr_decode_images): token grids int32 [B][n_tokens] -> images float32
+        [B][3][side][side] (None without readback)."""
+        g = np.ascontiguousarray(grids, dtype=np.int32)
+        if g.ndim == 1:
+            g = g[None]
+        if g.ndim != 2 or g.shape[1] != self.hparams["n_tokens"]:
+            raise ValueError(f"grids must be [B][{self.hparams['n_tokens']}]")
+        side = _check(lib().mgr_image_side(self.h))
+        out = np.empty((g.shape[0], 3, side, side), np.float32) if readback else None
+        _check(lib().mgr_decode_images(self.h, g.ctypes.data_as(ctypes.c_void_p), g.shape[0],
+                                       None if out is None else out.ctypes.data_as(ctypes.c_void_p)))
         return out
 
     def named(self, name: str) -> np.ndarray:

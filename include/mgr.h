@@ -52,6 +52,16 @@ int mgr_named(const mgr_model* m, const char* name, float* out, int64_t capacity
 int mgr_generate(mgr_model* m, const int32_t* class_ids, const uint64_t* seeds, int B, int steps,
                  float temperature, int32_t* out_tokens);
 
+/* The VQGAN decode of B token grids: grids [B][n_tokens] (I32 codebook ids, row-major h*L + w
+ * of the L x L latent grid) -> images [B][3][side][side] (fp32, channel planes, w innermost: the
+ * reference's image layout ne = {W, H, 3, 1} per image). The graph is the reference's decoder
+ * (mg::build_vqgan_decoder, src/mg-vqgan.cpp:62-110), the computation of its VqganFwd hook
+ * (include/mg-generate.hpp:17, tools/main.cpp:137-152), here for B images in one graph.
+ * images may be NULL: the decode then runs without the readback. */
+int mgr_decode_images(mgr_model* m, const int32_t* grids, int B, float* images);
+/* side of the decoded images: sqrt(n_tokens) * 2^(levels - 1); 0 if the model has no VQGAN */
+int mgr_image_side(const mgr_model* m);
+
 /* per-op device-time profile of the following forwards (each node timed on its own) */
 int mgr_profile_enable(mgr_model* m, int on);
 /* writes up to cap rows "name count ms\n" into buf (NUL-terminated) */

@@ -34,6 +34,12 @@ def lib():
         L.mgref_transformer_forward.argtypes = [ctypes.c_char_p, P, I64, I64, P, I64]
         L.mgref_generate.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_uint64, ctypes.c_int,
                                      ctypes.c_float, P, P, P]
+        L.mgref_conv2d.argtypes = [P, I64, I64, I64, I64, P, I64, I64, I64, ctypes.c_int, ctypes.c_int, P, I64]
+        L.mgref_group_norm.argtypes = [P, I64, I64, I64, I64, ctypes.c_int, ctypes.c_float, P, P, P]
+        L.mgref_upscale.argtypes = [P, I64, I64, I64, I64, ctypes.c_int, P]
+        L.mgref_vqgan_decode.argtypes = [ctypes.c_char_p, P, I64, P, I64, I64]
+        L.mgref_vqgan_graph_sig.argtypes = [ctypes.c_char_p, I64, I64, ctypes.c_char_p, I64]
+        L.mgref_vqgan_graph_sig.restype = I64
         _lib = L
     return _lib
 
@@ -94,3 +100,52 @@ def generate(gguf_path: str, class_id: int, seed: int, steps: int, temperature: 
     _check(lib().mgref_generate(gguf_path.encode(), class_id, seed, steps, temperature, _p(logits),
                                 _p(toks), _p(grid)))
     return toks, grid
+
+
+# ---- VQGAN decoder ops and graph (layout {W, H, C, N}; numpy arrays [N][C][H][W]) ----
+def conv2d(x, ker, stride, pad):
+    """x [N][IC][IH][IW], ker [OC][IC][KH][KW] -> [N][OC][OH][OW] (k_conv_2d, mg-cpu.cpp:165-190)"""
+    x = np.ascontiguousarray(x, np.float32)
+    ker = np.ascontiguousarray(ker, np.float32)
+    N, IC, IH, IW = x.shape
+    OC, _, KH, KW = ker.shape
+    OH, OW = (IH + 2 * pad - KH) // stride + 1, (IW + 2 * pad - KW) // stride + 1
+    y = np.empty((N, OC, OH, OW), np.float32)
+    _check(lib().mgref_conv2d(_p(x), IW, IH, IC, N, _p(ker), KW, KH, OC, stride, pad, _p(y), y.size))
+    return y
+
+
+def group_norm(x, groups, eps, gamma=None, beta=None):
+    """x [N][C][H][W]; with gamma/beta: the fused affine + SiLU node"""
+    x = np.ascontiguousarray(x, np.float32)
+    N, C, H, W = x.shape
+    g = None if gamma is None else np.ascontiguousarray(gamma, np.float32)
+    b = None if beta is None else np.ascontiguousarray(beta, np.float32)
+    y = np.empty_like(x)
+    _check(lib().mgref_group_norm(_p(x), W, H, C, N, groups, eps, _p(g), _p(b), _p(y)))
+    return y
+
+
+def upscale(x, f):
+    x = np.ascontiguousarray(x, np.float32)
+    N, C, H, W = x.shape
+    y = np.empty((N, C, H * f, W * f), np.float32)
+    _check(lib().mgref_upscale(_p(x), W, H, C, N, f, _p(y)))
+    return y
+
+
+def vqgan_decode(gguf_path: str, grid, side: int, arena_bytes: int = 1 << 30):
+    """the reference's decoder graph on its CPU executor: grid [n_tokens] -> image [3][side][side]"""
+    grid = np.ascontiguousarray(grid, np.int32).reshape(-1)
+    img = np.empty((3, side, side), np.float32)
+    _check(lib().mgref_vqgan_decode(gguf_path.encode(), _p(grid), grid.size, _p(img), img.size, arena_bytes))
+    return img
+
+
+def vqgan_graph_sig(gguf_path: str, n_tokens: int, arena_bytes: int = 1 << 30) -> str:
+    n = lib().mgref_vqgan_graph_sig(gguf_path.encode(), n_tokens, arena_bytes, None, 0)
+    if n < 0:
+        _check(-1)
+    buf = ctypes.create_string_buffer(n + 1)
+    lib().mgref_vqgan_graph_sig(gguf_path.encode(), n_tokens, arena_bytes, buf, n + 1)
+    return buf.value.decode()

@@ -1,7 +1,7 @@
 // ref_harness.cpp — C entry points over the reference's own CPU executor (TEST INFRASTRUCTURE).
 //
 // Linked against the reference sources where they lie (mg-tensor.cpp, mg-cpu/mg-cpu.cpp,
-// mg-model.cpp, mg-transformer.cpp) by oracle/Makefile into oracle/_ref/libmgref.so. Only
+// mg-model.cpp, mg-transformer.cpp, mg-generate.cpp, mg-vqgan.cpp) by oracle/Makefile into oracle/_ref/libmgref.so. Only
 // tests and bench.py's cpu_baseline leg load it. Each function builds the same graph the
 // reference builds and runs the reference's mg::compute (src/mg-cpu/mg-cpu.cpp:296-298),
 // so its results are the reference's F32 CPU semantics, not a restatement.
@@ -9,8 +9,10 @@
 #include "mg-model.hpp"
 #include "mg-tensor.hpp"
 #include "mg-transformer.hpp"
+#include "mg-vqgan.hpp"
 
 #include "graph_cases.h"
+#include "graph_sig.h"
 
 #include <cstdint>
 #include <cstring>
@@ -150,6 +152,87 @@ int mgref_generate(const char* gguf_path, int class_id, uint64_t seed, int steps
         generate(*model, cfg, false, fwd, vq);
         if (step != steps) { g_err = "fewer forwards than steps"; return -2; }
         return 0;
+    } catch (const std::exception& e) { g_err = e.what(); return -1; }
+}
+
+// conv_2d (mg-tensor.cpp:167-177) on the CPU executor's k_conv_2d (mg-cpu.cpp:165-190):
+// in {IW, IH, IC, N}, ker {KW, KH, IC, OC} -> out {OW, OH, OC, N}
+int mgref_conv2d(const float* in, int64_t IW, int64_t IH, int64_t IC, int64_t N, const float* ker,
+                 int64_t KW, int64_t KH, int64_t OC, int stride, int pad, float* out, int64_t out_len) {
+    try {
+        Context c((size_t)out_len * 4 + (16 << 20));   // the output node's storage is in the arena
+        int64_t ni[4] = {IW, IH, IC, N}, nk[4] = {KW, KH, IC, OC};
+        Tensor* ti = c.external(Type::F32, 4, ni, const_cast<float*>(in));
+        Tensor* tk = c.external(Type::F32, 4, nk, const_cast<float*>(ker));
+        Tensor* o = conv_2d(c, tk, ti, stride, pad);
+        if (o->nelements() != out_len) { g_err = "conv2d output size mismatch"; return -2; }
+        Graph g; g.build_forward(o); compute(c, g);
+        std::memcpy(out, o->data, (size_t)out_len * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) { g_err = e.what(); return -1; }
+}
+
+// group_norm / group_norm_affine_silu (mg-tensor.cpp:148-163) on the CPU executor
+// (mg-cpu.cpp:123-147, 262-276); gamma == NULL: no affine
+int mgref_group_norm(const float* x, int64_t W, int64_t H, int64_t C, int64_t N, int groups, float eps,
+                     const float* gamma, const float* beta, float* y) {
+    try {
+        const size_t n = (size_t)(W * H * C * N);
+        Context c(n * 4 + (16 << 20));
+        int64_t nx[4] = {W, H, C, N}, nc[4] = {C, 1, 1, 1};
+        Tensor* tx = c.external(Type::F32, 4, nx, const_cast<float*>(x));
+        Tensor* o = gamma ? group_norm_affine_silu(c, tx, c.external(Type::F32, 1, nc, const_cast<float*>(gamma)),
+                                                   c.external(Type::F32, 1, nc, const_cast<float*>(beta)), groups, eps)
+                          : group_norm(c, tx, groups, eps);
+        Graph g; g.build_forward(o); compute(c, g);
+        std::memcpy(y, o->data, n * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) { g_err = e.what(); return -1; }
+}
+
+// upscale (mg-tensor.cpp:179-184, mg-cpu.cpp:192-198)
+int mgref_upscale(const float* x, int64_t W, int64_t H, int64_t C, int64_t N, int f, float* y) {
+    try {
+        const size_t n = (size_t)(W * H * C * N) * f * f;
+        Context c(n * 4 + (16 << 20));
+        int64_t nx[4] = {W, H, C, N};
+        Tensor* o = upscale(c, c.external(Type::F32, 4, nx, const_cast<float*>(x)), f);
+        Graph g; g.build_forward(o); compute(c, g);
+        std::memcpy(y, o->data, n * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) { g_err = e.what(); return -1; }
+}
+
+// The reference's VQGAN decode of one token grid: Model::load + build_vqgan_decoder
+// (mg-vqgan.cpp:62-110) + the CPU executor, as tools/verify-vqgan.cpp runs it.
+// grid [n_tokens] -> image {W, H, 3, 1} (out_len floats). arena_bytes: the graph arena.
+int mgref_vqgan_decode(const char* gguf_path, const int32_t* grid, int64_t n_tokens, float* img,
+                       int64_t out_len, int64_t arena_bytes) {
+    try {
+        Context wctx(64 << 20);
+        auto model = Model::load(gguf_path, wctx);
+        Context ctx((size_t)arena_bytes);
+        Tensor* gt = ctx.tensor1d(Type::I32, n_tokens);
+        std::memcpy(gt->data, grid, (size_t)n_tokens * sizeof(int32_t));
+        Tensor* out = build_vqgan_decoder(ctx, *model, gt);
+        if (out->nelements() != out_len) { g_err = "image size mismatch"; return -2; }
+        Graph g; g.build_forward(out); compute(ctx, g);
+        std::memcpy(img, out->data, (size_t)out_len * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) { g_err = e.what(); return -1; }
+}
+
+// The signature (graph_sig.h) of the reference builder's decoder graph for one grid of
+// n_tokens ids; the graph is built, not run. Returns the signature length.
+int64_t mgref_vqgan_graph_sig(const char* gguf_path, int64_t n_tokens, int64_t arena_bytes, char* buf,
+                              int64_t cap) {
+    try {
+        Context wctx(64 << 20);
+        auto model = Model::load(gguf_path, wctx);
+        Context ctx((size_t)arena_bytes);
+        Tensor* gt = ctx.tensor1d(Type::I32, n_tokens);
+        Graph g; g.build_forward(build_vqgan_decoder(ctx, *model, gt));
+        return graph_sig::copy_out(graph_sig::describe(g), buf, cap);
     } catch (const std::exception& e) { g_err = e.what(); return -1; }
 }
 

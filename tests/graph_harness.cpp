@@ -3,9 +3,12 @@
 // oracle/ref_harness.cpp; tests/test_gpu_graph.py compares the two. Built by
 // __graft_entry__.build() into tests/_build/libgraph_harness.so.
 #include "mg-hip.hpp"
+#include "mg-model.hpp"
 #include "mg-tensor.hpp"
+#include "mg-vqgan.hpp"
 
 #include "graph_cases.h"
+#include "graph_sig.h"
 
 #include <cstdint>
 #include <cstring>
@@ -62,6 +65,24 @@ int gh_api_checks() {
     mg::Tensor* q = c.external(mg::Type::Q8_0, 2, qne, nullptr);
     if (!q->is_contiguous()) return 3;
     return 0;
+}
+
+// The signature (graph_sig.h) of build_vqgan_decoder's graph for B grids of n_tokens ids
+// (ids ne = {n_tokens} for B == 1, {n_tokens, B} otherwise); built, not run (host only).
+int64_t gh_vqgan_graph_sig(const char* gguf_path, int64_t n_tokens, int64_t B, int64_t arena_bytes, char* buf,
+                           int64_t cap) {
+    try {
+        mg::Context wctx(64 << 20);
+        auto model = mg::Model::load(gguf_path, wctx);
+        mg::Context ctx((size_t)arena_bytes);
+        mg::Tensor* ids = B == 1 ? ctx.tensor1d(mg::Type::I32, n_tokens) : ctx.tensor2d(mg::Type::I32, n_tokens, B);
+        mg::Graph g;
+        g.build_forward(mg::build_vqgan_decoder(ctx, *model, ids));
+        return graph_sig::copy_out(graph_sig::describe(g), buf, cap);
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
 }
 
 }  // extern "C"

@@ -91,3 +91,60 @@ def tokens(rng, S: int, B: int, vocab: int = 2025, n_codes: int = 1024, mask_id:
     m = rng.random((B, S - 1)) < 0.5
     t[:, 1:][m] = mask_id
     return t
+
+
+def vqgan_tensors(rng, E: int = 32, codebook: int = 64, filters: int = 32, mult=(1, 2), R: int = 1) -> dict:
+    """Random decoder weights under the converter's names (tools/convert_to_gguf.py:216-226),
+    numpy shapes (conv [OC][IC][KH][KW]); conv weights ~N(0, 1/fan_in) keep activations O(1)."""
+    t = {}
+
+    def conv(name, oc, ic, k, bias):
+        t[name + ".weight"] = (rng.standard_normal((oc, ic, k, k)) / np.sqrt(ic * k * k)).astype(np.float32)
+        if bias:
+            t[name + ".bias"] = (0.05 * rng.standard_normal(oc)).astype(np.float32)
+
+    def gn(name, c):
+        t[name + ".weight"] = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+        t[name + ".bias"] = (0.1 * rng.standard_normal(c)).astype(np.float32)
+
+    def block(p, cin, cout):
+        gn(p + "norm0", cin)
+        conv(p + "conv0", cout, cin, 3, False)
+        gn(p + "norm1", cout)
+        conv(p + "conv1", cout, cout, 3, False)
+        if cin != cout:
+            conv(p + "conv_res", cout, cout, 1, False)
+
+    t["vqgan.quantizer.codebook.weight"] = rng.standard_normal((codebook, E)).astype(np.float32)
+    width = filters * mult[-1]
+    conv("vqgan.decoder.conv_in", width, E, 3, True)
+    for l in range(R):
+        block(f"vqgan.decoder.res_blocks.0.{l}.", width, width)
+    for i in range(len(mult) - 1, -1, -1):
+        j, out = len(mult) - i, filters * mult[i]
+        for l in range(R):
+            block(f"vqgan.decoder.res_blocks.{j}.{l}.", width, out)
+            width = out
+        if i > 0:
+            conv(f"vqgan.decoder.res_blocks.{j}.{R + 1}", width, width, 3, True)
+    gn("vqgan.decoder.norm_out", width)
+    conv("vqgan.decoder.conv_out", 3, width, 3, True)
+    return t
+
+
+def write_vqgan_model(path: str, n_tokens: int = 16, E: int = 32, codebook: int = 64, filters: int = 32,
+                      mult=(1, 2), R: int = 1, seed: int = 0) -> int:
+    """A GGUF holding only a VQGAN decoder and its metadata; returns the image side."""
+    rng = np.random.default_rng(seed)
+    t = vqgan_tensors(rng, E, codebook, filters, mult, R)
+    L = int(round(n_tokens ** 0.5))
+    side = L * 2 ** (len(mult) - 1)
+    meta = [("general.architecture", "str", "maskgit"), ("general.name", "str", "synthetic-vqgan"),
+            ("general.alignment", "u32", ALIGN), ("maskgit.n_tokens", "u32", n_tokens),
+            ("maskgit.resolution", "u32", side),
+            ("maskgit.vqgan.codebook_size", "u32", codebook), ("maskgit.vqgan.embedding_dim", "u32", E),
+            ("maskgit.vqgan.filters", "u32", filters), ("maskgit.vqgan.num_res_blocks", "u32", R),
+            ("maskgit.vqgan.group_norm_groups", "u32", 32),
+            ("maskgit.vqgan.channel_multipliers", "i32_array", list(mult))]
+    write_gguf(path, meta, [(n, a.shape, GGML_F32, a.tobytes()) for n, a in t.items()])
+    return side

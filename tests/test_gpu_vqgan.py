@@ -1,7 +1,8 @@
 """GPU parity of the VQGAN decoder's ops (k_vqgan.hip) through the C ABI.
 
-Bars:
-  * Conv2D: against a float64 im2col product of the same fp32 operands, max|y - ref| <= 1e-5 *
+Reference values come from the pinned numpy oracle (oracle/vqgan.py), and for whole decoder
+graphs also from the reference's own CPU executor (oracle/_ref/libmgref.so). Bars:
+  * Conv2D: against the float64 sum of the same fp32 products rounded once, max|y - ref| <= 1e-5 *
     max|ref| (only the fp32 summation order differs from the reference's k_conv_2d,
     src/mg-cpu/mg-cpu.cpp:165-190), over 3x3 / 1x1 / 5x5 kernels, stride 1 and 2, padding,
     output tiles that do not fill 64 pixels or 64 channels, and batches of images;
@@ -16,6 +17,10 @@ import numpy as np
 import pytest
 
 import edge_maskgit_amd as ema
+from edge_maskgit_amd import runtime as rt
+from oracle import ref
+from oracle import vqgan as ov
+from tests import mg_gguf
 
 pytestmark = pytest.mark.gpu
 
@@ -25,21 +30,6 @@ def ctx():
     c = ema.Context(0)
     yield c
     c.close()
-
-
-def conv_ref(x, ker, stride, pad):
-    """x [N][IC][IH][IW], ker [OC][IC][KH][KW] -> [N][OC][OH][OW] in float64"""
-    N, IC, IH, IW = x.shape
-    OC, _, KH, KW = ker.shape
-    OH, OW = (IH + 2 * pad - KH) // stride + 1, (IW + 2 * pad - KW) // stride + 1
-    xp = np.zeros((N, IC, IH + 2 * pad, IW + 2 * pad), np.float64)
-    xp[:, :, pad:pad + IH, pad:pad + IW] = x
-    cols = np.empty((N, OH, OW, IC, KH, KW), np.float64)
-    for kh in range(KH):
-        for kw in range(KW):
-            cols[:, :, :, :, kh, kw] = xp[:, :, kh:kh + stride * OH:stride, kw:kw + stride * OW:stride].transpose(0, 2, 3, 1)
-    y = cols.reshape(N * OH * OW, -1) @ ker.reshape(OC, -1).astype(np.float64).T
-    return y.reshape(N, OH, OW, OC).transpose(0, 3, 1, 2)
 
 
 CONV = [  # IW, IH, IC, N, KW, KH, OC, stride, pad
@@ -63,25 +53,11 @@ def test_conv2d_vs_float64(ctx, IW, IH, IC, N, KW, KH, OC, stride, pad):
     y2 = ctx.download(dY, (N, OC, OH, OW), np.float32)
     for b in (dX, dK, dY):
         ctx.free(b)
-    ref = conv_ref(x, ker, stride, pad)
-    err = np.abs(y - ref).max() / np.abs(ref).max()
+    want = ov.conv2d(x, ker, stride, pad)
+    err = np.abs(y - want).max() / np.abs(want).max()
     print(f"  rel err vs float64 {err:.2e}")
     assert err <= 1e-5
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
-
-
-def gn_ref(x, G, eps, gamma=None, beta=None):
-    """the CPU executor's GroupNorm (+ affine + SiLU) on x [N][C][H][W], numpy"""
-    N, C, H, W = x.shape
-    xg = x.reshape(N, G, -1).astype(np.float64)
-    mean = xg.mean(axis=2, keepdims=True)
-    var = ((xg - mean) ** 2).mean(axis=2, keepdims=True)
-    inv = np.float32(1.0) / np.sqrt(var.astype(np.float32) + np.float32(eps))
-    y = ((xg - mean).astype(np.float32) * inv).reshape(N, C, H, W)
-    if gamma is not None:
-        xn = y * gamma[None, :, None, None] + beta[None, :, None, None]
-        y = xn / (np.float32(1.0) + np.exp(-xn))
-    return y.astype(np.float32)
 
 
 GN = [(16, 16, 512, 1, 32), (9, 7, 64, 2, 32), (64, 64, 128, 1, 32), (256, 256, 128, 1, 32),
@@ -104,11 +80,11 @@ def test_group_norm(ctx, W, H, C, N, G, affine):
     for b in (dX, dY, dG, dB):
         if b is not None:
             ctx.free(b)
-    ref = gn_ref(x, G, 1e-5, gamma, beta)
+    want = ov.group_norm(x, G, 1e-5, gamma, beta)
     if affine:
-        assert np.abs(y - ref).max() <= 1e-6 * np.abs(ref).max()
+        assert np.abs(y - want).max() <= 1e-6 * np.abs(want).max()
     else:
-        ulp = np.abs(y.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+        ulp = np.abs(y.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
         same = float((ulp == 0).mean())
         print(f"  bit-exact {same:.4f}, max {int(ulp.max())} ulp")
         assert ulp.max() <= 2 and same >= 0.99
@@ -139,3 +115,63 @@ def test_vqgan_ops_reject_bad_args(ctx):
     with pytest.raises(ema.MghError):
         ctx.upscale(d, 4, 4, 1, 1, 0, d)
     ctx.free(d)
+
+
+# ---- whole decoder graphs through mgr_decode_images (mg::HipRuntime) ----
+SMALL = [dict(n_tokens=16, E=32, codebook=64, filters=32, mult=(1, 2), R=1),
+         dict(n_tokens=64, E=32, codebook=48, filters=32, mult=(1, 1, 2), R=2)]
+
+
+@pytest.mark.parametrize("cfg", SMALL, ids=["L4-two-levels", "L8-three-levels-R2"])
+def test_decode_graph_vs_reference(tmp_path, cfg):
+    """the decoder graph on the GPU against the oracle composition and, where it is built, the
+    reference decoder on its CPU executor: max|img - ref| <= 1e-4 * max|ref| (float32 sums in
+    another order through every conv); B grids in one graph equal B single decodes bit for bit"""
+    print(f"decode graph {cfg}", flush=True)
+    path = str(tmp_path / "vq.gguf")
+    side = mg_gguf.write_vqgan_model(path, seed=5, **cfg)
+    t = mg_gguf.vqgan_tensors(np.random.default_rng(5), cfg["E"], cfg["codebook"], cfg["filters"], cfg["mult"], cfg["R"])
+    rng = np.random.default_rng(6)
+    grids = rng.integers(0, cfg["codebook"], (3, cfg["n_tokens"])).astype(np.int32)
+    with rt.TransformerRuntime(path) as m:
+        imgs = m.decode_images(grids)
+        singles = [m.decode_images(g[None])[0] for g in grids]
+    assert imgs.shape == (3, 3, side, side)
+    for b in range(3):
+        assert np.array_equal(imgs[b], singles[b])
+        want = ov.decode(t, grids[b:b + 1], cfg["E"], cfg["filters"], cfg["mult"], cfg["R"])[0]
+        err = np.abs(imgs[b] - want).max() / np.abs(want).max()
+        print(f"  image {b}: rel err vs oracle {err:.2e}")
+        assert err <= 1e-4
+        if ref.available():
+            want = ref.vqgan_decode(path, grids[b], side)
+            assert np.abs(imgs[b] - want).max() <= 1e-4 * np.abs(want).max()
+
+
+def test_decode_graph_production_size(tmp_path):
+    """the production decoder (256 tokens, 128 filters, multipliers 1,1,2,2,4, two res blocks:
+    a 256 x 256 image) on random weights: finite, repeatable bit for bit, and two grids in one
+    graph equal their single decodes; its convolutions, GroupNorms and up-samplings at these
+    shapes are checked against the oracle by the op tests above"""
+    path = str(tmp_path / "vq.gguf")
+    side = mg_gguf.write_vqgan_model(path, seed=7, n_tokens=256, E=256, codebook=1024, filters=128,
+                                     mult=(1, 1, 2, 2, 4), R=2)
+    grids = np.random.default_rng(8).integers(0, 1024, (2, 256)).astype(np.int32)
+    with rt.TransformerRuntime(path) as m:
+        a = m.decode_images(grids)
+        b = m.decode_images(grids)
+        one = m.decode_images(grids[1:])
+    assert a.shape == (2, 3, side, side) and side == 256
+    assert np.isfinite(a).all() and np.abs(a).max() > 0
+    assert np.array_equal(a, b)
+    assert np.array_equal(a[1], one[0])
+
+
+def test_decode_rejects_bad_grids(tmp_path):
+    path = str(tmp_path / "vq.gguf")
+    mg_gguf.write_vqgan_model(path, seed=0, **SMALL[0])
+    with rt.TransformerRuntime(path) as m:
+        with pytest.raises(ValueError):
+            m.decode_images(np.zeros((1, 15), np.int32))
+        with pytest.raises(ema.MghError, match="codebook"):
+            m.decode_images(np.full((1, 16), 64, np.int32))
