@@ -39,7 +39,8 @@ MGH_SYMBOLS = [
     "mgh_decode_step", "mgh_packed_weight_bytes_f16", "mgh_pack_weights_f16", "mgh_f32_to_f16",
     "mgh_gemm_h16", "mgh_gemm_h16_f32in", "mgh_gemm_h16_y16", "mgh_flash_attn_f16kv_o16", "mgh_flash_attn_f16in",
     "mgh_softmax", "mgh_binary", "mgh_scale", "mgh_unary", "mgh_gemm_f32_batched",
-    "mgh_gemm_h16_f32in_noalloc", "mgh_conv2d", "mgh_group_norm", "mgh_upscale",
+    "mgh_gemm_h16_f32in_noalloc", "mgh_conv2d", "mgh_group_norm", "mgh_upscale", "mgh_conv2d_ex",
+    "mgh_conv2d_packed_bytes", "mgh_conv2d_pack_weights",
 ]
 
 _lib = None
@@ -118,6 +119,10 @@ def lib():
         L.mgh_unary.argtypes = [P, I, P, I64, P]
         L.mgh_gemm_f32_batched.argtypes = [P, P, P, P, P, P, P, P, I, P, P]
         L.mgh_conv2d.argtypes = [P, P, I, I, I, I, P, I, I, I, I, I, P]
+        L.mgh_conv2d_ex.argtypes = [P, P, I, I, I, I, P, P, I, I, I, I, I, P, P, P]
+        L.mgh_conv2d_packed_bytes.argtypes = [I, I, I, I]
+        L.mgh_conv2d_packed_bytes.restype = ctypes.c_size_t
+        L.mgh_conv2d_pack_weights.argtypes = [P, P, I, I, I, I, P]
         L.mgh_group_norm.argtypes = [P, P, I, I, I, I, I, ctypes.c_float, P, P, P]
         L.mgh_upscale.argtypes = [P, P, I, I, I, I, I, P]
         L.mgh_graph_begin.argtypes = [P]
@@ -387,6 +392,19 @@ class Context:
     def conv2d(self, x, IW, IH, IC, N, ker, KW, KH, OC, stride, pad, y):
         P = self._ptr
         self._check(lib().mgh_conv2d(self.h, P(x), IW, IH, IC, N, P(ker), KW, KH, OC, stride, pad, P(y)))
+
+    def conv2d_ex(self, x, IW, IH, IC, N, ker, packed, KW, KH, OC, stride, pad, bias, resid, y):
+        P = self._ptr
+        self._check(lib().mgh_conv2d_ex(self.h, P(x), IW, IH, IC, N, P(ker), P(packed), KW, KH, OC, stride, pad,
+                                        P(bias), P(resid), P(y)))
+
+    @staticmethod
+    def conv2d_packed_bytes(KW, KH, IC, OC) -> int:
+        return lib().mgh_conv2d_packed_bytes(KW, KH, IC, OC)
+
+    def conv2d_pack_weights(self, ker, KW, KH, IC, OC, packed):
+        P = self._ptr
+        self._check(lib().mgh_conv2d_pack_weights(self.h, P(ker), KW, KH, IC, OC, P(packed)))
 
     def group_norm(self, x, W, H, C, N, groups, eps, gamma, beta, y):
         P = self._ptr

@@ -28,6 +28,8 @@
 //    deviations from the mean (each workgroup adds the pass-1 partials in chunk order, so every
 //    chunk sees the same mean), and the apply pass derives mean and variance the same way.
 //    Partials are summed in a fixed order: results do not depend on scheduling.
+#include <algorithm>
+
 #include "mgh_common.h"
 #include "mgh_kernels.h"
 
@@ -36,6 +38,198 @@ namespace mgh {
 namespace {
 
 constexpr int CBM = 64, CBN = 64, CBK = 16, CPAD = 4;
+
+// out[row + pp + e] = ((v[e] + bias[oc]) + resid[row + pp + e]) for the e with pp + e < M,
+// each addition rounded on its own (the graph's conv node, then its Add nodes); one 16-byte
+// store when the four pixels are in range and rows are 16-byte aligned (M % 4 == 0)
+__device__ __forceinline__ void conv_store(float* __restrict__ out, const float* __restrict__ bias,
+                                           const float* __restrict__ resid, size_t row, int oc, int pp, int M,
+                                           f32x4 v) {
+#pragma clang fp contract(off)
+    if (bias) {
+        const float b = bias[oc];
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = v[e] + b;
+    }
+    if (pp + 3 < M && (M & 3) == 0) {
+        if (resid) v = v + *(const f32x4*)(resid + row + pp);
+        *(f32x4*)(out + row + pp) = v;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (pp + e < M) out[row + pp + e] = resid ? v[e] + resid[row + pp + e] : v[e];
+    }
+}
+
+// ---- packed-weight implicit GEMM (IC % 16 == 0): K in tap-major order k = (kh*KW + kw)*IC + ic,
+// so a 16-wide K slab is one tap and 16 consecutive input channels: the im2col gather needs one
+// bounds check per pixel and slab, and its loads step through channel planes.
+constexpr int PBM = 128, PBN = 128, PBK = 16, PST = PBK + 4;   // LDS rows padded to 20 floats
+
+// SPLIT: blockIdx.z = image * splits + split; the split's K range [split*kps, +kps) is summed
+// into its own partial plane part[split][image][oc][pixel] (no bias or residual), which
+// k_conv_reduce adds up in split order
+template <bool SPLIT>
+__global__ __launch_bounds__(256, 2) void k_conv2d_pk(ConvPkArgs a) {
+    __shared__ __attribute__((aligned(16))) float As[2][PBM][PST];   // [pixel][k]
+    __shared__ __attribute__((aligned(16))) float Bs[2][PBN][PST];   // [channel][k]
+    const int M = a.OW * a.OH, K = a.IC * a.KW * a.KH, OC = a.OC;
+    const int z = blockIdx.z;
+    const int n = SPLIT ? z / a.splits : z, sp = SPLIT ? z - n * a.splits : 0;
+    const int kbeg = sp * a.kps, kend = min(K, kbeg + a.kps);
+    const int m0 = blockIdx.x * PBM, n0 = blockIdx.y * PBN;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, l16 = lane & 15, lg = lane >> 4;
+
+    // gather roles: pixel pa with channels 8cg..8cg+7 of the slab; weight row bo, k half bh
+    const int pa = tid & (PBM - 1), cg = tid >> 7;
+    const int p = m0 + pa;
+    const bool pv = p < M;
+    const int ow = pv ? p % a.OW : 0, oh = pv ? p / a.OW : 0;
+    const int iw0 = ow * a.stride - a.pad, ih0 = oh * a.stride - a.pad;
+    const size_t plane = (size_t)a.IW * a.IH;
+    const float* inb = a.in + ((size_t)n * a.IC + 8 * cg) * plane;
+    const int bo = tid >> 1, bh = tid & 1;
+    const bool bv = n0 + bo < OC;
+    const float* wrow = a.wpk + (size_t)(bv ? n0 + bo : 0) * K + 8 * bh;
+
+    float ra[8];
+    f32x4 rb[2];
+    auto load = [&](int k0) {
+        const int tap = k0 / a.IC, ic0 = k0 - tap * a.IC;
+        const int kh = tap / a.KW, kw = tap - kh * a.KW;
+        const int ih = ih0 + kh, iw = iw0 + kw;
+        if (pv && ih >= 0 && ih < a.IH && iw >= 0 && iw < a.IW) {
+            const float* src = inb + (size_t)ic0 * plane + (size_t)ih * a.IW + iw;
+#pragma unroll
+            for (int j = 0; j < 8; j++) ra[j] = src[j * plane];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) ra[j] = 0.f;
+        }
+        if (bv) {
+            rb[0] = *(const f32x4*)(wrow + k0);
+            rb[1] = *(const f32x4*)(wrow + k0 + 4);
+        } else {
+            rb[0] = rb[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    auto store = [&](int buf) {
+        *(f32x4*)&As[buf][pa][8 * cg] = f32x4{ra[0], ra[1], ra[2], ra[3]};
+        *(f32x4*)&As[buf][pa][8 * cg + 4] = f32x4{ra[4], ra[5], ra[6], ra[7]};
+        *(f32x4*)&Bs[buf][bo][8 * bh] = rb[0];
+        *(f32x4*)&Bs[buf][bo][8 * bh + 4] = rb[1];
+    };
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int nk = (kend - kbeg) / PBK;
+    load(kbeg);
+    store(0);
+    __syncthreads();
+    for (int t = 0; t < nk; t++) {
+        const int cur = t & 1;
+        if (t + 1 < nk) load(kbeg + (t + 1) * PBK);
+        // lane (l16, lg) holds k = 4lg .. 4lg+3 of a row; MFMA step kk contracts k = 4lg + kk
+        f32x4 af[4], bf[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) af[i] = *(const f32x4*)&As[cur][64 * wm + 16 * i + l16][4 * lg];
+#pragma unroll
+        for (int j = 0; j < 4; j++) bf[j] = *(const f32x4*)&Bs[cur][64 * wn + 16 * j + l16][4 * lg];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][kk], bf[j][kk], acc[i][j], 0, 0, 0);
+        // the other buffer was last read before the previous barrier
+        if (t + 1 < nk) store(cur ^ 1);
+        __syncthreads();
+    }
+    // register e of tile (i, j): pixel m0 + 64wm + 16i + 4lg + e, channel n0 + 64wn + 16j + l16
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int oc = n0 + 64 * wn + 16 * j + l16;
+        if (oc >= OC) continue;
+        const size_t row = ((size_t)(SPLIT ? sp * a.N + n : n) * OC + oc) * M;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            conv_store(a.out, SPLIT ? nullptr : a.bias, SPLIT ? nullptr : a.resid, row, oc,
+                       m0 + 64 * wm + 16 * i + 4 * lg, M, acc[i][j]);
+    }
+}
+
+// out[i] = ((sum over splits in order of part[s][i]) + bias[oc]) + resid[i]
+__global__ __launch_bounds__(256) void k_conv_reduce(const float* __restrict__ part, int splits, int64_t total,
+                                                     int M, int OC, const float* __restrict__ bias,
+                                                     const float* __restrict__ resid, float* __restrict__ out) {
+#pragma clang fp contract(off)
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        float v = part[i];
+        for (int sp = 1; sp < splits; sp++) v = v + part[(size_t)sp * total + i];
+        if (bias) v = v + bias[(i / M) % OC];
+        if (resid) v = v + resid[i];
+        out[i] = v;
+    }
+}
+
+// wpk[oc][(kh*KW + kw)*IC + ic] = ker[oc][ic][kh][kw]
+__global__ __launch_bounds__(256) void k_conv_pack(const float* __restrict__ ker, float* __restrict__ wpk, int IC,
+                                                   int taps, int64_t total) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int64_t K = (int64_t)IC * taps;
+        const int64_t oc = i / K, r = i - oc * K;
+        const int64_t tap = r / IC, ic = r - tap * IC;
+        wpk[i] = ker[oc * K + ic * taps + tap];
+    }
+}
+
+// ---- few output channels (OC <= 8, the 3-channel conv_out): one thread per output pixel,
+// products and sums in the reference loop's order (ic, kh, kw; out-of-image taps skipped) with
+// separate multiply and add — the same float operations as the CPU executor's k_conv_2d
+template <int OCN>
+__global__ __launch_bounds__(256) void k_conv2d_few(ConvArgs a) {
+#pragma clang fp contract(off)
+    const int M = a.OW * a.OH;
+    const int64_t gi = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (gi >= (int64_t)M * a.N) return;
+    const int n = (int)(gi / M), p = (int)(gi - (int64_t)n * M);
+    const int ow = p % a.OW, oh = p / a.OW;
+    const int K = a.IC * a.KH * a.KW;
+    const size_t plane = (size_t)a.IW * a.IH;
+    float acc[OCN];
+#pragma unroll
+    for (int o = 0; o < OCN; o++) acc[o] = 0.f;
+    for (int ic = 0; ic < a.IC; ic++) {
+        const float* xin = a.in + ((size_t)n * a.IC + ic) * plane;
+        for (int kh = 0; kh < a.KH; kh++) {
+            const int ih = oh * a.stride - a.pad + kh;
+            if (ih < 0 || ih >= a.IH) continue;
+            for (int kw = 0; kw < a.KW; kw++) {
+                const int iw = ow * a.stride - a.pad + kw;
+                if (iw < 0 || iw >= a.IW) continue;
+                const float v = xin[(size_t)ih * a.IW + iw];
+                const int k = (ic * a.KH + kh) * a.KW + kw;
+#pragma unroll
+                for (int o = 0; o < OCN; o++)
+                    if (o < a.OC) acc[o] = acc[o] + a.ker[(size_t)o * K + k] * v;
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 0; o < OCN; o++) {
+        if (o >= a.OC) break;
+        const size_t idx = ((size_t)n * a.OC + o) * M + p;
+        float v = acc[o];
+        if (a.bias) v = v + a.bias[o];
+        if (a.resid) v = v + a.resid[idx];
+        a.out[idx] = v;
+    }
+}
 
 // KSZ > 0: KW = KH = KSZ known at compile time (the index arithmetic then divides by a
 // constant); 0: any kernel size
@@ -120,18 +314,10 @@ __global__ __launch_bounds__(256) void k_conv2d_f32(ConvArgs a) {
     for (int j = 0; j < 2; j++) {
         const int oc = n0 + 32 * wn + 16 * j + r16;
         if (oc >= OC) continue;
-        float* o = a.out + ((size_t)n * OC + oc) * M;
+        const size_t row = ((size_t)n * OC + oc) * M;
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int pp = m0 + 32 * wm + 16 * i + 4 * g;
-            if (pp + 3 < M && (M & 3) == 0) {
-                *(f32x4*)(o + pp) = acc[i][j];
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (pp + e < M) o[pp + e] = acc[i][j][e];
-            }
-        }
+        for (int i = 0; i < 2; i++)
+            conv_store(a.out, a.bias, a.resid, row, oc, m0 + 32 * wm + 16 * i + 4 * g, M, acc[i][j]);
     }
 }
 
@@ -224,10 +410,79 @@ __global__ __launch_bounds__(256) void k_upscale(const float* __restrict__ x, fl
 hipError_t launch_conv2d_f32(const ConvArgs& a, hipStream_t s) {
     const int M = a.OW * a.OH;
     if (M == 0 || a.OC == 0 || a.N == 0) return hipSuccess;
+    if (a.OC <= kConvFewMax) {
+        const int64_t total = (int64_t)M * a.N;
+        const dim3 grid((unsigned)((total + 255) / 256));
+        if (a.OC <= 4) hipLaunchKernelGGL(k_conv2d_few<4>, grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL(k_conv2d_few<8>, grid, dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
     const dim3 grid((unsigned)((M + CBM - 1) / CBM), (unsigned)((a.OC + CBN - 1) / CBN), (unsigned)a.N), block(256);
     if (a.KW == 3 && a.KH == 3) hipLaunchKernelGGL(k_conv2d_f32<3>, grid, block, 0, s, a);
     else if (a.KW == 1 && a.KH == 1) hipLaunchKernelGGL(k_conv2d_f32<1>, grid, block, 0, s, a);
     else hipLaunchKernelGGL(k_conv2d_f32<0>, grid, block, 0, s, a);
+    return hipGetLastError();
+}
+
+ConvPkPlan conv_pk_plan(int M, int OC, int K) {
+    // about two workgroups per CU for one image: split K when its output tiles alone give
+    // fewer than 384 workgroups, keeping at least two 16-wide slabs per split. The plan does
+    // not depend on the batch, so an image's sums are the same whatever it is batched with.
+    ConvPkPlan p{1, K};
+    const int64_t tiles = (int64_t)((M + PBM - 1) / PBM) * ((OC + PBN - 1) / PBN);
+    const int slabs = K / PBK;
+    if (tiles >= 384 || slabs < 4) return p;
+    int want = (int)std::min<int64_t>((512 + tiles - 1) / tiles, slabs / 2);
+    const int per = (slabs + want - 1) / want;
+    p.kps = per * PBK;
+    p.splits = (slabs + per - 1) / per;
+    return p;
+}
+
+// images per split launch: grid z = images x splits stays within 65535
+static int conv_pk_group(int N, int splits) { return std::min(N, 65535 / splits); }
+
+size_t conv_pk_ws_bytes(int M, int OC, int N, int K) {
+    const ConvPkPlan p = conv_pk_plan(M, OC, K);
+    return p.splits > 1 ? (size_t)p.splits * conv_pk_group(N, p.splits) * OC * (size_t)M * sizeof(float) : 0;
+}
+
+hipError_t launch_conv_pack(const float* ker, float* wpk, int IC, int taps, int OC, hipStream_t s) {
+    const int64_t total = (int64_t)OC * IC * taps;
+    if (total == 0) return hipSuccess;
+    const int64_t g = std::min<int64_t>((total + 255) / 256, 8192);
+    hipLaunchKernelGGL(k_conv_pack, dim3((unsigned)g), dim3(256), 0, s, ker, wpk, IC, taps, total);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv2d_pk(const ConvPkArgs& a0, float* ws, hipStream_t s) {
+    const int M = a0.OW * a0.OH, K = a0.IC * a0.KW * a0.KH;
+    if (M == 0 || a0.OC == 0 || a0.N == 0) return hipSuccess;
+    const ConvPkPlan p = conv_pk_plan(M, a0.OC, K);
+    ConvPkArgs a = a0;
+    a.splits = p.splits;
+    a.kps = p.kps;
+    const dim3 block(256);
+    if (p.splits == 1) {
+        const dim3 grid((unsigned)((M + PBM - 1) / PBM), (unsigned)((a.OC + PBN - 1) / PBN), (unsigned)a.N);
+        hipLaunchKernelGGL(k_conv2d_pk<false>, grid, block, 0, s, a);
+        return hipGetLastError();
+    }
+    // groups of images: partials part[split][image of the group][oc][pixel] in ws, then reduced
+    const int G = conv_pk_group(a0.N, p.splits);
+    const size_t in_img = (size_t)a0.IC * a0.IW * a0.IH, out_img = (size_t)a0.OC * M;
+    for (int n0 = 0; n0 < a0.N; n0 += G) {
+        const int g = std::min(G, a0.N - n0);
+        a.in = a0.in + n0 * in_img;
+        a.out = ws;
+        a.N = g;
+        const dim3 grid((unsigned)((M + PBM - 1) / PBM), (unsigned)((a.OC + PBN - 1) / PBN), (unsigned)(g * p.splits));
+        hipLaunchKernelGGL(k_conv2d_pk<true>, grid, block, 0, s, a);
+        const int64_t total = (int64_t)g * out_img;
+        const int64_t nb = std::min<int64_t>((total + 255) / 256, 8192);
+        hipLaunchKernelGGL(k_conv_reduce, dim3((unsigned)nb), block, 0, s, ws, p.splits, total, M, a.OC, a0.bias,
+                           a0.resid ? a0.resid + n0 * out_img : nullptr, a0.out + n0 * out_img);
+    }
     return hipGetLastError();
 }
 

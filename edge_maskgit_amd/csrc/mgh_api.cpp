@@ -690,24 +690,77 @@ int mgh_unary(mgh_ctx* c, int act, const float* x, int64_t n, float* y) {
     return MGH_OK;
 }
 
-int mgh_conv2d(mgh_ctx* c, const float* in, int IW, int IH, int IC, int N, const float* ker, int KW, int KH,
-               int OC, int stride, int pad, float* out) {
-    if (!c) return MGH_ERR_ARG;
+namespace {
+
+int conv_shape(mgh_ctx* c, int IW, int IH, int IC, int N, int KW, int KH, int OC, int stride, int pad, int64_t* OW,
+               int64_t* OH) {
     if (IW <= 0 || IH <= 0 || IC <= 0 || N < 0 || KW <= 0 || KH <= 0 || OC <= 0 || stride <= 0 || pad < 0)
         return fail(c, MGH_ERR_ARG, "conv2d: need positive sizes, stride >= 1, pad >= 0");
-    const int64_t OW = ((int64_t)IW + 2 * pad - KW) / stride + 1, OH = ((int64_t)IH + 2 * pad - KH) / stride + 1;
-    if (IW + 2 * (int64_t)pad < KW || IH + 2 * (int64_t)pad < KH || OW <= 0 || OH <= 0)
+    if (IW + 2 * (int64_t)pad < KW || IH + 2 * (int64_t)pad < KH)
         return fail(c, MGH_ERR_ARG, "conv2d: kernel larger than the padded input");
-    // grid: x = ceil(OW*OH / 64) workgroups of 256 threads (at most 2^32 work-items), z = N
-    if ((int64_t)IW * IH > INT32_MAX || OW * OH > ((int64_t)1 << 30) || (int64_t)IC * KW * KH > INT32_MAX ||
-        (int64_t)N > 65535)
+    *OW = ((int64_t)IW + 2 * pad - KW) / stride + 1;
+    *OH = ((int64_t)IH + 2 * pad - KH) / stride + 1;
+    // grids: pixel tiles of 64 or 128 (or one thread per pixel) in x, N (x splits < 1024) in z
+    if ((int64_t)IW * IH > INT32_MAX || *OW * *OH > ((int64_t)1 << 30) || (int64_t)IC * KW * KH > INT32_MAX ||
+        (int64_t)N > 65535 || *OW * *OH * N > ((int64_t)1 << 31))
         return fail(c, MGH_ERR_UNSUPPORTED, "conv2d: shape too large");
+    return MGH_OK;
+}
+
+bool conv_packed_path(int IC, int OC) { return IC % 16 == 0 && OC > mgh::kConvFewMax; }
+
+}  // namespace
+
+int mgh_conv2d_ex(mgh_ctx* c, const float* in, int IW, int IH, int IC, int N, const float* ker, const float* wpk,
+                  int KW, int KH, int OC, int stride, int pad, const float* bias, const float* resid, float* out) {
+    if (!c) return MGH_ERR_ARG;
+    int64_t OW = 0, OH = 0;
+    if (int r = conv_shape(c, IW, IH, IC, N, KW, KH, OC, stride, pad, &OW, &OH)) return r;
     if (N == 0) return MGH_OK;
-    if (!in || !ker || !out) return fail(c, MGH_ERR_ARG, "conv2d: null pointer");
-    if (!aligned16(out)) return fail(c, MGH_ERR_ARG, "conv2d: d_out must be 16-byte aligned");
+    if (!in || !out || (!ker && !wpk)) return fail(c, MGH_ERR_ARG, "conv2d: null pointer");
+    if (!aligned16(out) || (resid && !aligned16(resid)) || (wpk && !aligned16(wpk)))
+        return fail(c, MGH_ERR_ARG, "conv2d: d_out, d_resid and d_packed must be 16-byte aligned");
+    const bool packed = conv_packed_path(IC, OC);
+    if (!ker && !packed)
+        return fail(c, MGH_ERR_ARG, "conv2d: this shape runs on the reference-layout kernel: pass d_ker");
     if (int r = set_dev(c)) return r;
-    mgh::ConvArgs a{in, ker, out, IW, IH, IC, (int)OW, (int)OH, OC, KW, KH, stride, pad, N};
-    MGH_HIP(c, mgh::launch_conv2d_f32(a, c->stream), "k_conv2d_f32");
+    const int M = (int)(OW * OH), K = IC * KW * KH;
+    if (!packed) {
+        mgh::ConvArgs a{in, ker, out, IW, IH, IC, (int)OW, (int)OH, OC, KW, KH, stride, pad, N, bias, resid};
+        MGH_HIP(c, mgh::launch_conv2d_f32(a, c->stream), "k_conv2d_f32");
+        return MGH_OK;
+    }
+    if (!wpk) {                          // tap-major copy of the weights in the context scratch
+        if (int r = ensure_scratch(c, (size_t)OC * K * sizeof(float))) return r;
+        MGH_HIP(c, mgh::launch_conv_pack(ker, (float*)c->scratch, IC, KW * KH, OC, c->stream), "k_conv_pack");
+        wpk = (const float*)c->scratch;
+    }
+    if (int r = ensure_qp_ws(c, mgh::conv_pk_ws_bytes(M, OC, N, K))) return r;
+    mgh::ConvPkArgs a{in, wpk, out, bias, resid, IW, IH, IC, (int)OW, (int)OH, OC, KW, KH, stride, pad, N, 1, K};
+    MGH_HIP(c, mgh::launch_conv2d_pk(a, (float*)c->qp_ws, c->stream), "k_conv2d_pk");
+    return MGH_OK;
+}
+
+int mgh_conv2d(mgh_ctx* c, const float* in, int IW, int IH, int IC, int N, const float* ker, int KW, int KH,
+               int OC, int stride, int pad, float* out) {
+    if (c && !ker && N > 0) return fail(c, MGH_ERR_ARG, "conv2d: null pointer");
+    return mgh_conv2d_ex(c, in, IW, IH, IC, N, ker, nullptr, KW, KH, OC, stride, pad, nullptr, nullptr, out);
+}
+
+size_t mgh_conv2d_packed_bytes(int KW, int KH, int IC, int OC) {
+    if (KW <= 0 || KH <= 0 || IC <= 0 || OC <= 0 || !conv_packed_path(IC, OC)) return 0;
+    return (size_t)KW * KH * IC * OC * sizeof(float);
+}
+
+int mgh_conv2d_pack_weights(mgh_ctx* c, const float* ker, int KW, int KH, int IC, int OC, float* wpk) {
+    if (!c) return MGH_ERR_ARG;
+    if (KW <= 0 || KH <= 0 || IC <= 0 || OC <= 0 || (int64_t)IC * KW * KH > INT32_MAX)
+        return fail(c, MGH_ERR_ARG, "conv2d_pack_weights: need positive sizes");
+    if (!conv_packed_path(IC, OC))
+        return fail(c, MGH_ERR_UNSUPPORTED, "conv2d_pack_weights: the packed kernel needs IC % 16 == 0 and OC > 8");
+    if (!ker || !wpk) return fail(c, MGH_ERR_ARG, "conv2d_pack_weights: null pointer");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_conv_pack(ker, wpk, IC, KW * KH, OC, c->stream), "k_conv_pack");
     return MGH_OK;
 }
 

@@ -187,8 +187,31 @@ struct ConvArgs {
     const float* ker;      // {KW, KH, IC, OC}
     float* out;            // {OW, OH, OC, N}
     int IW, IH, IC, OW, OH, OC, KW, KH, stride, pad, N;
+    const float* bias;     // [OC] or null: out = conv + bias
+    const float* resid;    // shape of out or null: then + resid
 };
+constexpr int kConvFewMax = 8;      // OC up to this: the one-thread-per-pixel kernel
+// the reference-layout kernels: one thread per pixel for OC <= kConvFewMax, else the
+// 64 x 64 fp32-MFMA implicit GEMM (any IC)
 hipError_t launch_conv2d_f32(const ConvArgs& a, hipStream_t s);
+
+// packed-weight fp32-MFMA implicit GEMM for IC % 16 == 0 (wpk from launch_conv_pack)
+struct ConvPkArgs {
+    const float* in;
+    const float* wpk;      // [OC][KH][KW][IC]
+    float* out;
+    const float* bias;
+    const float* resid;
+    int IW, IH, IC, OW, OH, OC, KW, KH, stride, pad, N;
+    int splits, kps;       // set by the launcher
+};
+struct ConvPkPlan {
+    int splits, kps;       // K split into `splits` ranges of kps values (a multiple of 16)
+};
+ConvPkPlan conv_pk_plan(int M, int OC, int K);   // per image: independent of the batch
+size_t conv_pk_ws_bytes(int M, int OC, int N, int K);    // split-K partials, 0 without a split
+hipError_t launch_conv_pack(const float* ker, float* wpk, int IC, int taps, int OC, hipStream_t s);
+hipError_t launch_conv2d_pk(const ConvPkArgs& a, float* ws, hipStream_t s);
 size_t group_norm_ws_bytes(int64_t W, int64_t H, int C, int N, int G);
 hipError_t launch_group_norm(const float* x, int64_t W, int64_t H, int C, int N, int G, float eps,
                              const float* gamma, const float* beta, float* y, void* ws, hipStream_t s);

@@ -118,7 +118,8 @@ struct HipRuntime::Impl {
     std::unordered_map<void*, size_t> alloc_size;
 
     // layout 0: the leaf's bytes as stored; 1: quantized weight in the int8-dot packed layout
-    // (mgh_pack_weights); 2: quantized weight dequantized into fp16 (mgh_pack_weights_f16)
+    // (mgh_pack_weights); 2: quantized weight dequantized into fp16 (mgh_pack_weights_f16);
+    // 3: F32 conv kernel {KW, KH, IC, OC} in the tap-major layout (mgh_conv2d_pack_weights)
     void* upload_leaf(const Tensor* t, int layout) {
         const size_t n = t->nbytes();
         const auto key = std::make_tuple((const void*)t->data, n, layout ? 100 * layout + (int)t->type : -1);
@@ -129,7 +130,12 @@ struct HipRuntime::Impl {
         check(mgh_alloc(ctx, n, &raw));
         check(mgh_h2d(ctx, raw, t->data, n));
         void* d = raw;
-        if (layout) {
+        if (layout == 3) {
+            const int KW = (int)t->ne[0], KH = (int)t->ne[1], IC = (int)t->ne[2], OC = (int)t->ne[3];
+            check(mgh_alloc(ctx, mgh_conv2d_packed_bytes(KW, KH, IC, OC), &d));
+            check(mgh_conv2d_pack_weights(ctx, (const float*)raw, KW, KH, IC, OC, (float*)d));
+            check(mgh_free(ctx, raw));
+        } else if (layout) {
             const int wt = t->type == Type::Q8_0 ? MGH_WTYPE_Q8_0 : MGH_WTYPE_Q4_K;
             const int K = (int)t->ne[0], N = (int)(t->nelements() / t->ne[0]);
             const size_t pb = layout == 2 ? mgh_packed_weight_bytes_f16(N, K) : mgh_packed_weight_bytes(wt, N, K);
@@ -485,6 +491,68 @@ const void* HipRuntime::run(Graph& g, bool readback) {
         }
     }
 
+    // Conv2D epilogue fusion (the VQGAN decoder, mg-vqgan.cpp:31-55): the Add of a per-channel
+    // bias viewed as {1, 1, C, 1} that is a conv's only consumer, and then an Add of a same-shaped
+    // tensor computed before the conv (the res block's h + x, or h + conv_res(h)), are evaluated
+    // in the conv's epilogue with the same roundings (out = (conv + bias) + resid); the absorbed
+    // Add nodes launch nothing and share the conv's buffer
+    struct ConvFuse {
+        const Tensor* bias = nullptr;
+        const Tensor* resid = nullptr;
+        const Tensor* out = nullptr;         // the last node it writes
+    };
+    std::unordered_map<const Tensor*, ConvFuse> cfuse;           // conv -> its fused Adds
+    std::unordered_map<const Tensor*, const Tensor*> absorbed;   // absorbed Add -> its conv
+    {
+        std::unordered_map<const Tensor*, int> uses, at;
+        for (int i = 0; i < n; i++) {
+            at[g.nodes[i]] = i;
+            for (const Tensor* s : g.nodes[i]->src)
+                if (s) uses[s]++;
+        }
+        auto f32c = [](const Tensor* x) { return x->type == Type::F32 && x->is_contiguous(); };
+        for (int i = 0; i < n; i++) {
+            const Tensor* t = g.nodes[i];
+            if (t->op == Op::Conv2D) cfuse[t].out = t;
+            if (t->op != Op::Add) continue;
+            const Tensor* a = t->src[0];
+            const Tensor* b = t->src[1];
+            // conv (+ bias already absorbed) whose only consumer is this Add, with no residual yet
+            auto open_conv = [&](const Tensor* x) -> const Tensor* {
+                if (uses[x] != 1 || !f32c(x)) return nullptr;
+                const Tensor* cv = x->op == Op::Conv2D ? x : (absorbed.count(x) ? absorbed.at(x) : nullptr);
+                if (!cv || cfuse.at(cv).out != x || cfuse.at(cv).resid) return nullptr;
+                return cv;
+            };
+            const Tensor* cv = open_conv(a);
+            const Tensor* rb = I.root(b);
+            if (cv && !cfuse.at(cv).bias && cfuse.at(cv).out == cv && rb->op == Op::None && f32c(rb) &&
+                b->ne[0] == 1 && b->ne[1] == 1 && b->ne[2] == a->ne[2] && b->ne[3] == 1 &&
+                rb->nelements() == a->ne[2] && b->is_contiguous()) {
+                cfuse[cv].bias = rb;
+                cfuse[cv].out = t;
+                absorbed[t] = cv;
+                continue;
+            }
+            if (!std::equal(a->ne, a->ne + 4, b->ne) || !f32c(a) || !f32c(b) || !f32c(t)) continue;
+            for (const Tensor* x : {b, a}) {                         // prefer the later operand
+                const Tensor* c2 = open_conv(x);
+                const Tensor* r = I.root(x == a ? b : a);
+                if (!c2 || (r->op != Op::None && (!at.count(r) || at.at(r) >= at.at(c2)))) continue;
+                cfuse[c2].resid = x == a ? b : a;
+                cfuse[c2].out = t;
+                absorbed[t] = c2;
+                break;
+            }
+        }
+        for (auto& kv : cfuse)                                        // the chain shares one buffer
+            if (kv.second.out != kv.first) {
+                I.owner[kv.first] = kv.second.out;
+                for (auto& ab : absorbed)
+                    if (ab.second == kv.first && ab.first != kv.second.out) I.owner[ab.first] = kv.second.out;
+            }
+    }
+
     // MG_DUMP_NAMED: named computed nodes are read back to their host data (mg-opencl.cpp
     // :1627-1641), each right after its kernel, while its buffer is still its own
     const bool dump_named = std::getenv("MG_DUMP_NAMED") != nullptr;
@@ -496,6 +564,10 @@ const void* HipRuntime::run(Graph& g, bool readback) {
         if (t->type != Type::F32 && t->op != Op::GetRows)
             throw std::runtime_error("HipRuntime: only F32 results are supported");
         if (grp_of.count(t) && I.addr.count(t)) {                 // computed with its group
+            release_after(i, t);
+            continue;
+        }
+        if (absorbed.count(t)) {                                   // evaluated by its conv
             release_after(i, t);
             continue;
         }
@@ -544,6 +616,12 @@ const void* HipRuntime::run(Graph& g, bool readback) {
         } else if (t->op == Op::MulMat && emit16.count(t) && I.codes.count(I.root(t->src[1]))) {
             out = nullptr;                                      // stored as fp16 only (below)
             I.addr[t] = out;
+        } else if (t->op == Op::Conv2D && cfuse.at(t).out != t) {
+            out = I.take(cfuse.at(t).out->nbytes());             // written once, by the conv
+            I.addr[t] = out;
+            I.addr[cfuse.at(t).out] = out;
+            for (auto& ab : absorbed)
+                if (ab.second == t) I.addr[ab.first] = out;
         } else {
             out = I.take(t->nbytes());
             I.addr[t] = out;
@@ -768,9 +846,14 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                 const int64_t dims[] = {x->ne[0], x->ne[1], x->ne[2], x->ne[3], k->ne[0], k->ne[1], k->ne[3]};
                 for (int64_t d : dims)
                     if (d > INT32_MAX) throw std::runtime_error("HipRuntime: Conv2D dimension too large");
-                I.check(mgh_conv2d(I.ctx, (const float*)I.dev(x), (int)x->ne[0], (int)x->ne[1], (int)x->ne[2],
-                                   (int)x->ne[3], (const float*)I.dev(k), (int)k->ne[0], (int)k->ne[1],
-                                   (int)k->ne[3], t->iparam[0], t->iparam[1], (float*)out));
+                const int KW = (int)k->ne[0], KH = (int)k->ne[1], IC = (int)k->ne[2], OC = (int)k->ne[3];
+                // tap-major weights packed once per leaf where the packed kernel runs
+                const bool pk = k->op == Op::None && mgh_conv2d_packed_bytes(KW, KH, IC, OC) > 0;
+                const ConvFuse& f = cfuse.at(t);
+                I.check(mgh_conv2d_ex(I.ctx, (const float*)I.dev(x), (int)x->ne[0], (int)x->ne[1], IC, (int)x->ne[3],
+                                      pk ? nullptr : (const float*)I.dev(k), pk ? (const float*)I.upload_leaf(k, 3) : nullptr,
+                                      KW, KH, OC, t->iparam[0], t->iparam[1], (const float*)I.dev(f.bias),
+                                      (const float*)I.dev(f.resid), (float*)out));
                 break;
             }
             case Op::GroupNorm: {

@@ -223,6 +223,16 @@ int mgh_gemm_f32_batched(mgh_ctx* ctx, const float* d_w, const int64_t w_ne[4], 
  *      mgh_conv2d: the Conv2D node (CPU mg-cpu.cpp:165-190; GPU k_conv2d_t,
  *      mg-opencl.cpp:985-1025, 1535-1566): ker {KW, KH, IC, OC}, out {OW, OH, OC, N} with
  *      OW = (IW + 2 pad - KW) / stride + 1; fp32 products and accumulation; d_out 16-byte aligned.
+ *      Kernels: OC <= 8 one thread per pixel in the reference loop's order (the CPU executor's
+ *      float operations exactly); IC % 16 == 0 an fp32-MFMA implicit GEMM over tap-major packed
+ *      weights (packed into the context scratch per call, or once by mgh_conv2d_pack_weights),
+ *      with K split across workgroups when the output alone gives too few; otherwise a 64 x 64
+ *      fp32-MFMA implicit GEMM over the reference layout.
+ *      mgh_conv2d_ex: the conv node with the decoder's following Add nodes fused:
+ *      out = (conv + bias[oc]) + resid, each addition rounded as its own node would (bias [OC]
+ *      or null; resid shaped as out, 16-byte aligned, or null); d_packed (optional, from
+ *      mgh_conv2d_pack_weights, mgh_conv2d_packed_bytes large) saves the per-call packing,
+ *      and for the packed path d_ker may then be null.
  *      mgh_group_norm: the GroupNorm node (mg-cpu.cpp:123-147, 262-276; mg-opencl.cpp:1027-1095,
  *      1568-1590): statistics per (n, group) in double, y = (x - mean) / sqrt(var + eps); with
  *      d_gamma and d_beta [C] also the fused per-channel affine and SiLU (both null: plain).
@@ -230,6 +240,12 @@ int mgh_gemm_f32_batched(mgh_ctx* ctx, const float* d_w, const int64_t w_ne[4], 
  *      (mg-cpu.cpp:192-198, mg-opencl.cpp:1096-1103, 1591-1599). ---- */
 int mgh_conv2d(mgh_ctx* ctx, const float* d_in, int IW, int IH, int IC, int N, const float* d_ker,
                int KW, int KH, int OC, int stride, int pad, float* d_out);
+int mgh_conv2d_ex(mgh_ctx* ctx, const float* d_in, int IW, int IH, int IC, int N, const float* d_ker,
+                  const float* d_packed, int KW, int KH, int OC, int stride, int pad, const float* d_bias,
+                  const float* d_resid, float* d_out);
+/* bytes of the packed copy (0: the shape does not take the packed kernel) */
+size_t mgh_conv2d_packed_bytes(int KW, int KH, int IC, int OC);
+int mgh_conv2d_pack_weights(mgh_ctx* ctx, const float* d_ker, int KW, int KH, int IC, int OC, float* d_packed);
 int mgh_group_norm(mgh_ctx* ctx, const float* d_x, int W, int H, int C, int N, int groups, float eps,
                    const float* d_gamma, const float* d_beta, float* d_y);
 int mgh_upscale(mgh_ctx* ctx, const float* d_x, int W, int H, int C, int N, int factor, float* d_y);

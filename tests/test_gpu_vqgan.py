@@ -32,10 +32,19 @@ def ctx():
     c.close()
 
 
+# kernels: OC <= 8 one thread per pixel ("few"); IC % 16 == 0 packed tap-major MFMA ("pk",
+# split over K when the output gives too few workgroups); else the reference-layout MFMA ("gen")
 CONV = [  # IW, IH, IC, N, KW, KH, OC, stride, pad
-    (9, 7, 5, 2, 3, 3, 7, 1, 1), (10, 10, 3, 1, 3, 3, 8, 2, 1), (8, 8, 33, 2, 1, 1, 65, 1, 0),
-    (5, 5, 2, 1, 5, 5, 3, 1, 2), (65, 33, 20, 1, 3, 3, 130, 1, 1), (16, 16, 256, 1, 3, 3, 512, 1, 1),
-    (32, 32, 128, 2, 3, 3, 64, 1, 1), (64, 64, 64, 1, 1, 1, 32, 1, 0), (7, 7, 4, 1, 3, 3, 3, 1, 0),
+    (9, 7, 5, 2, 3, 3, 7, 1, 1), (10, 10, 3, 1, 3, 3, 8, 2, 1), (5, 5, 2, 1, 5, 5, 3, 1, 2),
+    (7, 7, 4, 1, 3, 3, 3, 1, 0), (32, 32, 128, 1, 3, 3, 3, 1, 1),                     # few
+    (8, 8, 33, 2, 1, 1, 65, 1, 0), (65, 33, 20, 1, 3, 3, 130, 1, 1),                  # gen
+    (16, 16, 256, 1, 3, 3, 512, 1, 1), (16, 16, 512, 2, 3, 3, 512, 1, 1),             # pk, split
+    (32, 32, 128, 2, 3, 3, 64, 1, 1), (64, 64, 64, 1, 1, 1, 32, 1, 0),                # pk
+    (9, 7, 32, 1, 3, 3, 130, 2, 1), (13, 11, 48, 3, 3, 3, 200, 1, 1),                 # pk, tails
+    (128, 128, 128, 1, 3, 3, 128, 1, 1), (32, 32, 256, 1, 1, 1, 256, 1, 0),           # pk
+    (11, 6, 16, 1, 5, 5, 24, 1, 2),                                                   # pk, 5x5
+    (256, 192, 16, 1, 3, 3, 16, 1, 1),                                                # pk, no split
+    (4, 4, 512, 460, 3, 3, 16, 1, 1),             # pk, 144 splits: images launched in two groups
 ]
 
 
@@ -58,6 +67,63 @@ def test_conv2d_vs_float64(ctx, IW, IH, IC, N, KW, KH, OC, stride, pad):
     print(f"  rel err vs float64 {err:.2e}")
     assert err <= 1e-5
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+    if OC <= 8 and ref.available():
+        # the few-channel kernel performs the CPU executor's float operations in its order
+        assert np.array_equal(y, ref.conv2d(x, ker, stride, pad))
+
+
+@pytest.mark.parametrize("IW,IH,IC,KW,KH,OC", [(16, 16, 512, 3, 3, 512), (128, 128, 128, 3, 3, 128),
+                                                (32, 32, 128, 3, 3, 3), (65, 33, 20, 3, 3, 130)])
+def test_conv2d_batch_invariant(ctx, IW, IH, IC, KW, KH, OC):
+    """an image's output does not depend on the batch it is in (the split plan is per image)"""
+    print(f"conv2d batch IW={IW} IH={IH} IC={IC} OC={OC}", flush=True)
+    rng = np.random.default_rng(IC + OC)
+    x = rng.standard_normal((3, IC, IH, IW)).astype(np.float32)
+    ker = (rng.standard_normal((OC, IC, KH, KW)) / np.sqrt(IC * KH * KW)).astype(np.float32)
+    dX, dK, dY = ctx.upload(x), ctx.upload(ker), ctx.alloc(3 * OC * IH * IW * 4)
+    ctx.conv2d(dX, IW, IH, IC, 3, dK, KW, KH, OC, 1, 1, dY)
+    y3 = ctx.download(dY, (3, OC, IH, IW), np.float32)
+    for b in range(3):
+        d1 = ctx.upload(np.ascontiguousarray(x[b:b + 1]))
+        ctx.conv2d(d1, IW, IH, IC, 1, dK, KW, KH, OC, 1, 1, dY)
+        assert np.array_equal(ctx.download(dY, (1, OC, IH, IW), np.float32)[0], y3[b])
+        ctx.free(d1)
+    for d in (dX, dK, dY):
+        ctx.free(d)
+
+
+@pytest.mark.parametrize("IW,IH,IC,N,KW,KH,OC,stride,pad", [
+    (16, 16, 256, 1, 3, 3, 512, 1, 1), (32, 32, 128, 2, 3, 3, 64, 1, 1), (9, 7, 32, 1, 3, 3, 130, 2, 1),
+    (32, 32, 128, 1, 3, 3, 3, 1, 1), (65, 33, 20, 1, 3, 3, 130, 1, 1), (64, 64, 128, 1, 1, 1, 128, 1, 0),
+    (256, 192, 16, 1, 3, 3, 16, 1, 1)])
+def test_conv2d_ex_bias_residual_packed(ctx, IW, IH, IC, N, KW, KH, OC, stride, pad):
+    """the fused Add nodes: out = (conv + bias) + resid, each rounded as its own node, equal bit for
+    bit to the plain conv followed by the two additions in float32; the packed weights from
+    mgh_conv2d_pack_weights give the same bits as the per-call packing"""
+    print(f"conv2d_ex IW={IW} IH={IH} IC={IC} N={N} K={KW}x{KH} OC={OC} s={stride} p={pad}", flush=True)
+    rng = np.random.default_rng(IW + IC + OC)
+    x = rng.standard_normal((N, IC, IH, IW)).astype(np.float32)
+    ker = (rng.standard_normal((OC, IC, KH, KW)) / np.sqrt(IC * KH * KW)).astype(np.float32)
+    bias = rng.standard_normal(OC).astype(np.float32)
+    OH, OW = (IH + 2 * pad - KH) // stride + 1, (IW + 2 * pad - KW) // stride + 1
+    res = rng.standard_normal((N, OC, OH, OW)).astype(np.float32)
+    dX, dK, dB, dR = ctx.upload(x), ctx.upload(ker), ctx.upload(bias), ctx.upload(res)
+    dY = ctx.alloc(res.nbytes)
+    ctx.conv2d(dX, IW, IH, IC, N, dK, KW, KH, OC, stride, pad, dY)
+    plain = ctx.download(dY, res.shape, np.float32)
+    ctx.conv2d_ex(dX, IW, IH, IC, N, dK, None, KW, KH, OC, stride, pad, dB, dR, dY)
+    fused = ctx.download(dY, res.shape, np.float32)
+    assert np.array_equal(fused, (plain + bias[None, :, None, None]) + res)
+    nbytes = ctx.conv2d_packed_bytes(KW, KH, IC, OC)
+    assert (nbytes > 0) == (IC % 16 == 0 and OC > 8)
+    if nbytes:
+        dP = ctx.alloc(nbytes)
+        ctx.conv2d_pack_weights(dK, KW, KH, IC, OC, dP)
+        ctx.conv2d_ex(dX, IW, IH, IC, N, None, dP, KW, KH, OC, stride, pad, dB, dR, dY)
+        assert np.array_equal(ctx.download(dY, res.shape, np.float32), fused)
+        ctx.free(dP)
+    for b in (dX, dK, dB, dR, dY):
+        ctx.free(b)
 
 
 GN = [(16, 16, 512, 1, 32), (9, 7, 64, 2, 32), (64, 64, 128, 1, 32), (256, 256, 128, 1, 32),
@@ -114,6 +180,10 @@ def test_vqgan_ops_reject_bad_args(ctx):
         ctx.group_norm(d, 4, 4, 8, 1, 4, 1e-5, d, None, d)      # gamma without beta
     with pytest.raises(ema.MghError):
         ctx.upscale(d, 4, 4, 1, 1, 0, d)
+    with pytest.raises(ema.MghError):      # the generic kernel needs the reference-layout weights
+        ctx.conv2d_ex(d, 4, 4, 3, 1, None, d, 3, 3, 16, 1, 1, None, None, d)
+    with pytest.raises(ema.MghError):      # no packed kernel for IC % 16 != 0
+        ctx.conv2d_pack_weights(d, 3, 3, 3, 16, d)
     ctx.free(d)
 
 
