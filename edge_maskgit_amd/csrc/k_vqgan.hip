@@ -190,33 +190,75 @@ __global__ __launch_bounds__(256) void k_conv_pack(const float* __restrict__ ker
 
 // ---- few output channels (OC <= 8, the 3-channel conv_out): one thread per output pixel,
 // products and sums in the reference loop's order (ic, kh, kw; out-of-image taps skipped) with
-// separate multiply and add — the same float operations as the CPU executor's k_conv_2d
-template <int OCN>
+// separate multiply and add — the same float operations as the CPU executor's k_conv_2d.
+// KSZ = 3: the input values of ICB channels x 9 taps are loaded before they are summed, so a
+// thread has that many loads in flight (a skipped tap keeps the sum by a select, not by adding
+// zero); KSZ = 0: any kernel size, one tap at a time.
+template <int OCN, int KSZ>
 __global__ __launch_bounds__(256) void k_conv2d_few(ConvArgs a) {
 #pragma clang fp contract(off)
+    constexpr int ICB = 4;
     const int M = a.OW * a.OH;
     const int64_t gi = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (gi >= (int64_t)M * a.N) return;
     const int n = (int)(gi / M), p = (int)(gi - (int64_t)n * M);
     const int ow = p % a.OW, oh = p / a.OW;
-    const int K = a.IC * a.KH * a.KW;
+    const int KW = KSZ ? KSZ : a.KW, KH = KSZ ? KSZ : a.KH;
+    const int K = a.IC * KH * KW;
     const size_t plane = (size_t)a.IW * a.IH;
+    const int ih0 = oh * a.stride - a.pad, iw0 = ow * a.stride - a.pad;
     float acc[OCN];
 #pragma unroll
     for (int o = 0; o < OCN; o++) acc[o] = 0.f;
-    for (int ic = 0; ic < a.IC; ic++) {
-        const float* xin = a.in + ((size_t)n * a.IC + ic) * plane;
-        for (int kh = 0; kh < a.KH; kh++) {
-            const int ih = oh * a.stride - a.pad + kh;
-            if (ih < 0 || ih >= a.IH) continue;
-            for (int kw = 0; kw < a.KW; kw++) {
-                const int iw = ow * a.stride - a.pad + kw;
-                if (iw < 0 || iw >= a.IW) continue;
-                const float v = xin[(size_t)ih * a.IW + iw];
-                const int k = (ic * a.KH + kh) * a.KW + kw;
+    const float* xn = a.in + (size_t)n * a.IC * plane;
+    if (KSZ == 3) {
+        bool ok[9];
+        int off[9];
 #pragma unroll
-                for (int o = 0; o < OCN; o++)
-                    if (o < a.OC) acc[o] = acc[o] + a.ker[(size_t)o * K + k] * v;
+        for (int t = 0; t < 9; t++) {
+            const int ih = ih0 + t / 3, iw = iw0 + t % 3;
+            ok[t] = ih >= 0 && ih < a.IH && iw >= 0 && iw < a.IW;
+            off[t] = ok[t] ? ih * a.IW + iw : 0;
+        }
+        for (int ic0 = 0; ic0 < a.IC; ic0 += ICB) {
+            float v[ICB][9];
+#pragma unroll
+            for (int c = 0; c < ICB; c++) {
+                const bool cv = ic0 + c < a.IC;
+                const float* xin = xn + (size_t)(cv ? ic0 + c : 0) * plane;
+#pragma unroll
+                for (int t = 0; t < 9; t++) v[c][t] = ok[t] && cv ? xin[off[t]] : 0.f;
+            }
+#pragma unroll
+            for (int c = 0; c < ICB; c++) {
+                if (ic0 + c >= a.IC) break;
+#pragma unroll
+                for (int t = 0; t < 9; t++) {
+                    const int k = (ic0 + c) * 9 + t;
+#pragma unroll
+                    for (int o = 0; o < OCN; o++)
+                        if (o < a.OC) {
+                            const float s = acc[o] + a.ker[(size_t)o * K + k] * v[c][t];
+                            acc[o] = ok[t] ? s : acc[o];
+                        }
+                }
+            }
+        }
+    } else {
+        for (int ic = 0; ic < a.IC; ic++) {
+            const float* xin = xn + (size_t)ic * plane;
+            for (int kh = 0; kh < KH; kh++) {
+                const int ih = ih0 + kh;
+                if (ih < 0 || ih >= a.IH) continue;
+                for (int kw = 0; kw < KW; kw++) {
+                    const int iw = iw0 + kw;
+                    if (iw < 0 || iw >= a.IW) continue;
+                    const float v = xin[(size_t)ih * a.IW + iw];
+                    const int k = (ic * KH + kh) * KW + kw;
+#pragma unroll
+                    for (int o = 0; o < OCN; o++)
+                        if (o < a.OC) acc[o] = acc[o] + a.ker[(size_t)o * K + k] * v;
+                }
             }
         }
     }
@@ -324,7 +366,8 @@ __global__ __launch_bounds__(256) void k_conv2d_f32(ConvArgs a) {
 constexpr int GN_CHUNK = 4096;
 
 __device__ __forceinline__ double block_sum_d(double v, double* red) {
-    // fixed-order reduction: wave butterflies, then the 4 wave sums in wave order
+    // fixed-order reduction: wave butterflies, then the 4 wave sums in wave order; red[4] must
+    // not be in use by another reduction of the same block
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const uint64_t u = __builtin_bit_cast(uint64_t, v);
@@ -338,43 +381,79 @@ __device__ __forceinline__ double block_sum_d(double v, double* red) {
     return ((red[0] + red[1]) + red[2]) + red[3];
 }
 
-// mean of group ng from the pass-1 partials, summed in chunk order
-__device__ __forceinline__ double gn_mean(const double* part, int ng, int chunks, int64_t cnt) {
-    double s = 0.0;
-    for (int c = 0; c < chunks; c++) s += part[(size_t)ng * chunks + c];
-    return s / (double)cnt;
+// this thread's elements of a 4096-element chunk: VEC, 16-byte groups at 4t + 1024j (j < 4);
+// else single elements at t + 256j (j < 16); idx = -1 past the chunk's end
+template <bool VEC>
+__device__ __forceinline__ int64_t gn_idx(int64_t b, int64_t e, int j) {
+    const int64_t i = VEC ? b + 4 * (int64_t)threadIdx.x + 1024 * (j >> 2) + (j & 3) : b + threadIdx.x + 256 * j;
+    return i < e ? i : -1;
 }
 
-// PASS 0: partial sums of x; PASS 1: partial sums of (x - mean)^2
-template <int PASS>
+// per chunk of a group: S = sum of x and Q = sum of (x - S/n_c)^2, both in double, from the
+// chunk's values held in registers (one read of x)
+template <bool VEC>
 __global__ __launch_bounds__(256) void k_gn_stats(const float* __restrict__ x, double* __restrict__ part,
-                                                  double* __restrict__ part2, int64_t cnt, int chunks) {
-    __shared__ double red[4];
+                                                  int64_t cnt, int chunks) {
+    __shared__ double red[2][4];
     const int chunk = blockIdx.x, ng = blockIdx.y;
     const float* xg = x + (size_t)ng * cnt;
     const int64_t b = (int64_t)chunk * GN_CHUNK, e = min(cnt, b + GN_CHUNK);
-    const double mean = PASS ? gn_mean(part, ng, chunks, cnt) : 0.0;
-    double s = 0.0;
-    for (int64_t i = b + threadIdx.x; i < e; i += 256) {
-        const double d = (double)xg[i] - mean;
-        s += PASS ? d * d : d;
+    float v[16];
+    if (VEC) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int64_t i = b + 4 * (int64_t)threadIdx.x + 1024 * q;
+            const f32x4 w = i < e ? *(const f32x4*)(xg + i) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int r = 0; r < 4; r++) v[4 * q + r] = w[r];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const int64_t i = gn_idx<false>(b, e, j);
+            v[j] = i >= 0 ? xg[i] : 0.f;
+        }
     }
-    s = block_sum_d(s, red);
-    if (threadIdx.x == 0) (PASS ? part2 : part)[(size_t)ng * chunks + chunk] = s;
+    double s = 0.0;
+#pragma unroll
+    for (int j = 0; j < 16; j++) s += (double)v[j];           // out-of-chunk values are 0
+    const double S = block_sum_d(s, red[0]);
+    const double mc = S / (double)(e - b);
+    double q = 0.0;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const double d = (double)v[j] - mc;
+        if (gn_idx<VEC>(b, e, j) >= 0) q += d * d;
+    }
+    const double Q = block_sum_d(q, red[1]);
+    if (threadIdx.x == 0) {
+        part[2 * ((size_t)ng * chunks + chunk)] = S;
+        part[2 * ((size_t)ng * chunks + chunk) + 1] = Q;
+    }
 }
 
-template <bool AFFINE_SILU>
+// y = (float)(x - mean) * inv (+ affine + SiLU) over one chunk; mean and variance of the group
+// from its chunks' (S, Q): mean = sum S / n, n var = sum over chunks of Q_c + n_c (m_c - mean)^2
+// (the parallel form of the two-pass sum of squared deviations), each sum in a fixed order
+template <bool AFFINE_SILU, bool VEC>
 __global__ __launch_bounds__(256) void k_gn_apply(const float* __restrict__ x, const double* __restrict__ part,
-                                                  const double* __restrict__ part2,
                                                   const float* __restrict__ gamma, const float* __restrict__ beta,
                                                   float* __restrict__ y, int64_t cnt, int64_t plane, int cpg,
                                                   int G, int chunks, float eps) {
 #pragma clang fp contract(off)   // xn = y*gamma + beta rounds twice, as in the reference
+    __shared__ double red[2][4];
     const int chunk = blockIdx.x, ng = blockIdx.y;
-    const double mean = gn_mean(part, ng, chunks, cnt);
+    const double* pg = part + 2 * (size_t)ng * chunks;
+    double s = 0.0;
+    for (int c = threadIdx.x; c < chunks; c += 256) s += pg[2 * c];
+    const double mean = block_sum_d(s, red[0]) / (double)cnt;
     double q = 0.0;
-    for (int c = 0; c < chunks; c++) q += part2[(size_t)ng * chunks + c];
-    const double var = q / (double)cnt;
+    for (int c = threadIdx.x; c < chunks; c += 256) {
+        const double nc = (double)min((int64_t)GN_CHUNK, cnt - (int64_t)c * GN_CHUNK);
+        const double d = pg[2 * c] / nc - mean;
+        q += pg[2 * c + 1] + nc * d * d;
+    }
+    const double var = block_sum_d(q, red[1]) / (double)cnt;
     // fp32 sqrt and divide, each correctly rounded (evaluated in double, rounded once)
     const float sq = (float)sqrt((double)__fadd_rn((float)var, eps));
     const float inv = (float)(1.0 / (double)sq);
@@ -382,14 +461,29 @@ __global__ __launch_bounds__(256) void k_gn_apply(const float* __restrict__ x, c
     float* yg = y + (size_t)ng * cnt;
     const int c0 = (ng % G) * cpg;
     const int64_t b = (int64_t)chunk * GN_CHUNK, e = min(cnt, b + GN_CHUNK);
-    for (int64_t i = b + threadIdx.x; i < e; i += 256) {
-        float v = (float)((double)xg[i] - mean) * inv;
+    auto f = [&](float xv, float g, float bb) {
+        float v = (float)((double)xv - mean) * inv;
         if (AFFINE_SILU) {
-            const int c = c0 + (int)(i / plane);
-            v = v * gamma[c] + beta[c];
+            v = v * g + bb;
             v = v / (1.0f + expf(-v));
         }
-        yg[i] = v;
+        return v;
+    };
+    if (VEC) {
+#pragma unroll
+        for (int qd = 0; qd < 4; qd++) {
+            const int64_t i = b + 4 * (int64_t)threadIdx.x + 1024 * qd;
+            if (i >= e) break;
+            const f32x4 w = *(const f32x4*)(xg + i);
+            const int c = c0 + (int)(i / plane);              // plane % 4 == 0: one channel
+            const float g = AFFINE_SILU ? gamma[c] : 0.f, bb = AFFINE_SILU ? beta[c] : 0.f;
+            *(f32x4*)(yg + i) = f32x4{f(w[0], g, bb), f(w[1], g, bb), f(w[2], g, bb), f(w[3], g, bb)};
+        }
+    } else {
+        for (int64_t i = b + threadIdx.x; i < e; i += 256) {
+            const int c = c0 + (int)(i / plane);
+            yg[i] = f(xg[i], AFFINE_SILU ? gamma[c] : 0.f, AFFINE_SILU ? beta[c] : 0.f);
+        }
     }
 }
 
@@ -413,8 +507,14 @@ hipError_t launch_conv2d_f32(const ConvArgs& a, hipStream_t s) {
     if (a.OC <= kConvFewMax) {
         const int64_t total = (int64_t)M * a.N;
         const dim3 grid((unsigned)((total + 255) / 256));
-        if (a.OC <= 4) hipLaunchKernelGGL(k_conv2d_few<4>, grid, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL(k_conv2d_few<8>, grid, dim3(256), 0, s, a);
+        const bool k3 = a.KW == 3 && a.KH == 3;
+        if (a.OC <= 4) {
+            if (k3) hipLaunchKernelGGL((k_conv2d_few<4, 3>), grid, dim3(256), 0, s, a);
+            else hipLaunchKernelGGL((k_conv2d_few<4, 0>), grid, dim3(256), 0, s, a);
+        } else {
+            if (k3) hipLaunchKernelGGL((k_conv2d_few<8, 3>), grid, dim3(256), 0, s, a);
+            else hipLaunchKernelGGL((k_conv2d_few<8, 0>), grid, dim3(256), 0, s, a);
+        }
         return hipGetLastError();
     }
     const dim3 grid((unsigned)((M + CBM - 1) / CBM), (unsigned)((a.OC + CBN - 1) / CBN), (unsigned)a.N), block(256);
@@ -499,16 +599,21 @@ hipError_t launch_group_norm(const float* x, int64_t W, int64_t H, int C, int N,
     if (cnt == 0 || N == 0) return hipSuccess;
     const int chunks = (int)((cnt + GN_CHUNK - 1) / GN_CHUNK);
     double* part = (double*)ws;
-    double* part2 = part + (size_t)chunks * G * N;
     const dim3 grid((unsigned)chunks, (unsigned)(G * N)), block(256);
-    hipLaunchKernelGGL(k_gn_stats<0>, grid, block, 0, s, x, part, part2, cnt, chunks);
-    hipLaunchKernelGGL(k_gn_stats<1>, grid, block, 0, s, x, part, part2, cnt, chunks);
-    if (gamma)
-        hipLaunchKernelGGL(k_gn_apply<true>, grid, block, 0, s, x, part, part2, gamma, beta, y, cnt, plane, cpg, G,
-                           chunks, eps);
-    else
-        hipLaunchKernelGGL(k_gn_apply<false>, grid, block, 0, s, x, part, part2, gamma, beta, y, cnt, plane, cpg, G,
-                           chunks, eps);
+    // 16-byte accesses: planes of 4k elements (a group and a 4-group never straddle channels)
+    const bool vec = plane % 4 == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)y % 16) == 0;
+    if (vec) hipLaunchKernelGGL(k_gn_stats<true>, grid, block, 0, s, x, part, cnt, chunks);
+    else hipLaunchKernelGGL(k_gn_stats<false>, grid, block, 0, s, x, part, cnt, chunks);
+#define GN_APPLY(A, V) \
+    hipLaunchKernelGGL((k_gn_apply<A, V>), grid, block, 0, s, x, part, gamma, beta, y, cnt, plane, cpg, G, chunks, eps)
+    if (gamma) {
+        if (vec) GN_APPLY(true, true);
+        else GN_APPLY(true, false);
+    } else {
+        if (vec) GN_APPLY(false, true);
+        else GN_APPLY(false, false);
+    }
+#undef GN_APPLY
     return hipGetLastError();
 }
 

@@ -126,8 +126,10 @@ def test_conv2d_ex_bias_residual_packed(ctx, IW, IH, IC, N, KW, KH, OC, stride, 
         ctx.free(b)
 
 
+# planes of 4k elements take the 16-byte path (9 x 7, 5 x 3: single elements); a group spans
+# 1 .. 520 statistics chunks of 4096 (1040 x 1024 x 2 channels, one group: more chunks than threads)
 GN = [(16, 16, 512, 1, 32), (9, 7, 64, 2, 32), (64, 64, 128, 1, 32), (256, 256, 128, 1, 32),
-      (5, 3, 6, 3, 3), (32, 32, 256, 2, 32)]
+      (5, 3, 6, 3, 3), (32, 32, 256, 2, 32), (1040, 1024, 2, 1, 1)]
 
 
 @pytest.mark.parametrize("W,H,C,N,G", GN)
