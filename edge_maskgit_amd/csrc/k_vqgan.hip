@@ -163,6 +163,87 @@ __global__ __launch_bounds__(256, 2) void k_conv2d_pk(ConvPkArgs a) {
     }
 }
 
+// few output channels (OC <= 16, the 3-channel conv_out) on the same packed weights: a
+// workgroup computes 256 pixels x 16 channels, each wave 64 pixels x 16 channels
+constexpr int NBM = 256, NBN = 16;
+
+template <bool SPLIT>
+__global__ __launch_bounds__(256, 2) void k_conv2d_pkn(ConvPkArgs a) {
+    __shared__ __attribute__((aligned(16))) float As[2][NBM][PST];   // [pixel][k]
+    __shared__ __attribute__((aligned(16))) float Bs[2][NBN][PST];   // [channel][k]
+    const int M = a.OW * a.OH, K = a.IC * a.KW * a.KH, OC = a.OC;
+    const int z = blockIdx.z;
+    const int n = SPLIT ? z / a.splits : z, sp = SPLIT ? z - n * a.splits : 0;
+    const int kbeg = sp * a.kps, kend = min(K, kbeg + a.kps);
+    const int m0 = blockIdx.x * NBM, n0 = blockIdx.y * NBN;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, lg = lane >> 4;
+
+    // gather roles: pixel tid with the slab's 16 channels; threads < 64: weight row tid/4, k 4(tid%4)..
+    const int p = m0 + tid;
+    const bool pv = p < M;
+    const int ow = pv ? p % a.OW : 0, oh = pv ? p / a.OW : 0;
+    const int iw0 = ow * a.stride - a.pad, ih0 = oh * a.stride - a.pad;
+    const size_t plane = (size_t)a.IW * a.IH;
+    const float* inb = a.in + (size_t)n * a.IC * plane;
+    const int bo = tid >> 2, bq = tid & 3;
+    const bool bload = tid < 4 * NBN, bv = bload && n0 + bo < OC;
+    const float* wrow = a.wpk + (size_t)(bv ? n0 + bo : 0) * K + 4 * bq;
+
+    float ra[16];
+    f32x4 rb;
+    auto load = [&](int k0) {
+        const int tap = k0 / a.IC, ic0 = k0 - tap * a.IC;
+        const int kh = tap / a.KW, kw = tap - kh * a.KW;
+        const int ih = ih0 + kh, iw = iw0 + kw;
+        if (pv && ih >= 0 && ih < a.IH && iw >= 0 && iw < a.IW) {
+            const float* src = inb + (size_t)ic0 * plane + (size_t)ih * a.IW + iw;
+#pragma unroll
+            for (int j = 0; j < 16; j++) ra[j] = src[j * plane];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; j++) ra[j] = 0.f;
+        }
+        rb = bv ? *(const f32x4*)(wrow + k0) : f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            *(f32x4*)&As[buf][tid][4 * q] = f32x4{ra[4 * q], ra[4 * q + 1], ra[4 * q + 2], ra[4 * q + 3]};
+        if (bload) *(f32x4*)&Bs[buf][bo][4 * bq] = rb;
+    };
+
+    f32x4 acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int nk = (kend - kbeg) / PBK;
+    load(kbeg);
+    store(0);
+    __syncthreads();
+    for (int t = 0; t < nk; t++) {
+        const int cur = t & 1;
+        if (t + 1 < nk) load(kbeg + (t + 1) * PBK);
+        f32x4 af[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) af[i] = *(const f32x4*)&As[cur][64 * wave + 16 * i + l16][4 * lg];
+        const f32x4 bf = *(const f32x4*)&Bs[cur][l16][4 * lg];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][kk], bf[kk], acc[i], 0, 0, 0);
+        if (t + 1 < nk) store(cur ^ 1);
+        __syncthreads();
+    }
+    const int oc = n0 + l16;
+    if (oc >= OC) return;
+    const size_t row = ((size_t)(SPLIT ? sp * a.N + n : n) * OC + oc) * M;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        conv_store(a.out, SPLIT ? nullptr : a.bias, SPLIT ? nullptr : a.resid, row, oc, m0 + 64 * wave + 16 * i + 4 * lg,
+                   M, acc[i]);
+}
+
 // out[i] = ((sum over splits in order of part[s][i]) + bias[oc]) + resid[i]
 __global__ __launch_bounds__(256) void k_conv_reduce(const float* __restrict__ part, int splits, int64_t total,
                                                      int M, int OC, const float* __restrict__ bias,
@@ -524,12 +605,15 @@ hipError_t launch_conv2d_f32(const ConvArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+bool conv_pk_narrow(int OC) { return OC <= NBN; }
+
 ConvPkPlan conv_pk_plan(int M, int OC, int K) {
     // about two workgroups per CU for one image: split K when its output tiles alone give
     // fewer than 384 workgroups, keeping at least two 16-wide slabs per split. The plan does
     // not depend on the batch, so an image's sums are the same whatever it is batched with.
     ConvPkPlan p{1, K};
-    const int64_t tiles = (int64_t)((M + PBM - 1) / PBM) * ((OC + PBN - 1) / PBN);
+    const int bm = conv_pk_narrow(OC) ? NBM : PBM, bn = conv_pk_narrow(OC) ? NBN : PBN;
+    const int64_t tiles = (int64_t)((M + bm - 1) / bm) * ((OC + bn - 1) / bn);
     const int slabs = K / PBK;
     if (tiles >= 384 || slabs < 4) return p;
     int want = (int)std::min<int64_t>((512 + tiles - 1) / tiles, slabs / 2);
@@ -563,9 +647,13 @@ hipError_t launch_conv2d_pk(const ConvPkArgs& a0, float* ws, hipStream_t s) {
     a.splits = p.splits;
     a.kps = p.kps;
     const dim3 block(256);
+    const bool nar = conv_pk_narrow(a0.OC);
+    const unsigned gx = (unsigned)(nar ? (M + NBM - 1) / NBM : (M + PBM - 1) / PBM);
+    const unsigned gy = (unsigned)(nar ? (a0.OC + NBN - 1) / NBN : (a0.OC + PBN - 1) / PBN);
     if (p.splits == 1) {
-        const dim3 grid((unsigned)((M + PBM - 1) / PBM), (unsigned)((a.OC + PBN - 1) / PBN), (unsigned)a.N);
-        hipLaunchKernelGGL(k_conv2d_pk<false>, grid, block, 0, s, a);
+        const dim3 grid(gx, gy, (unsigned)a.N);
+        if (nar) hipLaunchKernelGGL(k_conv2d_pkn<false>, grid, block, 0, s, a);
+        else hipLaunchKernelGGL(k_conv2d_pk<false>, grid, block, 0, s, a);
         return hipGetLastError();
     }
     // groups of images: partials part[split][image of the group][oc][pixel] in ws, then reduced
@@ -576,8 +664,9 @@ hipError_t launch_conv2d_pk(const ConvPkArgs& a0, float* ws, hipStream_t s) {
         a.in = a0.in + n0 * in_img;
         a.out = ws;
         a.N = g;
-        const dim3 grid((unsigned)((M + PBM - 1) / PBM), (unsigned)((a.OC + PBN - 1) / PBN), (unsigned)(g * p.splits));
-        hipLaunchKernelGGL(k_conv2d_pk<true>, grid, block, 0, s, a);
+        const dim3 grid(gx, gy, (unsigned)(g * p.splits));
+        if (nar) hipLaunchKernelGGL(k_conv2d_pkn<true>, grid, block, 0, s, a);
+        else hipLaunchKernelGGL(k_conv2d_pk<true>, grid, block, 0, s, a);
         const int64_t total = (int64_t)g * out_img;
         const int64_t nb = std::min<int64_t>((total + 255) / 256, 8192);
         hipLaunchKernelGGL(k_conv_reduce, dim3((unsigned)nb), block, 0, s, ws, p.splits, total, M, a.OC, a0.bias,

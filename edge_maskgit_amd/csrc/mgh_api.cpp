@@ -707,7 +707,7 @@ int conv_shape(mgh_ctx* c, int IW, int IH, int IC, int N, int KW, int KH, int OC
     return MGH_OK;
 }
 
-bool conv_packed_path(int IC, int OC) { return IC % 16 == 0 && OC > mgh::kConvFewMax; }
+bool conv_packed_path(int IC, int OC) { return IC % 16 == 0 && OC > 0; }
 
 }  // namespace
 
@@ -757,7 +757,7 @@ int mgh_conv2d_pack_weights(mgh_ctx* c, const float* ker, int KW, int KH, int IC
     if (KW <= 0 || KH <= 0 || IC <= 0 || OC <= 0 || (int64_t)IC * KW * KH > INT32_MAX)
         return fail(c, MGH_ERR_ARG, "conv2d_pack_weights: need positive sizes");
     if (!conv_packed_path(IC, OC))
-        return fail(c, MGH_ERR_UNSUPPORTED, "conv2d_pack_weights: the packed kernel needs IC % 16 == 0 and OC > 8");
+        return fail(c, MGH_ERR_UNSUPPORTED, "conv2d_pack_weights: the packed kernel needs IC % 16 == 0");
     if (!ker || !wpk) return fail(c, MGH_ERR_ARG, "conv2d_pack_weights: null pointer");
     if (int r = set_dev(c)) return r;
     MGH_HIP(c, mgh::launch_conv_pack(ker, wpk, IC, KW * KH, OC, c->stream), "k_conv_pack");

@@ -191,11 +191,12 @@ struct ConvArgs {
     const float* resid;    // shape of out or null: then + resid
 };
 constexpr int kConvFewMax = 8;      // OC up to this: the one-thread-per-pixel kernel
-// the reference-layout kernels: one thread per pixel for OC <= kConvFewMax, else the
-// 64 x 64 fp32-MFMA implicit GEMM (any IC)
+// the reference-layout kernels (IC % 16 != 0): one thread per pixel for OC <= kConvFewMax,
+// else the 64 x 64 fp32-MFMA implicit GEMM
 hipError_t launch_conv2d_f32(const ConvArgs& a, hipStream_t s);
 
-// packed-weight fp32-MFMA implicit GEMM for IC % 16 == 0 (wpk from launch_conv_pack)
+// packed-weight fp32-MFMA implicit GEMM for IC % 16 == 0 (wpk from launch_conv_pack): tiles of
+// 128 pixels x 128 channels, or 256 x 16 when OC <= 16 (conv_pk_narrow)
 struct ConvPkArgs {
     const float* in;
     const float* wpk;      // [OC][KH][KW][IC]
@@ -208,6 +209,7 @@ struct ConvPkArgs {
 struct ConvPkPlan {
     int splits, kps;       // K split into `splits` ranges of kps values (a multiple of 16)
 };
+bool conv_pk_narrow(int OC);
 ConvPkPlan conv_pk_plan(int M, int OC, int K);   // per image: independent of the batch
 size_t conv_pk_ws_bytes(int M, int OC, int N, int K);    // split-K partials, 0 without a split
 hipError_t launch_conv_pack(const float* ker, float* wpk, int IC, int taps, int OC, hipStream_t s);

@@ -223,11 +223,12 @@ int mgh_gemm_f32_batched(mgh_ctx* ctx, const float* d_w, const int64_t w_ne[4], 
  *      mgh_conv2d: the Conv2D node (CPU mg-cpu.cpp:165-190; GPU k_conv2d_t,
  *      mg-opencl.cpp:985-1025, 1535-1566): ker {KW, KH, IC, OC}, out {OW, OH, OC, N} with
  *      OW = (IW + 2 pad - KW) / stride + 1; fp32 products and accumulation; d_out 16-byte aligned.
- *      Kernels: OC <= 8 one thread per pixel in the reference loop's order (the CPU executor's
- *      float operations exactly); IC % 16 == 0 an fp32-MFMA implicit GEMM over tap-major packed
- *      weights (packed into the context scratch per call, or once by mgh_conv2d_pack_weights),
- *      with K split across workgroups when the output alone gives too few; otherwise a 64 x 64
- *      fp32-MFMA implicit GEMM over the reference layout.
+ *      Kernels: IC % 16 == 0 an fp32-MFMA implicit GEMM over tap-major packed weights (packed
+ *      into the context scratch per call, or once by mgh_conv2d_pack_weights; 128 x 128 tiles,
+ *      256 x 16 for OC <= 16), with K split across workgroups when one image's output alone
+ *      gives too few (per image: results do not depend on the batch); otherwise, for OC <= 8,
+ *      one thread per pixel in the reference loop's order (the CPU executor's float operations
+ *      exactly), else a 64 x 64 fp32-MFMA implicit GEMM over the reference layout.
  *      mgh_conv2d_ex: the conv node with the decoder's following Add nodes fused:
  *      out = (conv + bias[oc]) + resid, each addition rounded as its own node would (bias [OC]
  *      or null; resid shaped as out, 16-byte aligned, or null); d_packed (optional, from

@@ -32,11 +32,13 @@ def ctx():
     c.close()
 
 
-# kernels: OC <= 8 one thread per pixel ("few"); IC % 16 == 0 packed tap-major MFMA ("pk",
-# split over K when the output gives too few workgroups); else the reference-layout MFMA ("gen")
+# kernels: IC % 16 == 0 packed tap-major MFMA ("pk": 128 x 128 tiles, "pkn": 256 x 16 for
+# OC <= 16; split over K when one image's output gives too few workgroups); else OC <= 8 one
+# thread per pixel ("few"), or the reference-layout MFMA ("gen")
 CONV = [  # IW, IH, IC, N, KW, KH, OC, stride, pad
     (9, 7, 5, 2, 3, 3, 7, 1, 1), (10, 10, 3, 1, 3, 3, 8, 2, 1), (5, 5, 2, 1, 5, 5, 3, 1, 2),
-    (7, 7, 4, 1, 3, 3, 3, 1, 0), (32, 32, 128, 1, 3, 3, 3, 1, 1),                     # few
+    (7, 7, 4, 1, 3, 3, 3, 1, 0), (32, 32, 128, 1, 3, 3, 3, 1, 1),                     # few, pkn
+    (256, 256, 128, 1, 3, 3, 3, 1, 1), (20, 9, 32, 2, 3, 3, 16, 2, 1),                # pkn
     (8, 8, 33, 2, 1, 1, 65, 1, 0), (65, 33, 20, 1, 3, 3, 130, 1, 1),                  # gen
     (16, 16, 256, 1, 3, 3, 512, 1, 1), (16, 16, 512, 2, 3, 3, 512, 1, 1),             # pk, split
     (32, 32, 128, 2, 3, 3, 64, 1, 1), (64, 64, 64, 1, 1, 1, 32, 1, 0),                # pk
@@ -67,8 +69,8 @@ def test_conv2d_vs_float64(ctx, IW, IH, IC, N, KW, KH, OC, stride, pad):
     print(f"  rel err vs float64 {err:.2e}")
     assert err <= 1e-5
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
-    if OC <= 8 and ref.available():
-        # the few-channel kernel performs the CPU executor's float operations in its order
+    if OC <= 8 and IC % 16 and ref.available():
+        # the one-thread-per-pixel kernel performs the CPU executor's float operations in its order
         assert np.array_equal(y, ref.conv2d(x, ker, stride, pad))
 
 
@@ -115,7 +117,7 @@ def test_conv2d_ex_bias_residual_packed(ctx, IW, IH, IC, N, KW, KH, OC, stride, 
     fused = ctx.download(dY, res.shape, np.float32)
     assert np.array_equal(fused, (plain + bias[None, :, None, None]) + res)
     nbytes = ctx.conv2d_packed_bytes(KW, KH, IC, OC)
-    assert (nbytes > 0) == (IC % 16 == 0 and OC > 8)
+    assert (nbytes > 0) == (IC % 16 == 0)
     if nbytes:
         dP = ctx.alloc(nbytes)
         ctx.conv2d_pack_weights(dK, KW, KH, IC, OC, dP)
