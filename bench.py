@@ -37,6 +37,11 @@ in config.csrc_sha256_16), else null with the reason in roofline.traffic_source.
 cpu_baseline = the reference's own CPU executor (mg-cpu k_mul_mat, single thread, built
 from the reference sources into oracle/_ref) on the dequantized weights, timed on this
 host over the same four GEMMs; if that library is absent, the C oracle's int8 path.
+extra.vqgan_decode = the production VQGAN decoder graph (256 tokens -> 256 x 256 image, 128
+filters, multipliers 1,1,2,2,4) on random-init weights through mgr_decode_images, for one image
+and a batch of 8: wall ms per decode with the ids already prepared and the image left in HBM,
+the per-op device profile, the conv kernels' fraction of the fp32 MFMA peak, and a bounded
+sample of the reference's CPU conv (--no-vqgan skips it; --only-vqgan measures only it).
 """
 from __future__ import annotations
 
@@ -452,6 +457,133 @@ def measure_decode_step(ctx, B, S=257, V=2025, reps=20):
     return ms
 
 
+# ---- VQGAN decoder (the production configuration of the reference's decoder graph) ----
+VQ = dict(n_tokens=256, E=256, codebook=1024, filters=128, mult=(1, 1, 2, 2, 4), R=2)
+
+
+def vqgan_convs(n_tokens, E, filters, mult, R, **_):
+    """(side, IC, OC, k) of every convolution of build_vqgan_decoder, in graph order"""
+    L = int(round(n_tokens ** 0.5))
+    out, side, w = [], L, filters * mult[-1]
+    out.append((side, E, w, 3))
+    for _ in range(R):
+        out += [(side, w, w, 3), (side, w, w, 3)]
+    for i in range(len(mult) - 1, -1, -1):
+        o = filters * mult[i]
+        for _ in range(R):
+            out += [(side, w, o, 3), (side, o, o, 3)] + ([(side, o, o, 1)] if w != o else [])
+            w = o
+        if i > 0:
+            side *= 2
+            out.append((side, w, w, 3))
+    out.append((side, w, 3, 3))
+    return out
+
+
+def write_vqgan_model(path, seed=11):
+    """random-init decoder weights under the converter's names (conv ~N(0, 1/fan_in), GroupNorm
+    gamma ~1 + N(0, 0.1), beta / biases ~N(0, 0.1) / N(0, 0.05), codebook ~N(0, 1))"""
+    from edge_maskgit_amd.gguf import write_gguf
+    rng = np.random.default_rng(seed)
+    E, F, mult, R = VQ["E"], VQ["filters"], VQ["mult"], VQ["R"]
+    out = []
+
+    def f32(name, a):
+        out.append((name, a.shape, 0, np.ascontiguousarray(a, np.float32).tobytes()))
+
+    def conv(name, oc, ic, k, bias):
+        f32(name + ".weight", rng.standard_normal((oc, ic, k, k), np.float32) / np.float32(np.sqrt(ic * k * k)))
+        if bias:
+            f32(name + ".bias", 0.05 * rng.standard_normal(oc, np.float32))
+
+    def gn(name, c):
+        f32(name + ".weight", 1 + 0.1 * rng.standard_normal(c, np.float32))
+        f32(name + ".bias", 0.1 * rng.standard_normal(c, np.float32))
+
+    def block(p, ci, co):
+        gn(p + "norm0", ci)
+        conv(p + "conv0", co, ci, 3, False)
+        gn(p + "norm1", co)
+        conv(p + "conv1", co, co, 3, False)
+        if ci != co:
+            conv(p + "conv_res", co, co, 1, False)
+
+    f32("vqgan.quantizer.codebook.weight", rng.standard_normal((VQ["codebook"], E), np.float32))
+    w = F * mult[-1]
+    conv("vqgan.decoder.conv_in", w, E, 3, True)
+    for l in range(R):
+        block(f"vqgan.decoder.res_blocks.0.{l}.", w, w)
+    for i in range(len(mult) - 1, -1, -1):
+        j, o = len(mult) - i, F * mult[i]
+        for l in range(R):
+            block(f"vqgan.decoder.res_blocks.{j}.{l}.", w, o)
+            w = o
+        if i > 0:
+            conv(f"vqgan.decoder.res_blocks.{j}.{R + 1}", w, w, 3, True)
+    gn("vqgan.decoder.norm_out", w)
+    conv("vqgan.decoder.conv_out", 3, w, 3, True)
+    meta = [("general.architecture", "str", "maskgit"), ("general.alignment", "u32", 32),
+            ("maskgit.n_tokens", "u32", VQ["n_tokens"]), ("maskgit.resolution", "u32", 256),
+            ("maskgit.vqgan.codebook_size", "u32", VQ["codebook"]), ("maskgit.vqgan.embedding_dim", "u32", E),
+            ("maskgit.vqgan.filters", "u32", F), ("maskgit.vqgan.num_res_blocks", "u32", R),
+            ("maskgit.vqgan.group_norm_groups", "u32", 32),
+            ("maskgit.vqgan.channel_multipliers", "i32_array", list(mult))]
+    write_gguf(path, meta, out)
+
+
+def measure_vqgan(path, steps=5, cpu=True):
+    """The production decoder graph (mgr_decode_images: mg::build_vqgan_decoder on HipRuntime)
+    for one image and for a batch of 8: wall clock per decode (ids in, image left in HBM), the
+    per-op device profile of one B=1 decode, and the conv kernels' fp32-MFMA roofline."""
+    from edge_maskgit_amd.runtime import TransformerRuntime
+    convs = vqgan_convs(**VQ)
+    conv_flop = sum(2.0 * s * s * ic * oc * k * k for s, ic, oc, k in convs)
+    res = {"model": "VQGAN decoder, 256 tokens -> 256 x 256 x 3, 128 filters, multipliers 1,1,2,2,4, "
+                    "2 res blocks per level, GroupNorm 32 (random-init weights)",
+           "conv_gflop_per_image": round(conv_flop / 1e9, 2)}
+    rng = np.random.default_rng(3)
+    with TransformerRuntime(path) as m:
+        for B in (1, 8):
+            g = rng.integers(0, VQ["codebook"], (B, VQ["n_tokens"])).astype(np.int32)
+            for _ in range(2):
+                m.decode_images(g, readback=False)       # the first call packs and uploads weights
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                m.decode_images(g, readback=False)
+            ms = (time.perf_counter() - t0) / steps * 1e3
+            res[f"b{B}"] = {"ms_per_decode": round(ms, 3), "ms_per_image": round(ms / B, 3),
+                            "tflops": round(conv_flop * B / (ms * 1e-3) / 1e12, 2)}
+        m.profile(True)
+        m.decode_images(rng.integers(0, VQ["codebook"], (1, VQ["n_tokens"])).astype(np.int32), readback=False)
+        prof = {n: {"count": c, "ms": round(t, 4)} for n, c, t in m.profile_report()}
+        m.profile(False)
+    res["per_op_device_ms_b1"] = prof
+    conv_ms = prof.get("Conv2D", {}).get("ms")
+    if conv_ms:
+        a = conv_flop / (conv_ms * 1e-3) / 1e12
+        res["roofline_conv_b1"] = {"bound": "mfma", "achieved": round(a, 2), "peak": 157.3, "unit": "TFLOP/s",
+                                   "frac": round(a / 157.3, 4), "kernel": "k_conv2d_pk (+ _pkn, split reduce)",
+                                   "note": "fp32 MFMA (the reference's conv arithmetic is fp32); all Conv2D "
+                                           "nodes of one decode, device time per node"}
+    if cpu:
+        from oracle import ref
+        if ref.available():
+            xs = [(16, 256, 512), (16, 512, 512)]
+            fl, t0 = 0.0, time.perf_counter()
+            for side, ic, oc in xs:
+                x = rng.standard_normal((1, ic, side, side), np.float32)
+                k = rng.standard_normal((oc, ic, 3, 3), np.float32) * np.float32(0.02)
+                ref.conv2d(x, k, 1, 1)
+                fl += 2.0 * side * side * ic * oc * 9
+            dt = time.perf_counter() - t0
+            res["cpu_baseline"] = {"value": round(fl / dt / 1e9, 3), "unit": "GFLOP/s", "cores": 1,
+                                   "kind": "reference",
+                                   "sample": f"reference mg-cpu k_conv_2d on the decoder's two 16x16 3x3 convs "
+                                             f"(256->512, 512->512: {fl/1e9:.2f} GFLOP in {dt:.1f} s); "
+                                             f"a whole decode at this rate: {conv_flop / (fl / dt) :.0f} s"}
+    return res
+
+
 def cpu_baseline(host, M, wtype, budget_s=15.0):
     """The reference CPU executor (libmgref) on dequantized weights, single thread, over the
     same four GEMMs; rows are processed in chunks until the budget is spent."""
@@ -517,6 +649,9 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run 10 plain device copies of BYTES (k_copy4d), to calibrate the "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters, and exit")
+    ap.add_argument("--no-vqgan", action="store_true", help="skip the VQGAN decoder measurement")
+    ap.add_argument("--only-vqgan", action="store_true",
+                    help="measure only the VQGAN decoder and print its record: the run a kernel profile wraps")
     ap.add_argument("--extra", action="store_true",
                     help="also measure Q8_0 M=4097 and Q4_K M=1025/4097 layers")
     a = ap.parse_args()
@@ -536,6 +671,14 @@ def main():
             ctx.copy_strided(src, (n, 1, 1, 1), (1, n, n, n), dst)
         ctx.sync()
         print(json.dumps({"copy_probe_bytes": n * 4, "launches": 10}), flush=True)
+        ctx.close()
+        return
+    if a.only_vqgan:
+        import tempfile
+        with tempfile.TemporaryDirectory() as d:
+            pv = os.path.join(d, "vqgan.gguf")
+            write_vqgan_model(pv)
+            print(json.dumps({"vqgan_decode": measure_vqgan(pv, a.steps, cpu=not a.no_cpu)}), flush=True)
         ctx.close()
         return
     if a.only_config:
@@ -629,6 +772,14 @@ def main():
                     "decode_step_device_ms": round(measure_decode_step(ctx, 64), 4),
                     "workload": f"64 images x 257 tokens, 8 steps, Q4_K 24 layers, {PATH_NAME[a.path]}; "
                                 "forward + on-device sampling per step, grids read back once"}
+    if not a.no_vqgan and not a.only_main:
+        import tempfile
+        with tempfile.TemporaryDirectory() as d:
+            pv = os.path.join(d, "vqgan.gguf")
+            t0 = time.perf_counter()
+            write_vqgan_model(pv)
+            log(f"[bench] VQGAN model written in {time.perf_counter() - t0:.1f} s")
+            extra["vqgan_decode"] = measure_vqgan(pv, cpu=not a.no_cpu)
     cpu = None if a.no_cpu else cpu_baseline(host, M, wtype)
     if not a.no_cpu and cpu is not None and cpu.get("kind") == "reference":
         extra["cpu_oracle_int8_omp"] = cpu_oracle_int8(host, M, wtype)   # a multi-core CPU point
