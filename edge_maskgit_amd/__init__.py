@@ -40,7 +40,8 @@ MGH_SYMBOLS = [
     "mgh_gemm_h16", "mgh_gemm_h16_f32in", "mgh_gemm_h16_y16", "mgh_flash_attn_f16kv_o16", "mgh_flash_attn_f16in",
     "mgh_softmax", "mgh_binary", "mgh_scale", "mgh_unary", "mgh_gemm_f32_batched",
     "mgh_gemm_h16_f32in_noalloc", "mgh_conv2d", "mgh_group_norm", "mgh_upscale", "mgh_conv2d_ex",
-    "mgh_conv2d_packed_bytes", "mgh_conv2d_pack_weights",
+    "mgh_conv2d_packed_bytes", "mgh_conv2d_pack_weights", "mgh_conv2d_i8_weight_bytes",
+    "mgh_conv2d_i8_pack_weights", "mgh_conv2d_i8",
 ]
 
 _lib = None
@@ -123,6 +124,10 @@ def lib():
         L.mgh_conv2d_packed_bytes.argtypes = [I, I, I, I]
         L.mgh_conv2d_packed_bytes.restype = ctypes.c_size_t
         L.mgh_conv2d_pack_weights.argtypes = [P, P, I, I, I, I, P]
+        L.mgh_conv2d_i8_weight_bytes.argtypes = [I, I, I, I]
+        L.mgh_conv2d_i8_weight_bytes.restype = ctypes.c_size_t
+        L.mgh_conv2d_i8_pack_weights.argtypes = [P, P, I, I, I, I, P]
+        L.mgh_conv2d_i8.argtypes = [P, P, I, I, I, I, P, I, I, I, I, I, P, P, P]
         L.mgh_group_norm.argtypes = [P, P, I, I, I, I, I, ctypes.c_float, P, P, P]
         L.mgh_upscale.argtypes = [P, P, I, I, I, I, I, P]
         L.mgh_graph_begin.argtypes = [P]
@@ -405,6 +410,19 @@ class Context:
     def conv2d_pack_weights(self, ker, KW, KH, IC, OC, packed):
         P = self._ptr
         self._check(lib().mgh_conv2d_pack_weights(self.h, P(ker), KW, KH, IC, OC, P(packed)))
+
+    @staticmethod
+    def conv2d_i8_weight_bytes(KW, KH, IC, OC) -> int:
+        return lib().mgh_conv2d_i8_weight_bytes(KW, KH, IC, OC)
+
+    def conv2d_i8_pack_weights(self, ker, KW, KH, IC, OC, wq):
+        P = self._ptr
+        self._check(lib().mgh_conv2d_i8_pack_weights(self.h, P(ker), KW, KH, IC, OC, P(wq)))
+
+    def conv2d_i8(self, x, IW, IH, IC, N, wq, KW, KH, OC, stride, pad, bias, resid, y):
+        P = self._ptr
+        self._check(lib().mgh_conv2d_i8(self.h, P(x), IW, IH, IC, N, P(wq), KW, KH, OC, stride, pad, P(bias),
+                                        P(resid), P(y)))
 
     def group_norm(self, x, W, H, C, N, groups, eps, gamma, beta, y):
         P = self._ptr

@@ -354,6 +354,121 @@ __global__ __launch_bounds__(256) void k_conv2d_few(ConvArgs a) {
     }
 }
 
+// ---- int8 conv: the reference's k_quantize_conv_w + k_conv2d_i8 (mg-opencl.cpp:598-664) ----
+// Weights per (oc, 32-block of k = (ic*KH + kh)*KW + kw): d = amax/127, id = d > 0 ? 1/d : 0,
+// code = round(w*id) half away from zero, stored as fp16 [OC][Kp] (Kp = 32 * blocks, zero past
+// K) with d in fp32 [OC][blocks]. One thread per (channel, block); runs once per weight.
+__global__ __launch_bounds__(256) void k_conv_quant_w(const float* __restrict__ ker, _Float16* __restrict__ qw,
+                                                      float* __restrict__ dw, int K, int OC, int nb) {
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (gid >= (int64_t)OC * nb) return;
+    const int oc = (int)(gid / nb), b = (int)(gid - (int64_t)oc * nb);
+    const int k0 = 32 * b, n = min(32, K - k0);
+    const float* w = ker + (size_t)oc * K + k0;
+    float amax = 0.f;
+    for (int i = 0; i < n; i++) amax = fmaxf(amax, fabsf(w[i]));
+    const float d = amax / 127.0f, id = d > 0.0f ? 1.0f / d : 0.0f;
+    dw[gid] = d;
+    _Float16* q = qw + (size_t)oc * nb * 32 + k0;
+    for (int i = 0; i < 32; i++) q[i] = i < n ? (_Float16)roundf(w[i] * id) : (_Float16)0.f;
+}
+
+// 64 output pixels x 64 output channels per workgroup, 2 x 2 waves of 32 x 32. Per 32-block of
+// k (the reference's order): four lanes gather one pixel's 32 im2col values (8 each, zero
+// outside the image and past K) and quantize them like k_quantize_q8 (block max by two xor
+// shuffles); codes go to LDS as fp16 (exact), with the weights' fp16 codes. One
+// v_mfma_f32_16x16x32_f16 per block and subtile gives the exact integer dot (every partial sum
+// is an integer below 2^24); then acc = acc + (dx*dw)*idot with each operation rounded to fp32,
+// blocks in order — the reference's `acc += dcm*dwl*(float)idot` as written.
+template <int KSZ>
+__global__ __launch_bounds__(256) void k_conv2d_i8(ConvI8Args a) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) _Float16 As[64][40];   // [pixel][k], rows padded to 80 B
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[64][40];   // [channel][k]
+    __shared__ __attribute__((aligned(16))) float dxs[64];
+    __shared__ __attribute__((aligned(16))) float dws[64];
+    const int KW = KSZ ? KSZ : a.KW, KH = KSZ ? KSZ : a.KH;
+    const int M = a.OW * a.OH, K = a.IC * KW * KH, OC = a.OC;
+    const int nb = (K + 31) / 32, Kp = 32 * nb;
+    const int n = blockIdx.z, m0 = blockIdx.x * 64, n0 = blockIdx.y * 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, l16 = lane & 15, lg = lane >> 4;
+
+    // gather role: pixel pl, k = 32b + 8c .. +7; weight role: channel row bo, same k chunk
+    const int pl = tid >> 2, c = tid & 3;
+    const int p = m0 + pl;
+    const bool pv = p < M;
+    const int ow = pv ? p % a.OW : 0, oh = pv ? p / a.OW : 0;
+    const int iw0 = ow * a.stride - a.pad, ih0 = oh * a.stride - a.pad;
+    const size_t plane = (size_t)a.IW * a.IH;
+    const float* inb = a.in + (size_t)n * a.IC * plane;
+    const bool bv = n0 + pl < OC;
+    const _Float16* wrow = a.qw + (size_t)(bv ? n0 + pl : 0) * Kp + 8 * c;
+
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < nb; b++) {
+        float v[8];
+        float amax = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int k = 32 * b + 8 * c + j;
+            float x = 0.f;
+            if (pv && k < K) {
+                const int kw = k % KW, t = k / KW, kh = t % KH, ic = t / KH;
+                const int ih = ih0 + kh, iw = iw0 + kw;
+                if (ih >= 0 && ih < a.IH && iw >= 0 && iw < a.IW) x = inb[(size_t)ic * plane + (size_t)ih * a.IW + iw];
+            }
+            v[j] = x;
+            amax = fmaxf(amax, fabsf(x));
+        }
+        amax = fmaxf(amax, __shfl_xor(amax, 1));
+        amax = fmaxf(amax, __shfl_xor(amax, 2));
+        const float d = amax / 127.0f, id = d > 0.0f ? 1.0f / d : 0.0f;
+        f16x8 q;
+#pragma unroll
+        for (int j = 0; j < 8; j++) q[j] = (_Float16)roundf(v[j] * id);
+        *(f16x8*)&As[pl][8 * c] = q;
+        if (c == 0) dxs[pl] = d;
+        *(f16x8*)&Bs[pl][8 * c] = bv ? *(const f16x8*)(wrow + 32 * b) : f16x8{};
+        if (tid < 64) dws[tid] = n0 + tid < OC ? a.dw[(size_t)(n0 + tid) * nb + b] : 0.f;
+        __syncthreads();
+        f16x8 af[2], bf[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) af[i] = *(const f16x8*)&As[32 * wm + 16 * i + l16][8 * lg];
+#pragma unroll
+        for (int j = 0; j < 2; j++) bf[j] = *(const f16x8*)&Bs[32 * wn + 16 * j + l16][8 * lg];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const f32x4 dx = *(const f32x4*)&dxs[32 * wm + 16 * i + 4 * lg];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const f32x4 F = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                const float dwv = dws[32 * wn + 16 * j + l16];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float sc = dx[r] * dwv;
+                    acc[i][j][r] = acc[i][j][r] + sc * F[r];
+                }
+            }
+        }
+        __syncthreads();
+    }
+    // register r of tile (i, j): pixel m0 + 32wm + 16i + 4lg + r, channel n0 + 32wn + 16j + l16
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int oc = n0 + 32 * wn + 16 * j + l16;
+        if (oc >= OC) continue;
+        const size_t row = ((size_t)n * OC + oc) * M;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            conv_store(a.out, a.bias, a.resid, row, oc, m0 + 32 * wm + 16 * i + 4 * lg, M, acc[i][j]);
+    }
+}
+
 // KSZ > 0: KW = KH = KSZ known at compile time (the index arithmetic then divides by a
 // constant); 0: any kernel size
 template <int KSZ>
@@ -606,6 +721,28 @@ hipError_t launch_conv2d_f32(const ConvArgs& a, hipStream_t s) {
 }
 
 bool conv_pk_narrow(int OC) { return OC <= NBN; }
+
+size_t conv_i8_codes_bytes(int K, int OC) { return (((size_t)OC * ((K + 31) / 32) * 32 * 2) + 255) & ~(size_t)255; }
+
+hipError_t launch_conv_quant_w(const float* ker, void* wq, int K, int OC, hipStream_t s) {
+    const int nb = (K + 31) / 32;
+    const int64_t total = (int64_t)OC * nb;
+    if (total == 0) return hipSuccess;
+    _Float16* qw = (_Float16*)wq;
+    float* dw = (float*)((char*)wq + conv_i8_codes_bytes(K, OC));
+    hipLaunchKernelGGL(k_conv_quant_w, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, ker, qw, dw, K, OC, nb);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv2d_i8(const ConvI8Args& a, hipStream_t s) {
+    const int M = a.OW * a.OH;
+    if (M == 0 || a.OC == 0 || a.N == 0) return hipSuccess;
+    const dim3 grid((unsigned)((M + 63) / 64), (unsigned)((a.OC + 63) / 64), (unsigned)a.N), block(256);
+    if (a.KW == 3 && a.KH == 3) hipLaunchKernelGGL(k_conv2d_i8<3>, grid, block, 0, s, a);
+    else if (a.KW == 1 && a.KH == 1) hipLaunchKernelGGL(k_conv2d_i8<1>, grid, block, 0, s, a);
+    else hipLaunchKernelGGL(k_conv2d_i8<0>, grid, block, 0, s, a);
+    return hipGetLastError();
+}
 
 ConvPkPlan conv_pk_plan(int M, int OC, int K) {
     // about two workgroups per CU for one image: split K when its output tiles alone give

@@ -764,6 +764,41 @@ int mgh_conv2d_pack_weights(mgh_ctx* c, const float* ker, int KW, int KH, int IC
     return MGH_OK;
 }
 
+size_t mgh_conv2d_i8_weight_bytes(int KW, int KH, int IC, int OC) {
+    if (KW <= 0 || KH <= 0 || IC <= 0 || OC <= 0 || (int64_t)IC * KW * KH > INT32_MAX) return 0;
+    const int K = IC * KW * KH;
+    return mgh::conv_i8_codes_bytes(K, OC) + (size_t)OC * ((K + 31) / 32) * sizeof(float);
+}
+
+int mgh_conv2d_i8_pack_weights(mgh_ctx* c, const float* ker, int KW, int KH, int IC, int OC, void* wq) {
+    if (!c) return MGH_ERR_ARG;
+    if (!mgh_conv2d_i8_weight_bytes(KW, KH, IC, OC))
+        return fail(c, MGH_ERR_ARG, "conv2d_i8_pack_weights: need positive sizes");
+    if (!ker || !wq) return fail(c, MGH_ERR_ARG, "conv2d_i8_pack_weights: null pointer");
+    if (!aligned16(wq)) return fail(c, MGH_ERR_ARG, "conv2d_i8_pack_weights: d_wq must be 16-byte aligned");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_conv_quant_w(ker, wq, IC * KW * KH, OC, c->stream), "k_conv_quant_w");
+    return MGH_OK;
+}
+
+int mgh_conv2d_i8(mgh_ctx* c, const float* in, int IW, int IH, int IC, int N, const void* wq, int KW, int KH,
+                  int OC, int stride, int pad, const float* bias, const float* resid, float* out) {
+    if (!c) return MGH_ERR_ARG;
+    int64_t OW = 0, OH = 0;
+    if (int r = conv_shape(c, IW, IH, IC, N, KW, KH, OC, stride, pad, &OW, &OH)) return r;
+    if (N == 0) return MGH_OK;
+    if (!in || !wq || !out) return fail(c, MGH_ERR_ARG, "conv2d_i8: null pointer");
+    if (!aligned16(out) || !aligned16(wq) || (resid && !aligned16(resid)))
+        return fail(c, MGH_ERR_ARG, "conv2d_i8: d_wq, d_out and d_resid must be 16-byte aligned");
+    if (int r = set_dev(c)) return r;
+    const int K = IC * KW * KH;
+    const _Float16* qw = (const _Float16*)wq;
+    const float* dw = (const float*)((const char*)wq + mgh::conv_i8_codes_bytes(K, OC));
+    mgh::ConvI8Args a{in, qw, dw, out, bias, resid, IW, IH, IC, (int)OW, (int)OH, OC, KW, KH, stride, pad, N};
+    MGH_HIP(c, mgh::launch_conv2d_i8(a, c->stream), "k_conv2d_i8");
+    return MGH_OK;
+}
+
 int mgh_group_norm(mgh_ctx* c, const float* x, int W, int H, int C, int N, int groups, float eps,
                    const float* gamma, const float* beta, float* y) {
     if (!c) return MGH_ERR_ARG;

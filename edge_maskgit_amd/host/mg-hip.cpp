@@ -119,7 +119,8 @@ struct HipRuntime::Impl {
 
     // layout 0: the leaf's bytes as stored; 1: quantized weight in the int8-dot packed layout
     // (mgh_pack_weights); 2: quantized weight dequantized into fp16 (mgh_pack_weights_f16);
-    // 3: F32 conv kernel {KW, KH, IC, OC} in the tap-major layout (mgh_conv2d_pack_weights)
+    // 3: F32 conv kernel {KW, KH, IC, OC} in the tap-major layout (mgh_conv2d_pack_weights);
+    // 4: the same kernel quantized per (channel, 32-block) for the int8 conv (mgh_conv2d_i8_pack_weights)
     void* upload_leaf(const Tensor* t, int layout) {
         const size_t n = t->nbytes();
         const auto key = std::make_tuple((const void*)t->data, n, layout ? 100 * layout + (int)t->type : -1);
@@ -130,10 +131,15 @@ struct HipRuntime::Impl {
         check(mgh_alloc(ctx, n, &raw));
         check(mgh_h2d(ctx, raw, t->data, n));
         void* d = raw;
-        if (layout == 3) {
+        if (layout == 3 || layout == 4) {
             const int KW = (int)t->ne[0], KH = (int)t->ne[1], IC = (int)t->ne[2], OC = (int)t->ne[3];
-            check(mgh_alloc(ctx, mgh_conv2d_packed_bytes(KW, KH, IC, OC), &d));
-            check(mgh_conv2d_pack_weights(ctx, (const float*)raw, KW, KH, IC, OC, (float*)d));
+            if (layout == 3) {
+                check(mgh_alloc(ctx, mgh_conv2d_packed_bytes(KW, KH, IC, OC), &d));
+                check(mgh_conv2d_pack_weights(ctx, (const float*)raw, KW, KH, IC, OC, (float*)d));
+            } else {
+                check(mgh_alloc(ctx, mgh_conv2d_i8_weight_bytes(KW, KH, IC, OC), &d));
+                check(mgh_conv2d_i8_pack_weights(ctx, (const float*)raw, KW, KH, IC, OC, d));
+            }
             check(mgh_free(ctx, raw));
         } else if (layout) {
             const int wt = t->type == Type::Q8_0 ? MGH_WTYPE_Q8_0 : MGH_WTYPE_Q4_K;
@@ -847,9 +853,19 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                 for (int64_t d : dims)
                     if (d > INT32_MAX) throw std::runtime_error("HipRuntime: Conv2D dimension too large");
                 const int KW = (int)k->ne[0], KH = (int)k->ne[1], IC = (int)k->ne[2], OC = (int)k->ne[3];
+                const ConvFuse& f = cfuse.at(t);
+                if (I.algo == MGH_ALGO_INT8 && k->op == Op::None && !std::getenv("MG_NO_ARM_CONV")) {
+                    // the int8 conv, with the int8-dot FC path as in the reference (both follow
+                    // cl_arm_integer_dot_product; MG_NO_ARM_CONV keeps the fp32 conv,
+                    // mg-opencl.cpp:1237-1242, 1541-1553)
+                    I.check(mgh_conv2d_i8(I.ctx, (const float*)I.dev(x), (int)x->ne[0], (int)x->ne[1], IC,
+                                          (int)x->ne[3], I.upload_leaf(k, 4), KW, KH, OC, t->iparam[0],
+                                          t->iparam[1], (const float*)I.dev(f.bias), (const float*)I.dev(f.resid),
+                                          (float*)out));
+                    break;
+                }
                 // tap-major weights packed once per leaf where the packed kernel runs
                 const bool pk = k->op == Op::None && mgh_conv2d_packed_bytes(KW, KH, IC, OC) > 0;
-                const ConvFuse& f = cfuse.at(t);
                 I.check(mgh_conv2d_ex(I.ctx, (const float*)I.dev(x), (int)x->ne[0], (int)x->ne[1], IC, (int)x->ne[3],
                                       pk ? nullptr : (const float*)I.dev(k), pk ? (const float*)I.upload_leaf(k, 3) : nullptr,
                                       KW, KH, OC, t->iparam[0], t->iparam[1], (const float*)I.dev(f.bias),
@@ -896,10 +912,14 @@ const void* HipRuntime::run(Graph& g, bool readback) {
             e.first++;
             e.second += ms;
         }
-        if (dump_named && !t->name.empty() && t->data) {
-            const auto a = I.addr.find(t);
-            if (a != I.addr.end() && a->second && !h16_store.count(t) && !I.pitch.count(t))
-                I.check(mgh_d2h(I.ctx, t->data, a->second, t->nbytes()));
+        if (dump_named) {
+            // a conv whose Add nodes were absorbed leaves the chain's last node in its buffer:
+            // that node is the one read back (the conv's own value never exists on its own)
+            const Tensor* d = t->op == Op::Conv2D && cfuse.count(t) ? cfuse.at(t).out : t;
+            const auto a = I.addr.find(d);
+            if (!d->name.empty() && d->data && a != I.addr.end() && a->second && !h16_store.count(d) &&
+                !I.pitch.count(d))
+                I.check(mgh_d2h(I.ctx, d->data, a->second, d->nbytes()));
         }
         release_after(i, t);
     }

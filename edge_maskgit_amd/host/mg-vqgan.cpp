@@ -36,20 +36,22 @@ struct DecoderBuilder {
 
     Tensor* channel_view(Tensor* v, int64_t C) { return reshape(c, v, {1, 1, C, 1}); }
 
+    // each GroupNorm, conv (+ bias) and res-block output is named after its weights' prefix
+    // (".out" for a block), so MG_DUMP_NAMED can read any of them back
     Tensor* gn_silu(const std::string& p, Tensor* x) {
-        return group_norm_affine_silu(c, x, w(p + ".weight"), w(p + ".bias"), kGroups, kEps);
+        return group_norm_affine_silu(c, x, w(p + ".weight"), w(p + ".bias"), kGroups, kEps)->named(p);
     }
 
     Tensor* conv(const std::string& p, Tensor* x, int pad, bool bias) {
         Tensor* y = conv_2d(c, w(p + ".weight"), x, 1, pad);
-        return bias ? add(c, y, channel_view(w(p + ".bias"), y->ne[2])) : y;
+        return (bias ? add(c, y, channel_view(w(p + ".bias"), y->ne[2])) : y)->named(p);
     }
 
     Tensor* res_block(const std::string& p, Tensor* x, int in_ch, int out_ch) {
         Tensor* h = conv(p + "conv0", gn_silu(p + "norm0", x), 1, false);
         h = conv(p + "conv1", gn_silu(p + "norm1", h), 1, false);
         Tensor* shortcut = in_ch == out_ch ? x : conv(p + "conv_res", h, 0, false);
-        return add(c, h, shortcut);
+        return add(c, h, shortcut)->named(p + "out");
     }
 };
 
@@ -75,7 +77,7 @@ Tensor* build_vqgan_decoder(Context& c, const Model& m, Tensor* ids) {
 
     Tensor* f = get_rows(c, d.w("vqgan.quantizer.codebook.weight"), ids);          // {E, n, B}
     f = reshape(c, f, {(int64_t)hp.vq_embedding_dim, L, L, B});
-    Tensor* x = d.conv("vqgan.decoder.conv_in", cont(c, permute(c, f, 2, 0, 1, 3)), 1, true);
+    Tensor* x = d.conv("vqgan.decoder.conv_in", cont(c, permute(c, f, 2, 0, 1, 3))->named("vqgan.decoder.conv_in.in"), 1, true);
 
     const int last = (int)mult.size() - 1;
     int width = hp.vq_filters * mult[last];
@@ -86,7 +88,7 @@ Tensor* build_vqgan_decoder(Context& c, const Model& m, Tensor* ids) {
             x = d.res_block(block_prefix(group, l) + ".", x, width, out);
             width = out;
         }
-        if (i > 0) x = d.conv(block_prefix(group, R + 1), upscale(c, x, 2), 1, true);
+        if (i > 0) x = d.conv(block_prefix(group, R + 1), upscale(c, x, 2)->named(block_prefix(group, R + 1) + ".in"), 1, true);
     }
     return d.conv("vqgan.decoder.conv_out", d.gn_silu("vqgan.decoder.norm_out", x), 1, true);
 }

@@ -213,6 +213,8 @@ int mgr_decode_images(mgr_model* m, const int32_t* grids, int B, float* images) 
         mg::Graph g;
         g.build_forward(out);
         m->named.clear();
+        for (const mg::Tensor* t : g.nodes)
+            if (!t->name.empty()) m->named.push_back(t);
         m->rt->invalidate(ids);               // new ids at a reused host address
         const void* d = m->rt->compute_device(g);
         mgh_ctx* c = m->rt->context();

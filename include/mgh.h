@@ -247,6 +247,17 @@ int mgh_conv2d_ex(mgh_ctx* ctx, const float* d_in, int IW, int IH, int IC, int N
 /* bytes of the packed copy (0: the shape does not take the packed kernel) */
 size_t mgh_conv2d_packed_bytes(int KW, int KH, int IC, int OC);
 int mgh_conv2d_pack_weights(mgh_ctx* ctx, const float* d_ker, int KW, int KH, int IC, int OC, float* d_packed);
+/* The int8 conv of the reference's integer-dot devices (k_quantize_conv_w + k_conv2d_i8,
+ * mg-opencl.cpp:598-664, 1541-1553): mgh_conv2d_i8_pack_weights quantizes the kernel once per
+ * output channel and 32-block of k = (ic*KH + kh)*KW + kw (d = amax/127, round half away from
+ * zero; buffer of mgh_conv2d_i8_weight_bytes: fp16 codes, then fp32 scales); mgh_conv2d_i8
+ * quantizes every output pixel's im2col column per 32-block the same way, sums the exact
+ * integer block dots as acc = acc + (dx*dw)*idot in block order (fp32, each operation
+ * rounded), then (+ bias[oc]) (+ resid) as mgh_conv2d_ex. */
+size_t mgh_conv2d_i8_weight_bytes(int KW, int KH, int IC, int OC);
+int mgh_conv2d_i8_pack_weights(mgh_ctx* ctx, const float* d_ker, int KW, int KH, int IC, int OC, void* d_wq);
+int mgh_conv2d_i8(mgh_ctx* ctx, const float* d_in, int IW, int IH, int IC, int N, const void* d_wq, int KW,
+                  int KH, int OC, int stride, int pad, const float* d_bias, const float* d_resid, float* d_out);
 int mgh_group_norm(mgh_ctx* ctx, const float* d_x, int W, int H, int C, int N, int groups, float eps,
                    const float* d_gamma, const float* d_beta, float* d_y);
 int mgh_upscale(mgh_ctx* ctx, const float* d_x, int W, int H, int C, int N, int factor, float* d_y);

@@ -33,7 +33,7 @@ int mgr_decode_params(const mgr_model* m, int32_t* n_tokens, int32_t* codebook, 
  * forward then runs without the final readback. */
 int mgr_forward(mgr_model* m, const int32_t* tokens, int S, int B, float* logits);
 
-/* A named node of the last mgr_forward graph (embd_post_norm, blk.<l>.attn_post,
+/* A named node of the last mgr_forward or mgr_decode_images graph (embd_post_norm, blk.<l>.attn_post,
  * blk.<l>.ffn_post, output_norm, output_logits: src/mg-transformer.cpp:47, 91, 98, 106, 109),
  * as the reference's verification tools read them: its values are current only if that
  * forward ran with MG_DUMP_NAMED set in the environment, which makes the runtime read every
@@ -57,7 +57,9 @@ int mgr_generate(mgr_model* m, const int32_t* class_ids, const uint64_t* seeds, 
  * reference's image layout ne = {W, H, 3, 1} per image). The graph is the reference's decoder
  * (mg::build_vqgan_decoder, src/mg-vqgan.cpp:62-110), the computation of its VqganFwd hook
  * (include/mg-generate.hpp:17, tools/main.cpp:137-152), here for B images in one graph.
- * images may be NULL: the decode then runs without the readback. */
+ * images may be NULL: the decode then runs without the readback. Each GroupNorm, conv (+ bias)
+ * and res-block output is named after its weights' prefix (res blocks: "<prefix>.out"; the
+ * inputs of conv_in and of each up-sampling conv: "<prefix>.in") for mgr_named. */
 int mgr_decode_images(mgr_model* m, const int32_t* grids, int B, float* images);
 /* side of the decoded images: sqrt(n_tokens) * 2^(levels - 1); 0 if the model has no VQGAN */
 int mgr_image_side(const mgr_model* m);

@@ -19,6 +19,11 @@ Parity pins (what checks each function; see tests/test_oracle.py):
   gemm_f32            reference CPU executor (libmgref) bit-exact
   layernorm_affine    reference CPU executor bit-exact
   attention           reference CPU executor (f32); f16kv = f32 path on rounded inputs
+  conv_quant_w,       exact-representation closed form (conv2d_i8 equals the reference CPU
+  conv2d_i8           fp32 conv bit for bit when every block quantizes exactly), power-of-two
+                      scale equivariance, an independently structured numpy restatement of the
+                      block grouping, and the int8 error bound against the fp32 conv
+                      (tests/test_oracle_vqgan.py)
   mt64_draws          the C++ standard's known answer (10000th output of seed 5489)
   uniform_draws       generate_canonical closed form over the engine's raw outputs
   decode_step         closed forms on uniform logits (categorical index = ceil(1024 u) - 1,
@@ -80,6 +85,8 @@ def lib():
         L.mgo_attention.argtypes = [P, P, P, P, I64, I64, I64, I64, ctypes.c_float, ctypes.c_int, P]
         L.mgo_get_rows.argtypes = [P, I64, I64, P, I64, P]
         L.mgo_merge_heads.argtypes = [P, I64, I64, I64, I64, P]
+        L.mgo_conv_quant_w.argtypes = [P, I64, I64, P, P]
+        L.mgo_conv2d_i8.argtypes = [P, I64, I64, I64, I64, P, P, I64, I64, I64, ctypes.c_int, ctypes.c_int, P]
         U64 = ctypes.c_uint64
         L.mgo_mt64_draws.argtypes = [U64, I64, P]
         L.mgo_mt64_draws.restype = None
@@ -182,6 +189,32 @@ def block_dots(wtype: int, wq, N: int, K: int, qx) -> np.ndarray:
     M = qx.shape[0]
     out = np.empty((M, N, K // 32), np.int32)
     lib().mgo_block_dots(wtype, _p(np.ascontiguousarray(wq)), N, K, _p(qx), M, _p(out))
+    return out
+
+
+# ---- VQGAN int8 conv (mg-opencl.cpp:598-664) -------------------------------------
+def conv_quant_w(ker):
+    """ker [OC][IC][KH][KW] -> (qw int8 [OC][nb*32], dw fp32 [OC][nb]), 32-blocks of the
+    kernel's own k = (ic*KH + kh)*KW + kw order"""
+    ker = _f32(ker)
+    OC = ker.shape[0]
+    K = ker.size // OC
+    nb = (K + 31) // 32
+    qw = np.empty((OC, nb * 32), np.int8)
+    dw = np.empty((OC, nb), np.float32)
+    lib().mgo_conv_quant_w(_p(ker), OC, K, _p(qw), _p(dw))
+    return qw, dw
+
+
+def conv2d_i8(x, qw, dw, KH, KW, stride=1, pad=0):
+    """x [N][IC][IH][IW] with quantized weights from conv_quant_w -> [N][OC][OH][OW]"""
+    x = _f32(x)
+    N, IC, IH, IW = x.shape
+    OC = qw.shape[0]
+    OH, OW = (IH + 2 * pad - KH) // stride + 1, (IW + 2 * pad - KW) // stride + 1
+    out = np.empty((N, OC, OH, OW), np.float32)
+    lib().mgo_conv2d_i8(_p(x), IW, IH, IC, N, _p(np.ascontiguousarray(qw, np.int8)), _p(_f32(dw)),
+                        KW, KH, OC, stride, pad, _p(out))
     return out
 
 

@@ -467,3 +467,68 @@ void mgo_merge_heads(const float* a, int64_t D, int64_t S, int64_t H, int64_t B,
                 memcpy(o + ((b * S + s) * H + h) * D, a + ((b * H + h) * S + s) * D,
                        (size_t)D * sizeof(float));
 }
+
+/* ------------------------------------------------------------------------------
+ * VQGAN int8 conv — k_quantize_conv_w and k_conv2d_i8, mg-opencl.cpp:598-664.
+ * Weights: per (oc, 32-block b of k), k = (ic*KH + kh)*KW + kw the kernel's own order,
+ *   amax over the block's min(32, K - 32b) values; d = amax/127; id = d>0 ? 1/d : 0;
+ *   q = round(w*id) (half away from zero); codes past K are 0. (The reference writes 32 codes
+ *   per block from oc*K + 32b, so for K % 32 != 0 its last block overruns into the next
+ *   channel's codes; here each channel's row is padded to nb*32 — the two agree for
+ *   K % 32 == 0, every convolution of the decoder.)
+ * Conv: for each image n, output pixel p and block b: the 32 im2col values
+ *   v[i] = in[n][ic][oh*stride - pad + kh][ow*stride - pad + kw] of k = 32b + i (0 outside the
+ *   image or past K) are quantized like k_quantize_q8 (dx, qx); idot = sum qx*qw (int32);
+ *   acc = acc + (dx*dw)*(float)idot, blocks in order, each operation rounded to fp32 (the
+ *   expression `dcm*dwl[nL]*(float)idot` evaluated as written, :651).
+ * ------------------------------------------------------------------------------ */
+void mgo_conv_quant_w(const float* ker, int64_t OC, int64_t K, int8_t* qw, float* dw) {
+    const int64_t nb = (K + 31) / 32;
+    for (int64_t oc = 0; oc < OC; oc++)
+        for (int64_t b = 0; b < nb; b++) {
+            const int64_t k0 = 32 * b, n = K - k0 < 32 ? K - k0 : 32;
+            const float* w = ker + oc * K + k0;
+            float amax = 0.0f;
+            for (int64_t i = 0; i < n; i++) amax = fmaxf(amax, fabsf(w[i]));
+            const float d = amax / 127.0f, id = d > 0.0f ? 1.0f / d : 0.0f;
+            dw[oc * nb + b] = d;
+            for (int64_t i = 0; i < 32; i++) qw[oc * nb * 32 + k0 + i] = i < n ? (int8_t)roundf(w[i] * id) : 0;
+        }
+}
+
+void mgo_conv2d_i8(const float* in, int64_t IW, int64_t IH, int64_t IC, int64_t N, const int8_t* qw,
+                   const float* dw, int64_t KW, int64_t KH, int64_t OC, int stride, int pad, float* out) {
+    const int64_t OW = (IW + 2 * pad - KW) / stride + 1, OH = (IH + 2 * pad - KH) / stride + 1;
+    const int64_t K = IC * KH * KW, nb = (K + 31) / 32, M = OW * OH;
+#pragma omp parallel for schedule(static)
+    for (int64_t np = 0; np < N * M; np++) {
+        const int64_t n = np / M, p = np % M, ow = p % OW, oh = p / OW;
+        float v[32];
+        int8_t qx[32];
+        float* o = out + n * OC * M + p;
+        for (int64_t oc = 0; oc < OC; oc++) o[oc * M] = 0.0f;
+        for (int64_t b = 0; b < nb; b++) {
+            float amax = 0.0f;
+            for (int64_t i = 0; i < 32; i++) {
+                const int64_t k = 32 * b + i;
+                float x = 0.0f;
+                if (k < K) {
+                    const int64_t kw = k % KW, t = k / KW, kh = t % KH, ic = t / KH;
+                    const int64_t ih = oh * stride - pad + kh, iw = ow * stride - pad + kw;
+                    if (ih >= 0 && ih < IH && iw >= 0 && iw < IW) x = in[((n * IC + ic) * IH + ih) * IW + iw];
+                }
+                v[i] = x;
+                amax = fmaxf(amax, fabsf(x));
+            }
+            const float d = amax / 127.0f, id = d > 0.0f ? 1.0f / d : 0.0f;
+            for (int64_t i = 0; i < 32; i++) qx[i] = (int8_t)roundf(v[i] * id);
+            for (int64_t oc = 0; oc < OC; oc++) {
+                const int8_t* w = qw + oc * nb * 32 + 32 * b;
+                int32_t idot = 0;
+                for (int64_t i = 0; i < 32; i++) idot += (int32_t)qx[i] * (int32_t)w[i];
+                const float s = d * dw[oc * nb + b];
+                o[oc * M] = o[oc * M] + s * (float)idot;
+            }
+        }
+    }
+}

@@ -91,6 +91,15 @@ void mgo_get_rows(const float* a, int64_t E, int64_t R, const int32_t* ids, int6
 void mgo_merge_heads(const float* a, int64_t D, int64_t S, int64_t H, int64_t B, float* o);
 
 /* library self-description */
+/* VQGAN int8 conv (mg-opencl.cpp:598-664): k_quantize_conv_w quantizes each output channel's
+ * weights ker[oc][k] (k = (ic*KH + kh)*KW + kw) per 32-block: qw [OC][nb*32] (zero past K),
+ * dw [OC][nb]; k_conv2d_i8 quantizes the gathered im2col column of every output pixel per
+ * 32-block of k (zero outside the image and past K) and sums acc = acc + (dx*dw)*idot over the
+ * blocks in order; out {OW, OH, OC, N}. */
+void mgo_conv_quant_w(const float* ker, int64_t OC, int64_t K, int8_t* qw, float* dw);
+void mgo_conv2d_i8(const float* in, int64_t IW, int64_t IH, int64_t IC, int64_t N, const int8_t* qw,
+                   const float* dw, int64_t KW, int64_t KH, int64_t OC, int stride, int pad, float* out);
+
 int mgo_version(void);
 
 /* ---- iterative decoding (mg_oracle_decode.cpp; src/mg-generate.cpp:82-121) ----

@@ -12,7 +12,8 @@ Arrays are numpy [N][C][H][W] (the reference's ne = {W, H, C, N}); conv kernels
                y = float32(x - mean) * inv; with gamma/beta the fused node's affine + SiLU
                (mg-cpu.cpp:262-276): xn = y * gamma + beta (two roundings), xn / (1 + exp(-xn))
   upscale      k_upscale (mg-cpu.cpp:192-198): nearest neighbour
-  decode       build_vqgan_decoder (src/mg-vqgan.cpp:62-110) composed from the above
+  decode       build_vqgan_decoder (src/mg-vqgan.cpp:62-110) composed from the above (or with
+               the int8 conv of oracle.conv2d_i8, mg-opencl.cpp:598-664)
 
 Parity pins (tests/test_oracle_vqgan.py): each primitive against the reference's own CPU
 executor (oracle/_ref/libmgref.so) and against closed forms (a delta kernel shifts the image,
@@ -66,8 +67,10 @@ def upscale(x, f):
     return np.asarray(x, np.float32).repeat(f, axis=2).repeat(f, axis=3)
 
 
-def decode(t: dict, grid, E: int, filters: int, mult, R: int):
-    """t: float tensors by GGUF name (numpy shapes); grid int [B][n_tokens] -> [B][3][side][side]"""
+def decode(t: dict, grid, E: int, filters: int, mult, R: int, int8: bool = False):
+    """t: float tensors by GGUF name (numpy shapes); grid int [B][n_tokens] -> [B][3][side][side].
+    int8: every conv is the reference's int8 conv (k_conv2d_i8 on k_quantize_conv_w weights,
+    restated by oracle.conv2d_i8), as its runtime runs them on integer-dot devices."""
     grid = np.asarray(grid).reshape(len(grid), -1)
     B, n = grid.shape
     L = int(round(n ** 0.5))
@@ -75,7 +78,13 @@ def decode(t: dict, grid, E: int, filters: int, mult, R: int):
     x = f.reshape(B, L, L, E).transpose(0, 3, 1, 2).astype(np.float32)   # [B][E][h][w]
 
     def conv(p, x, pad, bias):
-        y = conv2d(x, t[p + ".weight"], 1, pad)
+        w = t[p + ".weight"]
+        if int8:
+            from . import conv2d_i8, conv_quant_w
+            qw, dw = conv_quant_w(w)
+            y = conv2d_i8(x, qw, dw, w.shape[2], w.shape[3], 1, pad)
+        else:
+            y = conv2d(x, w, 1, pad)
         return y + t[p + ".bias"][None, :, None, None] if bias else y
 
     def gn_silu(p, x):

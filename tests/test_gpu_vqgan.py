@@ -17,6 +17,7 @@ import numpy as np
 import pytest
 
 import edge_maskgit_amd as ema
+import oracle
 from edge_maskgit_amd import runtime as rt
 from oracle import ref
 from oracle import vqgan as ov
@@ -249,3 +250,146 @@ def test_decode_rejects_bad_grids(tmp_path):
             m.decode_images(np.zeros((1, 15), np.int32))
         with pytest.raises(ema.MghError, match="codebook"):
             m.decode_images(np.full((1, 16), 64, np.int32))
+
+
+# ---- the int8 conv (mgh_conv2d_i8): bit-exact against the oracle's restatement of the
+# reference's k_quantize_conv_w + k_conv2d_i8 ----
+I8 = [  # IW, IH, IC, N, KW, KH, OC, stride, pad
+    (9, 7, 8, 2, 3, 3, 5, 1, 1), (10, 10, 5, 1, 3, 3, 70, 2, 1), (16, 16, 256, 1, 3, 3, 512, 1, 1),
+    (32, 32, 128, 2, 3, 3, 64, 1, 1), (64, 64, 128, 1, 1, 1, 128, 1, 0), (65, 33, 20, 1, 3, 3, 130, 1, 1),
+    (32, 32, 128, 1, 3, 3, 3, 1, 1), (11, 6, 16, 1, 5, 5, 24, 1, 2), (64, 64, 64, 1, 3, 3, 128, 1, 1),
+]
+
+
+@pytest.mark.parametrize("IW,IH,IC,N,KW,KH,OC,stride,pad", I8)
+def test_conv2d_i8_vs_oracle(ctx, IW, IH, IC, N, KW, KH, OC, stride, pad):
+    print(f"conv2d_i8 IW={IW} IH={IH} IC={IC} N={N} K={KW}x{KH} OC={OC} s={stride} p={pad}", flush=True)
+    rng = np.random.default_rng(IW + 3 * IC + OC)
+    x = (rng.standard_normal((N, IC, IH, IW)) * (2.0 ** rng.integers(-3, 4, (1, IC, 1, 1)))).astype(np.float32)
+    ker = (rng.standard_normal((OC, IC, KH, KW)) / np.sqrt(IC * KH * KW)).astype(np.float32)
+    bias = rng.standard_normal(OC).astype(np.float32)
+    OH, OW = (IH + 2 * pad - KH) // stride + 1, (IW + 2 * pad - KW) // stride + 1
+    res = rng.standard_normal((N, OC, OH, OW)).astype(np.float32)
+    K = IC * KH * KW
+    nb = (K + 31) // 32
+    nbytes = ctx.conv2d_i8_weight_bytes(KW, KH, IC, OC)
+    codes_bytes = (OC * nb * 32 * 2 + 255) // 256 * 256
+    assert nbytes == codes_bytes + OC * nb * 4
+    dX, dK, dB, dR, dQ = ctx.upload(x), ctx.upload(ker), ctx.upload(bias), ctx.upload(res), ctx.alloc(nbytes)
+    dY = ctx.alloc(res.nbytes)
+    ctx.conv2d_i8_pack_weights(dK, KW, KH, IC, OC, dQ)
+    raw = ctx.download(dQ, (nbytes,), np.uint8)
+    qw_gpu = raw[:OC * nb * 32 * 2].view(np.float16).reshape(OC, nb * 32)
+    dw_gpu = raw[codes_bytes:].view(np.float32).reshape(OC, nb)
+    qw, dw = oracle.conv_quant_w(ker)
+    assert np.array_equal(qw_gpu.astype(np.int32), qw.astype(np.int32)) and np.array_equal(dw_gpu, dw)
+    ctx.conv2d_i8(dX, IW, IH, IC, N, dQ, KW, KH, OC, stride, pad, None, None, dY)
+    y = ctx.download(dY, res.shape, np.float32)
+    want = oracle.conv2d_i8(x, qw, dw, KH, KW, stride, pad)
+    mism = int((y != want).sum())
+    print(f"  {mism} of {y.size} outputs differ from the oracle")
+    assert mism == 0
+    ctx.conv2d_i8(dX, IW, IH, IC, N, dQ, KW, KH, OC, stride, pad, dB, dR, dY)
+    assert np.array_equal(ctx.download(dY, res.shape, np.float32), (want + bias[None, :, None, None]) + res)
+    for b in (dX, dK, dB, dR, dQ, dY):
+        ctx.free(b)
+
+
+def _check_decoder_nodes(m, t, grid, cfg, int8):
+    """every node of one decode, recomputed from the GPU's own input to it (MG_DUMP_NAMED):
+    conv chains (conv + bias / + residual) bit-exact for the int8 conv, <= 1e-5 * max against
+    the float64 conv for the fp32 one; GroupNorm + SiLU <= 1e-6 * max; gather and up-sampling
+    exact. Returns the number of nodes checked."""
+    E, F, mult, R = cfg["E"], cfg["filters"], cfg["mult"], cfg["R"]
+    L = int(round(cfg["n_tokens"] ** 0.5))
+    n_checked = 0
+
+    def get(name, C, side):
+        return m.named(name).reshape(1, C, side, side)
+
+    def conv_ref(p, x, pad, bias=False, resid=None):
+        w = t[p + ".weight"]
+        if int8:
+            qw, dw = oracle.conv_quant_w(w)
+            y = oracle.conv2d_i8(x, qw, dw, w.shape[2], w.shape[3], 1, pad)
+        else:
+            y = ov.conv2d(x, w, 1, pad)
+        if bias:
+            y = y + t[p + ".bias"][None, :, None, None]
+        return y if resid is None else y + resid
+
+    def same(name, got, want, exact):
+        nonlocal n_checked
+        n_checked += 1
+        if exact:
+            assert np.array_equal(got, want), f"{name}: {int((got != want).sum())} values differ"
+        else:
+            err = np.abs(got - want).max() / max(np.abs(want).max(), 1e-30)
+            assert err <= (1e-5 if "norm" not in name else 1e-6), f"{name}: rel err {err:.2e}"
+
+    x_in = get("vqgan.decoder.conv_in.in", E, L)
+    same("conv_in.in", x_in, t["vqgan.quantizer.codebook.weight"][grid].reshape(1, L, L, E).transpose(0, 3, 1, 2), True)
+    width, side = F * mult[-1], L
+    x = get("vqgan.decoder.conv_in", width, side)
+    same("conv_in", x, conv_ref("vqgan.decoder.conv_in", x_in, 1, bias=True), int8)
+
+    def block(p, x, cin, cout):
+        n0 = get(p + "norm0", cin, side)
+        same(p + "norm0", n0, ov.group_norm(x, 32, 1e-5, t[p + "norm0.weight"], t[p + "norm0.bias"]), False)
+        c0 = get(p + "conv0", cout, side)
+        same(p + "conv0", c0, conv_ref(p + "conv0", n0, 1), int8)
+        n1 = get(p + "norm1", cout, side)
+        same(p + "norm1", n1, ov.group_norm(c0, 32, 1e-5, t[p + "norm1.weight"], t[p + "norm1.bias"]), False)
+        out = get(p + "out", cout, side)
+        if cin == cout:           # conv1 + x: the residual Add runs in conv1's epilogue
+            same(p + "out", out, conv_ref(p + "conv1", n1, 1, resid=x), int8)
+        else:                     # h + conv_res(h), the upstream shortcut quirk
+            h = get(p + "conv1", cout, side)
+            same(p + "conv1", h, conv_ref(p + "conv1", n1, 1), int8)
+            same(p + "out", out, conv_ref(p + "conv_res", h, 0, resid=h), int8)
+        return out
+
+    for l in range(R):
+        x = block(f"vqgan.decoder.res_blocks.0.{l}.", x, width, width)
+    for i in range(len(mult) - 1, -1, -1):
+        j, o = len(mult) - i, F * mult[i]
+        for l in range(R):
+            x = block(f"vqgan.decoder.res_blocks.{j}.{l}.", x, width, o)
+            width = o
+        if i > 0:
+            pu = f"vqgan.decoder.res_blocks.{j}.{R + 1}"
+            side *= 2
+            up = get(pu + ".in", width, side)
+            same(pu + ".in", up, ov.upscale(x, 2), True)
+            x = get(pu, width, side)
+            same(pu, x, conv_ref(pu, up, 1, bias=True), int8)
+    n = get("vqgan.decoder.norm_out", width, side)
+    same("norm_out", n, ov.group_norm(x, 32, 1e-5, t["vqgan.decoder.norm_out.weight"], t["vqgan.decoder.norm_out.bias"]), False)
+    img = get("vqgan.decoder.conv_out", 3, side)
+    same("conv_out", img, conv_ref("vqgan.decoder.conv_out", n, 1, bias=True), int8)
+    return n_checked, img
+
+
+@pytest.mark.parametrize("algo", [1, 2], ids=["int8-conv", "fp32-conv"])
+def test_decode_graph_per_node(tmp_path, monkeypatch, algo):
+    """the decoder graph node by node from the GPU's own inputs (a fixed bar at every depth: an
+    int8 conv requantizes its input, so a last-ulp difference in a GroupNorm output can move a
+    code of the next conv, and end to end only compounded noise could be bounded); the
+    runtime's int8 algorithm runs every conv as the reference's int8 conv, as its runtime does
+    on integer-dot devices, and MG_NO_ARM_CONV=1 keeps the fp32 conv there"""
+    cfg = SMALL[1]
+    path = str(tmp_path / "vq.gguf")
+    mg_gguf.write_vqgan_model(path, seed=9, **cfg)
+    t = mg_gguf.vqgan_tensors(np.random.default_rng(9), cfg["E"], cfg["codebook"], cfg["filters"], cfg["mult"], cfg["R"])
+    grid = np.random.default_rng(10).integers(0, cfg["codebook"], cfg["n_tokens"]).astype(np.int32)
+    monkeypatch.setenv("MG_DUMP_NAMED", "1")
+    with rt.TransformerRuntime(path, algo=algo) as m:
+        img = m.decode_images(grid[None])[0]
+        n, last = _check_decoder_nodes(m, t, grid, cfg, int8=algo == 1)
+    print(f"algo {algo}: {n} nodes checked")
+    assert n >= 20 and np.array_equal(img, last[0])
+    if algo == 1:
+        monkeypatch.setenv("MG_NO_ARM_CONV", "1")
+        with rt.TransformerRuntime(path, algo=1) as m:
+            m.decode_images(grid[None])
+            _check_decoder_nodes(m, t, grid, cfg, int8=False)

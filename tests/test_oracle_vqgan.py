@@ -9,7 +9,11 @@ the reference builder's (host only, no GPU).
     in another order), the fused node within 1e-6 * max, upscale exact, and the whole decoder on
     small synthetic models;
   * build_vqgan_decoder (include/mg-vqgan.hpp) emits the reference builder's graph node for node
-    (op, shape, strides, parameters, sources), on small models and at the production size.
+    (op, shape, strides, parameters, sources), on small models and at the production size;
+  * the int8 conv oracle (oracle.conv_quant_w / conv2d_i8): where every block quantizes exactly it
+    equals the reference CPU fp32 conv bit for bit; a vectorized restatement of the 32-block
+    grouping gives the same bits; power-of-two input scaling is exact; and it stays within the
+    quantization error of the fp32 conv.
 """
 import ctypes
 import os
@@ -17,6 +21,7 @@ import os
 import numpy as np
 import pytest
 
+import oracle
 from oracle import ref
 from oracle import vqgan as ov
 from tests import mg_gguf
@@ -148,3 +153,86 @@ def test_decoder_rejects_non_square_grid(tmp_path):
     mg_gguf.write_vqgan_model(path, seed=0, **SMALL[0])
     with pytest.raises(RuntimeError, match="square"):
         _our_sig(path, 15)
+
+
+# ---- the int8 conv of the reference's integer-dot devices (mg-opencl.cpp:598-664) ----
+
+def _exact_i8_case(rng, N, IC, IH, IW, OC, k):
+    """inputs +-127/128 and weights q * 2^-7 with a +-127 in every (channel, 32-block): every
+    block of both operands quantizes exactly (d = 1/128 resp. 2^-7), and every partial sum is a
+    multiple of 2^-14 below 2^10, so the int8 conv must equal the fp32 conv bit for bit"""
+    x = (rng.choice([-1.0, 1.0], (N, IC, IH, IW)) * (127 / 128)).astype(np.float32)
+    K = IC * k * k
+    q = rng.integers(-127, 128, (OC, K))
+    for b in range(0, K, 32):
+        q[:, b] = rng.choice([-127, 127], OC)
+    return x, (q * 2.0 ** -7).astype(np.float32).reshape(OC, IC, k, k), q
+
+
+@pytest.mark.parametrize("N,IC,IH,IW,OC,k,stride,pad", [(2, 8, 7, 9, 5, 3, 1, 1), (1, 32, 6, 6, 4, 3, 2, 1),
+                                                      (1, 64, 5, 4, 3, 1, 1, 0), (1, 5, 6, 5, 2, 3, 1, 2)])
+def test_conv_i8_exact_quantization_closed_form(N, IC, IH, IW, OC, k, stride, pad):
+    rng = np.random.default_rng(IC * 7 + OC)
+    x, ker, q = _exact_i8_case(rng, N, IC, IH, IW, OC, k)
+    qw, dw = oracle.conv_quant_w(ker)
+    K = IC * k * k
+    assert np.array_equal(qw[:, :K], q) and not qw[:, K:].any() and np.all(dw == np.float32(2.0 ** -7))
+    got = oracle.conv2d_i8(x, qw, dw, k, k, stride, pad)
+    assert np.array_equal(got, ov.conv2d(x, ker, stride, pad))
+    if ref.available():
+        assert np.array_equal(got, ref.conv2d(x, ker, stride, pad))
+
+
+def _round_away(v):
+    v = v.astype(np.float64)
+    return np.sign(v) * np.floor(np.abs(v) + 0.5)
+
+
+def _i8_numpy(x, ker, stride, pad):
+    """the int8 conv vectorized: im2col in the kernel's k order, [pixel][block][32] groups"""
+    N, IC, IH, IW = x.shape
+    OC, _, KH, KW = ker.shape
+    OH, OW = (IH + 2 * pad - KH) // stride + 1, (IW + 2 * pad - KW) // stride + 1
+    K = IC * KH * KW
+    nb = (K + 31) // 32
+    xp = np.zeros((N, IC, IH + 2 * pad, IW + 2 * pad), np.float32)
+    xp[:, :, pad:pad + IH, pad:pad + IW] = x
+    cols = np.zeros((N, OH * OW, nb * 32), np.float32)
+    for ic in range(IC):
+        for kh in range(KH):
+            for kw in range(KW):
+                patch = xp[:, ic, kh:kh + stride * (OH - 1) + 1:stride, kw:kw + stride * (OW - 1) + 1:stride]
+                cols[:, :, (ic * KH + kh) * KW + kw] = patch.reshape(N, -1)
+    w = np.zeros((OC, nb * 32), np.float32)
+    w[:, :K] = ker.reshape(OC, K)
+
+    def quant(a):
+        blk = a.reshape(a.shape[:-1] + (nb, 32))
+        d = np.abs(blk).max(-1) / np.float32(127)
+        inv = np.where(d > 0, np.float32(1) / np.where(d > 0, d, 1), 0).astype(np.float32)
+        return _round_away(blk * inv[..., None]).astype(np.int64), d.astype(np.float32)
+
+    qx, dx = quant(cols)
+    qw, dw = quant(w)
+    idot = np.einsum("nmbi,obi->nmob", qx, qw).astype(np.float32)
+    acc = np.zeros((N, OH * OW, OC), np.float32)
+    for b in range(nb):
+        acc = acc + (dx[:, :, None, b] * dw[None, None, :, b]) * idot[..., b]
+    return acc.transpose(0, 2, 1).reshape(N, OC, OH, OW)
+
+
+@pytest.mark.parametrize("N,IC,IH,IW,OC,k,stride,pad", [(2, 8, 7, 9, 5, 3, 1, 1), (1, 20, 6, 5, 7, 3, 2, 1),
+                                                      (1, 48, 4, 4, 9, 1, 1, 0)])
+def test_conv_i8_block_grouping_and_scaling(N, IC, IH, IW, OC, k, stride, pad):
+    """wide per-channel magnitude differences make the 32-block grouping matter: the loop oracle
+    equals the vectorized restatement bit for bit; inputs scaled by 4 give outputs scaled by 4
+    exactly; the int8 result stays within the quantization error of the fp32 conv"""
+    rng = np.random.default_rng(IC + OC + k)
+    x = (rng.standard_normal((N, IC, IH, IW)) * (2.0 ** rng.integers(-4, 5, (1, IC, 1, 1)))).astype(np.float32)
+    ker = (rng.standard_normal((OC, IC, k, k)) * (2.0 ** rng.integers(-3, 4, (OC, IC, 1, 1)))).astype(np.float32)
+    qw, dw = oracle.conv_quant_w(ker)
+    got = oracle.conv2d_i8(x, qw, dw, k, k, stride, pad)
+    assert np.array_equal(got, _i8_numpy(x, ker, stride, pad))
+    assert np.array_equal(oracle.conv2d_i8(4 * x, qw, dw, k, k, stride, pad), 4 * got)
+    f32 = ov.conv2d(x, ker, stride, pad)
+    assert np.abs(got - f32).max() <= 3e-2 * np.abs(f32).max()
