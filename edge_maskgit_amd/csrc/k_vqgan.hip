@@ -373,99 +373,109 @@ __global__ __launch_bounds__(256) void k_conv_quant_w(const float* __restrict__ 
     for (int i = 0; i < 32; i++) q[i] = i < n ? (_Float16)roundf(w[i] * id) : (_Float16)0.f;
 }
 
-// 64 output pixels x 64 output channels per workgroup, 2 x 2 waves of 32 x 32. Per 32-block of
-// k (the reference's order): four lanes gather one pixel's 32 im2col values (8 each, zero
-// outside the image and past K) and quantize them like k_quantize_q8 (block max by two xor
-// shuffles); codes go to LDS as fp16 (exact), with the weights' fp16 codes. One
-// v_mfma_f32_16x16x32_f16 per block and subtile gives the exact integer dot (every partial sum
-// is an integer below 2^24); then acc = acc + (dx*dw)*idot with each operation rounded to fp32,
-// blocks in order — the reference's `acc += dcm*dwl*(float)idot` as written.
-template <int KSZ>
-__global__ __launch_bounds__(256) void k_conv2d_i8(ConvI8Args a) {
+// One wave per workgroup, 16 output pixels x 16*NJ output channels, no LDS and no barriers.
+// Lane (l16, lg) gathers the 8 im2col values k = 32b + 8lg .. +7 of pixel l16 (the reference's
+// k order; zero outside the image and past K) — exactly its A fragment of
+// v_mfma_f32_16x16x32_f16 — and the block max of a pixel is two xor shuffles over its four
+// lanes; the codes are rounded like k_quantize_q8 and held as fp16 (exact). The lane loads its
+// B fragments (the weights' fp16 codes of channel l16 of each 16-channel subtile, same k) and
+// their block scales straight from memory. One MFMA per block and subtile is the exact integer
+// dot (every partial sum an integer below 2^24); acc = acc + (dx*dw)*idot, each operation
+// rounded to fp32, blocks in order — the reference's `acc += dcm*dwl*(float)idot` as written.
+// The next block's loads are issued before the current block's arithmetic.
+template <int KSZ, int NJ>
+__global__ __launch_bounds__(64) void k_conv2d_i8(ConvI8Args a) {
 #pragma clang fp contract(off)
-    __shared__ __attribute__((aligned(16))) _Float16 As[64][40];   // [pixel][k], rows padded to 80 B
-    __shared__ __attribute__((aligned(16))) _Float16 Bs[64][40];   // [channel][k]
-    __shared__ __attribute__((aligned(16))) float dxs[64];
-    __shared__ __attribute__((aligned(16))) float dws[64];
     const int KW = KSZ ? KSZ : a.KW, KH = KSZ ? KSZ : a.KH;
     const int M = a.OW * a.OH, K = a.IC * KW * KH, OC = a.OC;
     const int nb = (K + 31) / 32, Kp = 32 * nb;
-    const int n = blockIdx.z, m0 = blockIdx.x * 64, n0 = blockIdx.y * 64;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1, l16 = lane & 15, lg = lane >> 4;
-
-    // gather role: pixel pl, k = 32b + 8c .. +7; weight role: channel row bo, same k chunk
-    const int pl = tid >> 2, c = tid & 3;
-    const int p = m0 + pl;
+    const int n = blockIdx.z, m0 = blockIdx.x * 16, oc0 = blockIdx.y * 16 * NJ;
+    const int lane = threadIdx.x, l16 = lane & 15, lg = lane >> 4;
+    const int p = m0 + l16;
     const bool pv = p < M;
     const int ow = pv ? p % a.OW : 0, oh = pv ? p / a.OW : 0;
     const int iw0 = ow * a.stride - a.pad, ih0 = oh * a.stride - a.pad;
     const size_t plane = (size_t)a.IW * a.IH;
     const float* inb = a.in + (size_t)n * a.IC * plane;
-    const bool bv = n0 + pl < OC;
-    const _Float16* wrow = a.qw + (size_t)(bv ? n0 + pl : 0) * Kp + 8 * c;
+    const _Float16* wrow[NJ];
+    const float* drow[NJ];
+    bool cv[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int oc = oc0 + 16 * j + l16;
+        cv[j] = oc < OC;
+        wrow[j] = a.qw + (size_t)(cv[j] ? oc : 0) * Kp + 8 * lg;
+        drow[j] = a.dw + (size_t)(cv[j] ? oc : 0) * nb;
+    }
 
-    f32x4 acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int b = 0; b < nb; b++) {
-        float v[8];
-        float amax = 0.f;
+    float v[8];
+    f16x8 wq[NJ];
+    float dwv[NJ];
+    auto load = [&](int b, float (&vv)[8], f16x8 (&ww)[NJ], float (&dd)[NJ]) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const int k = 32 * b + 8 * c + j;
+            const int k = 32 * b + 8 * lg + j;
             float x = 0.f;
             if (pv && k < K) {
                 const int kw = k % KW, t = k / KW, kh = t % KH, ic = t / KH;
                 const int ih = ih0 + kh, iw = iw0 + kw;
                 if (ih >= 0 && ih < a.IH && iw >= 0 && iw < a.IW) x = inb[(size_t)ic * plane + (size_t)ih * a.IW + iw];
             }
-            v[j] = x;
-            amax = fmaxf(amax, fabsf(x));
+            vv[j] = x;
         }
-        amax = fmaxf(amax, __shfl_xor(amax, 1));
-        amax = fmaxf(amax, __shfl_xor(amax, 2));
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            ww[j] = cv[j] ? *(const f16x8*)(wrow[j] + 32 * b) : f16x8{};
+            dd[j] = cv[j] ? drow[j][b] : 0.f;
+        }
+    };
+
+    f32x4 acc[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    load(0, v, wq, dwv);
+    for (int b = 0; b < nb; b++) {
+        float nv[8];
+        f16x8 nwq[NJ];
+        float ndw[NJ];
+        if (b + 1 < nb) load(b + 1, nv, nwq, ndw);
+        float amax = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(v[j]));
+        amax = fmaxf(amax, __shfl_xor(amax, 16));
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
         const float d = amax / 127.0f, id = d > 0.0f ? 1.0f / d : 0.0f;
         f16x8 q;
 #pragma unroll
         for (int j = 0; j < 8; j++) q[j] = (_Float16)roundf(v[j] * id);
-        *(f16x8*)&As[pl][8 * c] = q;
-        if (c == 0) dxs[pl] = d;
-        *(f16x8*)&Bs[pl][8 * c] = bv ? *(const f16x8*)(wrow + 32 * b) : f16x8{};
-        if (tid < 64) dws[tid] = n0 + tid < OC ? a.dw[(size_t)(n0 + tid) * nb + b] : 0.f;
-        __syncthreads();
-        f16x8 af[2], bf[2];
+        float dx[4];                                  // scales of this lane's output rows 4lg + r
 #pragma unroll
-        for (int i = 0; i < 2; i++) af[i] = *(const f16x8*)&As[32 * wm + 16 * i + l16][8 * lg];
+        for (int r = 0; r < 4; r++) dx[r] = __shfl(d, 4 * lg + r);
 #pragma unroll
-        for (int j = 0; j < 2; j++) bf[j] = *(const f16x8*)&Bs[32 * wn + 16 * j + l16][8 * lg];
+        for (int j = 0; j < NJ; j++) {
+            const f32x4 F = __builtin_amdgcn_mfma_f32_16x16x32_f16(q, wq[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const f32x4 dx = *(const f32x4*)&dxs[32 * wm + 16 * i + 4 * lg];
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const f32x4 F = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                const float dwv = dws[32 * wn + 16 * j + l16];
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float sc = dx[r] * dwv;
-                    acc[i][j][r] = acc[i][j][r] + sc * F[r];
-                }
+            for (int r = 0; r < 4; r++) {
+                const float sc = dx[r] * dwv[j];
+                acc[j][r] = acc[j][r] + sc * F[r];
             }
         }
-        __syncthreads();
+        if (b + 1 < nb) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = nv[j];
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                wq[j] = nwq[j];
+                dwv[j] = ndw[j];
+            }
+        }
     }
-    // register r of tile (i, j): pixel m0 + 32wm + 16i + 4lg + r, channel n0 + 32wn + 16j + l16
+    // register r of subtile j: pixel m0 + 4lg + r, channel oc0 + 16j + l16
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int oc = n0 + 32 * wn + 16 * j + l16;
-        if (oc >= OC) continue;
-        const size_t row = ((size_t)n * OC + oc) * M;
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-            conv_store(a.out, a.bias, a.resid, row, oc, m0 + 32 * wm + 16 * i + 4 * lg, M, acc[i][j]);
+    for (int j = 0; j < NJ; j++) {
+        if (!cv[j]) continue;
+        const int oc = oc0 + 16 * j + l16;
+        conv_store(a.out, a.bias, a.resid, ((size_t)n * OC + oc) * M, oc, m0 + 4 * lg, M, acc[j]);
     }
 }
 
@@ -737,10 +747,21 @@ hipError_t launch_conv_quant_w(const float* ker, void* wq, int K, int OC, hipStr
 hipError_t launch_conv2d_i8(const ConvI8Args& a, hipStream_t s) {
     const int M = a.OW * a.OH;
     if (M == 0 || a.OC == 0 || a.N == 0) return hipSuccess;
-    const dim3 grid((unsigned)((M + 63) / 64), (unsigned)((a.OC + 63) / 64), (unsigned)a.N), block(256);
-    if (a.KW == 3 && a.KH == 3) hipLaunchKernelGGL(k_conv2d_i8<3>, grid, block, 0, s, a);
-    else if (a.KW == 1 && a.KH == 1) hipLaunchKernelGGL(k_conv2d_i8<1>, grid, block, 0, s, a);
-    else hipLaunchKernelGGL(k_conv2d_i8<0>, grid, block, 0, s, a);
+    // channels per wave: 64 while that leaves >= 2048 waves, else 32 while >= 512, else 16
+    const int64_t pt = ((int64_t)M + 15) / 16 * a.N;
+    const int nj = pt * ((a.OC + 63) / 64) >= 2048 ? 4 : pt * ((a.OC + 31) / 32) >= 512 ? 2 : 1;
+    const dim3 grid((unsigned)((M + 15) / 16), (unsigned)((a.OC + 16 * nj - 1) / (16 * nj)), (unsigned)a.N), block(64);
+    const int ks = a.KW == 3 && a.KH == 3 ? 3 : a.KW == 1 && a.KH == 1 ? 1 : 0;
+#define I8_LAUNCH(KS)                                                                           \
+    do {                                                                                        \
+        if (nj == 4) hipLaunchKernelGGL((k_conv2d_i8<KS, 4>), grid, block, 0, s, a);           \
+        else if (nj == 2) hipLaunchKernelGGL((k_conv2d_i8<KS, 2>), grid, block, 0, s, a);      \
+        else hipLaunchKernelGGL((k_conv2d_i8<KS, 1>), grid, block, 0, s, a);                   \
+    } while (0)
+    if (ks == 3) I8_LAUNCH(3);
+    else if (ks == 1) I8_LAUNCH(1);
+    else I8_LAUNCH(0);
+#undef I8_LAUNCH
     return hipGetLastError();
 }
 
