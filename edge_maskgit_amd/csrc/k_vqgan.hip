@@ -766,15 +766,19 @@ hipError_t launch_conv2d_i8(const ConvI8Args& a, hipStream_t s) {
 }
 
 ConvPkPlan conv_pk_plan(int M, int OC, int K) {
-    // about two workgroups per CU for one image: split K when its output tiles alone give
-    // fewer than 384 workgroups, keeping at least two 16-wide slabs per split. The plan does
-    // not depend on the batch, so an image's sums are the same whatever it is batched with.
+    // Split K when one image's output tiles give fewer than 384 workgroups: up to about 512
+    // workgroups, each split keeping >= 9 16-wide slabs. Measured on the decoder's convs at
+    // one image (split targets 128..1024 workgroups): shorter splits lose to their partial
+    // planes (16 x 16 x 512 -> 512: 31.5 us at 9 slabs per split, 39.1 at 5; the 8-slab 1x1
+    // conv at 128 x 128: 16.7 us unsplit, 30.6 in 4 splits), while the 64-128 px levels want
+    // about 512 workgroups. The plan does not depend on the batch, so an image's sums are the
+    // same whatever it is batched with.
     ConvPkPlan p{1, K};
     const int bm = conv_pk_narrow(OC) ? NBM : PBM, bn = conv_pk_narrow(OC) ? NBN : PBN;
     const int64_t tiles = (int64_t)((M + bm - 1) / bm) * ((OC + bn - 1) / bn);
     const int slabs = K / PBK;
-    if (tiles >= 384 || slabs < 4) return p;
-    int want = (int)std::min<int64_t>((512 + tiles - 1) / tiles, slabs / 2);
+    const int want = (int)std::min<int64_t>((512 + tiles - 1) / tiles, slabs / 9);
+    if (tiles >= 384 || want < 2) return p;
     const int per = (slabs + want - 1) / want;
     p.kps = per * PBK;
     p.splits = (slabs + per - 1) / per;

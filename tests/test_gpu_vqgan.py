@@ -47,7 +47,7 @@ CONV = [  # IW, IH, IC, N, KW, KH, OC, stride, pad
     (128, 128, 128, 1, 3, 3, 128, 1, 1), (32, 32, 256, 1, 1, 1, 256, 1, 0),           # pk
     (11, 6, 16, 1, 5, 5, 24, 1, 2),                                                   # pk, 5x5
     (256, 192, 16, 1, 3, 3, 16, 1, 1),                                                # pk, no split
-    (4, 4, 512, 460, 3, 3, 16, 1, 1),             # pk, 144 splits: images launched in two groups
+    (4, 4, 4096, 260, 3, 3, 16, 1, 1),            # pk, 256 splits: images launched in groups of 255 + 5
 ]
 
 
