@@ -42,6 +42,8 @@ filters, multipliers 1,1,2,2,4) on random-init weights through mgr_decode_images
 and a batch of 8: wall ms per decode with the ids already prepared and the image left in HBM,
 the per-op device profile, the conv kernels' fraction of the fp32 MFMA peak, and a bounded
 sample of the reference's CPU conv (--no-vqgan skips it; --only-vqgan measures only it).
+extra.generate_images = the reference's whole generate() (8 device-resident decode steps of a
+24-layer Q4_K transformer, then the VQGAN decode) for 1 and 8 images, wall clock per call.
 """
 from __future__ import annotations
 
@@ -339,7 +341,7 @@ def measure(ctx, M, wtype, steps, warmup, rotate_gb, use_graphs=True, path="pack
     return ms_step, ms_gemms, host
 
 
-def write_synthetic_model(path, n_layer, wtype, seed=0):
+def write_synthetic_model(path, n_layer, wtype, seed=0, write=True):
     """Random-init MaskGIT transformer GGUF (the cfg4/cfg5 recipe): FC weights ~N(0,0.02)
     in Q8_0 / Q4_K blocks (bench-local encoders), embeddings ~N(0,0.02), biases ~N(0,0.01),
     LN gamma ~1+N(0,0.02), beta ~N(0,0.01); hidden 768, 16 heads, MLP 3072, vocab 2025."""
@@ -384,6 +386,8 @@ def write_synthetic_model(path, n_layer, wtype, seed=0):
             ("maskgit.n_positions", "u32", P), ("maskgit.mask_token_id", "i32", V - 1),
             ("maskgit.layernorm_eps", "f32", 1e-12), ("maskgit.vqgan.codebook_size", "u32", 1024),
             ("maskgit.sampling.choice_temperature", "f32", 4.5)]
+    if not write:
+        return meta, out
     write_gguf(path, meta, out)
 
 
@@ -480,7 +484,7 @@ def vqgan_convs(n_tokens, E, filters, mult, R, **_):
     return out
 
 
-def write_vqgan_model(path, seed=11):
+def write_vqgan_model(path, seed=11, write=True):
     """random-init decoder weights under the converter's names (conv ~N(0, 1/fan_in), GroupNorm
     gamma ~1 + N(0, 0.1), beta / biases ~N(0, 0.1) / N(0, 0.05), codebook ~N(0, 1))"""
     from edge_maskgit_amd.gguf import write_gguf
@@ -528,10 +532,35 @@ def write_vqgan_model(path, seed=11):
             ("maskgit.vqgan.filters", "u32", F), ("maskgit.vqgan.num_res_blocks", "u32", R),
             ("maskgit.vqgan.group_norm_groups", "u32", 32),
             ("maskgit.vqgan.channel_multipliers", "i32_array", list(mult))]
+    if not write:
+        return meta, out
     write_gguf(path, meta, out)
 
 
-def measure_vqgan(path, steps=5, cpu=True):
+def write_maskgit_model(path, wtype, seed=5):
+    """transformer (24 layers) and VQGAN decoder in one GGUF, as a converted model holds them"""
+    from edge_maskgit_amd.gguf import write_gguf
+    mt, tt = write_synthetic_model(path, 24, wtype, seed=seed, write=False)
+    mv, tv = write_vqgan_model(path, write=False)
+    keys = {k for k, _, _ in mt}
+    write_gguf(path, mt + [e for e in mv if e[0] not in keys], tt + tv)
+
+
+def measure_generate_images(path, B, n_steps=8, reps=2, algo=2):
+    """generate() end to end: B images, n_steps device-resident decode steps, then the VQGAN
+    decode of the grids (mgr_generate_images); wall clock per call, images read back"""
+    from edge_maskgit_amd.runtime import TransformerRuntime
+    cls = (np.arange(B) * 37) % 1000
+    seeds = np.arange(B, dtype=np.uint64) + 42
+    with TransformerRuntime(path, algo=algo) as m:
+        m.generate_images(cls, seeds, n_steps)          # packs and uploads the weights
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            m.generate_images(cls, seeds, n_steps)
+        return (time.perf_counter() - t0) / reps * 1e3
+
+
+def measure_vqgan(path, steps=5, cpu=True, int8=True):
     """The production decoder graph (mgr_decode_images: mg::build_vqgan_decoder on HipRuntime)
     for one image and for a batch of 8: wall clock per decode (ids in, image left in HBM), the
     per-op device profile of one B=1 decode, and the conv kernels' fp32-MFMA roofline."""
@@ -557,6 +586,20 @@ def measure_vqgan(path, steps=5, cpu=True):
         m.decode_images(rng.integers(0, VQ["codebook"], (1, VQ["n_tokens"])).astype(np.int32), readback=False)
         prof = {n: {"count": c, "ms": round(t, 4)} for n, c, t in m.profile_report()}
         m.profile(False)
+    if int8:
+        # the reference's int8 conv (its default on integer-dot devices) under the int8 algorithm
+        with TransformerRuntime(path, algo=1) as m:
+            for B in (1, 8):
+                g = rng.integers(0, VQ["codebook"], (B, VQ["n_tokens"])).astype(np.int32)
+                for _ in range(2):
+                    m.decode_images(g, readback=False)
+                t0 = time.perf_counter()
+                for _ in range(steps):
+                    m.decode_images(g, readback=False)
+                ms = (time.perf_counter() - t0) / steps * 1e3
+                res.setdefault("int8_conv", {})[f"b{B}"] = {"ms_per_decode": round(ms, 3),
+                                                            "ms_per_image": round(ms / B, 3),
+                                                            "tops": round(conv_flop * B / (ms * 1e-3) / 1e12, 2)}
     res["per_op_device_ms_b1"] = prof
     conv_ms = prof.get("Conv2D", {}).get("ms")
     if conv_ms:
@@ -780,6 +823,17 @@ def main():
             write_vqgan_model(pv)
             log(f"[bench] VQGAN model written in {time.perf_counter() - t0:.1f} s")
             extra["vqgan_decode"] = measure_vqgan(pv, cpu=not a.no_cpu)
+            os.remove(pv)
+            pm = os.path.join(d, "maskgit_q4_k.gguf")
+            write_maskgit_model(pm, ema.WTYPE_Q4_K)
+            e2e = {}
+            for B in (1, 8):
+                ms = measure_generate_images(pm, B)
+                e2e[f"b{B}"] = {"ms_per_call": round(ms, 2), "ms_per_image": round(ms / B, 2)}
+            extra["generate_images"] = {
+                "workload": "generate() end to end: 24-layer Q4_K transformer (random-init), 8 decode steps "
+                            "on the device, then the production VQGAN decoder; images read back",
+                "path": "dequantize-fused fp16 FC, fp32 conv", **e2e}
     cpu = None if a.no_cpu else cpu_baseline(host, M, wtype)
     if not a.no_cpu and cpu is not None and cpu.get("kind") == "reference":
         extra["cpu_oracle_int8_omp"] = cpu_oracle_int8(host, M, wtype)   # a multi-core CPU point

@@ -301,6 +301,32 @@ int mgr_generate(mgr_model* m, const int32_t* class_ids, const uint64_t* seeds, 
     }
 }
 
+int mgr_generate_images(mgr_model* m, const int32_t* class_ids, const uint64_t* seeds, int B, int steps,
+                        float temperature, int32_t* out_tokens, float* images) {
+    if (!m || !images || B <= 0) {
+        g_err = "mgr_generate_images: bad argument";
+        return -1;
+    }
+    try {
+        const int n = m->model->hparams().n_tokens;
+        const int side = mgr_image_side(m);
+        if (n <= 0 || side <= 0) throw std::runtime_error("mgr_generate_images: the model has no VQGAN decoder");
+        std::vector<int32_t> grids((size_t)B * n);
+        if (int rc = mgr_generate(m, class_ids, seeds, B, steps, temperature, grids.data())) return rc;
+        if (out_tokens) std::memcpy(out_tokens, grids.data(), grids.size() * sizeof(int32_t));
+        // the decoder graph in groups of 8 images: its host arena (untouched node storage, the
+        // reference's Context semantics) stays bounded
+        const size_t per = (size_t)3 * side * side;
+        for (int b0 = 0; b0 < B; b0 += 8) {
+            const int nb = std::min(8, B - b0);
+            if (int rc = mgr_decode_images(m, grids.data() + (size_t)b0 * n, nb, images + (size_t)b0 * per)) return rc;
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e);
+    }
+}
+
 int mgr_profile_enable(mgr_model* m, int on) {
     if (!m) return -1;
     m->rt->profile_enable(on != 0);

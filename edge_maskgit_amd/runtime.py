@@ -17,7 +17,7 @@ from . import LIB_DIR, MghError
 MGR_SYMBOLS = ["mgr_load", "mgr_free", "mgr_last_error", "mgr_hparams", "mgr_device_name",
                "mgr_forward", "mgr_profile_enable", "mgr_profile_report", "mgr_gguf_info",
                "mgr_graph_stats", "mgr_decode_params", "mgr_generate", "mgr_named", "mgr_decode_images",
-               "mgr_image_side"]
+               "mgr_image_side", "mgr_generate_images"]
 
 _lib = None
 
@@ -47,6 +47,7 @@ def lib():
         L.mgr_named.argtypes = [P, ctypes.c_char_p, P, ctypes.c_int64]
         L.mgr_decode_images.argtypes = [P, P, I, P]
         L.mgr_image_side.argtypes = [P]
+        L.mgr_generate_images.argtypes = [P, P, P, I, I, ctypes.c_float, P, P]
         _lib = L
     return _lib
 
@@ -145,6 +146,24 @@ class TransformerRuntime:
         _check(lib().mgr_decode_images(self.h, g.ctypes.data_as(ctypes.c_void_p), g.shape[0],
                                        None if out is None else out.ctypes.data_as(ctypes.c_void_p)))
         return out
+
+    def generate_images(self, class_ids, seeds, steps: int = 8, temperature: float = -1.0):
+        """generate() end to end (mgr_generate_images): token grids int32 [B][n_tokens] and
+        images float32 [B][3][side][side]."""
+        cls = np.ascontiguousarray(class_ids, dtype=np.int32).reshape(-1)
+        sd = np.ascontiguousarray(seeds, dtype=np.uint64).reshape(-1)
+        if cls.shape != sd.shape:
+            raise ValueError("one seed per class id")
+        side = _check(lib().mgr_image_side(self.h))
+        if side <= 0:
+            raise MghError("mgr: the model has no VQGAN decoder")
+        grids = np.empty((cls.size, self.hparams["n_tokens"]), np.int32)
+        imgs = np.empty((cls.size, 3, side, side), np.float32)
+        _check(lib().mgr_generate_images(self.h, cls.ctypes.data_as(ctypes.c_void_p),
+                                         sd.ctypes.data_as(ctypes.c_void_p), cls.size, steps, temperature,
+                                         grids.ctypes.data_as(ctypes.c_void_p),
+                                         imgs.ctypes.data_as(ctypes.c_void_p)))
+        return grids, imgs
 
     def named(self, name: str) -> np.ndarray:
         """A named node of the last forward (its values are current only if that forward ran

@@ -64,6 +64,13 @@ int mgr_decode_images(mgr_model* m, const int32_t* grids, int B, float* images);
 /* side of the decoded images: sqrt(n_tokens) * 2^(levels - 1); 0 if the model has no VQGAN */
 int mgr_image_side(const mgr_model* m);
 
+/* The reference's whole generate() (src/mg-generate.cpp:39-123) for B images: mgr_generate's
+ * device-resident decoding, then the VQGAN decode of the final grids (mgr_decode_images, in
+ * groups of 8 images). images [B][3][side][side] as mgr_decode_images; out_tokens
+ * [B][n_tokens] receives the grids (may be NULL). */
+int mgr_generate_images(mgr_model* m, const int32_t* class_ids, const uint64_t* seeds, int B, int steps,
+                        float temperature, int32_t* out_tokens, float* images);
+
 /* per-op device-time profile of the following forwards (each node timed on its own) */
 int mgr_profile_enable(mgr_model* m, int on);
 /* writes up to cap rows "name count ms\n" into buf (NUL-terminated) */

@@ -148,3 +148,18 @@ def write_vqgan_model(path: str, n_tokens: int = 16, E: int = 32, codebook: int 
             ("maskgit.vqgan.channel_multipliers", "i32_array", list(mult))]
     write_gguf(path, meta, [(n, a.shape, GGML_F32, a.tobytes()) for n, a in t.items()])
     return side
+
+
+def write_maskgit_model(path: str, n_layer: int = 2, quant: str = "q8_0", seed: int = 0, n_pos: int = 17,
+                        E: int = 32, filters: int = 32, mult=(1, 2), R: int = 1) -> tuple:
+    """transformer and VQGAN decoder in one GGUF, as the reference's converter writes a model
+    (tools/convert_to_gguf.py:158-266); returns (transformer tensors, decoder tensors)."""
+    meta, t = synthetic_model(n_layer, quant, seed, n_pos=n_pos)
+    v = vqgan_tensors(np.random.default_rng(seed + 1), E, 1024, filters, mult, R)
+    L = int(round((n_pos - 1) ** 0.5))
+    meta = meta + [("maskgit.resolution", "u32", L * 2 ** (len(mult) - 1)),
+                   ("maskgit.vqgan.embedding_dim", "u32", E), ("maskgit.vqgan.filters", "u32", filters),
+                   ("maskgit.vqgan.num_res_blocks", "u32", R), ("maskgit.vqgan.group_norm_groups", "u32", 32),
+                   ("maskgit.vqgan.channel_multipliers", "i32_array", list(mult))]
+    write_gguf(path, meta, encode(t, quant) + [(n, a.shape, GGML_F32, a.tobytes()) for n, a in v.items()])
+    return t, v

@@ -393,3 +393,20 @@ def test_decode_graph_per_node(tmp_path, monkeypatch, algo):
         with rt.TransformerRuntime(path, algo=1) as m:
             m.decode_images(grid[None])
             _check_decoder_nodes(m, t, grid, cfg, int8=False)
+
+
+def test_generate_images_end_to_end(tmp_path):
+    """the reference's whole generate() on one model file (transformer + decoder): the grids of
+    mgr_generate_images equal mgr_generate's, its images equal mgr_decode_images of those grids
+    bit for bit and the oracle decoder's within 1e-4 * max"""
+    path = str(tmp_path / "maskgit.gguf")
+    _, v = mg_gguf.write_maskgit_model(path, n_layer=2, quant="q8_0", n_pos=17, E=32, filters=32, mult=(1, 2), R=1)
+    cls, seeds = np.array([3, 207, 999], np.int32), np.array([1, 42, 7], np.uint64)
+    with rt.TransformerRuntime(path) as m:
+        grids, imgs = m.generate_images(cls, seeds, steps=4)
+        assert np.array_equal(grids, m.generate(cls, seeds, steps=4))
+        assert np.array_equal(imgs, m.decode_images(grids))
+    assert grids.min() >= 0 and grids.max() < 1024 and imgs.shape == (3, 3, 8, 8)
+    for b in range(3):
+        want = ov.decode(v, grids[b:b + 1], 32, 32, (1, 2), 1)[0]
+        assert np.abs(imgs[b] - want).max() <= 1e-4 * np.abs(want).max()
