@@ -267,7 +267,8 @@ __global__ __launch_bounds__(64 * kHeadWaves<KT>) void k_attn_head(FaArgs a) {
     // the hardware exp2 (v_exp_f32, ~1 ulp)
     const float scale2 = a.scale * 1.4426950408889634f;
     const int nqt = (S + 15) / 16;
-    for (int qt = wave; qt < nqt; qt += nw) {
+    // workgroup z of gridDim.z takes query tiles z*nw + wave, + nw*gridDim.z, ...
+    for (int qt = blockIdx.z * nw + wave; qt < nqt; qt += nw * gridDim.z) {
         const int q0 = 16 * qt;
         // Q as the B operand: lane = query q0 + l16, k = d = 16c + 4lg + j
         f16x4 qf[DC];
@@ -384,8 +385,18 @@ __global__ __launch_bounds__(64 * kHeadWaves<KT>) void k_attn_head(FaArgs a) {
 template <int DC, int KT>
 void launch_head_t(const FaArgs& a, hipStream_t s) {
     const int nqt = (a.S + 15) / 16;
-    const int nw = std::min(kHeadWaves<KT>, std::max(1, (nqt + 1) / 2));  // ~2 query tiles per wave
-    const dim3 grid((unsigned)a.H, (unsigned)a.B), block((unsigned)(64 * nw));
+    const int64_t heads = (int64_t)a.H * a.B;
+    // A head's query tiles spread over qs workgroups (each restaging the head's K/V) while the
+    // heads alone give fewer than ~256 workgroups, keeping >= 6 waves per workgroup (staging
+    // with fewer threads costs more than the finer split gains); every query's arithmetic is
+    // the same either way. Measured at S = 257, 16 heads (cfg4 shapes, fp32 q/k/v): one image
+    // 10.8 us (3 workgroups per head) against ~15 us with 2 waves in 9 and 18 us unsplit;
+    // 8 images 14.2 against 18.0 us unsplit (2 per head, 9 waves); at 16 images (256 heads)
+    // splitting costs (29.4 against 21.4 us), so qs = 1 there, ~2 query tiles per wave.
+    int qs = (int)std::max<int64_t>(1, std::min<int64_t>(256 / std::max<int64_t>(heads, 1), (nqt + 5) / 6));
+    int nw = std::min(kHeadWaves<KT>, std::max(1, qs > 1 ? (nqt + qs - 1) / qs : (nqt + 1) / 2));
+    if (qs > 1) qs = (nqt + nw - 1) / nw;
+    const dim3 grid((unsigned)a.H, (unsigned)a.B, (unsigned)qs), block((unsigned)(64 * nw));
     const bool tail = a.S > 16 * (KT - 1);
     if (a.q16) {
         if (tail) hipLaunchKernelGGL((k_attn_head<DC, KT, true, true>), grid, block, 0, s, a);

@@ -141,6 +141,27 @@ def test_flash_attn_vs_oracle(ctx, D, S, H, B):
     assert np.array_equal(om, oracle.merge_heads(o, D, S, H, B))
 
 
+@pytest.mark.parametrize("D,S,H", [(48, 257, 16), (64, 130, 4), (48, 40, 1)])
+def test_flash_attn_split_queries_bit_identical(ctx, D, S, H):
+    """with few heads the whole-head kernel spreads a head's query tiles over several
+    workgroups; one image alone (split) and the same image repeated 16 times in a batch (at
+    H = 16 unsplit) give the same bits"""
+    rng = np.random.default_rng(D + S + H)
+    q, k, v = _qkv(rng, D, S, H, 1)
+    outs = []
+    for B in (1, 16):
+        qb, kb, vb = (np.ascontiguousarray(np.tile(a, (B, 1))) for a in (q, k, v))
+        st = (1, H * D, D, H * D * S)
+        dq, dk, dv = ctx.upload(qb), ctx.upload(kb), ctx.upload(vb)
+        do = ctx.alloc(D * S * H * B * 4)
+        ctx.flash_attn_f16kv(dq, dk, dv, st, D, S, H, B, 1.0 / np.sqrt(D), do)
+        outs.append(ctx.download(do, (B, D * S * H), np.float32))
+        for t in (dq, dk, dv, do):
+            ctx.free(t)
+    for b in range(16):
+        assert np.array_equal(outs[1][b], outs[0][0])
+
+
 @pytest.mark.parametrize("S", [257, 600])
 def test_flash_attn_o16_is_rounded_output(ctx, S):
     """The fp16-output variant stores exactly the fp32 attention output rounded to fp16."""
