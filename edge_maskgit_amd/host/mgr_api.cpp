@@ -190,6 +190,33 @@ int mgr_image_side(const mgr_model* m) {
     return (int)(L << (h.vq_channel_mult.size() - 1));   // one 2x up-sampling per level but the last
 }
 
+namespace {
+
+// one decoder graph for nb grids (the caller checked the arguments)
+void decode_group(mgr_model* m, const int32_t* grids, int nb, float* images) {
+    const mg::HParams& h = m->model->hparams();
+    const size_t need = vqgan_graph_bytes(h, nb);
+    if (!m->gctx || m->gctx_bytes < need) {
+        m->gctx.reset(new mg::Context(need));
+        m->gctx_bytes = need;
+    }
+    m->gctx->reset();
+    mg::Tensor* ids = m->gctx->tensor2d(mg::Type::I32, h.n_tokens, nb);
+    std::memcpy(ids->data, grids, (size_t)h.n_tokens * nb * sizeof(int32_t));
+    mg::Tensor* out = mg::build_vqgan_decoder(*m->gctx, *m->model, ids);
+    mg::Graph g;
+    g.build_forward(out);
+    m->named.clear();
+    for (const mg::Tensor* t : g.nodes)
+        if (!t->name.empty()) m->named.push_back(t);
+    m->rt->invalidate(ids);               // new ids at a reused host address
+    const void* d = m->rt->compute_device(g);
+    mgh_ctx* c = m->rt->context();
+    check(c, images ? mgh_d2h(c, images, d, out->nbytes()) : mgh_sync(c));
+}
+
+}  // namespace
+
 int mgr_decode_images(mgr_model* m, const int32_t* grids, int B, float* images) {
     if (!m || !grids || B <= 0) {
         g_err = "mgr_decode_images: bad argument";
@@ -197,28 +224,20 @@ int mgr_decode_images(mgr_model* m, const int32_t* grids, int B, float* images) 
     }
     try {
         const mg::HParams& h = m->model->hparams();
-        if (h.n_tokens <= 0 || h.vq_embedding_dim <= 0) throw std::runtime_error("mgr_decode_images: no VQGAN in the model");
-        const size_t need = vqgan_graph_bytes(h, B);
-        if (!m->gctx || m->gctx_bytes < need) {
-            m->gctx.reset(new mg::Context(need));
-            m->gctx_bytes = need;
-        }
-        m->gctx->reset();
-        mg::Tensor* ids = m->gctx->tensor2d(mg::Type::I32, h.n_tokens, B);
-        std::memcpy(ids->data, grids, (size_t)h.n_tokens * B * sizeof(int32_t));
+        const int side = mgr_image_side(m);
+        if (h.n_tokens <= 0 || h.vq_embedding_dim <= 0 || side <= 0)
+            throw std::runtime_error("mgr_decode_images: no VQGAN in the model");
         for (int64_t i = 0; i < (int64_t)h.n_tokens * B; i++)
             if (grids[i] < 0 || grids[i] >= h.vq_codebook_size)
                 throw std::runtime_error("mgr_decode_images: code id outside the codebook");
-        mg::Tensor* out = mg::build_vqgan_decoder(*m->gctx, *m->model, ids);
-        mg::Graph g;
-        g.build_forward(out);
-        m->named.clear();
-        for (const mg::Tensor* t : g.nodes)
-            if (!t->name.empty()) m->named.push_back(t);
-        m->rt->invalidate(ids);               // new ids at a reused host address
-        const void* d = m->rt->compute_device(g);
-        mgh_ctx* c = m->rt->context();
-        check(c, images ? mgh_d2h(c, images, d, out->nbytes()) : mgh_sync(c));
+        // groups of 8 images: the graph's host arena (untouched node storage, the reference's
+        // Context semantics) and the device buffers stay bounded; an image's result does not
+        // depend on the images decoded with it
+        const size_t per = (size_t)3 * side * side;
+        for (int b0 = 0; b0 < B; b0 += 8) {
+            const int nb = std::min(8, B - b0);
+            decode_group(m, grids + (size_t)b0 * h.n_tokens, nb, images ? images + (size_t)b0 * per : nullptr);
+        }
         return 0;
     } catch (const std::exception& e) {
         return fail(e);
@@ -314,14 +333,7 @@ int mgr_generate_images(mgr_model* m, const int32_t* class_ids, const uint64_t* 
         std::vector<int32_t> grids((size_t)B * n);
         if (int rc = mgr_generate(m, class_ids, seeds, B, steps, temperature, grids.data())) return rc;
         if (out_tokens) std::memcpy(out_tokens, grids.data(), grids.size() * sizeof(int32_t));
-        // the decoder graph in groups of 8 images: its host arena (untouched node storage, the
-        // reference's Context semantics) stays bounded
-        const size_t per = (size_t)3 * side * side;
-        for (int b0 = 0; b0 < B; b0 += 8) {
-            const int nb = std::min(8, B - b0);
-            if (int rc = mgr_decode_images(m, grids.data() + (size_t)b0 * n, nb, images + (size_t)b0 * per)) return rc;
-        }
-        return 0;
+        return mgr_decode_images(m, grids.data(), B, images);
     } catch (const std::exception& e) {
         return fail(e);
     }

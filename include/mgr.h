@@ -57,9 +57,11 @@ int mgr_generate(mgr_model* m, const int32_t* class_ids, const uint64_t* seeds, 
  * reference's image layout ne = {W, H, 3, 1} per image). The graph is the reference's decoder
  * (mg::build_vqgan_decoder, src/mg-vqgan.cpp:62-110), the computation of its VqganFwd hook
  * (include/mg-generate.hpp:17, tools/main.cpp:137-152), here for B images in one graph.
- * images may be NULL: the decode then runs without the readback. Each GroupNorm, conv (+ bias)
+ * images may be NULL: the decode then runs without the readback. The images are decoded in
+ * groups of 8 (an image's result does not depend on its group). Each GroupNorm, conv (+ bias)
  * and res-block output is named after its weights' prefix (res blocks: "<prefix>.out"; the
- * inputs of conv_in and of each up-sampling conv: "<prefix>.in") for mgr_named. */
+ * inputs of conv_in and of each up-sampling conv: "<prefix>.in") for mgr_named, whose values
+ * are those of the last group. */
 int mgr_decode_images(mgr_model* m, const int32_t* grids, int B, float* images);
 /* side of the decoded images: sqrt(n_tokens) * 2^(levels - 1); 0 if the model has no VQGAN */
 int mgr_image_side(const mgr_model* m);

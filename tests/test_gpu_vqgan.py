@@ -242,6 +242,18 @@ def test_decode_graph_production_size(tmp_path):
     assert np.array_equal(a[1], one[0])
 
 
+def test_decode_images_in_groups(tmp_path):
+    """11 grids decode as groups of 8 + 3: each image equals its single decode bit for bit"""
+    cfg = SMALL[0]
+    path = str(tmp_path / "vq.gguf")
+    mg_gguf.write_vqgan_model(path, seed=12, **cfg)
+    grids = np.random.default_rng(13).integers(0, cfg["codebook"], (11, cfg["n_tokens"])).astype(np.int32)
+    with rt.TransformerRuntime(path) as m:
+        imgs = m.decode_images(grids)
+        for b in (0, 7, 8, 10):
+            assert np.array_equal(imgs[b], m.decode_images(grids[b:b + 1])[0])
+
+
 def test_decode_rejects_bad_grids(tmp_path):
     path = str(tmp_path / "vq.gguf")
     mg_gguf.write_vqgan_model(path, seed=0, **SMALL[0])
