@@ -766,8 +766,7 @@ int mgh_conv2d_pack_weights(mgh_ctx* c, const float* ker, int KW, int KH, int IC
 
 size_t mgh_conv2d_i8_weight_bytes(int KW, int KH, int IC, int OC) {
     if (KW <= 0 || KH <= 0 || IC <= 0 || OC <= 0 || (int64_t)IC * KW * KH > INT32_MAX) return 0;
-    const int K = IC * KW * KH;
-    return mgh::conv_i8_codes_bytes(K, OC) + (size_t)OC * ((K + 31) / 32) * sizeof(float);
+    return mgh::conv_i8_weight_bytes(IC * KW * KH, OC);
 }
 
 int mgh_conv2d_i8_pack_weights(mgh_ctx* c, const float* ker, int KW, int KH, int IC, int OC, void* wq) {
@@ -790,11 +789,18 @@ int mgh_conv2d_i8(mgh_ctx* c, const float* in, int IW, int IH, int IC, int N, co
     if (!in || !wq || !out) return fail(c, MGH_ERR_ARG, "conv2d_i8: null pointer");
     if (!aligned16(out) || !aligned16(wq) || (resid && !aligned16(resid)))
         return fail(c, MGH_ERR_ARG, "conv2d_i8: d_wq, d_out and d_resid must be 16-byte aligned");
+    const int M = (int)(OW * OH), K = IC * KW * KH;
+    // grids: blocks / 4 (quantize pass) and channel tiles (GEMM pass) in y
+    if ((K + 31) / 32 > 4 * 65535 || (OC + 15) / 16 > 65535)
+        return fail(c, MGH_ERR_UNSUPPORTED, "conv2d_i8: IC*KW*KH or OC too large");
     if (int r = set_dev(c)) return r;
-    const int K = IC * KW * KH;
-    const _Float16* qw = (const _Float16*)wq;
+    if (int r = ensure_qp_ws(c, mgh::conv_i8_ws_bytes(M, K, N))) return r;
+    const size_t codes = mgh::conv_i8_ws_codes_bytes(M, K, N);
+    const int8_t* qw = (const int8_t*)wq;
     const float* dw = (const float*)((const char*)wq + mgh::conv_i8_codes_bytes(K, OC));
-    mgh::ConvI8Args a{in, qw, dw, out, bias, resid, IW, IH, IC, (int)OW, (int)OH, OC, KW, KH, stride, pad, N};
+    int8_t* qa = (int8_t*)c->qp_ws;
+    mgh::ConvI8Args a{in, qw, dw, out, bias, resid, qa, (float*)(qa + codes),
+                      IW, IH, IC, (int)OW, (int)OH, OC, KW, KH, stride, pad, N};
     MGH_HIP(c, mgh::launch_conv2d_i8(a, c->stream), "k_conv2d_i8");
     return MGH_OK;
 }

@@ -214,18 +214,25 @@ ConvPkPlan conv_pk_plan(int M, int OC, int K);   // per image: independent of th
 size_t conv_pk_ws_bytes(int M, int OC, int N, int K);    // split-K partials, 0 without a split
 hipError_t launch_conv_pack(const float* ker, float* wpk, int IC, int taps, int OC, hipStream_t s);
 hipError_t launch_conv2d_pk(const ConvPkArgs& a, float* ws, hipStream_t s);
-// int8 conv (the reference's k_conv2d_i8): weights from launch_conv_quant_w — fp16 codes
-// [OC][32*blocks] (conv_i8_codes_bytes, 256-byte aligned), then fp32 scales [OC][blocks]
+// int8 conv (the reference's k_conv2d_i8): weights from launch_conv_quant_w — int8 codes in
+// fragment order [ceil(OC/16)][blocks][16][32] (conv_i8_codes_bytes, 256-byte aligned), then
+// fp32 scales [ceil(OC/16)][blocks][16]; qa / dxa: the workspace of conv_i8_ws_bytes (the
+// im2col codes [N][ceil(M/16)][blocks][16][32], then their scales [N][ceil(M/16)][blocks][16])
 struct ConvI8Args {
     const float* in;
-    const _Float16* qw;
+    const int8_t* qw;
     const float* dw;
     float* out;
     const float* bias;
     const float* resid;
+    int8_t* qa;
+    float* dxa;
     int IW, IH, IC, OW, OH, OC, KW, KH, stride, pad, N;
 };
 size_t conv_i8_codes_bytes(int K, int OC);
+size_t conv_i8_weight_bytes(int K, int OC);
+size_t conv_i8_ws_codes_bytes(int M, int K, int N);   // the workspace's codes, 256-byte aligned
+size_t conv_i8_ws_bytes(int M, int K, int N);
 hipError_t launch_conv_quant_w(const float* ker, void* wq, int K, int OC, hipStream_t s);
 hipError_t launch_conv2d_i8(const ConvI8Args& a, hipStream_t s);
 size_t group_norm_ws_bytes(int64_t W, int64_t H, int C, int N, int G);

@@ -250,10 +250,12 @@ int mgh_conv2d_pack_weights(mgh_ctx* ctx, const float* d_ker, int KW, int KH, in
 /* The int8 conv of the reference's integer-dot devices (k_quantize_conv_w + k_conv2d_i8,
  * mg-opencl.cpp:598-664, 1541-1553): mgh_conv2d_i8_pack_weights quantizes the kernel once per
  * output channel and 32-block of k = (ic*KH + kh)*KW + kw (d = amax/127, round half away from
- * zero; buffer of mgh_conv2d_i8_weight_bytes: fp16 codes, then fp32 scales); mgh_conv2d_i8
+ * zero; buffer of mgh_conv2d_i8_weight_bytes: int8 codes [ceil(OC/16)][blocks][16][32], then
+ * fp32 scales [ceil(OC/16)][blocks][16], zero past OC and K); mgh_conv2d_i8
  * quantizes every output pixel's im2col column per 32-block the same way, sums the exact
  * integer block dots as acc = acc + (dx*dw)*idot in block order (fp32, each operation
- * rounded), then (+ bias[oc]) (+ resid) as mgh_conv2d_ex. */
+ * rounded), then (+ bias[oc]) (+ resid) as mgh_conv2d_ex. The quantized im2col matrix lives
+ * in the context's workspace (about 1.13 bytes per output pixel and k, grown on first use). */
 size_t mgh_conv2d_i8_weight_bytes(int KW, int KH, int IC, int OC);
 int mgh_conv2d_i8_pack_weights(mgh_ctx* ctx, const float* d_ker, int KW, int KH, int IC, int OC, void* d_wq);
 int mgh_conv2d_i8(mgh_ctx* ctx, const float* d_in, int IW, int IH, int IC, int N, const void* d_wq, int KW,

@@ -284,17 +284,19 @@ def test_conv2d_i8_vs_oracle(ctx, IW, IH, IC, N, KW, KH, OC, stride, pad):
     res = rng.standard_normal((N, OC, OH, OW)).astype(np.float32)
     K = IC * KH * KW
     nb = (K + 31) // 32
+    OT = (OC + 15) // 16                  # channel tiles: codes [OT][nb][16][32], scales [OT][nb][16]
     nbytes = ctx.conv2d_i8_weight_bytes(KW, KH, IC, OC)
-    codes_bytes = (OC * nb * 32 * 2 + 255) // 256 * 256
-    assert nbytes == codes_bytes + OC * nb * 4
+    codes_bytes = (OT * nb * 512 + 255) // 256 * 256
+    assert nbytes == codes_bytes + OT * nb * 16 * 4
     dX, dK, dB, dR, dQ = ctx.upload(x), ctx.upload(ker), ctx.upload(bias), ctx.upload(res), ctx.alloc(nbytes)
     dY = ctx.alloc(res.nbytes)
     ctx.conv2d_i8_pack_weights(dK, KW, KH, IC, OC, dQ)
     raw = ctx.download(dQ, (nbytes,), np.uint8)
-    qw_gpu = raw[:OC * nb * 32 * 2].view(np.float16).reshape(OC, nb * 32)
-    dw_gpu = raw[codes_bytes:].view(np.float32).reshape(OC, nb)
+    qw_all = raw[:OT * nb * 512].view(np.int8).reshape(OT, nb, 16, 32).transpose(0, 2, 1, 3).reshape(OT * 16, nb * 32)
+    dw_all = raw[codes_bytes:].view(np.float32).reshape(OT, nb, 16).transpose(0, 2, 1).reshape(OT * 16, nb)
     qw, dw = oracle.conv_quant_w(ker)
-    assert np.array_equal(qw_gpu.astype(np.int32), qw.astype(np.int32)) and np.array_equal(dw_gpu, dw)
+    assert np.array_equal(qw_all[:OC].astype(np.int32), qw.astype(np.int32)) and np.array_equal(dw_all[:OC], dw)
+    assert not qw_all[OC:].any() and not dw_all[OC:].any()      # padding channels: zero codes and scales
     ctx.conv2d_i8(dX, IW, IH, IC, N, dQ, KW, KH, OC, stride, pad, None, None, dY)
     y = ctx.download(dY, res.shape, np.float32)
     want = oracle.conv2d_i8(x, qw, dw, KH, KW, stride, pad)
