@@ -31,11 +31,12 @@ HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC",
 
 KERNEL_SOURCES = ["k_quant_act.hip", "k_gemm_i8.hip",
                   "k_pack_w.hip", "k_gemm_qp.hip", "k_layernorm.hip", "k_flash_attn.hip",
-                  "k_gemm_f32.hip", "k_glue.hip", "k_ops.hip", "k_vqgan.hip", "noalloc.hip", "k_decode.hip", "k_gemm_h16.hip", "mgh_api.cpp"]
-# Per-source extra flags. The int8 GEMM keeps MFMA results in VGPRs so the per-block
-# scale FMAs read them without v_accvgpr_read copies.
+                  "k_gemm_f32.hip", "k_glue.hip", "k_ops.hip", "k_vqgan.hip", "k_conv_i8.hip", "noalloc.hip", "k_decode.hip", "k_gemm_h16.hip", "mgh_api.cpp"]
+# Per-source extra flags. The int8 GEMMs keep MFMA results in VGPRs so the per-block
+# scale arithmetic reads them without v_accvgpr_read copies.
 EXTRA_FLAGS = {"k_gemm_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-               "k_gemm_qp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+               "k_gemm_qp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+               "k_conv_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 # C++ host runtime (graph API mirror, GGUF loader, transformer builder, HipRuntime, mgr C ABI):
 # plain host code over the libmgh C ABI, compiled with g++ into lib/libmg_hip.so.
 HOST_SOURCES = ["mg-tensor.cpp", "mg-model.cpp", "mg-transformer.cpp", "mg-vqgan.cpp", "mg-hip.cpp", "mgr_api.cpp"]

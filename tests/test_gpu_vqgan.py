@@ -270,6 +270,9 @@ I8 = [  # IW, IH, IC, N, KW, KH, OC, stride, pad
     (9, 7, 8, 2, 3, 3, 5, 1, 1), (10, 10, 5, 1, 3, 3, 70, 2, 1), (16, 16, 256, 1, 3, 3, 512, 1, 1),
     (32, 32, 128, 2, 3, 3, 64, 1, 1), (64, 64, 128, 1, 1, 1, 128, 1, 0), (65, 33, 20, 1, 3, 3, 130, 1, 1),
     (32, 32, 128, 1, 3, 3, 3, 1, 1), (11, 6, 16, 1, 5, 5, 24, 1, 2), (64, 64, 64, 1, 3, 3, 128, 1, 1),
+    # rows of 4 / 8 / 16 pixels (a ragged last 16-pixel tile, a partial last block at K = 180)
+    (8, 5, 32, 2, 3, 3, 20, 1, 1), (16, 8, 20, 1, 3, 3, 24, 1, 1), (4, 9, 64, 3, 3, 3, 40, 1, 1),
+    (12, 12, 32, 1, 3, 3, 16, 1, 1),
 ]
 
 
