@@ -235,16 +235,34 @@ __global__ __launch_bounds__(64) void k_conv_i8_gemm(ConvI8Args a) {
         int64_t B[CT];
         float W[CT];
     };
+    // block b of the ring; past the last block the stage re-reads the last block's codes with
+    // zero scales, so its products are +-0 and leave acc unchanged (acc starts at +0 and is
+    // never -0), and the ring runs without branches (with a branch per stage the compiler's
+    // load waits drained the ring)
+    // The scales come through raw buffer loads over their tile row's nb * 16 floats; a stage
+    // past the last block reads offset 0x80000000, outside that range, which loads 0 (the
+    // choice is made on the address, so nothing waits for a load to select its value).
+    __amdgpu_buffer_rsrc_t xr[RT], wr[CT];
+#pragma unroll
+    for (int i = 0; i < RT; i++)
+        xr[i] = __builtin_amdgcn_make_buffer_rsrc((void*)(a.dxa + af[i] * 16), (short)0, nb * 64, 0x00020000);
+#pragma unroll
+    for (int j = 0; j < CT; j++)
+        wr[j] = __builtin_amdgcn_make_buffer_rsrc((void*)(a.dw + bf[j] * 16), (short)0, nb * 64, 0x00020000);
     auto load = [&](Stage& s, int b) {
+        const bool live = b < nb;
+        const int xo = live ? (b * 16 + 4 * lg) * 4 : (int)0x80000000u;
+        const int wo = live ? (b * 16 + l16) * 4 : (int)0x80000000u;
+        b = min(b, nb - 1);
 #pragma unroll
         for (int i = 0; i < RT; i++) {
             s.A[i] = *(const int64_t*)(a.qa + (af[i] + b) * 512 + aoff);
-            s.X[i] = *(const f32x4*)(a.dxa + (af[i] + b) * 16 + 4 * lg);
+            s.X[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr[i], xo, 0, 0));
         }
 #pragma unroll
         for (int j = 0; j < CT; j++) {
             s.B[j] = *(const int64_t*)(a.qw + (bf[j] + b) * 512 + aoff);
-            s.W[j] = a.dw[(bf[j] + b) * 16 + l16];
+            s.W[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr[j], wo, 0, 0));
         }
     };
 
@@ -255,25 +273,27 @@ __global__ __launch_bounds__(64) void k_conv_i8_gemm(ConvI8Args a) {
         for (int j = 0; j < CT; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     Stage st[D];
 #pragma unroll
-    for (int s = 0; s < D; s++) load(st[s], min(s, nb - 1));
+    for (int s = 0; s < D; s++) load(st[s], s);
     for (int b0 = 0; b0 < nb; b0 += D) {
 #pragma unroll
         for (int s = 0; s < D; s++) {
-            if (b0 + s < nb) {
 #pragma unroll
-                for (int i = 0; i < RT; i++)
+            for (int i = 0; i < RT; i++)
 #pragma unroll
-                    for (int j = 0; j < CT; j++) {
-                        const i32x4 I = __builtin_amdgcn_mfma_i32_16x16x32_i8(st[s].A[i], st[s].B[j],
-                                                                               i32x4{0, 0, 0, 0}, 0, 0, 0);
+                for (int j = 0; j < CT; j++) {
+                    const i32x4 I = __builtin_amdgcn_mfma_i32_16x16x32_i8(st[s].A[i], st[s].B[j],
+                                                                           i32x4{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-                        for (int r = 0; r < 4; r++) {
-                            const float sc = st[s].X[i][r] * st[s].W[j];
-                            acc[i][j][r] = acc[i][j][r] + sc * (float)I[r];
-                        }
+                    for (int r = 0; r < 4; r++) {
+                        const float sc = st[s].X[i][r] * st[s].W[j];
+                        acc[i][j][r] = acc[i][j][r] + sc * (float)I[r];
                     }
-            }
-            load(st[s], min(b0 + s + D, nb - 1));
+                }
+            load(st[s], b0 + s + D);
+            // deep rings: keep each stage's loads behind its own arithmetic (hoisted into other
+            // registers, they become copies at the loop's back edge, each waiting for its
+            // load); 2- and 3-deep rings keep the scheduler free to overlap the stages
+            if (D >= 4) __builtin_amdgcn_sched_barrier(0);
         }
     }
     // register r of tile (i, j): pixel 16*(pt0 + i) + 4lg + r, channel 16*(ot0 + j) + l16
@@ -334,25 +354,41 @@ hipError_t launch_conv2d_i8(const ConvI8Args& a, hipStream_t s) {
         const dim3 g1((unsigned)PT, (unsigned)((nb + 3) / 4), (unsigned)a.N);
         hipLaunchKernelGGL(k_conv_im2col_q8<0>, g1, dim3(256), 0, s, a);
     }
-    // the largest wave tile (rows x channel tiles, no more tiles than the operands have) that
-    // still gives >= 2048 waves; 1 x 1 tiles otherwise
-    static const int cand[][2] = {{4, 4}, {4, 2}, {2, 2}, {4, 1}, {2, 1}};
+    // Wave tile (16-pixel rows x 16-channel tiles, no more tiles than the operands have) and
+    // ring depth, from timings of every variant on the decoder's GEMM shapes at 1 and 8 images
+    // (all bit-identical): the largest tile that still gives >= 2048 waves for 4 x 4, >= 1024
+    // for the others, else 1 x 1; deeper rings where waves are few (one wave's ring then has
+    // to cover a whole memory latency), shallower ones where occupancy hides it.
+    static const int cand[][3] = {{4, 4, 2048}, {4, 2, 1024}, {2, 2, 1024}, {4, 1, 1024}, {2, 1, 1024}};
     int rt = 1, ct = 1;
+    int64_t waves = (int64_t)PT * OT * a.N;
     for (const auto& c : cand) {
         if (c[0] > PT || c[1] > OT) continue;
-        if ((int64_t)((PT + c[0] - 1) / c[0]) * ((OT + c[1] - 1) / c[1]) * a.N >= 2048) {
+        const int64_t w = (int64_t)((PT + c[0] - 1) / c[0]) * ((OT + c[1] - 1) / c[1]) * a.N;
+        if (w >= c[2]) {
             rt = c[0];
             ct = c[1];
+            waves = w;
             break;
         }
     }
     const dim3 g2((unsigned)((PT + rt - 1) / rt), (unsigned)((OT + ct - 1) / ct), (unsigned)a.N), block(64);
-    if (rt == 4 && ct == 4) hipLaunchKernelGGL((k_conv_i8_gemm<4, 4, 2>), g2, block, 0, s, a);
-    else if (rt == 4 && ct == 2) hipLaunchKernelGGL((k_conv_i8_gemm<4, 2, 3>), g2, block, 0, s, a);
-    else if (rt == 2 && ct == 2) hipLaunchKernelGGL((k_conv_i8_gemm<2, 2, 4>), g2, block, 0, s, a);
-    else if (rt == 4) hipLaunchKernelGGL((k_conv_i8_gemm<4, 1, 3>), g2, block, 0, s, a);
-    else if (rt == 2) hipLaunchKernelGGL((k_conv_i8_gemm<2, 1, 4>), g2, block, 0, s, a);
-    else hipLaunchKernelGGL((k_conv_i8_gemm<1, 1, 8>), g2, block, 0, s, a);
+    if (rt == 4 && ct == 4) {
+        if (waves >= 8192) hipLaunchKernelGGL((k_conv_i8_gemm<4, 4, 2>), g2, block, 0, s, a);
+        else hipLaunchKernelGGL((k_conv_i8_gemm<4, 4, 4>), g2, block, 0, s, a);
+    } else if (rt == 4 && ct == 2) {
+        hipLaunchKernelGGL((k_conv_i8_gemm<4, 2, 4>), g2, block, 0, s, a);
+    } else if (rt == 2 && ct == 2) {
+        if (waves > 1024) hipLaunchKernelGGL((k_conv_i8_gemm<2, 2, 4>), g2, block, 0, s, a);
+        else hipLaunchKernelGGL((k_conv_i8_gemm<2, 2, 8>), g2, block, 0, s, a);
+    } else if (rt == 4) {
+        if (waves > 2048) hipLaunchKernelGGL((k_conv_i8_gemm<4, 1, 3>), g2, block, 0, s, a);
+        else hipLaunchKernelGGL((k_conv_i8_gemm<4, 1, 6>), g2, block, 0, s, a);
+    } else if (rt == 2) {
+        hipLaunchKernelGGL((k_conv_i8_gemm<2, 1, 4>), g2, block, 0, s, a);
+    } else {
+        hipLaunchKernelGGL((k_conv_i8_gemm<1, 1, 8>), g2, block, 0, s, a);
+    }
     return hipGetLastError();
 }
 

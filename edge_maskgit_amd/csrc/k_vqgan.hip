@@ -559,6 +559,22 @@ __global__ __launch_bounds__(256) void k_upscale(const float* __restrict__ x, fl
     y[i] = x[(cn * IH + oh / f) * IW + ow / f];
 }
 
+// Up-sampling by 2 on even widths (every decoder level): a thread reads two neighbouring
+// input values and writes them doubled, {a, a, b, b}, as one 16-byte store into each of the
+// two output rows.
+__global__ __launch_bounds__(256) void k_upscale2(const float2* __restrict__ x, f32x4* __restrict__ y, int IWh,
+                                                  int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const float2 v = x[i];
+    const int64_t row = i / IWh;                // input row (c*IH + ih) of an image
+    const int j = (int)(i - row * IWh);
+    const f32x4 o = {v.x, v.x, v.y, v.y};
+    f32x4* out = y + (size_t)row * 2 * IWh + j; // output rows 2*row and 2*row + 1, IWh vectors each
+    out[0] = o;
+    out[IWh] = o;
+}
+
 }  // namespace
 
 hipError_t launch_conv2d_f32(const ConvArgs& a, hipStream_t s) {
@@ -692,6 +708,12 @@ hipError_t launch_group_norm(const float* x, int64_t W, int64_t H, int C, int N,
 hipError_t launch_upscale(const float* x, int IW, int IH, int64_t CN, int f, float* y, hipStream_t s) {
     const int64_t total = (int64_t)IW * f * IH * f * CN;
     if (total == 0) return hipSuccess;
+    if (f == 2 && IW % 2 == 0 && ((uintptr_t)x & 7) == 0 && ((uintptr_t)y & 15) == 0) {
+        const int64_t pairs = (int64_t)IW / 2 * IH * CN;
+        hipLaunchKernelGGL(k_upscale2, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s, (const float2*)x,
+                           (f32x4*)y, IW / 2, pairs);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(k_upscale, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, x, y, IW, IH, f, total);
     return hipGetLastError();
 }

@@ -161,7 +161,8 @@ def test_group_norm(ctx, W, H, C, N, G, affine):
         assert ulp.max() <= 2 and same >= 0.99
 
 
-@pytest.mark.parametrize("W,H,C,N,f", [(16, 16, 512, 1, 2), (7, 5, 3, 2, 3), (128, 128, 128, 1, 2)])
+@pytest.mark.parametrize("W,H,C,N,f", [(16, 16, 512, 1, 2), (7, 5, 3, 2, 3), (128, 128, 128, 1, 2),
+                                        (7, 3, 5, 2, 2), (2, 9, 3, 3, 2), (6, 4, 2, 1, 1)])
 def test_upscale(ctx, W, H, C, N, f):
     rng = np.random.default_rng(W + C)
     x = rng.standard_normal((N, C, H, W)).astype(np.float32)
@@ -309,6 +310,62 @@ def test_conv2d_i8_vs_oracle(ctx, IW, IH, IC, N, KW, KH, OC, stride, pad):
     ctx.conv2d_i8(dX, IW, IH, IC, N, dQ, KW, KH, OC, stride, pad, dB, dR, dY)
     assert np.array_equal(ctx.download(dY, res.shape, np.float32), (want + bias[None, :, None, None]) + res)
     for b in (dX, dK, dB, dR, dQ, dY):
+        ctx.free(b)
+
+
+def _conv_i8_setup(ctx, rng, N, IC, IH, IW, OC, k):
+    x = (rng.standard_normal((N, IC, IH, IW)) * (2.0 ** rng.integers(-3, 4, (1, IC, 1, 1)))).astype(np.float32)
+    ker = (rng.standard_normal((OC, IC, k, k)) / np.sqrt(IC * k * k)).astype(np.float32)
+    dX, dK = ctx.upload(x), ctx.upload(ker)
+    dQ = ctx.alloc(ctx.conv2d_i8_weight_bytes(k, k, IC, OC))
+    ctx.conv2d_i8_pack_weights(dK, k, k, IC, OC, dQ)
+    return x, ker, dX, dK, dQ
+
+
+def test_conv2d_i8_large_tiles_vs_oracle(ctx):
+    """32 images of 64 x 64 with 64 output channels give the GEMM pass its 4 x 4 wave tiles
+    (2048 waves, 4-deep ring); K = 144 leaves a partial last block. Bit-exact."""
+    N, IC, IH, IW, OC = 32, 16, 64, 64, 64
+    print(f"conv2d_i8 large tiles N={N} IC={IC} {IH}x{IW} OC={OC}", flush=True)
+    rng = np.random.default_rng(77)
+    x, ker, dX, dK, dQ = _conv_i8_setup(ctx, rng, N, IC, IH, IW, OC, 3)
+    dY = ctx.alloc(N * OC * IH * IW * 4)
+    ctx.conv2d_i8(dX, IW, IH, IC, N, dQ, 3, 3, OC, 1, 1, None, None, dY)
+    y = ctx.download(dY, (N, OC, IH, IW), np.float32)
+    qw, dw = oracle.conv_quant_w(ker)
+    want = oracle.conv2d_i8(x, qw, dw, 3, 3, 1, 1)
+    mism = int((y != want).sum())
+    print(f"  {mism} of {y.size} outputs differ from the oracle")
+    assert mism == 0
+    for b in (dX, dK, dQ, dY):
+        ctx.free(b)
+
+
+# (IW, IH, IC, OC, N, sub-batch): the whole batch and its sub-batches take different GEMM wave
+# tiles and ring depths (4 x 4 with rings of 2 and 4, 4 x 2, 2 x 2 with rings of 4 and 8, 4 x 1
+# with rings of 3 and 6, 2 x 1, 1 x 1); every image's result must be bit-identical
+I8_BATCH = [(64, 64, 256, 256, 8, 1), (64, 64, 256, 256, 8, 4), (128, 128, 128, 128, 16, 1),
+            (128, 128, 128, 3, 16, 4), (96, 64, 64, 256, 2, 1), (32, 32, 512, 512, 4, 1)]
+
+
+@pytest.mark.parametrize("IW,IH,IC,OC,N,sub", I8_BATCH)
+def test_conv2d_i8_batch_invariant(ctx, IW, IH, IC, OC, N, sub):
+    print(f"conv2d_i8 batch invariance {IW}x{IH} IC={IC} OC={OC} N={N} in groups of {sub}", flush=True)
+    rng = np.random.default_rng(IW + IC + OC + N)
+    x, ker, dX, dK, dQ = _conv_i8_setup(ctx, rng, N, IC, IH, IW, OC, 3)
+    M = IW * IH
+    dY = ctx.alloc(N * OC * M * 4)
+    ctx.conv2d_i8(dX, IW, IH, IC, N, dQ, 3, 3, OC, 1, 1, None, None, dY)
+    whole = ctx.download(dY, (N, OC, IH, IW), np.float32)
+    for g in range(0, N, sub):
+        dXg = ctx.upload(np.ascontiguousarray(x[g:g + sub]))
+        dYg = ctx.alloc(sub * OC * M * 4)
+        ctx.conv2d_i8(dXg, IW, IH, IC, sub, dQ, 3, 3, OC, 1, 1, None, None, dYg)
+        part = ctx.download(dYg, (sub, OC, IH, IW), np.float32)
+        assert np.array_equal(part, whole[g:g + sub]), f"images {g}..{g + sub - 1} differ"
+        ctx.free(dXg)
+        ctx.free(dYg)
+    for b in (dX, dK, dQ, dY):
         ctx.free(b)
 
 
