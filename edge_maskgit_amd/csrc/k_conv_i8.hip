@@ -202,9 +202,9 @@ __global__ __launch_bounds__(256) void k_conv_im2col_q8p(ConvI8Args a, int bpw) 
         if (st) {
             const size_t frag = ((size_t)n * PT + (p >> 4)) * nb + b;
             u32x4* dst = (u32x4*)(a.qa + frag * 512 + (p & 15) * 32);
-            dst[0] = q[0];
-            dst[1] = q[1];
-            a.dxa[frag * 16 + (p & 15)] = d;
+            __builtin_nontemporal_store(q[0], dst);
+            __builtin_nontemporal_store(q[1], dst + 1);
+            __builtin_nontemporal_store(d, a.dxa + frag * 16 + (p & 15));
         }
     }
 }

@@ -137,7 +137,7 @@ __global__ __launch_bounds__(256, 2) void k_conv2d_pk(ConvPkArgs a) {
         const size_t row = ((size_t)(SPLIT ? sp * a.N + n : n) * OC + oc) * M;
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            conv_store(a.out, SPLIT ? nullptr : a.bias, SPLIT ? nullptr : a.resid, row, oc,
+            conv_store<!SPLIT>(a.out, SPLIT ? nullptr : a.bias, SPLIT ? nullptr : a.resid, row, oc,
                        m0 + 64 * wm + 16 * i + 4 * lg, M, acc[i][j]);
     }
 }
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(256, 2) void k_conv2d_pkn(ConvPkArgs a) {
     const size_t row = ((size_t)(SPLIT ? sp * a.N + n : n) * OC + oc) * M;
 #pragma unroll
     for (int i = 0; i < 4; i++)
-        conv_store(a.out, SPLIT ? nullptr : a.bias, SPLIT ? nullptr : a.resid, row, oc, m0 + 64 * wave + 16 * i + 4 * lg,
+        conv_store<!SPLIT>(a.out, SPLIT ? nullptr : a.bias, SPLIT ? nullptr : a.resid, row, oc, m0 + 64 * wave + 16 * i + 4 * lg,
                    M, acc[i]);
 }
 
