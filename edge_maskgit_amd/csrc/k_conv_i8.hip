@@ -209,6 +209,125 @@ __global__ __launch_bounds__(256) void k_conv_im2col_q8p(ConvI8Args a, int bpw) 
     }
 }
 
+// One pass (layers with many output pixels and >= 128 channels): a wave computes 64 output
+// pixels x 16*CT channels, quantizing its own im2col rows as k_conv_im2col_q8p does (lane =
+// pixel, the block's 32 values in registers, the next block's gathered while this one's
+// arithmetic runs) and handing the codes to the MFMA fragments through 2 KB of wave-private
+// LDS (each lane writes its pixel's 32 codes as one row, then reads its 8-byte fragment
+// pieces), then the same block-scaled exact GEMM as k_conv_i8_gemm. No workspace round trip:
+// the codes never reach HBM. Same codes and arithmetic, hence bit-identical results.
+template <int KSZ, int CT>
+__global__ __launch_bounds__(64) void k_conv_i8_fused(ConvI8Args a) {
+#pragma clang fp contract(off)
+    constexpr int KK = KSZ * KSZ;
+    const int M = a.OW * a.OH, K = a.IC * KK, nb = (K + 31) / 32, OT = (a.OC + 15) / 16;
+    const int lane = threadIdx.x, l16 = lane & 15, lg = lane >> 4;
+    const int p = blockIdx.x * 64 + lane, ot0 = blockIdx.y * CT, n = blockIdx.z;
+    const bool pv = p < M;
+    const int ow = pv ? p % a.OW : 0, oh = pv ? p / a.OW : 0;
+    const int iw0 = ow * a.stride - a.pad, ih0 = oh * a.stride - a.pad;
+    uint32_t toff[KK];
+#pragma unroll
+    for (int kh = 0; kh < KSZ; kh++)
+#pragma unroll
+        for (int kw = 0; kw < KSZ; kw++) {
+            const int ih = ih0 + kh, iw = iw0 + kw;
+            toff[kh * KSZ + kw] = pv && ih >= 0 && ih < a.IH && iw >= 0 && iw < a.IW
+                                      ? (uint32_t)(ih * a.IW + iw) * 4u : 0x80000000u;
+        }
+    const int plane = a.IW * a.IH;                     // IC * plane * 4 < 2^31 (host check)
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.in + (size_t)n * a.IC * plane), (short)0, a.IC * plane * 4, 0x00020000);
+    __shared__ __attribute__((aligned(16))) int8_t cs[64 * 32];   // [pixel][32 codes]
+    __shared__ __attribute__((aligned(16))) float dsc[64];        // the pixels' block scales
+    const int aoff = l16 * 32 + 8 * lg;
+    size_t bf[CT];
+#pragma unroll
+    for (int j = 0; j < CT; j++) bf[j] = (size_t)min(ot0 + j, OT - 1) * nb;
+    f32x4 acc[4][CT];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < CT; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto gather = [&](float (&v)[32], int b) {
+        if (KK == 1) {
+            gather_phase<KSZ, 0>(v, rs, toff, b, a.IC, K, plane * 4);
+            return;
+        }
+        switch (b % 9) {
+            case 0: gather_phase<KSZ, 0>(v, rs, toff, b, a.IC, K, plane * 4); break;
+            case 1: gather_phase<KSZ, 1>(v, rs, toff, b, a.IC, K, plane * 4); break;
+            case 2: gather_phase<KSZ, 2>(v, rs, toff, b, a.IC, K, plane * 4); break;
+            case 3: gather_phase<KSZ, 3>(v, rs, toff, b, a.IC, K, plane * 4); break;
+            case 4: gather_phase<KSZ, 4>(v, rs, toff, b, a.IC, K, plane * 4); break;
+            case 5: gather_phase<KSZ, 5>(v, rs, toff, b, a.IC, K, plane * 4); break;
+            case 6: gather_phase<KSZ, 6>(v, rs, toff, b, a.IC, K, plane * 4); break;
+            case 7: gather_phase<KSZ, 7>(v, rs, toff, b, a.IC, K, plane * 4); break;
+            default: gather_phase<KSZ, 8>(v, rs, toff, b, a.IC, K, plane * 4); break;
+        }
+    };
+    float v[32];
+    gather(v, 0);
+    for (int b = 0; b < nb; b++) {
+        int64_t B[CT];
+        float W[CT];
+#pragma unroll
+        for (int j = 0; j < CT; j++) {
+            B[j] = *(const int64_t*)(a.qw + (bf[j] + b) * 512 + aoff);
+            W[j] = a.dw[(bf[j] + b) * 16 + l16];
+        }
+        float amax = 0.f;
+#pragma unroll
+        for (int e = 0; e < 32; e++) amax = fmaxf(amax, fabsf(v[e]));
+        const float d = amax / 127.0f, id = d > 0.0f ? 1.0f / d : 0.0f;
+        u32x4 q[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float* x = v + 16 * h + 4 * w;
+                q[h][w] = (uint32_t)(uint8_t)round_half_away(x[0] * id) |
+                          (uint32_t)(uint8_t)round_half_away(x[1] * id) << 8 |
+                          (uint32_t)(uint8_t)round_half_away(x[2] * id) << 16 |
+                          (uint32_t)(uint8_t)round_half_away(x[3] * id) << 24;
+            }
+        if (b + 1 < nb) gather(v, b + 1);
+        __syncthreads();                               // the previous block's fragments are read
+        *(u32x4*)&cs[lane * 32] = q[0];
+        *(u32x4*)&cs[lane * 32 + 16] = q[1];
+        dsc[lane] = d;
+        __syncthreads();
+        int64_t A[4];
+        f32x4 X[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            A[i] = *(const int64_t*)&cs[(16 * i + l16) * 32 + 8 * lg];
+            X[i] = *(const f32x4*)&dsc[16 * i + 4 * lg];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < CT; j++) {
+                const i32x4 I = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[i], B[j], i32x4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float sc = X[i][r] * W[j];
+                    acc[i][j][r] = acc[i][j][r] + sc * (float)I[r];
+                }
+            }
+    }
+    // register r of tile (i, j): pixel 64*blockIdx.x + 16i + 4lg + r, channel 16*(ot0 + j) + l16
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < CT; j++) {
+            const int oc = 16 * (ot0 + j) + l16;
+            if (oc >= a.OC) continue;
+            conv_store(a.out, a.bias, a.resid, ((size_t)n * a.OC + oc) * M, oc, blockIdx.x * 64 + 16 * i + 4 * lg, M,
+                       acc[i][j]);
+        }
+}
+
 // Pass 2: one wave computes RT x CT tiles of 16 pixels x 16 channels straight from the
 // fragment-ordered codes (no LDS, no barriers). Per block, one v_mfma_i32_16x16x32_i8 per tile
 // gives the exact int32 block dots and acc = acc + (dx*dw)*(float)idot, each operation rounded
@@ -338,10 +457,25 @@ hipError_t launch_conv_quant_w(const float* ker, void* wq, int K, int OC, hipStr
     return hipGetLastError();
 }
 
+bool conv_i8_one_pass(int IW, int IH, int IC, int OW, int OH, int OC, int KW, int KH, int N) {
+    // 3 x 3 or 1 x 1 kernels, >= 8 channel tiles and >= 2048 waves of 64 pixels x 128 channels
+    // (measured: 256 x 256 x 128 at 8 images 552 against 803 us for the two passes, 128 x 128,
+    // 256 -> 128 at 8 images 244 against 391; at 1024 waves or fewer the two passes win or tie)
+    const int64_t waves = ((int64_t)OW * OH + 63) / 64 * (((OC + 15) / 16 + 7) / 8) * N;
+    return KW == KH && (KW == 3 || KW == 1) && (int64_t)IC * IW * IH * 4 < ((int64_t)1 << 31) &&
+           (OC + 15) / 16 >= 8 && waves >= 2048;
+}
+
 hipError_t launch_conv2d_i8(const ConvI8Args& a, hipStream_t s) {
     const int M = a.OW * a.OH;
     if (M == 0 || a.OC == 0 || a.N == 0) return hipSuccess;
     const int K = a.IC * a.KW * a.KH, nb = (K + 31) / 32, PT = (M + 15) / 16, OT = (a.OC + 15) / 16;
+    if (conv_i8_one_pass(a.IW, a.IH, a.IC, a.OW, a.OH, a.OC, a.KW, a.KH, a.N)) {
+        const dim3 grid((unsigned)((M + 63) / 64), (unsigned)((OT + 7) / 8), (unsigned)a.N), block(64);
+        if (a.KW == 3) hipLaunchKernelGGL((k_conv_i8_fused<3, 8>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((k_conv_i8_fused<1, 8>), grid, block, 0, s, a);
+        return hipGetLastError();
+    }
     const int ks = a.KW == a.KH && (a.KW == 3 || a.KW == 1) ? a.KW : 0;
     if (ks && (int64_t)a.IC * a.IW * a.IH * 4 < ((int64_t)1 << 31)) {
         // blocks per wave: enough (pixel group, block) pairs for >= 4096 waves

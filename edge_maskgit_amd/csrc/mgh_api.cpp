@@ -794,13 +794,16 @@ int mgh_conv2d_i8(mgh_ctx* c, const float* in, int IW, int IH, int IC, int N, co
     if ((K + 31) / 32 > 4 * 65535 || (OC + 15) / 16 > 65535)
         return fail(c, MGH_ERR_UNSUPPORTED, "conv2d_i8: IC*KW*KH or OC too large");
     if (int r = set_dev(c)) return r;
-    if (int r = ensure_qp_ws(c, mgh::conv_i8_ws_bytes(M, K, N))) return r;
-    const size_t codes = mgh::conv_i8_ws_codes_bytes(M, K, N);
+    int8_t* qa = nullptr;
+    float* dxa = nullptr;
+    if (!mgh::conv_i8_one_pass(IW, IH, IC, (int)OW, (int)OH, OC, KW, KH, N)) {   // two passes: codes in the workspace
+        if (int r = ensure_qp_ws(c, mgh::conv_i8_ws_bytes(M, K, N))) return r;
+        qa = (int8_t*)c->qp_ws;
+        dxa = (float*)(qa + mgh::conv_i8_ws_codes_bytes(M, K, N));
+    }
     const int8_t* qw = (const int8_t*)wq;
     const float* dw = (const float*)((const char*)wq + mgh::conv_i8_codes_bytes(K, OC));
-    int8_t* qa = (int8_t*)c->qp_ws;
-    mgh::ConvI8Args a{in, qw, dw, out, bias, resid, qa, (float*)(qa + codes),
-                      IW, IH, IC, (int)OW, (int)OH, OC, KW, KH, stride, pad, N};
+    mgh::ConvI8Args a{in, qw, dw, out, bias, resid, qa, dxa, IW, IH, IC, (int)OW, (int)OH, OC, KW, KH, stride, pad, N};
     MGH_HIP(c, mgh::launch_conv2d_i8(a, c->stream), "k_conv2d_i8");
     return MGH_OK;
 }

@@ -234,6 +234,8 @@ size_t conv_i8_weight_bytes(int K, int OC);
 size_t conv_i8_ws_codes_bytes(int M, int K, int N);   // the workspace's codes, 256-byte aligned
 size_t conv_i8_ws_bytes(int M, int K, int N);
 hipError_t launch_conv_quant_w(const float* ker, void* wq, int K, int OC, hipStream_t s);
+// true: launch_conv2d_i8 runs the one-pass kernel, which needs no workspace (qa / dxa unused)
+bool conv_i8_one_pass(int IW, int IH, int IC, int OW, int OH, int OC, int KW, int KH, int N);
 hipError_t launch_conv2d_i8(const ConvI8Args& a, hipStream_t s);
 size_t group_norm_ws_bytes(int64_t W, int64_t H, int C, int N, int G);
 hipError_t launch_group_norm(const float* x, int64_t W, int64_t H, int C, int N, int G, float eps,

@@ -341,26 +341,53 @@ def test_conv2d_i8_large_tiles_vs_oracle(ctx):
         ctx.free(b)
 
 
+def test_conv2d_i8_one_pass_vs_oracle(ctx):
+    """32 images of 64 x 64 with 136 output channels take the one-pass kernel (quantizer inside
+    the GEMM, 4096 waves; the second 128-channel tile is partial); K = 144 leaves a partial
+    last block. Bit-exact, with bias and residual."""
+    N, IC, IH, IW, OC = 32, 16, 64, 64, 136
+    print(f"conv2d_i8 one pass N={N} IC={IC} {IH}x{IW} OC={OC}", flush=True)
+    rng = np.random.default_rng(78)
+    x, ker, dX, dK, dQ = _conv_i8_setup(ctx, rng, N, IC, IH, IW, OC, 3)
+    bias = rng.standard_normal(OC).astype(np.float32)
+    res = rng.standard_normal((N, OC, IH, IW)).astype(np.float32)
+    dB, dR, dY = ctx.upload(bias), ctx.upload(res), ctx.alloc(res.nbytes)
+    qw, dw = oracle.conv_quant_w(ker)
+    want = oracle.conv2d_i8(x, qw, dw, 3, 3, 1, 1)
+    ctx.conv2d_i8(dX, IW, IH, IC, N, dQ, 3, 3, OC, 1, 1, None, None, dY)
+    y = ctx.download(dY, res.shape, np.float32)
+    mism = int((y != want).sum())
+    print(f"  {mism} of {y.size} outputs differ from the oracle")
+    assert mism == 0
+    ctx.conv2d_i8(dX, IW, IH, IC, N, dQ, 3, 3, OC, 1, 1, dB, dR, dY)
+    assert np.array_equal(ctx.download(dY, res.shape, np.float32), (want + bias[None, :, None, None]) + res)
+    for b in (dX, dK, dQ, dB, dR, dY):
+        ctx.free(b)
+
+
 # (IW, IH, IC, OC, N, sub-batch): the whole batch and its sub-batches take different GEMM wave
 # tiles and ring depths (4 x 4 with rings of 2 and 4, 4 x 2, 2 x 2 with rings of 4 and 8, 4 x 1
-# with rings of 3 and 6, 2 x 1, 1 x 1); every image's result must be bit-identical
-I8_BATCH = [(64, 64, 256, 256, 8, 1), (64, 64, 256, 256, 8, 4), (128, 128, 128, 128, 16, 1),
-            (128, 128, 128, 3, 16, 4), (96, 64, 64, 256, 2, 1), (32, 32, 512, 512, 4, 1)]
+# with rings of 3 and 6, 2 x 1, 1 x 1) or the one-pass kernel (3 x 3 and 1 x 1; 5 x 5 stays on
+# two passes); every image's result must be bit-identical
+I8_BATCH = [(64, 64, 256, 256, 8, 1, 3), (64, 64, 256, 256, 8, 4, 3), (128, 128, 128, 128, 16, 1, 3),
+            (128, 128, 128, 3, 16, 4, 3), (96, 64, 64, 256, 2, 1, 3), (32, 32, 512, 512, 4, 1, 3),
+            (128, 128, 256, 128, 16, 4, 1), (128, 128, 256, 64, 16, 1, 1), (128, 128, 16, 128, 16, 4, 5)]
 
 
-@pytest.mark.parametrize("IW,IH,IC,OC,N,sub", I8_BATCH)
-def test_conv2d_i8_batch_invariant(ctx, IW, IH, IC, OC, N, sub):
-    print(f"conv2d_i8 batch invariance {IW}x{IH} IC={IC} OC={OC} N={N} in groups of {sub}", flush=True)
-    rng = np.random.default_rng(IW + IC + OC + N)
-    x, ker, dX, dK, dQ = _conv_i8_setup(ctx, rng, N, IC, IH, IW, OC, 3)
+@pytest.mark.parametrize("IW,IH,IC,OC,N,sub,k", I8_BATCH)
+def test_conv2d_i8_batch_invariant(ctx, IW, IH, IC, OC, N, sub, k):
+    print(f"conv2d_i8 batch invariance {IW}x{IH} IC={IC} OC={OC} k={k} N={N} in groups of {sub}", flush=True)
+    rng = np.random.default_rng(IW + IC + OC + N + k)
+    x, ker, dX, dK, dQ = _conv_i8_setup(ctx, rng, N, IC, IH, IW, OC, k)
     M = IW * IH
+    pad = k // 2
     dY = ctx.alloc(N * OC * M * 4)
-    ctx.conv2d_i8(dX, IW, IH, IC, N, dQ, 3, 3, OC, 1, 1, None, None, dY)
+    ctx.conv2d_i8(dX, IW, IH, IC, N, dQ, k, k, OC, 1, pad, None, None, dY)
     whole = ctx.download(dY, (N, OC, IH, IW), np.float32)
     for g in range(0, N, sub):
         dXg = ctx.upload(np.ascontiguousarray(x[g:g + sub]))
         dYg = ctx.alloc(sub * OC * M * 4)
-        ctx.conv2d_i8(dXg, IW, IH, IC, sub, dQ, 3, 3, OC, 1, 1, None, None, dYg)
+        ctx.conv2d_i8(dXg, IW, IH, IC, sub, dQ, k, k, OC, 1, pad, None, None, dYg)
         part = ctx.download(dYg, (sub, OC, IH, IW), np.float32)
         assert np.array_equal(part, whole[g:g + sub]), f"images {g}..{g + sub - 1} differ"
         ctx.free(dXg)
