@@ -341,25 +341,27 @@ def test_conv2d_i8_large_tiles_vs_oracle(ctx):
         ctx.free(b)
 
 
-def test_conv2d_i8_one_pass_vs_oracle(ctx):
-    """32 images of 64 x 64 with 136 output channels take the one-pass kernel (quantizer inside
-    the GEMM, 4096 waves; the second 128-channel tile is partial); K = 144 leaves a partial
-    last block. Bit-exact, with bias and residual."""
-    N, IC, IH, IW, OC = 32, 16, 64, 64, 136
-    print(f"conv2d_i8 one pass N={N} IC={IC} {IH}x{IW} OC={OC}", flush=True)
-    rng = np.random.default_rng(78)
+@pytest.mark.parametrize("N,IC,IH,IW,OC,stride,pad", [(32, 16, 64, 64, 136, 1, 1), (16, 16, 64, 64, 1024, 2, 0)])
+def test_conv2d_i8_one_pass_vs_oracle(ctx, N, IC, IH, IW, OC, stride, pad):
+    """Shapes that take the one-pass kernel (quantizer inside the GEMM, >= 2048 waves): 32 images
+    of 64 x 64 with 136 output channels (the second 128-channel tile is partial), and stride 2
+    without padding (31 x 31 outputs, a ragged last pixel group); K = 144 leaves a partial last
+    block. Bit-exact, with bias and residual."""
+    print(f"conv2d_i8 one pass N={N} IC={IC} {IH}x{IW} OC={OC} stride={stride} pad={pad}", flush=True)
+    rng = np.random.default_rng(78 + stride)
     x, ker, dX, dK, dQ = _conv_i8_setup(ctx, rng, N, IC, IH, IW, OC, 3)
+    OH, OW = (IH + 2 * pad - 3) // stride + 1, (IW + 2 * pad - 3) // stride + 1
     bias = rng.standard_normal(OC).astype(np.float32)
-    res = rng.standard_normal((N, OC, IH, IW)).astype(np.float32)
+    res = rng.standard_normal((N, OC, OH, OW)).astype(np.float32)
     dB, dR, dY = ctx.upload(bias), ctx.upload(res), ctx.alloc(res.nbytes)
     qw, dw = oracle.conv_quant_w(ker)
-    want = oracle.conv2d_i8(x, qw, dw, 3, 3, 1, 1)
-    ctx.conv2d_i8(dX, IW, IH, IC, N, dQ, 3, 3, OC, 1, 1, None, None, dY)
+    want = oracle.conv2d_i8(x, qw, dw, 3, 3, stride, pad)
+    ctx.conv2d_i8(dX, IW, IH, IC, N, dQ, 3, 3, OC, stride, pad, None, None, dY)
     y = ctx.download(dY, res.shape, np.float32)
     mism = int((y != want).sum())
     print(f"  {mism} of {y.size} outputs differ from the oracle")
     assert mism == 0
-    ctx.conv2d_i8(dX, IW, IH, IC, N, dQ, 3, 3, OC, 1, 1, dB, dR, dY)
+    ctx.conv2d_i8(dX, IW, IH, IC, N, dQ, 3, 3, OC, stride, pad, dB, dR, dY)
     assert np.array_equal(ctx.download(dY, res.shape, np.float32), (want + bias[None, :, None, None]) + res)
     for b in (dX, dK, dQ, dB, dR, dY):
         ctx.free(b)
