@@ -199,9 +199,17 @@ __device__ __forceinline__ f16x4 load_h4(const float* p32, const _Float16* p16, 
     const f32x4 v = *(const f32x4*)(p32 + e);
     return f16x4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
 }
+// 8 consecutive elements (e % 8 == 0): one 16-byte load of fp16 rows when they are 16-byte
+// aligned (A16), two 8-byte loads otherwise; fp32 rows as two 16-byte loads, rounded
+template <bool I16, bool A16>
+__device__ __forceinline__ f16x8 load_h8(const float* p32, const _Float16* p16, int64_t e) {
+    if (I16 && A16) return *(const f16x8*)(p16 + e);
+    return cat8(load_h4<I16>(p32, p16, e), load_h4<I16>(p32, p16, e + 4));
+}
 
-// TAIL: S > 16 (KT - 1), so every key tile but the last is full (no masking there)
-template <int DC, int KT, bool I16, bool TAIL>
+// TAIL: S > 16 (KT - 1), so every key tile but the last is full (no masking there).
+// A16: fp16 inputs whose rows start on 16-byte boundaries (element strides multiples of 8).
+template <int DC, int KT, bool I16, bool TAIL, bool A16>
 __global__ __launch_bounds__(64 * kHeadWaves<KT>) void k_attn_head(FaArgs a) {
     constexpr int D = 16 * DC;
     constexpr int KLD = D + 8;         // K row stride (halves)
@@ -216,49 +224,59 @@ __global__ __launch_bounds__(64 * kHeadWaves<KT>) void k_attn_head(FaArgs a) {
     const int h = blockIdx.x, b = blockIdx.y;
     const int64_t base = (int64_t)b * a.st[3] + (int64_t)h * a.st[2];
 
-    // K row-major: one float4 of a key row per task. V transposed: a task loads a 4-key x
-    // 4-d block and stores it as four 8-byte rows of V^T.
-    // The staging is latency-bound (one workgroup per CU at typical shapes): each thread
-    // issues UK (K) or 4 x UV (V) loads before it stores any, so a few round trips fill LDS.
-    constexpr int KTASK = SP * (D / 4), VTASK = (SP / 4) * (D / 4);
-    constexpr int UK = 8, UV = 2;
-    for (int i0 = tid; i0 < KTASK; i0 += UK * blockDim.x) {
-        f16x4 kv[UK];
+    // The staging is latency-bound (one workgroup per CU at typical shapes), so each round
+    // issues all of a thread's K and V loads before it stores any, and the first query tile's
+    // Q is requested with them: at the usual shapes one round trip fills LDS.
+    // K row-major: a task moves 8 elements of a key row. V transposed: a task loads an
+    // 8-key x 8-d block and stores it as eight 16-byte rows of V^T.
+    constexpr int DW = D / 8;
+    constexpr int KTASK = SP * DW, VTASK = (SP / 8) * DW;
+    constexpr int UK = 8;              // K tasks per thread and round (one V task: 8 loads)
+    static_assert(KTASK == UK * VTASK, "one V task per UK K tasks");
+
+    const int nqt = (S + 15) / 16;
+    const int qstep = nw * gridDim.z;
+    int qt = blockIdx.z * nw + wave;   // workgroup z takes query tiles z*nw + wave, + qstep, ...
+    // Q as the B operand: lane = query 16t + l16, k = d = 16c + 4lg + j
+    f16x4 qf[DC];
+    auto load_q = [&](int t) {
+        const int qi = min(16 * t + l16, S - 1);
+        const int64_t qrow = base + (int64_t)qi * a.st[1];
+#pragma unroll
+        for (int c = 0; c < DC; c++) qf[c] = load_h4<I16>(a.q, a.q16, qrow + 16 * c + 4 * lg);
+    };
+    if (qt < nqt) load_q(qt);
+
+    // rounds are workgroup-uniform: round r0 takes K tasks UK*r0 .. UK*(r0 + nth) - 1 and V
+    // tasks r0 .. r0 + nth - 1
+    for (int r0 = 0; r0 < VTASK; r0 += blockDim.x) {
+        f16x8 kv[UK], vv[8];
+        const f16x8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
+        const int iv = r0 + tid, kg = iv / DW, dv = 8 * (iv - kg * DW);
 #pragma unroll
         for (int u = 0; u < UK; u++) {
-            const int idx = i0 + u * blockDim.x;
-            const int t = idx / (D / 4), d = 4 * (idx - t * (D / 4));
-            kv[u] = f16x4{0, 0, 0, 0};
-            if (idx < KTASK && t < S) kv[u] = load_h4<I16>(a.k, a.k16, base + (int64_t)t * a.st[1] + d);
+            const int idx = UK * r0 + u * blockDim.x + tid;
+            const int t = idx / DW, d = 8 * (idx - t * DW);
+            kv[u] = z8;
+            if (idx < KTASK && t < S) kv[u] = load_h8<I16, A16>(a.k, a.k16, base + (int64_t)t * a.st[1] + d);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int t = 8 * kg + i;
+            vv[i] = z8;
+            if (iv < VTASK && t < S) vv[i] = load_h8<I16, A16>(a.v, a.v16, base + (int64_t)t * a.st[1] + dv);
         }
 #pragma unroll
         for (int u = 0; u < UK; u++) {
-            const int idx = i0 + u * blockDim.x;
-            const int t = idx / (D / 4), d = 4 * (idx - t * (D / 4));
-            if (idx < KTASK) *(f16x4*)&Ks[t * KLD + d] = kv[u];
+            const int idx = UK * r0 + u * blockDim.x + tid;
+            const int t = idx / DW, d = 8 * (idx - t * DW);
+            if (idx < KTASK) *(f16x8*)&Ks[t * KLD + d] = kv[u];
         }
-    }
-    for (int i0 = tid; i0 < VTASK; i0 += UV * blockDim.x) {
-        f16x4 vv[UV][4];
+        if (iv < VTASK) {
 #pragma unroll
-        for (int u = 0; u < UV; u++) {
-            const int idx = i0 + u * blockDim.x;
-            const int kg = idx / (D / 4), d = 4 * (idx - kg * (D / 4));
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int t = 4 * kg + i;
-                vv[u][i] = f16x4{0, 0, 0, 0};
-                if (idx < VTASK && t < S) vv[u][i] = load_h4<I16>(a.v, a.v16, base + (int64_t)t * a.st[1] + d);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < UV; u++) {
-            const int idx = i0 + u * blockDim.x;
-            const int kg = idx / (D / 4), d = 4 * (idx - kg * (D / 4));
-            if (idx >= VTASK) continue;
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                *(f16x4*)&Vt[(d + j) * VT + 4 * kg] = f16x4{vv[u][0][j], vv[u][1][j], vv[u][2][j], vv[u][3][j]};
+            for (int j = 0; j < 8; j++)
+                *(f16x8*)&Vt[(dv + j) * VT + 8 * kg] = f16x8{vv[0][j], vv[1][j], vv[2][j], vv[3][j],
+                                                            vv[4][j], vv[5][j], vv[6][j], vv[7][j]};
         }
     }
     __syncthreads();
@@ -266,18 +284,8 @@ __global__ __launch_bounds__(64 * kHeadWaves<KT>) void k_attn_head(FaArgs a) {
     // scores in log2 units: exp(s*scale - max) = exp2(s*scale*log2(e) - max'), evaluated with
     // the hardware exp2 (v_exp_f32, ~1 ulp)
     const float scale2 = a.scale * 1.4426950408889634f;
-    const int nqt = (S + 15) / 16;
-    // workgroup z of gridDim.z takes query tiles z*nw + wave, + nw*gridDim.z, ...
-    for (int qt = blockIdx.z * nw + wave; qt < nqt; qt += nw * gridDim.z) {
+    for (; qt < nqt; qt += qstep) {
         const int q0 = 16 * qt;
-        // Q as the B operand: lane = query q0 + l16, k = d = 16c + 4lg + j
-        f16x4 qf[DC];
-        {
-            const int qi = min(q0 + l16, S - 1);
-            const int64_t qrow = base + (int64_t)qi * a.st[1];
-#pragma unroll
-            for (int c = 0; c < DC; c++) qf[c] = load_h4<I16>(a.q, a.q16, qrow + 16 * c + 4 * lg);
-        }
         // scores: register r of key tile t holds key 16t + 4lg + r of query q0 + l16
         f32x4 sc[KT];
         float mx = -INFINITY;
@@ -309,6 +317,8 @@ __global__ __launch_bounds__(64 * kHeadWaves<KT>) void k_attn_head(FaArgs a) {
         }
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // the scores are done with Q: request the next tile's while this one's P . V runs
+        if (qt + qstep < nqt) load_q(qt + qstep);
         // scale2 > 0 (checked at launch), so the max of the scaled scores is the scaled max;
         // p = exp2(s * scale2 - max) as one fma, and exp2(-inf) = 0 for the masked keys
         const float mxs = mx * scale2;
@@ -398,12 +408,17 @@ void launch_head_t(const FaArgs& a, hipStream_t s) {
     if (qs > 1) qs = (nqt + nw - 1) / nw;
     const dim3 grid((unsigned)a.H, (unsigned)a.B, (unsigned)qs), block((unsigned)(64 * nw));
     const bool tail = a.S > 16 * (KT - 1);
-    if (a.q16) {
-        if (tail) hipLaunchKernelGGL((k_attn_head<DC, KT, true, true>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((k_attn_head<DC, KT, true, false>), grid, block, 0, s, a);
+    // fp16 rows 16-byte aligned (the pointers are, head_ok): one load per 8 elements
+    const bool a16 = a.st[1] % 8 == 0 && a.st[2] % 8 == 0 && a.st[3] % 8 == 0;
+    if (a.q16 && a16) {
+        if (tail) hipLaunchKernelGGL((k_attn_head<DC, KT, true, true, true>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((k_attn_head<DC, KT, true, false, true>), grid, block, 0, s, a);
+    } else if (a.q16) {
+        if (tail) hipLaunchKernelGGL((k_attn_head<DC, KT, true, true, false>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((k_attn_head<DC, KT, true, false, false>), grid, block, 0, s, a);
     } else {
-        if (tail) hipLaunchKernelGGL((k_attn_head<DC, KT, false, true>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((k_attn_head<DC, KT, false, false>), grid, block, 0, s, a);
+        if (tail) hipLaunchKernelGGL((k_attn_head<DC, KT, false, true, false>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((k_attn_head<DC, KT, false, false, false>), grid, block, 0, s, a);
     }
 }
 

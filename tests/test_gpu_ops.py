@@ -181,16 +181,19 @@ def test_flash_attn_o16_is_rounded_output(ctx, S):
     assert np.array_equal(h.view(np.uint16), o.astype(np.float16).view(np.uint16))
 
 
-@pytest.mark.parametrize("D,S,H,B", [(48, 257, 16, 2), (48, 1, 2, 1), (64, 130, 4, 1), (32, 512, 2, 1)])
-def test_flash_attn_f16in_equals_rounded_inputs(ctx, D, S, H, B):
+@pytest.mark.parametrize("D,S,H,B,pad", [(48, 257, 16, 2, 0), (48, 1, 2, 1, 0), (64, 130, 4, 1, 0), (32, 512, 2, 1, 0),
+                                         (48, 257, 4, 2, 4), (16, 33, 1, 3, 4), (64, 512, 2, 1, 12)])
+def test_flash_attn_f16in_equals_rounded_inputs(ctx, D, S, H, B, pad):
     """The fp16-input variant on q/k/v rounded to fp16 gives the same bits as the fp32-input
     attention (which rounds its inputs to fp16 on load), for both output types, with q/k/v
-    read through the strides of one wide [S*B][3*H*D] buffer (the fused QKV output)."""
-    print(f"flash_attn_f16in D={D} S={S} H={H} B={B}", flush=True)
+    read through the strides of one wide [S*B][3*H*D + pad] buffer (the fused QKV output; a
+    pad of 4 or 12 halves leaves fp16 rows 8-byte but not 16-byte aligned)."""
+    print(f"flash_attn_f16in D={D} S={S} H={H} B={B} pad={pad}", flush=True)
     rng = np.random.default_rng(7 * D + S)
     E = H * D
-    wide = rng.standard_normal((B * S, 3 * E)).astype(np.float16)
-    st = (1, 3 * E, D, 3 * E * S)
+    R = 3 * E + pad
+    wide = rng.standard_normal((B * S, R)).astype(np.float16)
+    st = (1, R, D, R * S)
     ost = (1, E, D, E * S)
     d32 = ctx.upload(wide.astype(np.float32))
     d16 = ctx.upload(wide)
