@@ -37,7 +37,7 @@ MGH_SYMBOLS = [
     "mgh_layernorm_affine", "mgh_flash_attn_f16kv", "mgh_gemm_f32", "mgh_get_rows", "mgh_add",
     "mgh_copy_strided", "mgh_decode_state_bytes", "mgh_decode_work_bytes", "mgh_decode_init",
     "mgh_decode_step", "mgh_packed_weight_bytes_f16", "mgh_pack_weights_f16", "mgh_f32_to_f16",
-    "mgh_gemm_h16", "mgh_gemm_h16_f32in", "mgh_gemm_h16_y16", "mgh_flash_attn_f16kv_o16", "mgh_flash_attn_f16in",
+    "mgh_gemm_h16", "mgh_gemm_h16_f32in", "mgh_gemm_h16_y16", "mgh_gemm_h16_ln", "mgh_flash_attn_f16kv_o16", "mgh_flash_attn_f16in",
     "mgh_softmax", "mgh_binary", "mgh_scale", "mgh_unary", "mgh_gemm_f32_batched",
     "mgh_gemm_h16_f32in_noalloc", "mgh_conv2d", "mgh_group_norm", "mgh_upscale", "mgh_conv2d_ex",
     "mgh_conv2d_packed_bytes", "mgh_conv2d_pack_weights", "mgh_conv2d_i8_weight_bytes",
@@ -105,6 +105,7 @@ def lib():
         L.mgh_gemm_h16.argtypes = [P, P, I, I, P, I, P, I, P, P]
         L.mgh_gemm_h16_f32in.argtypes = [P, P, I, I, P, I, P, I, P, P]
         L.mgh_gemm_h16_y16.argtypes = [P, P, I, I, P, I, P, I, P, P]
+        L.mgh_gemm_h16_ln.argtypes = [P, P, I, I, P, I, P, I, P, P, P, P, ctypes.c_float, P, I, P, P, P]
         L.mgh_gemm_h16_f32in_noalloc.argtypes = [P, P, I, I, P, I, P, I, P, P]
         L.mgh_flash_attn_f16kv_o16.argtypes = [P, P, P, P, P, I, I, I, I, ctypes.c_float, P, P]
         L.mgh_flash_attn_f16in.argtypes = [P, P, P, P, P, I, I, I, I, ctypes.c_float, P, P, P]
@@ -319,6 +320,14 @@ class Context:
     def gemm_h16(self, wp16, N, K, x16, M, bias, act, resid, y):
         P = self._ptr
         self._check(lib().mgh_gemm_h16(self.h, P(wp16), N, K, P(x16), M, P(bias), act, P(resid), P(y)))
+
+    def gemm_h16_ln(self, wp16, N, K, x16, M, bias, act, resid, y, gamma, beta, eps, y_ln, emit=0, codes=None,
+                    dx=None, s4=None):
+        """gemm_h16 into y, then the LayerNorm-affine of y's rows into y_ln (and the emitted
+        operand), as gemm_h16 followed by layernorm_affine(y)."""
+        P = self._ptr
+        self._check(lib().mgh_gemm_h16_ln(self.h, P(wp16), N, K, P(x16), M, P(bias), act, P(resid), P(y), P(gamma),
+                                          P(beta), eps, P(y_ln), emit, P(codes), P(dx), P(s4)))
 
     def gemm_h16_y16(self, wp16, N, K, x16, M, bias, act, resid, y16):
         P = self._ptr

@@ -36,6 +36,7 @@
 
 #include "mgh_common.h"
 #include "mgh_kernels.h"
+#include "k_ln_row.h"
 
 namespace mgh {
 
@@ -371,6 +372,20 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
     }
 }
 
+// One float4 of a split-K output: the splits' partials in split order, then +bias -> act ->
+// +resid (part: the float4 in split 0's partial tile; the next split's is q_stride further)
+template <int ACT>
+__device__ __forceinline__ f32x4 split_sum4(const f32x4* part, size_t q_stride, int splits, const float* bias,
+                                            int n, const float* resid, size_t o) {
+    f32x4 v = __builtin_nontemporal_load(part);
+    for (int k = 1; k < splits; k++) v += __builtin_nontemporal_load(part + (size_t)k * q_stride);
+    if (bias) v += *(const f32x4*)(bias + n);
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = act_h<ACT>(v[e]);
+    if (resid) v += *(const f32x4*)(resid + o);
+    return v;
+}
+
 // Split-K epilogue: one thread per output float4; sums the splits' row-major partial tiles in
 // split order, then +bias -> act -> +resid.
 template <int ACT, int BM, int BN>
@@ -387,19 +402,87 @@ __global__ __launch_bounds__(256) void k_gemm_h16_reduce(GemmH16Args g) {
     tile_origin(lt, tiles_m, tiles_n, BM, BN, g.ph, m0, n0);
     const int m = m0 + r, n = n0 + c;
     if (m >= M || n >= N) return;
-    const f32x4* part = (const f32x4*)(g.ws + (size_t)lt * splits * BM * BN) + q;
-    f32x4 v = __builtin_nontemporal_load(part);
-    for (int k = 1; k < splits; k++) v += __builtin_nontemporal_load(part + (size_t)k * Q);
-    if (g.bias) v += *(const f32x4*)(g.bias + n);
-#pragma unroll
-    for (int e = 0; e < 4; e++) v[e] = act_h<ACT>(v[e]);
     const size_t o = (size_t)m * N + n;
-    if (g.resid) v += *(const f32x4*)(g.resid + o);
+    const f32x4 v = split_sum4<ACT>((const f32x4*)(g.ws + (size_t)lt * splits * BM * BN) + q, Q, splits, g.bias, n,
+                                    g.resid, o);
     if (g.y16)
         __builtin_nontemporal_store(f16x4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]},
                                     (f16x4*)(g.y16 + o));
     else
         __builtin_nontemporal_store(v, (f32x4*)(g.y + o));
+}
+
+// Split-K epilogue followed by the LayerNorm-affine of each output row (N = 256 C, no
+// activation): one wave per row sums the row's float4s with k_gemm_h16_reduce's arithmetic,
+// stores them to y and normalizes the row from registers with the LayerNorm kernel's own
+// code (ln_affine_row), so y and every LayerNorm output equal those of k_gemm_h16_reduce
+// followed by k_layernorm_affine on y, in one launch.
+template <int C, int EMIT>
+__global__ __launch_bounds__(256) void k_gemm_h16_reduce_ln(GemmH16Args g, int bm, int bn, LnArgs ln) {
+    const int M = g.M, N = g.N, splits = g.splits;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= M) return;                       // whole wave exits together
+    const int tiles_m = (M + bm - 1) / bm, tiles_n = (N + bn - 1) / bn;
+    const int tm = row / bm, r = row - tm * bm;
+    // the logical tile of (tm, tn): the inverse of tile_origin's panel order
+    const int panel = tm / g.ph, pm = min(g.ph, tiles_m - panel * g.ph);
+    const size_t tile = (size_t)bm * bn, q_stride = tile / 4;
+    // every partial of a round (up to KB splits x C float4s), the bias and the residual are
+    // requested before any is summed: a few round trips per row, not one per split and chunk
+    constexpr int KB = 4;
+    const f32x4* pc[C];
+    f32x4 v[C], bb[C], rb[C];
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        const int n = 4 * (lane + 64 * c);
+        const int tn = n / bn;
+        const int lt = panel * g.ph * tiles_n + (tm - panel * g.ph) + pm * tn;
+        pc[c] = (const f32x4*)(g.ws + (size_t)lt * splits * tile + (size_t)r * bn + (n - tn * bn));
+        v[c] = bb[c] = rb[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (g.bias) bb[c] = *(const f32x4*)(g.bias + n);
+        if (g.resid) rb[c] = *(const f32x4*)(g.resid + (size_t)row * N + n);
+    }
+    for (int k0 = 0; k0 < splits; k0 += KB) {
+        f32x4 pv[KB][C];
+#pragma unroll
+        for (int kk = 0; kk < KB; kk++)
+            if (k0 + kk < splits)
+#pragma unroll
+                for (int c = 0; c < C; c++) pv[kk][c] = __builtin_nontemporal_load(pc[c] + (size_t)(k0 + kk) * q_stride);
+        // split order per element, as split_sum4: v = p0, then v + p1, v + p2, ...
+#pragma unroll
+        for (int kk = 0; kk < KB; kk++)
+            if (k0 + kk < splits)
+#pragma unroll
+                for (int c = 0; c < C; c++) v[c] = k0 + kk == 0 ? pv[kk][c] : v[c] + pv[kk][c];
+    }
+    // then +bias -> +resid (no activation), each rounded, as split_sum4<0>
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        if (g.bias) v[c] += bb[c];
+        if (g.resid) v[c] += rb[c];
+        __builtin_nontemporal_store(v[c], (f32x4*)(g.y + (size_t)row * N + 4 * (lane + 64 * c)));
+    }
+    ln_affine_row<C, EMIT>(v, lane, row, ln.gamma, ln.beta, ln.y, ln.eps, ln.codes, ln.dx, ln.s4);
+}
+
+template <int EMIT>
+hipError_t launch_reduce_ln_e(const GemmH16Args& a, int bm, int bn, const LnArgs& ln, hipStream_t s) {
+    const dim3 grid((unsigned)((a.M + 3) / 4)), block(256);
+    switch (a.N / 256) {
+#define MGH_RLN(CV)                                                                                       \
+    case CV: hipLaunchKernelGGL((k_gemm_h16_reduce_ln<CV, EMIT>), grid, block, 0, s, a, bm, bn, ln); break;
+        MGH_RLN(1) MGH_RLN(2) MGH_RLN(3) MGH_RLN(4) MGH_RLN(5) MGH_RLN(6) MGH_RLN(7) MGH_RLN(8)
+#undef MGH_RLN
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_reduce_ln(const GemmH16Args& a, int bm, int bn, const LnArgs& ln, hipStream_t s) {
+    if (ln.emit == 1) return launch_reduce_ln_e<1>(a, bm, bn, ln, s);
+    if (ln.emit == 2) return launch_reduce_ln_e<2>(a, bm, bn, ln, s);
+    return launch_reduce_ln_e<0>(a, bm, bn, ln, s);
 }
 
 // Skinny-M FC (M <= 16 * MT, decode- and GEMV-shaped calls): one workgroup per 16 weight rows,
@@ -601,12 +684,13 @@ hipError_t launch_f32_to_f16(const float* x, _Float16* h, int64_t n, hipStream_t
 }
 
 template <int BM, bool XF32, int NS, int WMR, int BN>
-static hipError_t launch_h16_t(const GemmH16Args& a, hipStream_t s) {
+static hipError_t launch_h16_t(const GemmH16Args& a, hipStream_t s, const LnArgs* ln) {
     const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     const int splits = std::max(a.splits, 1);
     const dim3 block(128 * WMR);
     if (splits > 1) {
         hipLaunchKernelGGL((k_gemm_h16<0, BM, true, XF32, NS, WMR, BN>), dim3(tiles * splits), block, 0, s, a);
+        if (ln) return launch_reduce_ln(a, BM, BN, *ln, s);
         const size_t n4 = (size_t)tiles * BM * BN / 4;
         const dim3 rg((unsigned)((n4 + 255) / 256)), rb(256);
         if (a.act == 1) hipLaunchKernelGGL((k_gemm_h16_reduce<1, BM, BN>), rg, rb, 0, s, a);
@@ -620,19 +704,21 @@ static hipError_t launch_h16_t(const GemmH16Args& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a0, hipStream_t s) {
+hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a0, hipStream_t s, const LnArgs* ln) {
     GemmH16Args a = a0;
     a.ph = p.ph;
     const bool xf = a.xf != nullptr;
     if (p.wmr != 2) return hipErrorInvalidValue;
+    // the reduce takes the LayerNorm only when K is split, without activation or fp16 output
+    if (ln && (p.splits < 2 || a.act != 0 || a.y16 || !a.y || a.N % 256 || a.N > 2048)) return hipErrorInvalidValue;
     if (p.bn == 128 && p.ns == 2) {
-        if (p.bm == 128 && !xf) return launch_h16_t<128, false, 2, 2, 128>(a, s);
-        if (p.bm == 64) return xf ? launch_h16_t<64, true, 2, 2, 128>(a, s) : launch_h16_t<64, false, 2, 2, 128>(a, s);
+        if (p.bm == 128 && !xf) return launch_h16_t<128, false, 2, 2, 128>(a, s, ln);
+        if (p.bm == 64) return xf ? launch_h16_t<64, true, 2, 2, 128>(a, s, ln) : launch_h16_t<64, false, 2, 2, 128>(a, s, ln);
     }
-    if (p.bn == 128 && p.ns == 3 && p.bm == 64 && !xf) return launch_h16_t<64, false, 3, 2, 128>(a, s);
+    if (p.bn == 128 && p.ns == 3 && p.bm == 64 && !xf) return launch_h16_t<64, false, 3, 2, 128>(a, s, ln);
     if (p.bn == 64 && p.ns == 3) {
-        if (p.bm == 64) return xf ? launch_h16_t<64, true, 3, 2, 64>(a, s) : launch_h16_t<64, false, 3, 2, 64>(a, s);
-        if (p.bm == 32) return xf ? launch_h16_t<32, true, 3, 2, 64>(a, s) : launch_h16_t<32, false, 3, 2, 64>(a, s);
+        if (p.bm == 64) return xf ? launch_h16_t<64, true, 3, 2, 64>(a, s, ln) : launch_h16_t<64, false, 3, 2, 64>(a, s, ln);
+        if (p.bm == 32) return xf ? launch_h16_t<32, true, 3, 2, 64>(a, s, ln) : launch_h16_t<32, false, 3, 2, 64>(a, s, ln);
     }
     return hipErrorInvalidValue;
 }

@@ -12,38 +12,18 @@
 // sum separately), and the sqrt/reciprocal are rounded correctly.
 //
 // Every LN output in the transformer feeds a quantized FC GEMM (and is kept in fp32 as the
-// next residual). EMIT selects the operand written alongside y:
-//   0: none;
-//   1: int8-dot operand of k_gemm_qp — the k_quantize_act_q8 rule (mg-opencl.cpp:424-434)
-//      applied to y: fp16 codes [rows][D], dx [rows][D/32], sx [rows][D/32];
-//   2: dequant-fp16 operand — y rounded to fp16, unit dx, ux = fp32 block sums of the
-//      rounded values (k_round_act_f16's output).
-// Layout: one wave per row; lane l holds float4 chunks c = 0..C-1 at element 4*(l + 64c),
-// so the 8 lanes of a 32-element block are adjacent (xor-shuffle block reductions).
-// HBM-bound: 4 B read + 4 B written per element (+2 + 8/32 B with an emitted operand).
+// next residual). EMIT selects the operand written alongside y (k_ln_row.h): none, the
+// int8-dot operand of k_gemm_qp, or the fp16-rounded y of the dequantize-fused path.
+// Layout: one wave per row (ln_affine_row, shared with the split-K reduce that feeds a
+// LayerNorm). HBM-bound: 4 B read + 4 B written per element (+2 + 8/32 B with an emitted
+// operand).
 #include "mgh_common.h"
 #include "mgh_kernels.h"
+#include "k_ln_row.h"
 
 namespace mgh {
 
 namespace {
-
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-
-// xor-butterfly sum of a double over the wave; the two 32-bit halves are shuffled
-// explicitly so no overload can narrow the value
-__device__ __forceinline__ double shfl_xor_d(double v, int o) {
-    const uint64_t u = __builtin_bit_cast(uint64_t, v);
-    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)u, o);
-    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(u >> 32), o);
-    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
-}
-
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += shfl_xor_d(v, o);
-    return v;
-}
 
 template <int C, int EMIT>
 __global__ __launch_bounds__(256) void k_layernorm_affine(const float* __restrict__ x,
@@ -53,7 +33,6 @@ __global__ __launch_bounds__(256) void k_layernorm_affine(const float* __restric
                                                           void* __restrict__ codes,
                                                           float* __restrict__ dx,
                                                           void* __restrict__ s4) {
-#pragma clang fp contract(off)   // y = v*gamma + beta rounds twice, as in the reference
     constexpr int D = 256 * C;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -62,70 +41,7 @@ __global__ __launch_bounds__(256) void k_layernorm_affine(const float* __restric
     f32x4 v[C];
 #pragma unroll
     for (int c = 0; c < C; c++) v[c] = *(const f32x4*)(xr + 4 * (lane + 64 * c));
-    double s = 0.0;
-#pragma unroll
-    for (int c = 0; c < C; c++) s += ((double)v[c].x + (double)v[c].y) + ((double)v[c].z + (double)v[c].w);
-    const double mean = wave_sum_d(s) / (double)D;
-    double q = 0.0;
-#pragma unroll
-    for (int c = 0; c < C; c++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const double d = (double)v[c][e] - mean;
-            q += d * d;
-        }
-    const double var = wave_sum_d(q) / (double)D;
-    // 1/sqrt in fp32 with each step correctly rounded, as the reference CPU computes it: the
-    // fp32 sqrt and divide are evaluated in double and rounded once to fp32 (exact for sqrt
-    // and division since 53 >= 2*24 + 2); the device's fp32 sqrt is not correctly rounded.
-    const float sq = (float)sqrt((double)__fadd_rn((float)var, eps));
-    const float inv = (float)(1.0 / (double)sq);
-    float* yr = y + (size_t)row * D;
-#pragma unroll
-    for (int c = 0; c < C; c++) {
-        const int k = 4 * (lane + 64 * c);
-        const f32x4 g = *(const f32x4*)(gamma + k);
-        const f32x4 b = *(const f32x4*)(beta + k);
-        f32x4 o;
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            o[e] = (float)((double)v[c][e] - mean) * inv * g[e] + b[e];
-        __builtin_nontemporal_store(o, (f32x4*)(yr + k));   // streamed: read again layers later
-        if (EMIT == 1) {
-            // k_quantize_act_q8 on the 32-element block of lanes 8j..8j+7
-            float a = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
-            a = fmaxf(a, __shfl_xor(a, 1));
-            a = fmaxf(a, __shfl_xor(a, 2));
-            a = fmaxf(a, __shfl_xor(a, 4));
-            const float d = a / 127.0f;
-            const float id = d > 0.0f ? 1.0f / d : 0.0f;
-            const int q0 = (int)roundf(o.x * id), q1 = (int)roundf(o.y * id);
-            const int q2 = (int)roundf(o.z * id), q3 = (int)roundf(o.w * id);
-            int sq = q0 + q1 + q2 + q3;
-            sq += __shfl_xor(sq, 1);
-            sq += __shfl_xor(sq, 2);
-            sq += __shfl_xor(sq, 4);
-            *(f16x4*)((_Float16*)codes + (size_t)row * D + k) =
-                f16x4{(_Float16)q0, (_Float16)q1, (_Float16)q2, (_Float16)q3};
-            if ((lane & 7) == 0) {
-                const size_t blk = (size_t)row * (D / 32) + (k >> 5);
-                dx[blk] = d;
-                ((int32_t*)s4)[blk] = sq;
-            }
-        } else if (EMIT == 2) {
-            const f16x4 h = {(_Float16)o.x, (_Float16)o.y, (_Float16)o.z, (_Float16)o.w};
-            float su = ((float)h.x + (float)h.y) + ((float)h.z + (float)h.w);
-            su += __shfl_xor(su, 1);
-            su += __shfl_xor(su, 2);
-            su += __shfl_xor(su, 4);
-            __builtin_nontemporal_store(h, (f16x4*)((_Float16*)codes + (size_t)row * D + k));
-            if ((lane & 7) == 0) {
-                const size_t blk = (size_t)row * (D / 32) + (k >> 5);
-                if (dx) dx[blk] = 1.0f;
-                if (s4) ((float*)s4)[blk] = su;
-            }
-        }
-    }
+    ln_affine_row<C, EMIT>(v, lane, row, gamma, beta, y, eps, codes, dx, s4);
 }
 
 template <int EMIT>

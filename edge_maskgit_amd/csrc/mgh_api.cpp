@@ -957,6 +957,41 @@ int mgh_gemm_h16_y16(mgh_ctx* c, const void* wp16, int N, int K, const void* x16
     return run_gemm_h16(c, a);
 }
 
+int mgh_gemm_h16_ln(mgh_ctx* c, const void* wp16, int N, int K, const void* x16, int M, const float* bias,
+                    int act, const float* resid, float* y, const float* gamma, const float* beta, float eps,
+                    float* y_ln, int emit, void* codes, float* dx, void* s4) {
+    if (!c) return MGH_ERR_ARG;
+    if (int r = check_h16(c, "gemm_h16_ln", wp16, N, K, x16, M, bias, act, resid, y)) return r;
+    if (N % 256 || N > 2048) return fail(c, MGH_ERR_UNSUPPORTED, "gemm_h16_ln: needs N % 256 == 0 and N <= 2048");
+    if (emit < 0 || emit > 2) return fail(c, MGH_ERR_ARG, "gemm_h16_ln: emit must be 0, 1 or 2");
+    if (M == 0) return MGH_OK;
+    if (!gamma || !beta || !y_ln) return fail(c, MGH_ERR_ARG, "gemm_h16_ln: null pointer");
+    if (emit && (!codes || (emit == 1 && (!dx || !s4))))
+        return fail(c, MGH_ERR_ARG, "gemm_h16_ln: emit needs d_codes (and d_dx, d_s4 for INT8)");
+    if (!aligned16(gamma) || !aligned16(beta) || !aligned16(y_ln) || !aligned16(codes) || ((uintptr_t)dx & 3u) ||
+        ((uintptr_t)s4 & 3u))
+        return fail(c, MGH_ERR_ARG, "gemm_h16_ln: gamma/beta/y_ln/codes must be 16-byte aligned");
+    if (int r = set_dev(c)) return r;
+    mgh::GemmH16Args a{};
+    a.x = (const _Float16*)x16; a.w = (const _Float16*)wp16;
+    a.bias = bias; a.resid = resid; a.y = y;
+    a.M = M; a.N = N; a.K = K; a.act = act;
+    const mgh::H16Plan p = mgh::gemm_h16_plan(M, N, K, false);
+    if (!mgh::use_gemv_h16(M, K) && p.splits > 1 && act == 0) {
+        // the split-K reduce normalizes each row as it leaves: one launch fewer
+        if (int r = ensure_qp_ws(c, p.ws_bytes)) return r;
+        a.splits = p.splits;
+        a.ws = (float*)c->qp_ws;
+        const mgh::LnArgs ln{gamma, beta, eps, y_ln, emit, codes, dx, s4};
+        MGH_HIP(c, mgh::launch_gemm_h16(p, a, c->stream, &ln), "k_gemm_h16 + k_gemm_h16_reduce_ln");
+        return MGH_OK;
+    }
+    if (int r = run_gemm_h16(c, a)) return r;
+    MGH_HIP(c, mgh::launch_layernorm_affine(y, gamma, beta, y_ln, M, N, eps, emit, codes, dx, s4, c->stream),
+            "k_layernorm_affine");
+    return MGH_OK;
+}
+
 int mgh_gemm_h16_f32in(mgh_ctx* c, const void* wp16, int N, int K, const float* x, int M,
                        const float* bias, int act, const float* resid, float* y) {
     if (!c) return MGH_ERR_ARG;

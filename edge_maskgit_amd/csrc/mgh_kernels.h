@@ -169,10 +169,24 @@ struct H16Plan {
     size_t ws_bytes;
 };
 H16Plan gemm_h16_plan(int M, int N, int K, bool xf32);
+// LayerNorm-affine of a GEMM's output rows taken by the split-K reduce (k_gemm_h16_reduce_ln):
+// gamma/beta [N] and the LayerNorm outputs as launch_layernorm_affine takes them
+struct LnArgs {
+    const float* gamma;
+    const float* beta;
+    float eps;
+    float* y;              // [M][N] fp32
+    int emit;              // MGH_EMIT_* operand written alongside y
+    void* codes;
+    float* dx;
+    void* s4;
+};
 size_t packed_weight_bytes_f16(int64_t N, int64_t K);
 hipError_t launch_pack_weights_f16(int wtype, const void* w, void* out, int N, int K, hipStream_t s);
 hipError_t launch_f32_to_f16(const float* x, _Float16* h, int64_t n, hipStream_t s);
-hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a, hipStream_t s);
+// ln: the split-K reduce also writes the LayerNorm-affine of y's rows (the plan must split K;
+// act 0, fp32 y, N % 256 == 0, N <= 2048)
+hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a, hipStream_t s, const LnArgs* ln = nullptr);
 // skinny-M form of the same product (1 <= M <= kGemvMaxRows; no workspace), and the rule that
 // picks it over the tiled plan
 constexpr int kGemvMaxRows = 32;

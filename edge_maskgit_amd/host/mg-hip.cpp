@@ -497,6 +497,29 @@ const void* HipRuntime::run(Graph& g, bool readback) {
         }
     }
 
+    // post-norm pairs (mg-transformer.cpp:88-90, 95-97): a dequantize-fused FC without
+    // activation whose only consumer is a Norm over its rows runs as one mgh_gemm_h16_ln call,
+    // which for split-K plans (a few hundred rows) normalizes the rows in the reduce, one
+    // launch fewer; the Norm node then launches nothing. Same bits as the two nodes apart.
+    std::unordered_map<const Tensor*, const Tensor*> ln_pair;     // FC -> its Norm
+    if (I.algo == MGH_ALGO_DEQ_F16) {
+        std::unordered_map<const Tensor*, std::vector<const Tensor*>> cons;
+        for (const Tensor* t : g.nodes)
+            for (const Tensor* s : t->src)
+                if (s) cons[I.root(s)].push_back(t);
+        for (const Tensor* t : g.nodes) {
+            if (t->op != Op::MulMat || !quant(t->src[0]) || grp_of.count(t) || emit16.count(t) ||
+                t == g.nodes.back() || t->iparam[0] != 0)
+                continue;
+            const auto& cs = cons[t];
+            if (cs.size() != 1 || cs[0]->op != Op::Norm || cs[0]->src[0] != t) continue;
+            const int64_t N = t->src[0]->ne[1];
+            if (cs[0]->ne[0] != N || N % 256 || N > 2048 || cs[0]->nelements() != t->nelements()) continue;
+            ln_pair[t] = cs[0];
+        }
+    }
+    std::unordered_set<const Tensor*> ln_done;                    // Norms computed with their FC
+
     // Conv2D epilogue fusion (the VQGAN decoder, mg-vqgan.cpp:31-55): the Add of a per-channel
     // bias viewed as {1, 1, C, 1} that is a conv's only consumer, and then an Add of a same-shaped
     // tensor computed before the conv (the res block's h + x, or h + conv_res(h)), are evaluated
@@ -563,6 +586,44 @@ const void* HipRuntime::run(Graph& g, bool readback) {
     // :1627-1641), each right after its kernel, while its buffer is still its own
     const bool dump_named = std::getenv("MG_DUMP_NAMED") != nullptr;
 
+    auto dump_node = [&](const Tensor* d) {
+        const auto a = I.addr.find(d);
+        if (!d->name.empty() && d->data && a != I.addr.end() && a->second && !h16_store.count(d) &&
+            !I.pitch.count(d))
+            I.check(mgh_d2h(I.ctx, d->data, a->second, d->nbytes()));
+    };
+    // a Norm's affine parameters (unit when absent) and the FC operand it emits: int8 codes
+    // (flat 32-blocks, so any FC row length that is a multiple of 32 reads the same codes), or
+    // for the dequantize-fused path the fp16-rounded y, when a quantized FC reads it
+    struct NormOut {
+        const float* gamma;
+        const float* beta;
+        int emit = MGH_EMIT_NONE;
+        Impl::Codes cd;
+    };
+    auto norm_out = [&](const Tensor* t) {
+        NormOut o;
+        const int D = (int)t->ne[0];
+        const int rows = (int)(t->nelements() / D);
+        o.gamma = (const float*)I.dev(t->src[1]);
+        o.beta = (const float*)I.dev(t->src[2]);
+        if (!t->src[1] || !t->src[2]) {
+            const auto u = I.unit(D);
+            o.gamma = (const float*)u.first;
+            o.beta = (const float*)u.second;
+        }
+        if ((I.algo == MGH_ALGO_INT8 || I.algo == MGH_ALGO_DEQ_F16) && fc_uses.count(t)) {
+            o.emit = I.algo == MGH_ALGO_INT8 ? MGH_EMIT_INT8 : MGH_EMIT_DEQ_F16;
+            const size_t T = (size_t)D / 32;
+            o.cd.q = I.take((size_t)rows * D * 2);
+            if (o.emit == MGH_EMIT_INT8) {         // the dequant-fused GEMM reads only the fp16 y
+                o.cd.dx = I.take((size_t)rows * T * 4);
+                o.cd.sx = I.take((size_t)rows * T * 4);
+            }
+        }
+        return o;
+    };
+
     // ---- run ----
     for (int i = 0; i < n; i++) {
         Tensor* t = g.nodes[i];
@@ -570,6 +631,11 @@ const void* HipRuntime::run(Graph& g, bool readback) {
         if (t->type != Type::F32 && t->op != Op::GetRows)
             throw std::runtime_error("HipRuntime: only F32 results are supported");
         if (grp_of.count(t) && I.addr.count(t)) {                 // computed with its group
+            release_after(i, t);
+            continue;
+        }
+        if (ln_done.count(t)) {                                    // normalized with its FC
+            if (dump_named) dump_node(t);
             release_after(i, t);
             continue;
         }
@@ -677,6 +743,16 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                         cd.q = I.take((size_t)M * N * 2);
                         I.check(mgh_gemm_h16_y16(I.ctx, wp, N, K, c->second.q, M, bias, act, resid, cd.q));
                         I.codes[t] = cd;
+                    } else if (c != I.codes.end() && ln_pair.count(t)) {
+                        const Tensor* nr = ln_pair.at(t);
+                        void* yl = I.take(nr->nbytes());
+                        I.addr[nr] = yl;
+                        const NormOut o = norm_out(nr);
+                        I.check(mgh_gemm_h16_ln(I.ctx, wp, N, K, c->second.q, M, bias, act, resid, (float*)out,
+                                                o.gamma, o.beta, nr->fparam[0], (float*)yl, o.emit, o.cd.q,
+                                                (float*)o.cd.dx, o.cd.sx));
+                        if (o.emit) I.codes[nr] = o.cd;
+                        ln_done.insert(nr);
                     } else if (c != I.codes.end())
                         I.check(mgh_gemm_h16(I.ctx, wp, N, K, c->second.q, M, bias, act, resid, (float*)out));
                     else
@@ -706,30 +782,10 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                 const Tensor* x = t->src[0];
                 const int D = (int)t->ne[0];
                 const int rows = (int)(t->nelements() / D);
-                const float* gm = (const float*)I.dev(t->src[1]);
-                const float* bt = (const float*)I.dev(t->src[2]);
-                if (!t->src[1] || !t->src[2]) {
-                    const auto u = I.unit(D);
-                    gm = (const float*)u.first;
-                    bt = (const float*)u.second;
-                }
-                int emit = MGH_EMIT_NONE;
-                Impl::Codes cd;
-                // one FC operand for every quantized FC that reads this LN: int8 codes (flat
-                // 32-blocks, so any FC row length that is a multiple of 32 reads the same codes),
-                // or for the dequantize-fused path the fp16-rounded y
-                if ((I.algo == MGH_ALGO_INT8 || I.algo == MGH_ALGO_DEQ_F16) && fc_uses.count(t)) {
-                    emit = I.algo == MGH_ALGO_INT8 ? MGH_EMIT_INT8 : MGH_EMIT_DEQ_F16;
-                    const size_t T = (size_t)D / 32;
-                    cd.q = I.take((size_t)rows * D * 2);
-                    if (emit == MGH_EMIT_INT8) {       // the dequant-fused GEMM reads only the fp16 y
-                        cd.dx = I.take((size_t)rows * T * 4);
-                        cd.sx = I.take((size_t)rows * T * 4);
-                    }
-                }
-                I.check(mgh_layernorm_affine(I.ctx, (const float*)I.dev(x), gm, bt, rows, D, t->fparam[0],
-                                             (float*)out, emit, cd.q, (float*)cd.dx, cd.sx));
-                if (emit) I.codes[t] = cd;
+                const NormOut o = norm_out(t);
+                I.check(mgh_layernorm_affine(I.ctx, (const float*)I.dev(x), o.gamma, o.beta, rows, D, t->fparam[0],
+                                             (float*)out, o.emit, o.cd.q, (float*)o.cd.dx, o.cd.sx));
+                if (o.emit) I.codes[t] = o.cd;
                 break;
             }
             case Op::FlashAttention: {
@@ -912,15 +968,9 @@ const void* HipRuntime::run(Graph& g, bool readback) {
             e.first++;
             e.second += ms;
         }
-        if (dump_named) {
-            // a conv whose Add nodes were absorbed leaves the chain's last node in its buffer:
-            // that node is the one read back (the conv's own value never exists on its own)
-            const Tensor* d = t->op == Op::Conv2D && cfuse.count(t) ? cfuse.at(t).out : t;
-            const auto a = I.addr.find(d);
-            if (!d->name.empty() && d->data && a != I.addr.end() && a->second && !h16_store.count(d) &&
-                !I.pitch.count(d))
-                I.check(mgh_d2h(I.ctx, d->data, a->second, d->nbytes()));
-        }
+        // a conv whose Add nodes were absorbed leaves the chain's last node in its buffer: that
+        // node is the one read back (the conv's own value never exists on its own)
+        if (dump_named) dump_node(t->op == Op::Conv2D && cfuse.count(t) ? cfuse.at(t).out : t);
         release_after(i, t);
     }
 

@@ -293,6 +293,17 @@ int mgh_gemm_h16_f32in(mgh_ctx* ctx, const void* d_wp16, int N, int K, const flo
  * reference (its runtime grows scratch buffers on demand, mg-opencl.cpp:1130-1134). */
 int mgh_gemm_h16_f32in_noalloc(mgh_ctx* ctx, const void* d_wp16, int N, int K, const float* d_x, int M,
                                const float* d_bias, int act, const float* d_resid, float* d_y);
+/* mgh_gemm_h16 followed by mgh_layernorm_affine of its output rows, the pair a post-norm
+ * layer runs (reference: the MulMat node with its fused residual, mg-opencl.cpp:320-411, then
+ * the Norm(affine) node, :705-727; mg-transformer.cpp:88-90, 95-97): y as mgh_gemm_h16 writes it and
+ * d_y_ln, d_codes, d_dx, d_s4 as mgh_layernorm_affine(y) writes them (gamma/beta [N], N % 256
+ * == 0, N <= 2048), bit for bit. When the product splits K (a few hundred activation rows)
+ * and act is 0, the split-K reduce normalizes each row as it leaves, one launch instead of
+ * two. No single reference counterpart: the reference runs the two nodes as two dispatches. */
+int mgh_gemm_h16_ln(mgh_ctx* ctx, const void* d_wp16, int N, int K, const void* d_x16, int M,
+                    const float* d_bias, int act, const float* d_resid, float* d_y, const float* d_gamma,
+                    const float* d_beta, float eps, float* d_y_ln, int emit, void* d_codes, float* d_dx,
+                    void* d_s4);
 /* the same product stored rounded to fp16 (d_y16 [M][N]): the operand of a following
  * dequantize-fused FC (no counterpart in the reference, where the next FC rounds its fp32
  * input; the result is identical) */

@@ -230,3 +230,54 @@ def test_gemm_h16_rejects_bad_args(ctx):
     with pytest.raises(ema.MghError):
         ctx.f32_to_f16(buf, 12, buf)
     ctx.free(buf)
+
+
+# mgh_gemm_h16_ln: the first five split K (the reduce normalizes the rows: panel heights 1 and 8,
+# a partial last panel, LayerNorm widths 256..2048), the rest run the LayerNorm kernel after the
+# GEMM (no split, the skinny-M kernel, the long-K plan)
+LN_SHAPES = [(257, 768, 3072), (1025, 768, 3072), (700, 2048, 3072), (300, 256, 3072), (200, 512, 2048),
+             (257, 768, 768), (16, 768, 3072), (513, 2048, 1024), (4112, 768, 3072)]
+
+
+@pytest.mark.parametrize("M,N,K", LN_SHAPES)
+@pytest.mark.parametrize("emit", [0, 1, 2])
+@pytest.mark.parametrize("act", [0, 1])
+def test_gemm_h16_ln_equals_gemm_then_layernorm(ctx, M, N, K, emit, act):
+    """mgh_gemm_h16_ln gives the bits of mgh_gemm_h16 followed by mgh_layernorm_affine on its
+    output: y, the normalized rows and every emitted operand (with an activation the fused
+    reduce is not used and the pair runs as two launches)."""
+    res = M % 2 == 1
+    print(f"gemm_h16_ln M={M} N={N} K={K} emit={emit} act={act} resid={res}", flush=True)
+    rng = np.random.default_rng(M + N + K + 3 * emit + act)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    dP = _pack16(ctx, ema.WTYPE_Q8_0, oracle.quantize(ema.WTYPE_Q8_0, w), N, K)
+    x16 = rng.standard_normal((M, K)).astype(np.float16)
+    bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+    gamma = (1.0 + 0.1 * rng.standard_normal(N)).astype(np.float32)
+    beta = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    dX, dB, dG, dBe = ctx.upload(x16), ctx.upload(bias), ctx.upload(gamma), ctx.upload(beta)
+    dR = ctx.upload(rng.standard_normal((M, N)).astype(np.float32)) if res else None
+    T = N // 32
+    outs = []
+    for fused in (False, True):
+        y, yl = ctx.alloc(M * N * 4), ctx.alloc(M * N * 4)
+        c, dx, s4 = (ctx.alloc(M * N * 2), ctx.alloc(M * T * 4), ctx.alloc(M * T * 4)) if emit else (None, None, None)
+        if fused:
+            ctx.gemm_h16_ln(dP, N, K, dX, M, dB, act, dR, y, dG, dBe, 1e-5, yl, emit, c, dx, s4)
+        else:
+            ctx.gemm_h16(dP, N, K, dX, M, dB, act, dR, y)
+            ctx.layernorm_affine(y, dG, dBe, M, N, 1e-5, yl, emit, c, dx, s4)
+        o = [ctx.download(y, (M, N), np.float32).view(np.uint32), ctx.download(yl, (M, N), np.float32).view(np.uint32)]
+        if emit:
+            o += [ctx.download(c, (M, N), np.float16).view(np.uint16), ctx.download(dx, (M, T), np.float32).view(np.uint32),
+                  ctx.download(s4, (M, T), np.uint32)]
+        outs.append(o)
+        for t in (y, yl, c, dx, s4):
+            if t is not None:
+                ctx.free(t)
+    for t in (dP, dX, dB, dG, dBe, dR):
+        if t is not None:
+            ctx.free(t)
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
+    assert np.isfinite(outs[1][1].view(np.float32)).all()
