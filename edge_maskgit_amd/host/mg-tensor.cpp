@@ -2,6 +2,8 @@
 // interface of include/mg-tensor.hpp (the reference's graph API, src/mg-tensor.cpp).
 #include "mg-tensor.hpp"
 
+#include <unordered_set>
+
 #include <cstdio>
 #include <stdexcept>
 #include <string>
@@ -261,11 +263,8 @@ Tensor* cont(Context& c, Tensor* a) { return c.make(a->type, a->n_dims, a->ne, O
 
 // ---- graph: post-order walk from the output (leaves are not nodes) ----
 namespace {
-void visit(std::vector<Tensor*>& order, std::vector<const Tensor*>& seen, Tensor* t) {
-    if (!t || t->op == Op::None) return;
-    for (const Tensor* s : seen)
-        if (s == t) return;
-    seen.push_back(t);
+void visit(std::vector<Tensor*>& order, std::unordered_set<const Tensor*>& seen, Tensor* t) {
+    if (!t || t->op == Op::None || !seen.insert(t).second) return;
     for (Tensor* s : t->src) visit(order, seen, s);
     order.push_back(t);
 }
@@ -275,7 +274,8 @@ void visit(std::vector<Tensor*>& order, std::vector<const Tensor*>& seen, Tensor
 // (reference src/mg-tensor.cpp:241).
 void Graph::build_forward(Tensor* out) {
     nodes.clear();
-    std::vector<const Tensor*> seen;
+    std::unordered_set<const Tensor*> seen;      // a set: the transformer graph has ~450 nodes
+    seen.reserve(1024);
     visit(nodes, seen, out);
 }
 
