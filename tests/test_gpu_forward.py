@@ -155,6 +155,38 @@ def test_forward_batch_rows_match_single(models):
     assert err <= 1e-3
 
 
+def test_forward_graph_and_plan_reuse(models, monkeypatch):
+    """A model handle keeps its last forward graph per batch shape and the runtime the plan of
+    the last graph it ran: shape changes, a generate() in between (which builds its own graph
+    into the same context) and the unfused-attention switch all give a fresh handle's logits,
+    bit for bit."""
+    path, _ = models["q8_0"]
+    rng = np.random.default_rng(29)
+    t2, t1 = mg_gguf.tokens(rng, 257, 2), mg_gguf.tokens(rng, 257, 1)
+    print("forward graph / plan reuse", flush=True)
+
+    def fresh(tok):
+        with rt.TransformerRuntime(path, algo=2) as f:
+            return f.forward(tok)
+
+    want2, want1 = fresh(t2), fresh(t1)
+    monkeypatch.setenv("MG_NO_FLASH_ATTN", "1")
+    want1u = fresh(t1)
+    monkeypatch.delenv("MG_NO_FLASH_ATTN")
+    assert not np.array_equal(want1u, want1)          # the switch changes the graph
+    got = []
+    with rt.TransformerRuntime(path, algo=2) as m:
+        got += [m.forward(t2), m.forward(t1), m.forward(t2)]
+        m.generate([3], [5], 2)
+        got += [m.forward(t2), m.forward(t1)]
+        monkeypatch.setenv("MG_NO_FLASH_ATTN", "1")
+        got.append(m.forward(t1))
+        monkeypatch.delenv("MG_NO_FLASH_ATTN")
+        got.append(m.forward(t1))
+    for i, (a, b) in enumerate(zip(got, [want2, want1, want2, want2, want1, want1u, want1])):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"call {i}"
+
+
 @pytest.mark.parametrize("algo", [2, 1])
 def test_forward_full_cfg4_properties(tmp_path, algo):
     """cfg4 at full size (24 layers Q8_0, hidden 768, 16 heads, MLP 3072, batch 16 x 257
