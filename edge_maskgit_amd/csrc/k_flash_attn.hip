@@ -403,8 +403,13 @@ void launch_head_t(const FaArgs& a, hipStream_t s) {
     // 10.8 us (3 workgroups per head) against ~15 us with 2 waves in 9 and 18 us unsplit;
     // 8 images 14.2 against 18.0 us unsplit (2 per head, 9 waves); at 16 images (256 heads)
     // splitting costs (29.4 against 21.4 us), so qs = 1 there, ~2 query tiles per wave.
+    // With the staging down to one round trip, four waves per workgroup (one per SIMD) win
+    // where that finer split still gives every workgroup its own CU: S = 257, one image 7.4
+    // against 8.5 us (3 workgroups of 6 waves), two images 7.6 against 8.7; 3, 5, 6 or 9 waves
+    // 8.4-9.8 us at one image.
     int qs = (int)std::max<int64_t>(1, std::min<int64_t>(256 / std::max<int64_t>(heads, 1), (nqt + 5) / 6));
     int nw = std::min(kHeadWaves<KT>, std::max(1, qs > 1 ? (nqt + qs - 1) / qs : (nqt + 1) / 2));
+    if (qs > 1 && kHeadWaves<KT> >= 4 && heads * ((nqt + 3) / 4) <= 256) nw = 4;
     if (qs > 1) qs = (nqt + nw - 1) / nw;
     const dim3 grid((unsigned)a.H, (unsigned)a.B, (unsigned)qs), block((unsigned)(64 * nw));
     const bool tail = a.S > 16 * (KT - 1);
