@@ -187,6 +187,24 @@ def test_forward_graph_and_plan_reuse(models, monkeypatch):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"call {i}"
 
 
+def test_forward_small_batch_fuses_post_norm_pairs(models):
+    """At one image the down-proj splits K, so each post-norm pair (FC + residual, then the
+    LayerNorm) runs as one mgh_gemm_h16_ln call whose reduce normalizes the rows: the per-op
+    profile shows every FC + LayerNorm pair as one entry and only the two LayerNorms outside
+    the layers (embeddings, MLM head) on their own."""
+    path, _ = models["q8_0"]
+    tok = mg_gguf.tokens(np.random.default_rng(31), 257, 1)
+    with rt.TransformerRuntime(path, algo=2) as m:
+        m.forward(tok)
+        m.profile(True)
+        m.forward(tok, readback=False)
+        rows = {name: cnt for name, cnt, _ in m.profile_report()}
+        m.profile(False)
+    print(f"per-op profile: {rows}", flush=True)
+    assert rows.get("MulMat(q)+Norm") == 2 * L
+    assert rows.get("Norm") == 2
+
+
 @pytest.mark.parametrize("algo", [2, 1])
 def test_forward_full_cfg4_properties(tmp_path, algo):
     """cfg4 at full size (24 layers Q8_0, hidden 768, 16 heads, MLP 3072, batch 16 x 257

@@ -281,3 +281,22 @@ def test_gemm_h16_ln_equals_gemm_then_layernorm(ctx, M, N, K, emit, act):
     for a, b in zip(*outs):
         assert np.array_equal(a, b)
     assert np.isfinite(outs[1][1].view(np.float32)).all()
+
+
+def test_gemm_h16_ln_rejects_bad_arguments(ctx):
+    """mgh_gemm_h16_ln: LayerNorm widths other than multiples of 256 up to 2048 are
+    unsupported, emit modes are 0..2 and an emitted operand needs its buffers."""
+    N, K, M = 768, 768, 4
+    w, x, y = ctx.alloc(2048 * K * 2), ctx.alloc(M * K * 2), ctx.alloc(M * 2048 * 4)
+    g, b, yl = ctx.alloc(2048 * 4), ctx.alloc(2048 * 4), ctx.alloc(M * 2048 * 4)
+    for bad_n in (384, 2304):
+        with pytest.raises(ema.MghError):
+            ctx.gemm_h16_ln(w, bad_n, K, x, M, None, 0, None, y, g, b, 1e-5, yl)
+    with pytest.raises(ema.MghError):
+        ctx.gemm_h16_ln(w, N, K, x, M, None, 0, None, y, g, b, 1e-5, yl, emit=3)
+    with pytest.raises(ema.MghError):
+        ctx.gemm_h16_ln(w, N, K, x, M, None, 0, None, y, g, b, 1e-5, yl, emit=2)      # no codes buffer
+    with pytest.raises(ema.MghError):
+        ctx.gemm_h16_ln(w, N, K, x, M, None, 0, None, y, None, b, 1e-5, yl)            # no gamma
+    for t in (w, x, y, g, b, yl):
+        ctx.free(t)
