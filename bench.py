@@ -28,8 +28,9 @@ quantized to Q8_0, biases ~ N(0,0.01), residuals ~ N(0,1), seeded.
 
 value = 2*M*K*N summed over the four GEMMs / step time, in TOPS.
 roofline = the dominant kernel (k_gemm_h16, resp. k_gemm_qp), HBM-bound: algorithmic bytes of
-its launches (quantized weights once + fp16 activations (+ block scales on the int8 path) +
-fp32 output + bias + residual) divided by its average launch duration, timed with HIP events
+its launches (quantized weights once + the activations it reads: fp32 on the h16 path, fp16
+codes + block scales on the int8 path + fp32 output + bias + residual) divided by its average
+launch duration, timed with HIP events
 on the stream it runs on; traffic = the measured HBM bytes of those launches (rocprofv3
 FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy), from profiles/traffic_*.json, reported only
 when that file was measured on the same kernel sources (SHA-256 of edge_maskgit_amd/csrc, also
@@ -246,8 +247,9 @@ def layer_ops(M, layer=LAYER):
 
 def gemm_alg_bytes(M, wtype, path="h16", layer=LAYER):
     """Algorithmic HBM bytes of the four GEMM launches of one step: the quantized weights
-    once, the fp16 activations (int8-dot path: fp16 codes + fp32 block scales (+ block sums for
-    Q4_K)), the fp32 output, bias and residual."""
+    once, the activations the launch reads (h16 path: the fp32 rows, rounded in the kernel;
+    int8-dot path: fp16 codes + fp32 block scales (+ block sums for Q4_K)), the fp32 output,
+    bias and residual."""
     tot = 0
     for _, N, K, act, res in layer:
         nb = K // 32
