@@ -805,6 +805,10 @@ def main():
             extra["transformer_fwd_cfg4"] = {
                 "model": "24 layers Q8_0 random-init, hidden 768, 16 heads, MLP 3072, vocab 2025",
                 "batch": "16 images x 257 tokens (M=4112)", **fwd4}
+            # the same model on one image (M = 257): latency-bound kernels, the single-image call
+            f1, f1nr, _ = measure_forward(path, 1, 20, 5, algo=ALGO[a.path])
+            extra["transformer_fwd_b1"] = {"path": PATH_NAME[a.path], "batch": "1 image x 257 tokens (M=257)",
+                                           "ms": round(f1, 3), "ms_no_logits_readback": round(f1nr, 3)}
             if a.extra:
                 path5 = os.path.join(d, "cfg5_q4_k.gguf")
                 write_synthetic_model(path5, 24, ema.WTYPE_Q4_K, seed=5)
