@@ -73,16 +73,20 @@ LAYER = [  # name, N, K, act, residual
 CFG1 = [("cfg1", 3072, 768, ema.ACT_NONE, False)]   # configs[0]: one Q8_0 FC GEMM at M=257
 
 
-KERNEL = {"packed": "k_gemm_qp", "raw": "k_gemm_q_i8", "h16": "k_gemm_h16"}
-PATH_NAME = {"packed": "int8_dot", "raw": "int8_dot_raw", "h16": "dequant_f16"}
+KERNEL = {"packed": "k_gemm_qp", "raw": "k_gemm_q_i8", "h16": "k_gemm_h16", "dq": "k_gemm_h16<WQ=8|12>"}
+PATH_NAME = {"packed": "int8_dot", "raw": "int8_dot_raw", "h16": "dequant_f16", "dq": "dequant_q"}
 WORKLOAD_PATH = {
     "h16": "dequantize-fused path (weights dequantized once to fp16 at upload; per FC one GEMM "
            "launch: fp32 activations rounded to fp16 as they are read, fp16 MFMA with fp32 "
            "accumulation, fused epilogue)",
     "packed": "int8-dot path (per FC: per-32 int8 activation quantization + exact block dots with "
               "per-block scales applied in fp32)",
-    "raw": "int8-dot path on GGUF blocks as stored"}
-ALGO = {"packed": 1, "raw": 1, "h16": 2}
+    "raw": "int8-dot path on GGUF blocks as stored",
+    "dq": "dequantize-fused path on the quantized bytes (per FC one GEMM launch reading the Q8_0 / "
+          "Q4_K blocks, regrouped once at upload into MFMA fragment order at the GGUF byte count, "
+          "decoded to fp16 in registers inside the K loop; fp32 activations rounded to fp16 as they "
+          "are read; fp16 MFMA with fp32 accumulation; fused epilogue)"}
+ALGO = {"packed": 1, "raw": 1, "h16": 2, "dq": 2}
 
 
 def log(*a):
@@ -120,6 +124,12 @@ class LayerSet:
                 ctx.sync()
                 ctx.free(w)
                 w = wp
+            elif path == "dq":
+                wp = ctx.alloc(ema.packed_weight_bytes_dq(wtype, N, K))
+                ctx.pack_weights_dq(wtype, w, N, K, wp)
+                ctx.sync()
+                ctx.free(w)
+                w = wp
             elif path == "packed":
                 wp = ctx.alloc(ema.packed_weight_bytes(wtype, N, K))
                 ctx.pack_weights(wtype, w, N, K, wp)
@@ -147,6 +157,10 @@ class LayerSet:
             if self.path == "h16":         # fp32 activations rounded to fp16 inside the GEMM
                 c.gemm_h16_f32in(d["w"], d["N"], d["K"], d["x"], self.M, d["b"], d["act"], d["r"], d["y"])
                 continue
+            if self.path == "dq":
+                c.gemm_dq_f32in(self.wtype, d["w"], d["N"], d["K"], d["x"], self.M, d["b"], d["act"], d["r"],
+                                d["y"])
+                continue
             if self.path == "packed":
                 c.quantize_act_q8_codes16(d["x"], self.M, d["K"], d["qx"], d["dx"], d["sx"])
             else:
@@ -154,7 +168,7 @@ class LayerSet:
             self._gemm(d)
 
     def gemms_only(self):
-        if self.path == "h16":             # the GEMM launches are the whole step
+        if self.path in ("h16", "dq"):     # the GEMM launches are the whole step
             self.step()
             return
         for d in self.g:
@@ -253,7 +267,7 @@ def gemm_alg_bytes(M, wtype, path="h16", layer=LAYER):
     tot = 0
     for _, N, K, act, res in layer:
         nb = K // 32
-        if path == "h16":                  # fp32 activations read by the GEMM itself
+        if path in ("h16", "dq"):          # fp32 activations read by the GEMM itself
             tot += N * row_bytes(wtype, K) + M * K * 4 + M * N * 4 + N * 4
         else:
             tot += N * row_bytes(wtype, K) + M * K * 2 + M * N * 4 + N * 4
@@ -680,11 +694,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--graphs", action="store_true",
                     help="replay a captured HIP graph per step instead of enqueuing the kernels one by one")
-    ap.add_argument("--path", choices=["packed", "h16", "raw"], default="h16",
+    ap.add_argument("--path", choices=["packed", "h16", "raw", "dq"], default="h16",
                     help="packed: int8-dot path on the device-native weight layout; h16: "
                          "dequantize-fused fp16 path; raw: int8-dot on GGUF blocks as stored")
     ap.add_argument("--no-fwd", action="store_true", help="skip the transformer forward (cfg4)")
-    ap.add_argument("--only-config", choices=["cfg1", "m4097"], default=None,
+    ap.add_argument("--only-config", choices=["cfg1", "m4097", "q4k_m1025", "q4k_m4097"], default=None,
                     help="measure only this workload of --path (cfg1: one Q8_0 FC at M=257; m4097: "
                          "the four Q8_0 FCs at M=4097) and print its timing: the run a kernel "
                          "profile of that workload wraps")
@@ -727,10 +741,11 @@ def main():
         ctx.close()
         return
     if a.only_config:
-        M1, lay = (257, CFG1) if a.only_config == "cfg1" else (4097, LAYER)
-        s1, g1, _ = measure(ctx, M1, ema.WTYPE_Q8_0, a.steps, a.warmup, a.rotate_gb, use_graphs=a.graphs,
+        M1, lay = (257, CFG1) if a.only_config == "cfg1" else (1025 if "m1025" in a.only_config else 4097, LAYER)
+        wt1 = ema.WTYPE_Q4_K if a.only_config.startswith("q4k") else ema.WTYPE_Q8_0
+        s1, g1, _ = measure(ctx, M1, wt1, a.steps, a.warmup, a.rotate_gb, use_graphs=a.graphs,
                             path=a.path, layer=lay)
-        ab = step_alg_bytes(M1, ema.WTYPE_Q8_0, lay)
+        ab = step_alg_bytes(M1, wt1, lay)
         print(json.dumps({"config": a.only_config, "path": PATH_NAME[a.path], "M": M1, "ms_per_step": round(s1, 5),
                           "tops": round(layer_ops(M1, lay) / (s1 * 1e-3) / 1e12, 2),
                           "alg_bytes_per_step": ab, "alg_gbs": round(ab / (s1 * 1e-3) / 1e9, 1)}), flush=True)

@@ -42,6 +42,8 @@ MGH_SYMBOLS = [
     "mgh_gemm_h16_f32in_noalloc", "mgh_conv2d", "mgh_group_norm", "mgh_upscale", "mgh_conv2d_ex",
     "mgh_conv2d_packed_bytes", "mgh_conv2d_pack_weights", "mgh_conv2d_i8_weight_bytes",
     "mgh_conv2d_i8_pack_weights", "mgh_conv2d_i8",
+    "mgh_packed_weight_bytes_dq", "mgh_pack_weights_dq", "mgh_gemm_dq", "mgh_gemm_dq_f32in",
+    "mgh_gemm_dq_y16", "mgh_gemm_dq_ln",
 ]
 
 _lib = None
@@ -107,6 +109,13 @@ def lib():
         L.mgh_gemm_h16_y16.argtypes = [P, P, I, I, P, I, P, I, P, P]
         L.mgh_gemm_h16_ln.argtypes = [P, P, I, I, P, I, P, I, P, P, P, P, ctypes.c_float, P, I, P, P, P]
         L.mgh_gemm_h16_f32in_noalloc.argtypes = [P, P, I, I, P, I, P, I, P, P]
+        L.mgh_packed_weight_bytes_dq.argtypes = [I, I, I]
+        L.mgh_packed_weight_bytes_dq.restype = SZ
+        L.mgh_pack_weights_dq.argtypes = [P, I, P, I, I, P]
+        L.mgh_gemm_dq.argtypes = [P, I, P, I, I, P, I, P, I, P, P]
+        L.mgh_gemm_dq_f32in.argtypes = [P, I, P, I, I, P, I, P, I, P, P]
+        L.mgh_gemm_dq_y16.argtypes = [P, I, P, I, I, P, I, P, I, P, P]
+        L.mgh_gemm_dq_ln.argtypes = [P, I, P, I, I, P, I, P, I, P, P, P, P, ctypes.c_float, P, I, P, P, P]
         L.mgh_flash_attn_f16kv_o16.argtypes = [P, P, P, P, P, I, I, I, I, ctypes.c_float, P, P]
         L.mgh_flash_attn_f16in.argtypes = [P, P, P, P, P, I, I, I, I, ctypes.c_float, P, P, P]
         L.mgh_decode_state_bytes.argtypes = [I]
@@ -142,6 +151,12 @@ def lib():
 
 def packed_weight_bytes_f16(N: int, K: int) -> int:
     return int(lib().mgh_packed_weight_bytes_f16(N, K))
+
+
+def packed_weight_bytes_dq(wtype: int, N: int, K: int) -> int:
+    """bytes of the K-loop-dequant weight layout (GGUF-sized: 1.0625 / 0.5625 bytes per weight
+    for N % 16 == 0)"""
+    return int(lib().mgh_packed_weight_bytes_dq(wtype, N, K))
 
 
 def decode_state_bytes(B: int) -> int:
@@ -351,6 +366,27 @@ class Context:
     def gemm_h16_f32in(self, wp16, N, K, x, M, bias, act, resid, y):
         P = self._ptr
         self._check(lib().mgh_gemm_h16_f32in(self.h, P(wp16), N, K, P(x), M, P(bias), act, P(resid), P(y)))
+
+    def pack_weights_dq(self, wtype, w, N, K, wdq):
+        self._check(lib().mgh_pack_weights_dq(self.h, wtype, self._ptr(w), N, K, self._ptr(wdq)))
+
+    def gemm_dq(self, wtype, wdq, N, K, x16, M, bias, act, resid, y):
+        P = self._ptr
+        self._check(lib().mgh_gemm_dq(self.h, wtype, P(wdq), N, K, P(x16), M, P(bias), act, P(resid), P(y)))
+
+    def gemm_dq_f32in(self, wtype, wdq, N, K, x, M, bias, act, resid, y):
+        P = self._ptr
+        self._check(lib().mgh_gemm_dq_f32in(self.h, wtype, P(wdq), N, K, P(x), M, P(bias), act, P(resid), P(y)))
+
+    def gemm_dq_y16(self, wtype, wdq, N, K, x16, M, bias, act, resid, y16):
+        P = self._ptr
+        self._check(lib().mgh_gemm_dq_y16(self.h, wtype, P(wdq), N, K, P(x16), M, P(bias), act, P(resid), P(y16)))
+
+    def gemm_dq_ln(self, wtype, wdq, N, K, x16, M, bias, act, resid, y, gamma, beta, eps, y_ln, emit=0,
+                   codes=None, dx=None, s4=None):
+        P = self._ptr
+        self._check(lib().mgh_gemm_dq_ln(self.h, wtype, P(wdq), N, K, P(x16), M, P(bias), act, P(resid), P(y),
+                                         P(gamma), P(beta), eps, P(y_ln), emit, P(codes), P(dx), P(s4)))
 
     def gemm_h16_f32in_noalloc(self, wp16, N, K, x, M, bias, act, resid, y):
         """mgh_gemm_h16_f32in with its scratch in the library's fixed per-GPU array."""

@@ -56,15 +56,30 @@ constexpr int kCpr = F32 ? 16 : 8;
 template <int CPR>
 __device__ __forceinline__ int swz(int r) { return (r / (16 / CPR)) & (CPR - 1); }
 
-// NS-deep ring of K stages
-template <int BM, int BN, bool XF32, int NS>
+// Weight bytes per K stage (64 values) for BN rows, and the per-stage side data the K-loop
+// dequantization needs (Q8_0: fp16 block scales; Q4_K: the super-block headers).
+template <int WQ, int BN>
+constexpr int kWStage = WQ == 0 ? BN * 128 : (WQ == 8 ? BN * 64 : BN * 32);
+template <int WQ, int BN>
+constexpr int kWAux = WQ == 0 ? 0 : (WQ == 8 ? 1024 : BN * 16);
+
+// NS-deep ring of K stages. Weights: fp16 [stage][row][swizzled 16-byte chunks] (WQ 0), or the
+// stage's 16-row groups of the K-loop-dequant layout as stored (1 KB of Q8_0 codes, 512 bytes
+// of Q4_K nibbles per group) plus their scales / headers in `aux` (Q8_0: 256 bytes per wave,
+// of which its groups' 64-byte scale rows fill the first GPW * 64; Q4_K: the 256-byte headers
+// of the tile's groups in order).
+template <int BM, int BN, bool XF32, int NS, int WQ>
 struct HLds {
-    u32x4 w[NS][BN * kCpr<false>];      // [stage][row][swizzled 16-byte chunks] fp16
+    u32x4 w[NS][kWStage<WQ, BN> / 16];
+    u32x4 aux[NS][WQ ? kWAux<WQ, BN> / 16 : 1];
     u32x4 x[NS][BM * kCpr<XF32>];
 };
 
 __device__ __forceinline__ void dma16(const void* g, void* lds) {
     __builtin_amdgcn_global_load_lds(g, (lds_void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void*)lds, 4, 0, 0);
 }
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 template <int N>
@@ -93,6 +108,106 @@ __device__ __forceinline__ void tile_origin(int lt, int tiles_m, int tiles_n, in
 
 __device__ __forceinline__ uint32_t f16_bits(float v) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+// 8-byte LDS / global reads go through this vector type: reading the ring through HIP's uint2
+// struct made the compiler wait for every outstanding LDS DMA before the read (vmcnt(0)).
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Q8_0 fragment: eight codes stored as q + 128 (bytes of c.x, c.y in K order) and the block's
+// fp16 scale d -> d * q rounded to fp16. Each code byte b becomes the fp16 1024 + b (exponent
+// byte 0x64 placed above it by v_perm), minus 1152 gives q exactly, and the fp16 product
+// rounds d * q (exact in fp32) once to nearest even: the value k_pack_w16 stores.
+__device__ __forceinline__ f16x8 deq_q8(u32x2 c, uint32_t dbits) {
+    const uint32_t E = 0x64646464u;
+    const h16x2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)dbits);
+    const h16x2 dd = {d, d};
+    auto pair = [&](uint32_t w, uint32_t sel) {
+        return (__builtin_bit_cast(h16x2, __builtin_amdgcn_perm(E, w, sel)) + off) * dd;
+    };
+    const h16x2 p0 = pair(c.x, 0x04010400u), p1 = pair(c.x, 0x04030402u);
+    const h16x2 p2 = pair(c.y, 0x04010400u), p3 = pair(c.y, 0x04030402u);
+    return f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+// Q4_K fragment: eight 4-bit values (byte e of c: element e in the low nibble, element e + 4
+// in the high one) of sub-block j of a super-block with header h (fp16 d | fp16 dmin, then
+// the 12 bytes of packed 6-bit scales / mins) -> (d*sc) * q - dmin*m rounded to fp16. d*sc and
+// (d*sc)*q are exact in fp32, so the fma rounds once, as the multiply-then-subtract of
+// k_pack_w16; then one rounding to fp16.
+__device__ __forceinline__ f16x8 deq_q4(uint32_t c, u32x4 h, int j) {
+    // j is the same for the whole wave: the masks select the j < 4 form (6 low bits of byte j
+    // of scales[0..3] / [4..7]) or the j >= 4 form (4 bits of byte j - 4 of scales[8..11] plus
+    // the top 2 bits of byte j - 4 of scales[0..3] / [4..7]) without a branch
+    const int sh = 8 * (j & 3);
+    const bool first = j < 4;
+    const uint32_t m1 = first ? 63u : 0u, m2 = first ? 0u : 15u, m3 = first ? 0u : 0xC0u;
+    const uint32_t by = h.y >> sh, bz = h.z >> sh, bw = h.w >> sh;
+    const uint32_t sc = (by & m1) | (bw & m2) | ((by & m3) >> 2);
+    const uint32_t mn = (bz & m1) | ((bw >> 4) & m2) | ((bz & m3) >> 2);
+    const float s = h2f(h.x & 0xFFFFu) * (float)sc;
+    const float m = h2f(h.x >> 16) * (float)mn;
+    const uint32_t lo = c & 0x0F0F0F0Fu, hn = (c >> 4) & 0x0F0F0F0Fu;
+    f16x8 r;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        r[e] = (_Float16)__builtin_fmaf(s, (float)((lo >> (8 * e)) & 0xFFu), -m);
+        r[e + 4] = (_Float16)__builtin_fmaf(s, (float)((hn >> (8 * e)) & 0xFFu), -m);
+    }
+    return r;
+}
+
+// K-loop-dequant layout (packed_weight_bytes_dq): one thread per 32-value block (row n, block t
+// = 2 * stage + half) writes its codes / nibbles to their fragment slots and its scale / header.
+template <int WTYPE>
+__global__ __launch_bounds__(256) void k_pack_wdq(const uint8_t* __restrict__ w, uint8_t* __restrict__ out,
+                                                  int N, int K) {
+    const int T = K / 32, S = K / 64;
+    const int64_t blk = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (blk >= (int64_t)N * T) return;
+    const int64_t n = blk / T;
+    const int t = (int)(blk - n * T);
+    const int64_t G = ((int64_t)N + 15) / 16, g = n / 16;
+    const int r = (int)(n % 16), st = t / 2, h = t % 2;
+    if (WTYPE == 8) {
+        const uint8_t* b = w + blk * 34;
+        uint8_t* cb = out + (g * S + st) * 1024 + 512 * h + 8 * r;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            uint32_t v0 = 0, v1 = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                v0 |= (uint32_t)(uint8_t)(b[2 + 8 * q + e] ^ 0x80u) << (8 * e);
+                v1 |= (uint32_t)(uint8_t)(b[2 + 8 * q + 4 + e] ^ 0x80u) << (8 * e);
+            }
+            *(uint2*)(cb + 128 * q) = uint2{v0, v1};
+        }
+        uint16_t* sc = (uint16_t*)(out + G * S * 1024);
+        sc[(g * S + st) * 32 + 16 * h + r] = (uint16_t)(b[0] | (b[1] << 8));
+    } else {
+        const int sbi = t / 8, j = t % 8;
+        const uint8_t* sb = w + (n * (T / 8) + sbi) * 144;
+        const uint8_t* qs = sb + 16 + 32 * (j >> 1);
+        const int sh = 4 * (j & 1);
+        uint8_t* cb = out + (g * S + st) * 512 + 256 * h + 4 * r;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            uint32_t v = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t lo = (qs[8 * q + e] >> sh) & 15u, hi = (qs[8 * q + 4 + e] >> sh) & 15u;
+                v |= (lo | (hi << 4)) << (8 * e);
+            }
+            *(uint32_t*)(cb + 64 * q) = v;
+        }
+        if (j == 0) {
+            const uint32_t* src = (const uint32_t*)sb;
+            u32x4* hd = (u32x4*)(out + G * S * 512);
+            hd[(g * (K / 256) + sbi) * 16 + r] = u32x4{src[0], src[1], src[2], src[3]};
+        }
+    }
 }
 
 // One thread per 32-value block: the block's 32 dequantized values as fp16 (4 x 16 bytes).
@@ -161,7 +276,7 @@ __global__ __launch_bounds__(256) void k_f32_to_f16(const f32x4* __restrict__ x,
 template <int WMR, int BN>
 constexpr int kH16MinBlocks = (WMR == 2 && BN == 128) ? 2 : 1;
 
-template <int ACT, int BM, bool PART, bool XF32, int NS, int WMR, int BN>
+template <int ACT, int BM, bool PART, bool XF32, int NS, int WMR, int BN, int WQ>
 __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h16(GemmH16Args g) {
     constexpr int NW = 2 * WMR;                 // waves
     constexpr int NTH = 64 * NW;                // threads
@@ -170,14 +285,23 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
     constexpr int WN = BN / 2;                  // weight rows per wave
     constexpr int I = WN / 16;                  // 16-row weight subtiles per wave
     constexpr int CPW = kCpr<false>, CPX = kCpr<XF32>;  // chunks per stage row
-    constexpr int CW = BN * CPW / 64 / NW;      // weight DMA instructions per wave and stage
+    constexpr int GPW = BN / 16 / NW;           // 16-row weight groups per wave (dequant layout)
+    // weight DMA instructions per wave and stage (every lane of every DMA moves bytes: an
+    // exec-masked DMA would make the compiler wait for all of them before any LDS read):
+    // fp16 rows; one 16-byte-per-lane DMA per 1 KB Q8_0 group; Q4_K: two 512-byte groups per
+    // 16-byte DMA, or a single group as two 4-byte-per-lane DMAs
+    constexpr int CW = WQ == 0 ? BN * CPW / 64 / NW : (WQ == 8 ? GPW : (GPW == 2 ? 1 : 2));
+    // scale / header DMAs (4 bytes per lane): Q8_0 one (the wave's scale rows, then padding),
+    // Q4_K one per 256-byte header group
+    constexpr int CA = WQ == 0 ? 0 : (WQ == 8 ? 1 : GPW);
+    static_assert(WQ == 0 || (BN % (16 * NW) == 0 && GPW <= 2), "dequant layout: whole groups per wave");
     constexpr int CX = BM * CPX / 64 / NW;      // activation DMA instructions per wave and stage
     static_assert(CW >= 1 && CX >= 1 && RW % 16 == 0, "tile shape");
     constexpr int MID = I * J / 2;              // MFMAs issued before a stage boundary
-    constexpr int NR = I + (XF32 ? 2 : 1) * J;  // LDS reads per K half
+    constexpr int NR = (WQ ? 2 : 1) * I + (XF32 ? 2 : 1) * J;  // LDS reads per K half
     constexpr int NI = NR < I * J ? NR : I * J;  // MFMA : LDS-read pairs in the interleave
-    static_assert(NS >= 2 && (NS - 1) * (CW + CX) < 64, "ring depth");
-    __shared__ HLds<BM, BN, XF32, NS> L;
+    static_assert(NS >= 2 && (NS - 1) * (CW + CX + CA) < 64, "ring depth");
+    __shared__ HLds<BM, BN, XF32, NS, WQ> L;
 
     const int K = g.K, M = g.M, N = g.N;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
@@ -195,11 +319,41 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
     // holds that row's chunk slot ^ swz(row)
     const uint8_t* srcw[CW];
     const uint8_t* srcx[CX];
+    const uint8_t* srca[CA > 0 ? CA : 1];
+    const int S = K / 64;
+    // dequant layout: this wave's groups of the tile (past the last group: the last one, whose
+    // values only reach discarded rows)
+    const int G = (N + 15) / 16;
+    if (WQ == 0) {
 #pragma unroll
-    for (int q = 0; q < CW; q++) {
-        const int r = (64 / CPW) * (wave + NW * q) + lane / CPW;
-        const int n = min(n0 + r, N - 1);
-        srcw[q] = (const uint8_t*)g.w + (size_t)n * K * 2 + ((lane % CPW) ^ swz<CPW>(r)) * 16;
+        for (int q = 0; q < CW; q++) {
+            const int r = (64 / CPW) * (wave + NW * q) + lane / CPW;
+            const int n = min(n0 + r, N - 1);
+            srcw[q] = (const uint8_t*)g.w + (size_t)n * K * 2 + ((lane % CPW) ^ swz<CPW>(r)) * 16;
+        }
+    } else if (WQ == 8) {
+#pragma unroll
+        for (int q = 0; q < CW; q++) {
+            const int gi = min(n0 / 16 + wave * GPW + q, G - 1);
+            srcw[q] = (const uint8_t*)g.w + (size_t)gi * S * 1024 + lane * 16;
+        }
+        // lanes 16 * GPW.. repeat the wave's last scale row into the padding
+        const int gi = min(n0 / 16 + wave * GPW + min(lane / 16, GPW - 1), G - 1);
+        srca[0] = (const uint8_t*)g.w + (size_t)G * S * 1024 + (size_t)gi * S * 64 + (lane % 16) * 4;
+    } else {
+        if (GPW == 2) {
+            const int gi = min(n0 / 16 + wave * 2 + lane / 32, G - 1);
+            srcw[0] = (const uint8_t*)g.w + (size_t)gi * S * 512 + (lane % 32) * 16;
+        } else {
+            const int gi = min(n0 / 16 + wave, G - 1);
+#pragma unroll
+            for (int q = 0; q < CW; q++) srcw[q] = (const uint8_t*)g.w + (size_t)gi * S * 512 + q * 256 + lane * 4;
+        }
+#pragma unroll
+        for (int q = 0; q < CA; q++) {
+            const int ga = min(n0 / 16 + wave * GPW + q, G - 1);
+            srca[q] = (const uint8_t*)g.w + (size_t)G * S * 512 + (size_t)ga * (K / 256) * 256 + lane * 4;
+        }
     }
 #pragma unroll
     for (int q = 0; q < CX; q++) {
@@ -208,21 +362,52 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
         const uint8_t* base = XF32 ? (const uint8_t*)g.xf + (size_t)m * K * 4 : (const uint8_t*)g.x + (size_t)m * K * 2;
         srcx[q] = base + ((lane % CPX) ^ swz<CPX>(r)) * 16;
     }
-    const int S = K / 64;
     const int s_beg = (int)((int64_t)ks * S / splits), s_end = (int)((int64_t)(ks + 1) * S / splits);
     const int SL = s_end - s_beg;
     const int s0 = ((m0 / BM) + 4 * (n0 / BN)) % SL;          // K rotation
     auto kst = [&](int s) { int v = s + s0; return s_beg + (v >= SL ? v - SL : v); };
     auto dma_stage = [&](int st, int s) {
-        const size_t ofs = (size_t)kst(s) * 16;
+        const int ks_ = kst(s);
+        const size_t ofs = (size_t)ks_ * 16;
+        if (WQ == 0) {
 #pragma unroll
-        for (int d = 0; d < CW; d++) dma16(srcw[d] + ofs * CPW, &L.w[st][(wave + NW * d) * 64]);
+            for (int d = 0; d < CW; d++) dma16(srcw[d] + ofs * CPW, &L.w[st][(wave + NW * d) * 64]);
+        } else if (WQ == 8) {
+#pragma unroll
+            for (int d = 0; d < CW; d++) dma16(srcw[d] + (size_t)ks_ * 1024, &L.w[st][(wave * GPW + d) * 64]);
+            dma4(srca[0] + (size_t)ks_ * 64, &L.aux[st][wave * 16]);
+        } else {
+            if (GPW == 2) {
+                dma16(srcw[0] + (size_t)ks_ * 512, &L.w[st][wave * 64]);
+            } else {
+#pragma unroll
+                for (int d = 0; d < CW; d++) dma4(srcw[d] + (size_t)ks_ * 512, &L.w[st][wave * 32 + d * 16]);
+            }
+#pragma unroll
+            for (int d = 0; d < CA; d++) dma4(srca[d] + (size_t)(ks_ >> 2) * 256, &L.aux[st][(wave * GPW + d) * 16]);
+        }
 #pragma unroll
         for (int d = 0; d < CX; d++) dma16(srcx[d] + ofs * CPX, &L.x[st][(wave + NW * d) * 64]);
     };
     // fragment of 16 rows from r0 (r0 % 16 == 0), K half kb: lane (l16, lq) takes 8 values
     auto frag = [&](const u32x4* B, int r0, int kb) {
         return __builtin_bit_cast(f16x8, B[(r0 + l16) * CPW + ((4 * kb + lq) ^ swz<CPW>(l16))]);
+    };
+    // weight fragment of rows r0..r0+15 of the tile (r0 % 16 == 0), K half kb of ring stage st
+    // (global K stage ksg): fp16 as stored, or dequantized from the group's codes / nibbles
+    auto wfrag = [&](int st, int r0, int kb, int ksg) -> f16x8 {
+        if constexpr (WQ == 0) {
+            return frag(L.w[st], r0, kb);
+        } else if constexpr (WQ == 8) {
+            const int gi = r0 >> 4;
+            const u32x2 c = ((const u32x2*)&L.w[st][gi * 64])[kb * 64 + lane];
+            const uint32_t d = ((const uint16_t*)&L.aux[st][(gi / GPW) * 16 + (gi % GPW) * 4])[kb * 16 + l16];
+            return deq_q8(c, d);
+        } else {
+            const int gi = r0 >> 4;
+            const uint32_t c = ((const uint32_t*)&L.w[st][gi * 32])[kb * 64 + lane];
+            return deq_q4(c, L.aux[st][gi * 16 + l16], (2 * ksg + kb) & 7);
+        }
     };
     // activation fragment: fp16 rows as stored, or fp32 rows rounded to fp16 on the way in
     auto xfrag = [&](const u32x4* B, int r0, int kb) {
@@ -245,12 +430,12 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
     // awaited and stage s+NS goes into stage s's buffer (its fragments are in registers by
     // then). Requests past the last stage re-load it into buffers that are never read, so
     // every boundary issues the same DMA count and the vmcnt waits stay exact.
-    constexpr int NDMA = CW + CX;
+    constexpr int NDMA = CW + CA + CX;
 #pragma unroll
     for (int k = 0; k < NS; k++) dma_stage(k, min(k, SL - 1));
     stage_sync<(NS - 1) * NDMA>();              // stage 0 has landed (mine, then everyone's)
 #pragma unroll
-    for (int i = 0; i < I; i++) a[0][i] = frag(L.w[0], WN * wn + 16 * i, 0);
+    for (int i = 0; i < I; i++) a[0][i] = wfrag(0, WN * wn + 16 * i, 0, kst(0));
 #pragma unroll
     for (int j = 0; j < J; j++) b[0][j] = xfrag(L.x[0], RW * wm + 16 * j, 0);
 
@@ -262,9 +447,10 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
         for (int q = q0; q < q1; q++)
             acc[q % I][q / I] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ca[q % I], cb[q / I], acc[q % I][q / I], 0, 0, 0);
     };
-    auto half_inner = [&](const f16x8 (&ca)[I], const f16x8 (&cb)[J], f16x8 (&na)[I], f16x8 (&nb)[J], int st) {
+    auto half_inner = [&](const f16x8 (&ca)[I], const f16x8 (&cb)[J], f16x8 (&na)[I], f16x8 (&nb)[J], int st,
+                          int ksg) {
 #pragma unroll
-        for (int i = 0; i < I; i++) na[i] = frag(L.w[st], WN * wn + 16 * i, 1);
+        for (int i = 0; i < I; i++) na[i] = wfrag(st, WN * wn + 16 * i, 1, ksg);
 #pragma unroll
         for (int j = 0; j < J; j++) nb[j] = xfrag(L.x[st], RW * wm + 16 * j, 1);
         mfma_all(ca, cb, 0, I * J);
@@ -286,7 +472,7 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
         // (a 2-deep ring waits for everything, so it skips the re-loads past the end)
         if (NS > 2 ? s + 1 < SL : s + NS < SL) dma_stage(st, min(s + NS, SL - 1));
 #pragma unroll
-        for (int i = 0; i < I; i++) na[i] = frag(L.w[stn], WN * wn + 16 * i, 0);
+        for (int i = 0; i < I; i++) na[i] = wfrag(stn, WN * wn + 16 * i, 0, kst(s + 1 < SL ? s + 1 : s));
 #pragma unroll
         for (int j = 0; j < J; j++) nb[j] = xfrag(L.x[stn], RW * wm + 16 * j, 0);
         mfma_all(ca, cb, MID, I * J);
@@ -295,7 +481,7 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
     int st = 0;
     for (int s = 0; s < SL; s++) {
         const int stn = st + 1 == NS ? 0 : st + 1;
-        half_inner(a[0], b[0], a[1], b[1], st);
+        half_inner(a[0], b[0], a[1], b[1], st, kst(s));
         half_boundary(a[1], b[1], a[0], b[0], s, st, stn);
         st = stn;
     }
@@ -323,7 +509,7 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
     constexpr int HR = RW < 64 ? RW : 64;
     constexpr int HPW = RW / HR;                // passes per wave row
     constexpr int JH = HR / 16;                 // activation subtiles per pass
-    static_assert(HR * P * 4 <= (int)sizeof(HLds<BM, BN, XF32, NS>), "transpose buffer fits the ring");
+    static_assert(HR * P * 4 <= (int)sizeof(HLds<BM, BN, XF32, NS, WQ>), "transpose buffer fits the ring");
     constexpr int TR = BN / 4;                  // threads per output row
     float* T = (float*)&L;
     const int c = 4 * (tid % TR);               // this thread's 4 columns
@@ -493,7 +679,7 @@ hipError_t launch_reduce_ln(const GemmH16Args& a, int bm, int bn, const LnArgs& 
 // (deterministic) and the epilogue is the one of k_gemm_h16: +bias -> act -> +resid, fp32 or
 // fp16 out. Same operand rounding as k_gemm_h16 (fp32 activations rounded to fp16, nearest
 // even), so the two differ only in the fp32 summation order.
-template <int ACT, bool XF32, int MT, int KS>
+template <int ACT, bool XF32, int MT, int KS, int WQ>
 __global__ __launch_bounds__(64 * KS) void k_gemv_h16(GemmH16Args g) {
     constexpr int U = 4;                        // K steps in flight per wave
     __shared__ f32x4 part[KS][MT][64];
@@ -502,7 +688,27 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_h16(GemmH16Args g) {
     const int n0 = blockIdx.x * 16;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r16 = lane & 15, g4 = lane >> 4;
-    const _Float16* wrow = g.w + (size_t)min(n0 + r16, N - 1) * K + 8 * g4;
+    const _Float16* wrow = (const _Float16*)g.w + (size_t)min(n0 + r16, N - 1) * K + 8 * g4;
+    // K-loop-dequant layout: this workgroup's 16-row group (n0 / 16)
+    const int S = K / 64, grp = n0 / 16;
+    const uint8_t* wq = (const uint8_t*)g.w;
+    const size_t gsz = WQ == 8 ? 1024 : 512;
+    const uint8_t* wgrp = wq + (size_t)grp * S * gsz;
+    const uint8_t* wside = wq + (size_t)((N + 15) / 16) * S * gsz;
+    // weight fragment of 32-deep K step t (stage t / 2, half t % 2)
+    auto wld = [&](int t) -> f16x8 {
+        if constexpr (WQ == 0) {
+            return *(const f16x8*)(wrow + 32 * t);
+        } else if constexpr (WQ == 8) {
+            const u32x2 c = *(const u32x2*)(wgrp + (size_t)(t >> 1) * 1024 + 512 * (t & 1) + 8 * lane);
+            const uint32_t d = ((const uint16_t*)wside)[((size_t)grp * S + (t >> 1)) * 32 + 16 * (t & 1) + r16];
+            return deq_q8(c, d);
+        } else {
+            const uint32_t c = *(const uint32_t*)(wgrp + (size_t)(t >> 1) * 512 + 256 * (t & 1) + 4 * lane);
+            const u32x4 h = ((const u32x4*)wside)[((size_t)grp * (K / 256) + (t >> 3)) * 16 + r16];
+            return deq_q4(c, h, t & 7);
+        }
+    };
     size_t xofs[MT];
     bool xin[MT];
 #pragma unroll
@@ -527,7 +733,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_h16(GemmH16Args g) {
         f16x8 a[U], b[U][MT];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            a[u] = *(const f16x8*)(wrow + 32 * (t + u * KS));
+            a[u] = wld(t + u * KS);
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) b[u][mt] = xfrag(mt, t + u * KS);
         }
@@ -538,7 +744,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_h16(GemmH16Args g) {
                 acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], b[u][mt], acc[mt], 0, 0, 0);
     }
     for (; t < T; t += KS) {
-        const f16x8 a = *(const f16x8*)(wrow + 32 * t);
+        const f16x8 a = wld(t);
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xfrag(mt, t), acc[mt], 0, 0, 0);
     }
@@ -565,14 +771,22 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_h16(GemmH16Args g) {
         *(f32x4*)(g.y + o) = v;
 }
 
-template <bool XF32, int MT>
-static hipError_t launch_gemv_t(const GemmH16Args& a, hipStream_t s) {
+template <bool XF32, int MT, int WQ>
+static hipError_t launch_gemv_w(const GemmH16Args& a, hipStream_t s) {
     constexpr int KS = 8;
     const dim3 grid((unsigned)((a.N + 15) / 16)), block(64 * KS);
-    if (a.act == 1) hipLaunchKernelGGL((k_gemv_h16<1, XF32, MT, KS>), grid, block, 0, s, a);
-    else if (a.act == 2) hipLaunchKernelGGL((k_gemv_h16<2, XF32, MT, KS>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((k_gemv_h16<0, XF32, MT, KS>), grid, block, 0, s, a);
+    if (a.act == 1) hipLaunchKernelGGL((k_gemv_h16<1, XF32, MT, KS, WQ>), grid, block, 0, s, a);
+    else if (a.act == 2) hipLaunchKernelGGL((k_gemv_h16<2, XF32, MT, KS, WQ>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_gemv_h16<0, XF32, MT, KS, WQ>), grid, block, 0, s, a);
     return hipGetLastError();
+}
+
+template <bool XF32, int MT>
+static hipError_t launch_gemv_t(const GemmH16Args& a, hipStream_t s) {
+    if (a.wq == 8) return launch_gemv_w<XF32, MT, 8>(a, s);
+    if (a.wq == 12) return launch_gemv_w<XF32, MT, 12>(a, s);
+    if (a.wq == 0) return launch_gemv_w<XF32, MT, 0>(a, s);
+    return hipErrorInvalidValue;
 }
 
 // Skinny-M kernel or tiled plan: measured on the four FC shapes with cold operands (fp32
@@ -589,7 +803,7 @@ hipError_t launch_gemv_h16(const GemmH16Args& a, hipStream_t s) {
     return xf ? launch_gemv_t<true, 2>(a, s) : launch_gemv_t<false, 2>(a, s);
 }
 
-H16Plan gemm_h16_plan(int M, int N, int K, bool xf32) {
+H16Plan gemm_h16_plan(int M, int N, int K, bool xf32, int wq) {
     H16Plan p{};
     p.ns = 2;
     p.bn = 128;
@@ -675,6 +889,31 @@ hipError_t launch_pack_weights_f16(int wtype, const void* w, void* out, int N, i
     return hipGetLastError();
 }
 
+size_t packed_weight_bytes_dq(int wtype, int64_t N, int64_t K) {
+    const int64_t G = (N + 15) / 16;
+    if (wtype == 8) return (size_t)(G * (K / 64) * (1024 + 64));
+    if (wtype == 12) return (size_t)(G * ((K / 64) * 512 + (K / 256) * 256));
+    return 0;
+}
+
+hipError_t launch_pack_weights_dq(int wtype, const void* w, void* out, int N, int K, hipStream_t s) {
+    const int64_t blocks = (int64_t)N * (K / 32);
+    if (blocks == 0) return hipSuccess;
+    // rows past N in the last 16-row group: zero codes and scales
+    const size_t bytes = packed_weight_bytes_dq(wtype, N, K);
+    if (N % 16) {
+        if (hipError_t e = launch_fill_u32((uint32_t*)out, 0u, bytes / 4, s)) return e;
+    }
+    const dim3 grid((unsigned)((blocks + 255) / 256)), block(256);
+    if (wtype == 8)
+        hipLaunchKernelGGL(k_pack_wdq<8>, grid, block, 0, s, (const uint8_t*)w, (uint8_t*)out, N, K);
+    else if (wtype == 12)
+        hipLaunchKernelGGL(k_pack_wdq<12>, grid, block, 0, s, (const uint8_t*)w, (uint8_t*)out, N, K);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 hipError_t launch_f32_to_f16(const float* x, _Float16* h, int64_t n, hipStream_t s) {
     const int64_t n8 = n / 8;
     if (n8 == 0) return hipSuccess;
@@ -683,13 +922,13 @@ hipError_t launch_f32_to_f16(const float* x, _Float16* h, int64_t n, hipStream_t
     return hipGetLastError();
 }
 
-template <int BM, bool XF32, int NS, int WMR, int BN>
-static hipError_t launch_h16_t(const GemmH16Args& a, hipStream_t s, const LnArgs* ln) {
+template <int BM, bool XF32, int NS, int WMR, int BN, int WQ>
+static hipError_t launch_h16_w(const GemmH16Args& a, hipStream_t s, const LnArgs* ln) {
     const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     const int splits = std::max(a.splits, 1);
     const dim3 block(128 * WMR);
     if (splits > 1) {
-        hipLaunchKernelGGL((k_gemm_h16<0, BM, true, XF32, NS, WMR, BN>), dim3(tiles * splits), block, 0, s, a);
+        hipLaunchKernelGGL((k_gemm_h16<0, BM, true, XF32, NS, WMR, BN, WQ>), dim3(tiles * splits), block, 0, s, a);
         if (ln) return launch_reduce_ln(a, BM, BN, *ln, s);
         const size_t n4 = (size_t)tiles * BM * BN / 4;
         const dim3 rg((unsigned)((n4 + 255) / 256)), rb(256);
@@ -697,11 +936,19 @@ static hipError_t launch_h16_t(const GemmH16Args& a, hipStream_t s, const LnArgs
         else if (a.act == 2) hipLaunchKernelGGL((k_gemm_h16_reduce<2, BM, BN>), rg, rb, 0, s, a);
         else hipLaunchKernelGGL((k_gemm_h16_reduce<0, BM, BN>), rg, rb, 0, s, a);
     } else {
-        if (a.act == 1) hipLaunchKernelGGL((k_gemm_h16<1, BM, false, XF32, NS, WMR, BN>), dim3(tiles), block, 0, s, a);
-        else if (a.act == 2) hipLaunchKernelGGL((k_gemm_h16<2, BM, false, XF32, NS, WMR, BN>), dim3(tiles), block, 0, s, a);
-        else hipLaunchKernelGGL((k_gemm_h16<0, BM, false, XF32, NS, WMR, BN>), dim3(tiles), block, 0, s, a);
+        if (a.act == 1) hipLaunchKernelGGL((k_gemm_h16<1, BM, false, XF32, NS, WMR, BN, WQ>), dim3(tiles), block, 0, s, a);
+        else if (a.act == 2) hipLaunchKernelGGL((k_gemm_h16<2, BM, false, XF32, NS, WMR, BN, WQ>), dim3(tiles), block, 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_h16<0, BM, false, XF32, NS, WMR, BN, WQ>), dim3(tiles), block, 0, s, a);
     }
     return hipGetLastError();
+}
+
+template <int BM, bool XF32, int NS, int WMR, int BN>
+static hipError_t launch_h16_t(const GemmH16Args& a, hipStream_t s, const LnArgs* ln) {
+    if (a.wq == 8) return launch_h16_w<BM, XF32, NS, WMR, BN, 8>(a, s, ln);
+    if (a.wq == 12) return launch_h16_w<BM, XF32, NS, WMR, BN, 12>(a, s, ln);
+    if (a.wq == 0) return launch_h16_w<BM, XF32, NS, WMR, BN, 0>(a, s, ln);
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a0, hipStream_t s, const LnArgs* ln) {

@@ -137,7 +137,7 @@ int run_gemm_h16(mgh_ctx* c, mgh::GemmH16Args a) {
         MGH_HIP(c, mgh::launch_gemv_h16(a, c->stream), "k_gemv_h16");
         return MGH_OK;
     }
-    const mgh::H16Plan p = mgh::gemm_h16_plan(a.M, a.N, a.K, a.xf != nullptr);
+    const mgh::H16Plan p = mgh::gemm_h16_plan(a.M, a.N, a.K, a.xf != nullptr, a.wq);
     a.splits = p.splits;
     if (p.splits > 1) {
         if (int r = ensure_qp_ws(c, p.ws_bytes)) return r;
@@ -931,52 +931,46 @@ int mgh_f32_to_f16(mgh_ctx* c, const float* x, int64_t n, void* x16) {
     return MGH_OK;
 }
 
-int mgh_gemm_h16(mgh_ctx* c, const void* wp16, int N, int K, const void* x16, int M,
-                 const float* bias, int act, const float* resid, float* y) {
+}  // extern "C"
+
+namespace {
+
+// The dequantize-fused FC entry points, for either weight form: wq 0 (fp16 [N][K] from
+// mgh_pack_weights_f16) or 8 / 12 (the K-loop-dequant layout of mgh_pack_weights_dq).
+int gemm_h16_any(mgh_ctx* c, const char* fn, int wq, const void* w, int N, int K, const void* x16, int M,
+                 const float* bias, int act, const float* resid, float* y, _Float16* y16) {
     if (!c) return MGH_ERR_ARG;
-    if (int r = check_h16(c, "gemm_h16", wp16, N, K, x16, M, bias, act, resid, y)) return r;
+    if (int r = check_h16(c, fn, w, N, K, x16, M, bias, act, resid, y16 ? (const float*)y16 : y)) return r;
     if (M == 0) return MGH_OK;
     if (int r = set_dev(c)) return r;
     mgh::GemmH16Args a{};
-    a.x = (const _Float16*)x16; a.w = (const _Float16*)wp16;
-    a.bias = bias; a.resid = resid; a.y = y;
+    a.x = (const _Float16*)x16; a.w = w; a.wq = wq;
+    a.bias = bias; a.resid = resid; a.y = y16 ? nullptr : y; a.y16 = y16;
     a.M = M; a.N = N; a.K = K; a.act = act;
     return run_gemm_h16(c, a);
 }
 
-int mgh_gemm_h16_y16(mgh_ctx* c, const void* wp16, int N, int K, const void* x16, int M,
-                     const float* bias, int act, const float* resid, void* y16) {
+int gemm_h16_ln_any(mgh_ctx* c, const char* fn, int wq, const void* w, int N, int K, const void* x16, int M,
+                    const float* bias, int act, const float* resid, float* y, const float* gamma,
+                    const float* beta, float eps, float* y_ln, int emit, void* codes, float* dx, void* s4) {
     if (!c) return MGH_ERR_ARG;
-    if (int r = check_h16(c, "gemm_h16_y16", wp16, N, K, x16, M, bias, act, resid, (const float*)y16)) return r;
+    const std::string f(fn);
+    if (int r = check_h16(c, fn, w, N, K, x16, M, bias, act, resid, y)) return r;
+    if (N % 256 || N > 2048) return fail(c, MGH_ERR_UNSUPPORTED, f + ": needs N % 256 == 0 and N <= 2048");
+    if (emit < 0 || emit > 2) return fail(c, MGH_ERR_ARG, f + ": emit must be 0, 1 or 2");
     if (M == 0) return MGH_OK;
-    if (int r = set_dev(c)) return r;
-    mgh::GemmH16Args a{};
-    a.x = (const _Float16*)x16; a.w = (const _Float16*)wp16;
-    a.bias = bias; a.resid = resid; a.y16 = (_Float16*)y16;
-    a.M = M; a.N = N; a.K = K; a.act = act;
-    return run_gemm_h16(c, a);
-}
-
-int mgh_gemm_h16_ln(mgh_ctx* c, const void* wp16, int N, int K, const void* x16, int M, const float* bias,
-                    int act, const float* resid, float* y, const float* gamma, const float* beta, float eps,
-                    float* y_ln, int emit, void* codes, float* dx, void* s4) {
-    if (!c) return MGH_ERR_ARG;
-    if (int r = check_h16(c, "gemm_h16_ln", wp16, N, K, x16, M, bias, act, resid, y)) return r;
-    if (N % 256 || N > 2048) return fail(c, MGH_ERR_UNSUPPORTED, "gemm_h16_ln: needs N % 256 == 0 and N <= 2048");
-    if (emit < 0 || emit > 2) return fail(c, MGH_ERR_ARG, "gemm_h16_ln: emit must be 0, 1 or 2");
-    if (M == 0) return MGH_OK;
-    if (!gamma || !beta || !y_ln) return fail(c, MGH_ERR_ARG, "gemm_h16_ln: null pointer");
+    if (!gamma || !beta || !y_ln) return fail(c, MGH_ERR_ARG, f + ": null pointer");
     if (emit && (!codes || (emit == 1 && (!dx || !s4))))
-        return fail(c, MGH_ERR_ARG, "gemm_h16_ln: emit needs d_codes (and d_dx, d_s4 for INT8)");
+        return fail(c, MGH_ERR_ARG, f + ": emit needs d_codes (and d_dx, d_s4 for INT8)");
     if (!aligned16(gamma) || !aligned16(beta) || !aligned16(y_ln) || !aligned16(codes) || ((uintptr_t)dx & 3u) ||
         ((uintptr_t)s4 & 3u))
-        return fail(c, MGH_ERR_ARG, "gemm_h16_ln: gamma/beta/y_ln/codes must be 16-byte aligned");
+        return fail(c, MGH_ERR_ARG, f + ": gamma/beta/y_ln/codes must be 16-byte aligned");
     if (int r = set_dev(c)) return r;
     mgh::GemmH16Args a{};
-    a.x = (const _Float16*)x16; a.w = (const _Float16*)wp16;
+    a.x = (const _Float16*)x16; a.w = w; a.wq = wq;
     a.bias = bias; a.resid = resid; a.y = y;
     a.M = M; a.N = N; a.K = K; a.act = act;
-    const mgh::H16Plan p = mgh::gemm_h16_plan(M, N, K, false);
+    const mgh::H16Plan p = mgh::gemm_h16_plan(M, N, K, false, wq);
     if (!mgh::use_gemv_h16(M, K) && p.splits > 1 && act == 0) {
         // the split-K reduce normalizes each row as it leaves: one launch fewer
         if (int r = ensure_qp_ws(c, p.ws_bytes)) return r;
@@ -992,14 +986,14 @@ int mgh_gemm_h16_ln(mgh_ctx* c, const void* wp16, int N, int K, const void* x16,
     return MGH_OK;
 }
 
-int mgh_gemm_h16_f32in(mgh_ctx* c, const void* wp16, int N, int K, const float* x, int M,
+int gemm_h16_f32in_any(mgh_ctx* c, const char* fn, int wq, const void* w, int N, int K, const float* x, int M,
                        const float* bias, int act, const float* resid, float* y) {
     if (!c) return MGH_ERR_ARG;
-    if (int r = check_h16(c, "gemm_h16_f32in", wp16, N, K, x, M, bias, act, resid, y)) return r;
+    if (int r = check_h16(c, fn, w, N, K, x, M, bias, act, resid, y)) return r;
     if (M == 0) return MGH_OK;
     if (int r = set_dev(c)) return r;
     mgh::GemmH16Args a{};
-    a.w = (const _Float16*)wp16;
+    a.w = w; a.wq = wq;
     a.bias = bias; a.resid = resid; a.y = y;
     a.M = M; a.N = N; a.K = K; a.act = act;
     if (M < 2048) {
@@ -1017,6 +1011,85 @@ int mgh_gemm_h16_f32in(mgh_ctx* c, const void* wp16, int N, int K, const float* 
     return run_gemm_h16(c, a);
 }
 
+int check_dq(mgh_ctx* c, const char* fn, int wtype, int N, int K) {
+    if (!c) return MGH_ERR_ARG;
+    if (wtype != MGH_WTYPE_Q8_0 && wtype != MGH_WTYPE_Q4_K)
+        return fail(c, MGH_ERR_ARG, std::string(fn) + ": wtype must be MGH_WTYPE_Q8_0 (8) or MGH_WTYPE_Q4_K (12)");
+    if (wtype == MGH_WTYPE_Q4_K && K % 256 == 0 && K > 0) return MGH_OK;
+    if (wtype == MGH_WTYPE_Q4_K) return fail(c, MGH_ERR_ARG, std::string(fn) + ": Q4_K needs K % 256 == 0");
+    return MGH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mgh_gemm_h16(mgh_ctx* c, const void* wp16, int N, int K, const void* x16, int M,
+                 const float* bias, int act, const float* resid, float* y) {
+    return gemm_h16_any(c, "gemm_h16", 0, wp16, N, K, x16, M, bias, act, resid, y, nullptr);
+}
+
+int mgh_gemm_h16_y16(mgh_ctx* c, const void* wp16, int N, int K, const void* x16, int M,
+                     const float* bias, int act, const float* resid, void* y16) {
+    return gemm_h16_any(c, "gemm_h16_y16", 0, wp16, N, K, x16, M, bias, act, resid, nullptr, (_Float16*)y16);
+}
+
+int mgh_gemm_h16_ln(mgh_ctx* c, const void* wp16, int N, int K, const void* x16, int M, const float* bias,
+                    int act, const float* resid, float* y, const float* gamma, const float* beta, float eps,
+                    float* y_ln, int emit, void* codes, float* dx, void* s4) {
+    return gemm_h16_ln_any(c, "gemm_h16_ln", 0, wp16, N, K, x16, M, bias, act, resid, y, gamma, beta, eps, y_ln,
+                           emit, codes, dx, s4);
+}
+
+int mgh_gemm_h16_f32in(mgh_ctx* c, const void* wp16, int N, int K, const float* x, int M,
+                       const float* bias, int act, const float* resid, float* y) {
+    return gemm_h16_f32in_any(c, "gemm_h16_f32in", 0, wp16, N, K, x, M, bias, act, resid, y);
+}
+
+size_t mgh_packed_weight_bytes_dq(int wtype, int N, int K) {
+    if (N <= 0 || K <= 0 || K % 64) return 0;
+    if (wtype == MGH_WTYPE_Q4_K && K % 256) return 0;
+    return mgh::packed_weight_bytes_dq(wtype, N, K);
+}
+
+int mgh_pack_weights_dq(mgh_ctx* c, int wtype, const void* w, int N, int K, void* wdq) {
+    if (!c) return MGH_ERR_ARG;
+    if (int r = check_quant_shape(c, wtype, N, K, 0)) return r;
+    if (int r = check_dq(c, "pack_weights_dq", wtype, N, K)) return r;
+    if (!w || !wdq) return fail(c, MGH_ERR_ARG, "pack_weights_dq: null pointer");
+    if (!aligned16(wdq) || ((uintptr_t)w & 3u))
+        return fail(c, MGH_ERR_ARG, "pack_weights_dq: output must be 16-byte aligned, input 4-byte aligned");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_pack_weights_dq(wtype, w, wdq, N, K, c->stream), "k_pack_wdq");
+    return MGH_OK;
+}
+
+int mgh_gemm_dq(mgh_ctx* c, int wtype, const void* wdq, int N, int K, const void* x16, int M,
+                const float* bias, int act, const float* resid, float* y) {
+    if (int r = check_dq(c, "gemm_dq", wtype, N, K)) return r;
+    return gemm_h16_any(c, "gemm_dq", wtype, wdq, N, K, x16, M, bias, act, resid, y, nullptr);
+}
+
+int mgh_gemm_dq_y16(mgh_ctx* c, int wtype, const void* wdq, int N, int K, const void* x16, int M,
+                    const float* bias, int act, const float* resid, void* y16) {
+    if (int r = check_dq(c, "gemm_dq_y16", wtype, N, K)) return r;
+    return gemm_h16_any(c, "gemm_dq_y16", wtype, wdq, N, K, x16, M, bias, act, resid, nullptr, (_Float16*)y16);
+}
+
+int mgh_gemm_dq_ln(mgh_ctx* c, int wtype, const void* wdq, int N, int K, const void* x16, int M,
+                   const float* bias, int act, const float* resid, float* y, const float* gamma,
+                   const float* beta, float eps, float* y_ln, int emit, void* codes, float* dx, void* s4) {
+    if (int r = check_dq(c, "gemm_dq_ln", wtype, N, K)) return r;
+    return gemm_h16_ln_any(c, "gemm_dq_ln", wtype, wdq, N, K, x16, M, bias, act, resid, y, gamma, beta, eps, y_ln,
+                           emit, codes, dx, s4);
+}
+
+int mgh_gemm_dq_f32in(mgh_ctx* c, int wtype, const void* wdq, int N, int K, const float* x, int M,
+                      const float* bias, int act, const float* resid, float* y) {
+    if (int r = check_dq(c, "gemm_dq_f32in", wtype, N, K)) return r;
+    return gemm_h16_f32in_any(c, "gemm_dq_f32in", wtype, wdq, N, K, x, M, bias, act, resid, y);
+}
+
 int mgh_gemm_h16_f32in_noalloc(mgh_ctx* c, const void* wp16, int N, int K, const float* x, int M,
                                const float* bias, int act, const float* resid, float* y) {
     if (!c) return MGH_ERR_ARG;
@@ -1025,7 +1098,7 @@ int mgh_gemm_h16_f32in_noalloc(mgh_ctx* c, const void* wp16, int N, int K, const
     // the same launches as mgh_gemm_h16_f32in, with the rounded activations (M >= 2048) and the
     // split-K partials placed in the fixed scratch array instead of context buffers
     mgh::GemmH16Args a{};
-    a.w = (const _Float16*)wp16;
+    a.w = wp16;
     a.bias = bias; a.resid = resid; a.y = y;
     a.M = M; a.N = N; a.K = K; a.act = act;
     if (mgh::use_gemv_h16(M, K)) {               // skinny-M kernel: no scratch at all
@@ -1036,7 +1109,7 @@ int mgh_gemm_h16_f32in_noalloc(mgh_ctx* c, const void* wp16, int N, int K, const
     }
     const bool round_pass = M >= 2048;
     const size_t x16_b = round_pass ? round256((size_t)M * K * 2) : 0;
-    const mgh::H16Plan p = mgh::gemm_h16_plan(M, N, K, !round_pass);
+    const mgh::H16Plan p = mgh::gemm_h16_plan(M, N, K, !round_pass, 0);
     const size_t need = x16_b + (p.splits > 1 ? round256(p.ws_bytes) : 0);
     const size_t cap = mgh::noalloc_scratch_bytes();
     if (need > cap)

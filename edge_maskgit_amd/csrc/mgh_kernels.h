@@ -153,7 +153,9 @@ hipError_t launch_decode_step(DecodeArgs a, void* state, void* work, hipStream_t
 struct GemmH16Args {
     const _Float16* x;     // [M][K] fp16 activations, or
     const float* xf;       // [M][K] fp32 activations rounded to fp16 in the kernel (x unused)
-    const _Float16* w;     // [N][K]
+    const void* w;         // wq 0: fp16 [N][K]; wq 8 / 12: the K-loop-dequant layout of
+                           // launch_pack_weights_dq (Q8_0 / Q4_K bytes, GGUF-sized)
+    int wq;                // weight form: 0 fp16, 8 Q8_0, 12 Q4_K
     const float* bias;     // [N] or null
     const float* resid;    // [M][N] or null
     float* y;              // [M][N]
@@ -168,7 +170,7 @@ struct H16Plan {
     int ph;                // tile order: panel height in activation-row tiles
     size_t ws_bytes;
 };
-H16Plan gemm_h16_plan(int M, int N, int K, bool xf32);
+H16Plan gemm_h16_plan(int M, int N, int K, bool xf32, int wq);
 // LayerNorm-affine of a GEMM's output rows taken by the split-K reduce (k_gemm_h16_reduce_ln):
 // gamma/beta [N] and the LayerNorm outputs as launch_layernorm_affine takes them
 struct LnArgs {
@@ -183,6 +185,16 @@ struct LnArgs {
 };
 size_t packed_weight_bytes_f16(int64_t N, int64_t K);
 hipError_t launch_pack_weights_f16(int wtype, const void* w, void* out, int N, int K, hipStream_t s);
+// K-loop-dequant weight layout (the operand of the wq = 8 / 12 forms of k_gemm_h16 and
+// k_gemv_h16): the GGUF bytes regrouped into 16-row groups and 64-deep K stages, so that one
+// 16-byte-per-lane DMA moves whole MFMA fragments; the same byte count per weight as the GGUF
+// blocks (Q8_0 1.0625, Q4_K 0.5625) for N % 16 == 0, rows padded to a multiple of 16.
+//   Q8_0: codes [G][K/64][2][4][16][8] u8 (q + 128), then scales [G][K/64][2][16] fp16
+//   Q4_K: nibbles [G][K/64][2][4][16][4] (byte e: element e low, e + 4 high), then the raw
+//         16-byte super-block headers (d, dmin, packed 6-bit scales) [G][K/256][16][16]
+// with G = ceil(N / 16) row groups; [2][4][16] = K half, 8-wide K slice, row in the group.
+size_t packed_weight_bytes_dq(int wtype, int64_t N, int64_t K);
+hipError_t launch_pack_weights_dq(int wtype, const void* w, void* out, int N, int K, hipStream_t s);
 hipError_t launch_f32_to_f16(const float* x, _Float16* h, int64_t n, hipStream_t s);
 // ln: the split-K reduce also writes the LayerNorm-affine of y's rows (the plan must split K;
 // act 0, fp32 y, N % 256 == 0, N <= 2048)

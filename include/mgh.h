@@ -310,6 +310,31 @@ int mgh_gemm_h16_ln(mgh_ctx* ctx, const void* d_wp16, int N, int K, const void* 
 int mgh_gemm_h16_y16(mgh_ctx* ctx, const void* d_wp16, int N, int K, const void* d_x16, int M,
                      const float* d_bias, int act, const float* d_resid, void* d_y16);
 
+/* ---- dequantize-fused FC path on the quantized bytes: the same product as mgh_gemm_h16
+ *      (the reference's k_mul_mat_q8_0_t2_h / k_mul_mat_q4k_t2_h, mg-opencl.cpp:320-411, which
+ *      decode every weight inside the K loop: DEQ_Q8 :386-387, deq_q4k_elem :252-262), reading
+ *      the Q8_0 / Q4_K bytes on every call instead of an fp16 copy. mgh_pack_weights_dq
+ *      regroups the GGUF blocks once, at upload, into 16-row groups of 64-deep K stages laid
+ *      out in MFMA fragment order (Q8_0: int8 codes + fp16 block scales, 1.0625 bytes per
+ *      weight; Q4_K: 4-bit values + the raw 16-byte super-block headers, 0.5625 bytes per
+ *      weight; rows padded to a multiple of 16; buffer size mgh_packed_weight_bytes_dq). The
+ *      kernels decode each weight to d*q, resp. (d*sc)*q - dmin*m rounded once to fp16 -- the
+ *      value mgh_pack_weights_f16 stores -- as the MFMA fragments are read, so results equal
+ *      mgh_gemm_h16's for the same tile plan. Shapes and alignment as mgh_gemm_h16 (K % 64 == 0,
+ *      Q4_K K % 256 == 0, N % 4 == 0, 16-byte aligned operands). ---- */
+size_t mgh_packed_weight_bytes_dq(int wtype, int N, int K);
+int mgh_pack_weights_dq(mgh_ctx* ctx, int wtype, const void* d_w, int N, int K, void* d_wdq);
+int mgh_gemm_dq(mgh_ctx* ctx, int wtype, const void* d_wdq, int N, int K, const void* d_x16, int M,
+                const float* d_bias, int act, const float* d_resid, float* d_y);
+int mgh_gemm_dq_f32in(mgh_ctx* ctx, int wtype, const void* d_wdq, int N, int K, const float* d_x, int M,
+                      const float* d_bias, int act, const float* d_resid, float* d_y);
+int mgh_gemm_dq_y16(mgh_ctx* ctx, int wtype, const void* d_wdq, int N, int K, const void* d_x16, int M,
+                    const float* d_bias, int act, const float* d_resid, void* d_y16);
+int mgh_gemm_dq_ln(mgh_ctx* ctx, int wtype, const void* d_wdq, int N, int K, const void* d_x16, int M,
+                   const float* d_bias, int act, const float* d_resid, float* d_y, const float* d_gamma,
+                   const float* d_beta, float eps, float* d_y_ln, int emit, void* d_codes, float* d_dx,
+                   void* d_s4);
+
 /* ---- iterative decoding on the device: one step of the reference's generate() loop,
  *      src/mg-generate.cpp:82-121, for B images whose logits [B][S][V] are already in HBM.
  *      Image b draws from std::mt19937_64(seeds[b]) through uniform_real_distribution<double>

@@ -1,0 +1,167 @@
+"""GPU parity of the dequantize-fused FC path on the quantized bytes: mgh_pack_weights_dq and
+mgh_gemm_dq / _f32in / _y16 / _ln (k_gemm_h16.hip, weight forms 8 and 12: the Q8_0 / Q4_K
+bytes are read on every call and decoded to fp16 as the MFMA fragments are read; k_gemv_h16
+for a few activation rows).
+
+Bars:
+  * the decoded weights are the values mgh_pack_weights_f16 stores (pinned to the oracle's
+    dequantization in test_gpu_h16.py), so every output equals mgh_gemm_h16's on the fp16 copy
+    of the same weights bit for bit: both run the same tile plan, and a wrong byte, scale,
+    nibble, sub-block or group shows as a different bit pattern;
+  * the path as a whole: within 1e-3 * max|y| of the reference's dequantize-then-F32 product
+    on the fp32 activations (oracle.gemm_q_deq_f32, mg-cpu.cpp:48-72 semantics);
+  * the layout holds exactly the GGUF byte count for N % 16 == 0 (1.0625 / 0.5625 bytes per
+    weight) and pads the last 16-row group otherwise.
+"""
+import numpy as np
+import pytest
+
+import edge_maskgit_amd as ema
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = ema.Context(0)
+    yield c
+    c.close()
+
+
+def _rel(y, ref):
+    return float(np.abs(y - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def _gguf_bytes(wtype, N, K):
+    return N * (K // 32) * 34 if wtype == ema.WTYPE_Q8_0 else N * (K // 256) * 144
+
+
+def _weights(ctx, wtype, N, K, seed):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    w[0, :64] = 0.0                       # an all-zero block (d = 0)
+    w[-1, 32:64] *= 40.0                  # a large-scale block
+    wq = oracle.quantize(wtype, w)
+    dW = ctx.upload(wq)
+    dP16 = ctx.alloc(ema.packed_weight_bytes_f16(N, K))
+    ctx.pack_weights_f16(wtype, dW, N, K, dP16)
+    nb = ema.packed_weight_bytes_dq(wtype, N, K)
+    dQ = ctx.alloc(nb)
+    ctx.pack_weights_dq(wtype, dW, N, K, dQ)
+    ctx.free(dW)
+    return wq, dP16, dQ, nb
+
+
+@pytest.mark.parametrize("wtype", [ema.WTYPE_Q8_0, ema.WTYPE_Q4_K])
+@pytest.mark.parametrize("N,K", [(16, 256), (96, 512), (100, 768), (2304, 768), (768, 3072)])
+def test_dq_layout_size(wtype, N, K):
+    G = (N + 15) // 16
+    got = ema.packed_weight_bytes_dq(wtype, N, K)
+    assert got == _gguf_bytes(wtype, 16 * G, K)
+    if N % 16 == 0:
+        assert got == _gguf_bytes(wtype, N, K)
+
+
+# skinny-M kernel (M <= 16, or <= 32 with K <= 1024) and tiled plans: few tiles (64 x 64 on a
+# 3-deep ring, 32-row tiles), split K, 128-row tiles, fp16 operands; N = 100 and 132 end in a
+# partial 16-row group
+SHAPES = [(1, 2304, 768), (7, 132, 256), (16, 768, 3072), (32, 768, 768), (33, 100, 768),
+          (65, 128, 768), (257, 3072, 768), (257, 768, 3072), (1025, 2304, 768), (1025, 768, 768),
+          (1025, 3072, 768), (1025, 768, 3072), (4097, 2304, 768), (4112, 768, 3072)]
+
+
+@pytest.mark.parametrize("wtype", [ema.WTYPE_Q8_0, ema.WTYPE_Q4_K])
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_dq_f32in_equals_fp16_copy(ctx, wtype, M, N, K):
+    act, res = (1, False) if (M + N) % 2 else (0, True)
+    print(f"gemm_dq_f32in wtype={wtype} M={M} N={N} K={K} act={act} resid={res}", flush=True)
+    rng = np.random.default_rng(M + 3 * N + K + wtype)
+    wq, dP16, dQ, _ = _weights(ctx, wtype, N, K, M + N + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+    resid = rng.standard_normal((M, N)).astype(np.float32) if res else None
+    dX, dB = ctx.upload(x), ctx.upload(bias)
+    dR = ctx.upload(resid) if res else None
+    dY, dY16 = ctx.alloc(M * N * 4), ctx.alloc(M * N * 4)
+    ctx.gemm_dq_f32in(wtype, dQ, N, K, dX, M, dB, act, dR, dY)
+    y = ctx.download(dY, (M, N), np.float32)
+    ctx.gemm_h16_f32in(dP16, N, K, dX, M, dB, act, dR, dY16)
+    y16 = ctx.download(dY16, (M, N), np.float32)
+    for t in (dP16, dQ, dX, dB, dR, dY, dY16):
+        if t is not None:
+            ctx.free(t)
+    assert np.array_equal(y.view(np.uint32), y16.view(np.uint32))
+    if M * N * K <= 1025 * 3072 * 768:
+        ref = oracle.gemm_q_deq_f32(wtype, wq, N, K, x, bias=bias, act=act, resid=resid)
+        err = _rel(y, ref)
+        print(f"  rel err vs dequantize-then-F32 {err:.2e}")
+        assert err <= 1e-3
+
+
+@pytest.mark.parametrize("wtype", [ema.WTYPE_Q8_0, ema.WTYPE_Q4_K])
+@pytest.mark.parametrize("M,N,K", [(12, 768, 768), (257, 2304, 768), (1025, 3072, 768), (4112, 768, 3072)])
+def test_gemm_dq_fp16_operand_and_y16(ctx, wtype, M, N, K):
+    """fp16 activations (the LayerNorm's operand form) and fp16 output: equal to the fp16-copy
+    kernel, bit for bit."""
+    print(f"gemm_dq/_y16 wtype={wtype} M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M * 5 + N + K)
+    _, dP16, dQ, _ = _weights(ctx, wtype, N, K, M * 3 + N)
+    x16 = rng.standard_normal((M, K)).astype(np.float16)
+    bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+    dX, dB = ctx.upload(x16), ctx.upload(bias)
+    dA, dB2 = ctx.alloc(M * N * 4), ctx.alloc(M * N * 4)
+    for act in (0, 1):
+        ctx.gemm_dq(wtype, dQ, N, K, dX, M, dB, act, None, dA)
+        ctx.gemm_h16(dP16, N, K, dX, M, dB, act, None, dB2)
+        a, b = ctx.download(dA, (M, N), np.float32), ctx.download(dB2, (M, N), np.float32)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"act {act}"
+    ctx.gemm_dq_y16(wtype, dQ, N, K, dX, M, dB, 1, None, dA)
+    ctx.gemm_h16_y16(dP16, N, K, dX, M, dB, 1, None, dB2)
+    a, b = ctx.download(dA, (M, N), np.uint16), ctx.download(dB2, (M, N), np.uint16)
+    assert np.array_equal(a, b)
+    for t in (dP16, dQ, dX, dB, dA, dB2):
+        ctx.free(t)
+
+
+@pytest.mark.parametrize("wtype", [ema.WTYPE_Q8_0, ema.WTYPE_Q4_K])
+@pytest.mark.parametrize("M,N,K", [(257, 768, 3072), (1025, 768, 768), (4112, 768, 3072)])
+def test_gemm_dq_ln_equals_fp16_copy(ctx, wtype, M, N, K):
+    """the post-norm pair (FC + residual, then LayerNorm-affine of its rows; the split-K reduce
+    normalizes the rows where the plan splits K) on the quantized bytes: y and the LayerNorm
+    outputs equal the fp16-copy pair's bit for bit"""
+    print(f"gemm_dq_ln wtype={wtype} M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M + N * 7 + K)
+    _, dP16, dQ, _ = _weights(ctx, wtype, N, K, M + 11)
+    x16 = rng.standard_normal((M, K)).astype(np.float16)
+    bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+    resid = rng.standard_normal((M, N)).astype(np.float32)
+    gamma = (1 + 0.02 * rng.standard_normal(N)).astype(np.float32)
+    beta = (0.01 * rng.standard_normal(N)).astype(np.float32)
+    up = [ctx.upload(a) for a in (x16, bias, resid, gamma, beta)]
+    dX, dB, dR, dG, dBe = up
+    outs = []
+    for kind in ("dq", "h16"):
+        dY, dL, dC = ctx.alloc(M * N * 4), ctx.alloc(M * N * 4), ctx.alloc(M * N * 2)
+        if kind == "dq":
+            ctx.gemm_dq_ln(wtype, dQ, N, K, dX, M, dB, 0, dR, dY, dG, dBe, 1e-12, dL, emit=2, codes=dC)
+        else:
+            ctx.gemm_h16_ln(dP16, N, K, dX, M, dB, 0, dR, dY, dG, dBe, 1e-12, dL, emit=2, codes=dC)
+        outs.append([ctx.download(dY, (M, N), np.uint32), ctx.download(dL, (M, N), np.uint32),
+                     ctx.download(dC, (M, N), np.uint16)])
+        for t in (dY, dL, dC):
+            ctx.free(t)
+    for t in up + [dP16, dQ]:
+        ctx.free(t)
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
+
+
+def test_pack_dq_rejects_bad_shapes(ctx):
+    dW = ctx.alloc(1024)
+    with pytest.raises(ema.MghError):
+        ctx.pack_weights_dq(ema.WTYPE_Q4_K, dW, 4, 128, dW)          # Q4_K needs K % 256 == 0
+    with pytest.raises(ema.MghError):
+        ctx.pack_weights_dq(7, dW, 4, 256, dW)                        # not a quantized type
+    ctx.free(dW)
+    assert ema.packed_weight_bytes_dq(ema.WTYPE_Q4_K, 4, 128) == 0
