@@ -7,17 +7,24 @@ layer's four Q8_0 FC GEMMs at M = 1025 tokens (32x32 grid + class token), fp32 a
     out   768 -> 768   (+bias +residual)
     up    768 -> 3072  (+bias, GELU)
     down 3072 -> 768   (+bias +residual)
-A step runs each FC of the chosen production path, all inputs already resident in HBM, the
-weights prepared once at upload (outside the timed region, as the reference uploads each
-weight once):
-  --path h16 (default, the dequantize-fused path; it meets the 1e-3 * max|y| bar against the
-    reference's dequantize-then-F32 product): k_gemm_h16 on the weights dequantized to fp16 at
-    upload, the fp32 activations rounded to fp16 as they are read: fp16 MFMA, fp32 accumulation,
-    fused bias/GELU/residual epilogue;
+A step runs each FC of the chosen path, all inputs already resident in HBM, the weights
+prepared once at upload (outside the timed region, as the reference uploads each weight once):
+  --path dq (default, the headline): the dequantize-fused path on the quantized bytes --
+    k_gemm_fc<..., WQ=8> reads the Q8_0 blocks on every call (regrouped once at upload into
+    MFMA fragment order, 1.0625 bytes per weight, the GGUF size) and decodes each weight to
+    fp16 inside the K loop, as the reference's k_mul_mat_q8_0_t2_h does; the fp32 activations
+    are rounded to fp16 as they are read; fp16 MFMA, fp32 accumulation, fused
+    bias/GELU/residual epilogue. It meets the 1e-3 * max|y| bar against the reference's
+    dequantize-then-F32 product;
+  --path h16: the same product on fp16 weight copies made at upload (k_gemm_fc<..., WQ=0>,
+    2 bytes per weight read, no decoding in the K loop; identical outputs);
   --path packed (the int8-dot path, bit-exact int32 block dots of the reference's int8
     kernels): per-32 int8 activation quantization (k_quantize_act_q8, codes as fp16), then
-    k_gemm_qp on the packed codes with per-block scales applied in fp32.
-The other path is measured on the same workload and reported under extra.
+    k_gemm_qp on the packed codes with per-block scales applied in fp32;
+  --path raw: the int8-dot path on one-byte operands: int8 activation codes and the GGUF blocks
+    as stored, on int8 MFMA (k_gemm_q_i8).
+Every path is measured on every GEMM workload of the metric (Q8_0 and Q4_K at M = 1025 and
+4097) and reported under extra.<wtype>_m<M> with its TOPS and fraction of the HBM roofline.
 The step's kernels are enqueued one by one on the context's stream (--graphs instead captures
 each buffer set's step once as a HIP graph and replays it; for these few-kernel steps the
 graph launch measured slower). Buffers rotate over >= --rotate-gb of distinct sets so the 256 MB
@@ -27,10 +34,10 @@ step on two buffer sets (warm caches) for comparison. Synthetic data: x ~ N(0,1)
 quantized to Q8_0, biases ~ N(0,0.01), residuals ~ N(0,1), seeded.
 
 value = 2*M*K*N summed over the four GEMMs / step time, in TOPS.
-roofline = the dominant kernel (k_gemm_h16, resp. k_gemm_qp), HBM-bound: algorithmic bytes of
-its launches (quantized weights once + the activations it reads: fp32 on the h16 path, fp16
-codes + block scales on the int8 path + fp32 output + bias + residual) divided by its average
-launch duration, timed with HIP events
+roofline = the dominant kernel (k_gemm_fc on the dq / h16 paths, k_gemm_qp / k_gemm_q_i8 on the
+int8 paths), HBM-bound: algorithmic bytes of its launches (quantized weights once + the
+activations it reads: fp32 on the dq / h16 paths, int8 codes + block scales on the int8 paths +
+fp32 output + bias + residual) divided by its average launch duration, timed with HIP events
 on the stream it runs on; traffic = the measured HBM bytes of those launches (rocprofv3
 FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy), from profiles/traffic_*.json, reported only
 when that file was measured on the same kernel sources (SHA-256 of edge_maskgit_amd/csrc, also
@@ -73,7 +80,13 @@ LAYER = [  # name, N, K, act, residual
 CFG1 = [("cfg1", 3072, 768, ema.ACT_NONE, False)]   # configs[0]: one Q8_0 FC GEMM at M=257
 
 
-KERNEL = {"packed": "k_gemm_qp", "raw": "k_gemm_q_i8", "h16": "k_gemm_h16", "dq": "k_gemm_h16<WQ=8|12>"}
+KERNEL = {"packed": "k_gemm_qp", "raw": "k_gemm_q_i8", "h16": "k_gemm_fc<..., WQ=0>",
+          "dq": "k_gemm_fc<..., WQ=8|12>"}
+# profiles/traffic_<name>_cfg2_q8_m1025.json: the counter-measured HBM bytes of each path's step
+TRAFFIC_FILE = {"dq": "k_gemm_fc_dq", "h16": "k_gemm_fc_f16", "packed": "k_gemm_qp", "raw": "k_gemm_q_i8"}
+# bytes each path's GEMM kernel reads per weight, Q8_0 / Q4_K
+WEIGHT_BYTES = {"dq": {8: 1.0625, 12: 0.5625}, "raw": {8: 1.0625, 12: 0.5625},
+                "h16": {8: 2.0, 12: 2.0}, "packed": {8: 2.125, 12: 2.25}}
 PATH_NAME = {"packed": "int8_dot", "raw": "int8_dot_raw", "h16": "dequant_f16", "dq": "dequant_q"}
 WORKLOAD_PATH = {
     "h16": "dequantize-fused path (weights dequantized once to fp16 at upload; per FC one GEMM "
@@ -262,15 +275,15 @@ def layer_ops(M, layer=LAYER):
 def gemm_alg_bytes(M, wtype, path="h16", layer=LAYER):
     """Algorithmic HBM bytes of the four GEMM launches of one step: the quantized weights
     once, the activations the launch reads (h16 path: the fp32 rows, rounded in the kernel;
-    int8-dot path: fp16 codes + fp32 block scales (+ block sums for Q4_K)), the fp32 output,
+    int8-dot paths: fp16-held or one-byte codes + fp32 block scales (+ block sums for Q4_K)), the fp32 output,
     bias and residual."""
     tot = 0
     for _, N, K, act, res in layer:
         nb = K // 32
         if path in ("h16", "dq"):          # fp32 activations read by the GEMM itself
             tot += N * row_bytes(wtype, K) + M * K * 4 + M * N * 4 + N * 4
-        else:
-            tot += N * row_bytes(wtype, K) + M * K * 2 + M * N * 4 + N * 4
+        else:                              # int8 codes: fp16-held (packed) or one byte (raw)
+            tot += N * row_bytes(wtype, K) + M * K * (2 if path == "packed" else 1) + M * N * 4 + N * 4
             tot += M * nb * 4 * (2 if wtype == ema.WTYPE_Q4_K else 1)
         if res:
             tot += M * N * 4
@@ -643,6 +656,20 @@ def measure_vqgan(path, steps=5, cpu=True, int8=True):
     return res
 
 
+def host_cpu():
+    """nproc, the CPU model name and OMP_NUM_THREADS of the host the CPU baseline runs on"""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu_model": model, "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
 def cpu_baseline(host, M, wtype, budget_s=15.0):
     """The reference CPU executor (libmgref) on dequantized weights, single thread, over the
     same four GEMMs; rows are processed in chunks until the budget is spent."""
@@ -662,7 +689,7 @@ def cpu_baseline(host, M, wtype, budget_s=15.0):
                 ops += 2.0 * (r1 - r0) * N * K
             rows_done = r1
         dt = time.perf_counter() - t0
-        return {"value": round(ops / dt / 1e12, 6), "unit": "TOPS", "cores": 1, "kind": "reference",
+        return {"value": round(ops / dt / 1e12, 6), "unit": "TOPS", "cores": 1, "kind": "reference", **host_cpu(),
                 "sample": f"reference mg-cpu k_mul_mat (F32, dequantized Q8_0 weights), the same four "
                           f"GEMMs on rows 0..{rows_done - 1} of M={M} ({ops/1e9:.2f} Gop in {dt:.1f} s)"}
     return cpu_oracle_int8(host, M, wtype)
@@ -681,7 +708,7 @@ def cpu_oracle_int8(host, M, wtype, rows=None):
         oracle.gemm_q_i8(wtype, h["wq"], N, K, qx, dx, bias=h["bias"], act=act)
         ops += 2.0 * rows * N * K
     dt = time.perf_counter() - t0
-    return {"value": round(ops / dt / 1e12, 6), "unit": "TOPS", "cores": nth, "kind": "port",
+    return {"value": round(ops / dt / 1e12, 6), "unit": "TOPS", "cores": nth, "kind": "port", **host_cpu(),
             "sample": f"C oracle int8-dot path (OpenMP), four GEMMs on {rows} of {M} rows ({ops/1e9:.2f} Gop in {dt:.1f} s)"}
 
 
@@ -694,7 +721,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--graphs", action="store_true",
                     help="replay a captured HIP graph per step instead of enqueuing the kernels one by one")
-    ap.add_argument("--path", choices=["packed", "h16", "raw", "dq"], default="h16",
+    ap.add_argument("--path", choices=["packed", "h16", "raw", "dq"], default="dq",
                     help="packed: int8-dot path on the device-native weight layout; h16: "
                          "dequantize-fused fp16 path; raw: int8-dot on GGUF blocks as stored")
     ap.add_argument("--no-fwd", action="store_true", help="skip the transformer forward (cfg4)")
@@ -712,7 +739,7 @@ def main():
     ap.add_argument("--only-vqgan", action="store_true",
                     help="measure only the VQGAN decoder and print its record: the run a kernel profile wraps")
     ap.add_argument("--extra", action="store_true",
-                    help="also measure Q8_0 M=4097 and Q4_K M=1025/4097 layers")
+                    help="also measure the cfg5 forward (Q4_K, 64 images) and the 64-image generate loop")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
@@ -764,25 +791,48 @@ def main():
              "step_hbm_roofline_us": round(step_alg_bytes(M, wtype) / (HBM_PEAK_GBS * 1e9) * 1e6, 2),
              "step_frac_of_hbm_roofline": round(step_alg_bytes(M, wtype) / (HBM_PEAK_GBS * 1e9)
                                                 / (ms_step * 1e-3), 4)}
-    other = "packed" if a.path == "h16" else "h16"
-    if not a.only_main:
+    if a.only_main:
+        a.no_fwd, a.no_cpu = True, True
+    else:
         # the same step with warm caches: two buffer sets, so weights and activations stay in
         # the MALL (and largely in the L2s) between steps; reported beside the cold headline
         hs, hg, _ = measure(ctx, M, wtype, a.steps, a.warmup, 0.0, use_graphs=a.graphs, path=a.path)
         extra["cfg2_hot_cache"] = {"ms_per_step": round(hs, 5), "tops": round(ops / (hs * 1e-3) / 1e12, 2),
                                    "buffer_sets": 2}
-    if a.only_main:
-        a.no_fwd, a.no_cpu, a.extra = True, True, False
-    # the other production path on the same workload
-    if not a.only_main:
-        so, go, _ = measure(ctx, M, wtype, a.steps, a.warmup, a.rotate_gb, use_graphs=a.graphs, path=other)
-        extra[f"cfg2_{PATH_NAME[other]}"] = {
-            "ms_per_step": round(so, 5), "tops": round(ops / (so * 1e-3) / 1e12, 2),
-            "gemm_tops": round(ops / (go * 1e-3) / 1e12, 2), "kernel": KERNEL[other]}
-        # the single Q8_0 FC GEMM at M=257 (weight-streaming shape), both paths
+        # every path on every GEMM workload of the metric (configs[1], [2]): Q8_0 at M = 1025 and
+        # 4097, Q4_K at M = 1025 and 4097; per path the step time, TOPS and the fraction of the
+        # HBM roofline on the metric's algorithmic bytes (quantized weights once, fp32 activations
+        # and outputs once), plus the bytes the path's kernels actually read per weight
+        paths = [p for p in ("dq", "h16", "packed", "raw") if p != a.path]
+        for (mm, wt) in ((1025, ema.WTYPE_Q8_0), (4097, ema.WTYPE_Q8_0), (1025, ema.WTYPE_Q4_K),
+                         (4097, ema.WTYPE_Q4_K)):
+            key = f"{'q8_0' if wt == ema.WTYPE_Q8_0 else 'q4_k'}_m{mm}"
+            ab = step_alg_bytes(mm, wt)
+            ent = {"alg_bytes_per_step": ab,
+                   "hbm_roofline_us": round(ab / (HBM_PEAK_GBS * 1e9) * 1e6, 2)}
+            for pth in ([a.path] if (mm, wt) != (M, wtype) else []) + paths:
+                if wt == ema.WTYPE_Q4_K and pth == "raw" and mm > 1025:
+                    continue
+                st = max(10, a.steps // 2) if mm > 1025 else a.steps
+                sm, sg, _ = measure(ctx, mm, wt, st, a.warmup, a.rotate_gb, use_graphs=a.graphs, path=pth)
+                ent[PATH_NAME[pth]] = {
+                    "kernel": KERNEL[pth], "weight_bytes_read": WEIGHT_BYTES[pth][wt],
+                    "ms_per_step": round(sm, 5), "tops": round(layer_ops(mm) / (sm * 1e-3) / 1e12, 2),
+                    "gemm_tops": round(layer_ops(mm) / (sg * 1e-3) / 1e12, 2),
+                    "frac_of_hbm_roofline": round(ab / (HBM_PEAK_GBS * 1e9) / (sm * 1e-3), 4)}
+            if (mm, wt) == (M, wtype):
+                ent[PATH_NAME[a.path]] = {"kernel": KERNEL[a.path], "weight_bytes_read": WEIGHT_BYTES[a.path][wt],
+                                          "ms_per_step": round(ms_step, 5), "tops": round(value, 2),
+                                          "gemm_tops": round(ops / (ms_gemms * 1e-3) / 1e12, 2),
+                                          "frac_of_hbm_roofline": extra["step_frac_of_hbm_roofline"],
+                                          "note": "the headline measurement"}
+            extra[key] = ent
+        # the single Q8_0 FC GEMM at M=257 (weight-streaming shape), every path
         extra["cfg1_m257"] = {}
         ab1 = step_alg_bytes(257, wtype, CFG1)
-        for pth in (a.path, other):
+        for pth in (a.path, "h16", "packed", "raw"):
+            if PATH_NAME[pth] in extra["cfg1_m257"]:
+                continue
             s1, _, _ = measure(ctx, 257, wtype, a.steps, a.warmup, a.rotate_gb, use_graphs=a.graphs,
                                path=pth, layer=CFG1)
             extra["cfg1_m257"][PATH_NAME[pth]] = {
@@ -790,20 +840,6 @@ def main():
                 "alg_gbs": round(ab1 / (s1 * 1e-3) / 1e9, 1),
                 "frac_of_hbm_roofline": round(ab1 / (HBM_PEAK_GBS * 1e9) / (s1 * 1e-3), 4)}
         extra["cfg1_m257"]["alg_bytes"] = ab1
-    if a.extra:
-        for (mm, wt) in ((4097, ema.WTYPE_Q8_0), (1025, ema.WTYPE_Q4_K), (4097, ema.WTYPE_Q4_K)):
-            key = f"{'q8_0' if wt == ema.WTYPE_Q8_0 else 'q4_k'}_m{mm}"
-            for pth in (a.path, other):        # the production path, then the other one
-                s, g, _ = measure(ctx, mm, wt, max(10, a.steps // 2), a.warmup, a.rotate_gb,
-                                  use_graphs=a.graphs, path=pth)
-                r = {"ms_per_step": round(s, 5), "tops": round(layer_ops(mm) / (s * 1e-3) / 1e12, 2),
-                     "gemm_tops": round(layer_ops(mm) / (g * 1e-3) / 1e12, 2),
-                     "frac_of_hbm_roofline": round(step_alg_bytes(mm, wt) / (HBM_PEAK_GBS * 1e9)
-                                                   / (s * 1e-3), 4)}
-                if pth == a.path:
-                    extra[key] = r
-                else:
-                    extra[key][PATH_NAME[pth]] = r
     if not a.no_fwd:
         import tempfile
         with tempfile.TemporaryDirectory() as d:
@@ -812,7 +848,9 @@ def main():
             write_synthetic_model(path, 24, ema.WTYPE_Q8_0)
             log(f"[bench] cfg4 model written in {time.perf_counter() - t0:.1f} s")
             fwd4 = {}
-            for pth in (a.path, other):
+            for pth in (a.path, "h16", "packed"):
+                if PATH_NAME[pth] in fwd4:
+                    continue
                 fwd, fwd_nr, prof = measure_forward(path, 16, max(3, a.steps // 10), 2, algo=ALGO[pth],
                                                     profile=True)
                 fwd4[PATH_NAME[pth]] = {"ms": round(fwd, 3), "ms_no_logits_readback": round(fwd_nr, 3),
@@ -860,7 +898,7 @@ def main():
         extra["cpu_oracle_int8_omp"] = cpu_oracle_int8(host, M, wtype)   # a multi-core CPU point
     digest = csrc_digest()
     traffic, traffic_src = measured_traffic(
-        os.path.join(ROOT, "profiles", f"traffic_{KERNEL[a.path]}_cfg2_q8_m1025.json"), digest)
+        os.path.join(ROOT, "profiles", f"traffic_{TRAFFIC_FILE[a.path]}_cfg2_q8_m1025.json"), digest)
     line = {
         "metric": "Q8_0/Q4_K GEMM TOPS + % roofline at M=1025/4097; transformer fwd ms",
         "value": round(value, 3),
@@ -872,7 +910,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16" if a.path == "h16" else "int8",
+        "dtype": "f16" if a.path in ("h16", "dq") else "int8",
         "data": "synthetic",
         "config": {"workload": "cfg2: one MaskGIT layer's four Q8_0 FC GEMMs (QKV 768->2304, "
                                "out 768->768 +resid, up 768->3072 +GELU, down 3072->768 +resid), "

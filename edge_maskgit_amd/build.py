@@ -31,7 +31,7 @@ HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC",
 
 KERNEL_SOURCES = ["k_quant_act.hip", "k_gemm_i8.hip",
                   "k_pack_w.hip", "k_gemm_qp.hip", "k_layernorm.hip", "k_flash_attn.hip",
-                  "k_gemm_f32.hip", "k_glue.hip", "k_ops.hip", "k_vqgan.hip", "k_conv_i8.hip", "noalloc.hip", "k_decode.hip", "k_gemm_h16.hip", "mgh_api.cpp"]
+                  "k_gemm_f32.hip", "k_glue.hip", "k_ops.hip", "k_vqgan.hip", "k_conv_i8.hip", "noalloc.hip", "k_decode.hip", "k_gemm_fc.hip", "mgh_api.cpp"]
 # Per-source extra flags. The int8 GEMMs keep MFMA results in VGPRs so the per-block
 # scale arithmetic reads them without v_accvgpr_read copies.
 EXTRA_FLAGS = {"k_gemm_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],

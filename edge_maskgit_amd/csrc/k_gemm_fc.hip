@@ -1,8 +1,17 @@
-// k_gemm_h16.hip — the dequantize-fused FC path: Q8_0 / Q4_K weights dequantized once at
-// upload into fp16, activations in fp16, fp32 accumulation on MFMA, fused epilogue.
+// k_gemm_fc.hip — the dequantize-fused FC path: y = act(x . w^T + bias) + resid with fp16
+// operands on MFMA and fp32 accumulation, the weights in one of three forms (template WQ):
+//   WQ 8 / 12: the Q8_0 / Q4_K bytes themselves, read on every call and decoded to fp16 in
+//              registers as the MFMA fragments are read (the layout of launch_pack_weights_dq:
+//              the GGUF blocks regrouped once into 16-row groups of 64-deep K stages, in MFMA
+//              fragment order, at the GGUF byte count);
+//   WQ 0:      an fp16 copy [N][K] made once at upload (launch_pack_weights_f16), 2 bytes per
+//              weight, no decoding in the K loop.
+// Both decode each weight to the same fp16 value, so the two forms give identical outputs for
+// the same tile plan.
 //
 // Semantics: the reference's fp16-slab dequant GEMMs k_mul_mat_q8_0_t2_h / k_mul_mat_q4k_t2_h
-// (src/mg-opencl/mg-opencl.cpp:320-411): every weight is expanded to its float value
+// (src/mg-opencl/mg-opencl.cpp:320-411), which decode every weight inside the K loop (DEQ_Q8
+// :386-387, deq_q4k_elem :252-262):
 //   Q8_0: w = d * q            Q4_K: w = (d * sc) * q - dmin * m      (fp32, then to fp16)
 // and the activations are rounded to fp16 (vstore_half_rte); the products accumulate in fp32,
 // then y = act(acc + bias) + resid (mg-opencl.cpp:485-491). The outputs stay within 1e-3 of
@@ -13,15 +22,16 @@
 //  * y tile BN (128 or 64) weight rows x BM (128, 64 or 32) activation rows per 256-thread
 //    workgroup (2 x 2 waves, each BN/2 x BM/2 outputs as v_mfma_f32_16x16x32_f16 tiles); K
 //    stage 64. gemm_h16_plan picks the tile, the ring depth and the K split per shape.
-//  * Operands move with global_load_lds (16 bytes per lane) straight into a 2- or 3-deep LDS
-//    ring: one instruction moves whole 128-byte row segments, XOR-swizzled so the MFMA
-//    fragment reads are bank-conflict free (the layout of k_gemm_qp.hip). The stage
-//    hand-over is an explicit vmcnt/lgkmcnt wait and s_barrier (stage_sync), which keeps the
-//    prefetched stages in flight.
-//  * Software pipeline: the fragments of the next K half are read from LDS while the current
-//    half's MFMAs issue; the stage boundary (vmcnt wait, barrier, next DMA, first fragment
-//    reads of the new stage) sits between two halves of the second K half's MFMAs, so the MFMA
-//    pipe keeps work while the wave waits.
+//  * Operands move with global_load_lds (16 bytes per lane; 4 for the Q8_0 scales and the Q4_K
+//    headers) straight into a 2- or 3-deep LDS ring: one instruction moves whole 128-byte row
+//    segments (fp16 weights, activations: XOR-swizzled so the MFMA fragment reads are
+//    bank-conflict free) or whole 16-row groups of quantized weights (already in fragment
+//    order). The stage hand-over is an explicit vmcnt/lgkmcnt wait and s_barrier
+//    (stage_sync), which keeps the prefetched stages in flight.
+//  * Software pipeline: the fragments of the next K half are read from LDS (and decoded) while
+//    the current half's MFMAs issue; the stage boundary (vmcnt wait, barrier, next DMA, first
+//    fragment reads of the new stage) sits between two halves of the second K half's MFMAs, so
+//    the MFMA pipe keeps work while the wave waits.
 //  * K rotation: output tiles that share operand rows start their K loop at different stages,
 //    so the first touch of each K slice (an L2 miss) is spread over the kernel instead of
 //    being paid by every tile in the same step.
@@ -30,7 +40,7 @@
 //    residual are applied on the way out. With y16 the result is stored rounded to fp16 (the
 //    operand form of a following dequantize-fused FC, which would round it to fp16 anyway).
 //  * Split-K for shapes with too few tiles: each split writes its partial tile row-major into a
-//    workspace (same transposed path) and k_gemm_h16_reduce sums the splits in split order
+//    workspace (same transposed path) and k_gemm_fc_reduce sums the splits in split order
 //    (deterministic) and applies the epilogue.
 #include <algorithm>
 
@@ -44,6 +54,24 @@ namespace {
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+// 8-byte LDS / global reads go through this vector type: reading the ring through HIP's uint2
+// struct made the compiler wait for every outstanding LDS DMA before the read (vmcnt(0)).
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// fp32 pairs -> fp16, round to nearest even: gfx950's v_cvt_pk_f16_f32, one instruction per
+// pair (a scalar cast per value costs a conversion plus a pack)
+__device__ __forceinline__ h16x2 cvt2_f16(float a, float b) { return __builtin_convertvector(f32x2{a, b}, h16x2); }
+__device__ __forceinline__ f16x4 cvt4_f16(f32x4 a) {
+    const h16x2 p0 = cvt2_f16(a[0], a[1]), p1 = cvt2_f16(a[2], a[3]);
+    return f16x4{p0[0], p0[1], p1[0], p1[1]};
+}
+__device__ __forceinline__ f16x8 cvt8_f16(f32x4 a, f32x4 b) {
+    const h16x2 p0 = cvt2_f16(a[0], a[1]), p1 = cvt2_f16(a[2], a[3]);
+    const h16x2 p2 = cvt2_f16(b[0], b[1]), p3 = cvt2_f16(b[2], b[3]);
+    return f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
 
 // Stage geometry: a stage is 64 K values; one row's stage segment is CPR 16-byte chunks (fp16
 // rows: 8, fp32 rows: 16), whole 128-byte lines. Chunk j of row r sits in slot j ^ swz(r): a
@@ -110,11 +138,6 @@ __device__ __forceinline__ uint32_t f16_bits(float v) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v);
 }
 
-typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
-// 8-byte LDS / global reads go through this vector type: reading the ring through HIP's uint2
-// struct made the compiler wait for every outstanding LDS DMA before the read (vmcnt(0)).
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
 // Q8_0 fragment: eight codes stored as q + 128 (bytes of c.x, c.y in K order) and the block's
 // fp16 scale d -> d * q rounded to fp16. Each code byte b becomes the fp16 1024 + b (exponent
 // byte 0x64 placed above it by v_perm), minus 1152 gives q exactly, and the fp16 product
@@ -150,13 +173,13 @@ __device__ __forceinline__ f16x8 deq_q4(uint32_t c, u32x4 h, int j) {
     const float s = h2f(h.x & 0xFFFFu) * (float)sc;
     const float m = h2f(h.x >> 16) * (float)mn;
     const uint32_t lo = c & 0x0F0F0F0Fu, hn = (c >> 4) & 0x0F0F0F0Fu;
-    f16x8 r;
+    f32x4 a, b;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-        r[e] = (_Float16)__builtin_fmaf(s, (float)((lo >> (8 * e)) & 0xFFu), -m);
-        r[e + 4] = (_Float16)__builtin_fmaf(s, (float)((hn >> (8 * e)) & 0xFFu), -m);
+        a[e] = __builtin_fmaf(s, (float)((lo >> (8 * e)) & 0xFFu), -m);
+        b[e] = __builtin_fmaf(s, (float)((hn >> (8 * e)) & 0xFFu), -m);
     }
-    return r;
+    return cvt8_f16(a, b);
 }
 
 // K-loop-dequant layout (packed_weight_bytes_dq): one thread per 32-value block (row n, block t
@@ -261,9 +284,7 @@ __global__ __launch_bounds__(256) void k_f32_to_f16(const f32x4* __restrict__ x,
                                                     int64_t n8) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n8) return;
-    const f32x4 a = x[2 * i], b = x[2 * i + 1];
-    h[i] = u32x4{f16_bits(a[0]) | (f16_bits(a[1]) << 16), f16_bits(a[2]) | (f16_bits(a[3]) << 16),
-                 f16_bits(b[0]) | (f16_bits(b[1]) << 16), f16_bits(b[2]) | (f16_bits(b[3]) << 16)};
+    h[i] = __builtin_bit_cast(u32x4, cvt8_f16(x[2 * i], x[2 * i + 1]));
 }
 
 }  // namespace
@@ -277,7 +298,7 @@ template <int WMR, int BN>
 constexpr int kH16MinBlocks = (WMR == 2 && BN == 128) ? 2 : 1;
 
 template <int ACT, int BM, bool PART, bool XF32, int NS, int WMR, int BN, int WQ>
-__global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h16(GemmH16Args g) {
+__global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_fc(GemmH16Args g) {
     constexpr int NW = 2 * WMR;                 // waves
     constexpr int NTH = 64 * NW;                // threads
     constexpr int RW = BM / WMR;                // activation rows per wave
@@ -290,15 +311,20 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
     // exec-masked DMA would make the compiler wait for all of them before any LDS read):
     // fp16 rows; one 16-byte-per-lane DMA per 1 KB Q8_0 group; Q4_K: two 512-byte groups per
     // 16-byte DMA, or a single group as two 4-byte-per-lane DMAs
-    constexpr int CW = WQ == 0 ? BN * CPW / 64 / NW : (WQ == 8 ? GPW : (GPW == 2 ? 1 : 2));
+    constexpr int CW = WQ == 0 ? BN * CPW / 64 / NW : (WQ == 8 ? GPW : (GPW >= 2 ? GPW / 2 : 2));
     // scale / header DMAs (4 bytes per lane): Q8_0 one (the wave's scale rows, then padding),
     // Q4_K one per 256-byte header group
     constexpr int CA = WQ == 0 ? 0 : (WQ == 8 ? 1 : GPW);
-    static_assert(WQ == 0 || (BN % (16 * NW) == 0 && GPW <= 2), "dequant layout: whole groups per wave");
+    static_assert(WQ == 0 || (BN % (16 * NW) == 0 && GPW <= 4 && (WQ == 8 || GPW == 1 || GPW % 2 == 0)),
+                  "dequant layout: whole groups per wave");
     constexpr int CX = BM * CPX / 64 / NW;      // activation DMA instructions per wave and stage
     static_assert(CW >= 1 && CX >= 1 && RW % 16 == 0, "tile shape");
     constexpr int MID = I * J / 2;              // MFMAs issued before a stage boundary
     constexpr int NR = (WQ ? 2 : 1) * I + (XF32 ? 2 : 1) * J;  // LDS reads per K half
+    // dequantizing forms: MFMAs that carry the LDS reads (two each), VALU per later MFMA
+    constexpr int NRD = (NR + 1) / 2 < I * J ? (NR + 1) / 2 : I * J - 1;
+    constexpr int VK = (WQ == 8 ? 14 : 34) * I + (XF32 ? 5 : 0) * J;   // decoding VALU per K half
+    constexpr int VPM = (VK + (I * J - NRD) - 1) / (I * J - NRD);
     constexpr int NI = NR < I * J ? NR : I * J;  // MFMA : LDS-read pairs in the interleave
     static_assert(NS >= 2 && (NS - 1) * (CW + CX + CA) < 64, "ring depth");
     __shared__ HLds<BM, BN, XF32, NS, WQ> L;
@@ -341,9 +367,12 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
         const int gi = min(n0 / 16 + wave * GPW + min(lane / 16, GPW - 1), G - 1);
         srca[0] = (const uint8_t*)g.w + (size_t)G * S * 1024 + (size_t)gi * S * 64 + (lane % 16) * 4;
     } else {
-        if (GPW == 2) {
-            const int gi = min(n0 / 16 + wave * 2 + lane / 32, G - 1);
-            srcw[0] = (const uint8_t*)g.w + (size_t)gi * S * 512 + (lane % 32) * 16;
+        if (GPW >= 2) {
+#pragma unroll
+            for (int q = 0; q < CW; q++) {
+                const int gi = min(n0 / 16 + wave * GPW + 2 * q + lane / 32, G - 1);
+                srcw[q] = (const uint8_t*)g.w + (size_t)gi * S * 512 + (lane % 32) * 16;
+            }
         } else {
             const int gi = min(n0 / 16 + wave, G - 1);
 #pragma unroll
@@ -377,8 +406,9 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
             for (int d = 0; d < CW; d++) dma16(srcw[d] + (size_t)ks_ * 1024, &L.w[st][(wave * GPW + d) * 64]);
             dma4(srca[0] + (size_t)ks_ * 64, &L.aux[st][wave * 16]);
         } else {
-            if (GPW == 2) {
-                dma16(srcw[0] + (size_t)ks_ * 512, &L.w[st][wave * 64]);
+            if (GPW >= 2) {
+#pragma unroll
+                for (int d = 0; d < CW; d++) dma16(srcw[d] + (size_t)ks_ * 512, &L.w[st][(wave * GPW + 2 * d) * 32]);
             } else {
 #pragma unroll
                 for (int d = 0; d < CW; d++) dma4(srcw[d] + (size_t)ks_ * 512, &L.w[st][wave * 32 + d * 16]);
@@ -415,8 +445,7 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
         const int r = r0 + l16, c = 8 * kb + 2 * lq;
         const f32x4 v0 = __builtin_bit_cast(f32x4, B[r * CPX + (c ^ swz<CPX>(l16))]);
         const f32x4 v1 = __builtin_bit_cast(f32x4, B[r * CPX + ((c + 1) ^ swz<CPX>(l16))]);
-        return f16x8{(_Float16)v0[0], (_Float16)v0[1], (_Float16)v0[2], (_Float16)v0[3],
-                     (_Float16)v1[0], (_Float16)v1[1], (_Float16)v1[2], (_Float16)v1[3]};
+        return cvt8_f16(v0, v1);
     };
 
     f32x4 acc[I][J];
@@ -454,12 +483,23 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
 #pragma unroll
         for (int j = 0; j < J; j++) nb[j] = xfrag(L.x[st], RW * wm + 16 * j, 1);
         mfma_all(ca, cb, 0, I * J);
+        if constexpr (WQ == 0) {
 #pragma unroll
-        for (int t = 0; t < NI; t++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
+            for (int t = 0; t < NI; t++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
+            }
+            if (I * J > NI) __builtin_amdgcn_sched_group_barrier(0x008, I * J - NI, 0);
+        } else {
+            // the next half's LDS reads ride on the first MFMAs (two per MFMA), its decoding
+            // (VALU) on the remaining ones, so the matrix pipe keeps issuing while it runs
+#pragma unroll
+            for (int t = 0; t < I * J; t++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (t < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                else __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
+            }
         }
-        if (I * J > NI) __builtin_amdgcn_sched_group_barrier(0x008, I * J - NI, 0);
     };
     auto half_boundary = [&](const f16x8 (&ca)[I], const f16x8 (&cb)[J], f16x8 (&na)[I], f16x8 (&nb)[J],
                              int s, int st, int stn) {
@@ -550,7 +590,7 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_h1
             const size_t idx = (size_t)m * N + n;
             if (g.resid) o += rv[p];
             if (g.y16)
-                __builtin_nontemporal_store(f16x4{(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]},
+                __builtin_nontemporal_store(cvt4_f16(o),
                                             (f16x4*)(g.y16 + idx));
             else
                 __builtin_nontemporal_store(o, (f32x4*)(g.y + idx));
@@ -575,7 +615,7 @@ __device__ __forceinline__ f32x4 split_sum4(const f32x4* part, size_t q_stride, 
 // Split-K epilogue: one thread per output float4; sums the splits' row-major partial tiles in
 // split order, then +bias -> act -> +resid.
 template <int ACT, int BM, int BN>
-__global__ __launch_bounds__(256) void k_gemm_h16_reduce(GemmH16Args g) {
+__global__ __launch_bounds__(256) void k_gemm_fc_reduce(GemmH16Args g) {
     const int M = g.M, N = g.N, splits = g.splits;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const size_t idx4 = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -592,19 +632,19 @@ __global__ __launch_bounds__(256) void k_gemm_h16_reduce(GemmH16Args g) {
     const f32x4 v = split_sum4<ACT>((const f32x4*)(g.ws + (size_t)lt * splits * BM * BN) + q, Q, splits, g.bias, n,
                                     g.resid, o);
     if (g.y16)
-        __builtin_nontemporal_store(f16x4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]},
+        __builtin_nontemporal_store(cvt4_f16(v),
                                     (f16x4*)(g.y16 + o));
     else
         __builtin_nontemporal_store(v, (f32x4*)(g.y + o));
 }
 
 // Split-K epilogue followed by the LayerNorm-affine of each output row (N = 256 C, no
-// activation): one wave per row sums the row's float4s with k_gemm_h16_reduce's arithmetic,
+// activation): one wave per row sums the row's float4s with k_gemm_fc_reduce's arithmetic,
 // stores them to y and normalizes the row from registers with the LayerNorm kernel's own
-// code (ln_affine_row), so y and every LayerNorm output equal those of k_gemm_h16_reduce
+// code (ln_affine_row), so y and every LayerNorm output equal those of k_gemm_fc_reduce
 // followed by k_layernorm_affine on y, in one launch.
 template <int C, int EMIT>
-__global__ __launch_bounds__(256) void k_gemm_h16_reduce_ln(GemmH16Args g, int bm, int bn, LnArgs ln) {
+__global__ __launch_bounds__(256) void k_gemm_fc_reduce_ln(GemmH16Args g, int bm, int bn, LnArgs ln) {
     const int M = g.M, N = g.N, splits = g.splits;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= M) return;                       // whole wave exits together
@@ -657,7 +697,7 @@ hipError_t launch_reduce_ln_e(const GemmH16Args& a, int bm, int bn, const LnArgs
     const dim3 grid((unsigned)((a.M + 3) / 4)), block(256);
     switch (a.N / 256) {
 #define MGH_RLN(CV)                                                                                       \
-    case CV: hipLaunchKernelGGL((k_gemm_h16_reduce_ln<CV, EMIT>), grid, block, 0, s, a, bm, bn, ln); break;
+    case CV: hipLaunchKernelGGL((k_gemm_fc_reduce_ln<CV, EMIT>), grid, block, 0, s, a, bm, bn, ln); break;
         MGH_RLN(1) MGH_RLN(2) MGH_RLN(3) MGH_RLN(4) MGH_RLN(5) MGH_RLN(6) MGH_RLN(7) MGH_RLN(8)
 #undef MGH_RLN
         default: return hipErrorInvalidValue;
@@ -676,11 +716,11 @@ hipError_t launch_reduce_ln(const GemmH16Args& a, int bm, int bn, const LnArgs& 
 // bytes of its weight row per step straight into registers (no LDS staging: every weight is
 // read once) and multiplies on v_mfma_f32_16x16x32_f16 against the activation rows, taken as MT
 // 16-row MFMA tiles (rows past M are zero). The KS partial tiles are summed in LDS in wave order
-// (deterministic) and the epilogue is the one of k_gemm_h16: +bias -> act -> +resid, fp32 or
-// fp16 out. Same operand rounding as k_gemm_h16 (fp32 activations rounded to fp16, nearest
+// (deterministic) and the epilogue is the one of k_gemm_fc: +bias -> act -> +resid, fp32 or
+// fp16 out. Same operand rounding as k_gemm_fc (fp32 activations rounded to fp16, nearest
 // even), so the two differ only in the fp32 summation order.
 template <int ACT, bool XF32, int MT, int KS, int WQ>
-__global__ __launch_bounds__(64 * KS) void k_gemv_h16(GemmH16Args g) {
+__global__ __launch_bounds__(64 * KS) void k_gemv_fc(GemmH16Args g) {
     constexpr int U = 4;                        // K steps in flight per wave
     __shared__ f32x4 part[KS][MT][64];
     const int K = g.K, M = g.M, N = g.N;
@@ -721,9 +761,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_h16(GemmH16Args g) {
         if (!xin[mt]) return f16x8{0, 0, 0, 0, 0, 0, 0, 0};
         if (!XF32) return *(const f16x8*)(g.x + xofs[mt] + 32 * t);
         const f32x4* p = (const f32x4*)(g.xf + xofs[mt] + 32 * t);
-        const f32x4 v0 = p[0], v1 = p[1];
-        return f16x8{(_Float16)v0[0], (_Float16)v0[1], (_Float16)v0[2], (_Float16)v0[3],
-                     (_Float16)v1[0], (_Float16)v1[1], (_Float16)v1[2], (_Float16)v1[3]};
+        return cvt8_f16(p[0], p[1]);
     };
     f32x4 acc[MT];
 #pragma unroll
@@ -766,7 +804,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_h16(GemmH16Args g) {
     const size_t o = (size_t)m * N + n;
     if (g.resid) v += *(const f32x4*)(g.resid + o);
     if (g.y16)
-        *(f16x4*)(g.y16 + o) = f16x4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+        *(f16x4*)(g.y16 + o) = cvt4_f16(v);
     else
         *(f32x4*)(g.y + o) = v;
 }
@@ -775,9 +813,9 @@ template <bool XF32, int MT, int WQ>
 static hipError_t launch_gemv_w(const GemmH16Args& a, hipStream_t s) {
     constexpr int KS = 8;
     const dim3 grid((unsigned)((a.N + 15) / 16)), block(64 * KS);
-    if (a.act == 1) hipLaunchKernelGGL((k_gemv_h16<1, XF32, MT, KS, WQ>), grid, block, 0, s, a);
-    else if (a.act == 2) hipLaunchKernelGGL((k_gemv_h16<2, XF32, MT, KS, WQ>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((k_gemv_h16<0, XF32, MT, KS, WQ>), grid, block, 0, s, a);
+    if (a.act == 1) hipLaunchKernelGGL((k_gemv_fc<1, XF32, MT, KS, WQ>), grid, block, 0, s, a);
+    else if (a.act == 2) hipLaunchKernelGGL((k_gemv_fc<2, XF32, MT, KS, WQ>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_gemv_fc<0, XF32, MT, KS, WQ>), grid, block, 0, s, a);
     return hipGetLastError();
 }
 
@@ -928,17 +966,17 @@ static hipError_t launch_h16_w(const GemmH16Args& a, hipStream_t s, const LnArgs
     const int splits = std::max(a.splits, 1);
     const dim3 block(128 * WMR);
     if (splits > 1) {
-        hipLaunchKernelGGL((k_gemm_h16<0, BM, true, XF32, NS, WMR, BN, WQ>), dim3(tiles * splits), block, 0, s, a);
+        hipLaunchKernelGGL((k_gemm_fc<0, BM, true, XF32, NS, WMR, BN, WQ>), dim3(tiles * splits), block, 0, s, a);
         if (ln) return launch_reduce_ln(a, BM, BN, *ln, s);
         const size_t n4 = (size_t)tiles * BM * BN / 4;
         const dim3 rg((unsigned)((n4 + 255) / 256)), rb(256);
-        if (a.act == 1) hipLaunchKernelGGL((k_gemm_h16_reduce<1, BM, BN>), rg, rb, 0, s, a);
-        else if (a.act == 2) hipLaunchKernelGGL((k_gemm_h16_reduce<2, BM, BN>), rg, rb, 0, s, a);
-        else hipLaunchKernelGGL((k_gemm_h16_reduce<0, BM, BN>), rg, rb, 0, s, a);
+        if (a.act == 1) hipLaunchKernelGGL((k_gemm_fc_reduce<1, BM, BN>), rg, rb, 0, s, a);
+        else if (a.act == 2) hipLaunchKernelGGL((k_gemm_fc_reduce<2, BM, BN>), rg, rb, 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_fc_reduce<0, BM, BN>), rg, rb, 0, s, a);
     } else {
-        if (a.act == 1) hipLaunchKernelGGL((k_gemm_h16<1, BM, false, XF32, NS, WMR, BN, WQ>), dim3(tiles), block, 0, s, a);
-        else if (a.act == 2) hipLaunchKernelGGL((k_gemm_h16<2, BM, false, XF32, NS, WMR, BN, WQ>), dim3(tiles), block, 0, s, a);
-        else hipLaunchKernelGGL((k_gemm_h16<0, BM, false, XF32, NS, WMR, BN, WQ>), dim3(tiles), block, 0, s, a);
+        if (a.act == 1) hipLaunchKernelGGL((k_gemm_fc<1, BM, false, XF32, NS, WMR, BN, WQ>), dim3(tiles), block, 0, s, a);
+        else if (a.act == 2) hipLaunchKernelGGL((k_gemm_fc<2, BM, false, XF32, NS, WMR, BN, WQ>), dim3(tiles), block, 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_fc<0, BM, false, XF32, NS, WMR, BN, WQ>), dim3(tiles), block, 0, s, a);
     }
     return hipGetLastError();
 }

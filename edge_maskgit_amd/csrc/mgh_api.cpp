@@ -134,7 +134,7 @@ int run_gemm_qp(mgh_ctx* c, int wtype, mgh::GemmArgs a, bool dbg) {
 // The fp16 dequantize-fused GEMM with its split-K plan (workspace from the context).
 int run_gemm_h16(mgh_ctx* c, mgh::GemmH16Args a) {
     if (mgh::use_gemv_h16(a.M, a.K)) {
-        MGH_HIP(c, mgh::launch_gemv_h16(a, c->stream), "k_gemv_h16");
+        MGH_HIP(c, mgh::launch_gemv_h16(a, c->stream), "k_gemv_fc");
         return MGH_OK;
     }
     const mgh::H16Plan p = mgh::gemm_h16_plan(a.M, a.N, a.K, a.xf != nullptr, a.wq);
@@ -143,7 +143,7 @@ int run_gemm_h16(mgh_ctx* c, mgh::GemmH16Args a) {
         if (int r = ensure_qp_ws(c, p.ws_bytes)) return r;
         a.ws = (float*)c->qp_ws;
     }
-    MGH_HIP(c, mgh::launch_gemm_h16(p, a, c->stream), "k_gemm_h16");
+    MGH_HIP(c, mgh::launch_gemm_h16(p, a, c->stream), "k_gemm_fc");
     return MGH_OK;
 }
 
@@ -977,7 +977,7 @@ int gemm_h16_ln_any(mgh_ctx* c, const char* fn, int wq, const void* w, int N, in
         a.splits = p.splits;
         a.ws = (float*)c->qp_ws;
         const mgh::LnArgs ln{gamma, beta, eps, y_ln, emit, codes, dx, s4};
-        MGH_HIP(c, mgh::launch_gemm_h16(p, a, c->stream, &ln), "k_gemm_h16 + k_gemm_h16_reduce_ln");
+        MGH_HIP(c, mgh::launch_gemm_h16(p, a, c->stream, &ln), "k_gemm_fc + k_gemm_fc_reduce_ln");
         return MGH_OK;
     }
     if (int r = run_gemm_h16(c, a)) return r;
@@ -1104,7 +1104,7 @@ int mgh_gemm_h16_f32in_noalloc(mgh_ctx* c, const void* wp16, int N, int K, const
     if (mgh::use_gemv_h16(M, K)) {               // skinny-M kernel: no scratch at all
         if (int r = set_dev(c)) return r;
         a.xf = x;
-        MGH_HIP(c, mgh::launch_gemv_h16(a, c->stream), "k_gemv_h16");
+        MGH_HIP(c, mgh::launch_gemv_h16(a, c->stream), "k_gemv_fc");
         return MGH_OK;
     }
     const bool round_pass = M >= 2048;
@@ -1126,7 +1126,7 @@ int mgh_gemm_h16_f32in_noalloc(mgh_ctx* c, const void* wp16, int N, int K, const
     }
     a.splits = p.splits;
     if (p.splits > 1) a.ws = (float*)((char*)base + x16_b);
-    MGH_HIP(c, mgh::launch_gemm_h16(p, a, c->stream), "k_gemm_h16");
+    MGH_HIP(c, mgh::launch_gemm_h16(p, a, c->stream), "k_gemm_fc");
     return MGH_OK;
 }
 

@@ -147,7 +147,7 @@ size_t decode_work_bytes(int B, int S);
 hipError_t launch_decode_seed(int B, void* state, hipStream_t s);
 hipError_t launch_decode_step(DecodeArgs a, void* state, void* work, hipStream_t s);
 
-// Dequantize-fused fp16 path (k_gemm_h16.hip): weights dequantized once into fp16 [N][K],
+// Dequantize-fused fp16 path (k_gemm_fc.hip): weights dequantized once into fp16 [N][K],
 // fp16 activations, fp32 accumulation, y = act(x . w^T + bias) + resid. K % 64 == 0,
 // N % 4 == 0, 16-byte aligned operands.
 struct GemmH16Args {
@@ -171,7 +171,7 @@ struct H16Plan {
     size_t ws_bytes;
 };
 H16Plan gemm_h16_plan(int M, int N, int K, bool xf32, int wq);
-// LayerNorm-affine of a GEMM's output rows taken by the split-K reduce (k_gemm_h16_reduce_ln):
+// LayerNorm-affine of a GEMM's output rows taken by the split-K reduce (k_gemm_fc_reduce_ln):
 // gamma/beta [N] and the LayerNorm outputs as launch_layernorm_affine takes them
 struct LnArgs {
     const float* gamma;
@@ -185,8 +185,8 @@ struct LnArgs {
 };
 size_t packed_weight_bytes_f16(int64_t N, int64_t K);
 hipError_t launch_pack_weights_f16(int wtype, const void* w, void* out, int N, int K, hipStream_t s);
-// K-loop-dequant weight layout (the operand of the wq = 8 / 12 forms of k_gemm_h16 and
-// k_gemv_h16): the GGUF bytes regrouped into 16-row groups and 64-deep K stages, so that one
+// K-loop-dequant weight layout (the operand of the wq = 8 / 12 forms of k_gemm_fc and
+// k_gemv_fc): the GGUF bytes regrouped into 16-row groups and 64-deep K stages, so that one
 // 16-byte-per-lane DMA moves whole MFMA fragments; the same byte count per weight as the GGUF
 // blocks (Q8_0 1.0625, Q4_K 0.5625) for N % 16 == 0, rows padded to a multiple of 16.
 //   Q8_0: codes [G][K/64][2][4][16][8] u8 (q + 128), then scales [G][K/64][2][16] fp16

@@ -179,10 +179,38 @@ struct HipRuntime::Impl {
     }
     std::unordered_map<void*, size_t> alloc_size;
 
+    // the dequantize-fused FC path, on the quantized bytes (MGH_ALGO_DEQ_Q) or on fp16 copies
+    bool deq() const { return algo == MGH_ALGO_DEQ_F16 || algo == MGH_ALGO_DEQ_Q; }
+    // the dequantize-fused FC entry points for this algorithm's weight form (wt: the GGUF type)
+    int fc(int wt, const void* w, int N, int K, const void* x16, int M, const float* b, int act, const float* r,
+           float* y) {
+        return algo == MGH_ALGO_DEQ_Q ? mgh_gemm_dq(ctx, wt, w, N, K, x16, M, b, act, r, y)
+                                      : mgh_gemm_h16(ctx, w, N, K, x16, M, b, act, r, y);
+    }
+    int fc_y16(int wt, const void* w, int N, int K, const void* x16, int M, const float* b, int act,
+               const float* r, void* y16) {
+        return algo == MGH_ALGO_DEQ_Q ? mgh_gemm_dq_y16(ctx, wt, w, N, K, x16, M, b, act, r, y16)
+                                      : mgh_gemm_h16_y16(ctx, w, N, K, x16, M, b, act, r, y16);
+    }
+    int fc_f32in(int wt, const void* w, int N, int K, const float* x, int M, const float* b, int act,
+                 const float* r, float* y) {
+        return algo == MGH_ALGO_DEQ_Q ? mgh_gemm_dq_f32in(ctx, wt, w, N, K, x, M, b, act, r, y)
+                                      : mgh_gemm_h16_f32in(ctx, w, N, K, x, M, b, act, r, y);
+    }
+    int fc_ln(int wt, const void* w, int N, int K, const void* x16, int M, const float* b, int act, const float* r,
+              float* y, const float* gamma, const float* beta, float eps, float* y_ln, int emit, void* codes,
+              float* dx, void* s4) {
+        return algo == MGH_ALGO_DEQ_Q
+                   ? mgh_gemm_dq_ln(ctx, wt, w, N, K, x16, M, b, act, r, y, gamma, beta, eps, y_ln, emit, codes, dx, s4)
+                   : mgh_gemm_h16_ln(ctx, w, N, K, x16, M, b, act, r, y, gamma, beta, eps, y_ln, emit, codes, dx,
+                                     s4);
+    }
+
     // layout 0: the leaf's bytes as stored; 1: quantized weight in the int8-dot packed layout
     // (mgh_pack_weights); 2: quantized weight dequantized into fp16 (mgh_pack_weights_f16);
     // 3: F32 conv kernel {KW, KH, IC, OC} in the tap-major layout (mgh_conv2d_pack_weights);
-    // 4: the same kernel quantized per (channel, 32-block) for the int8 conv (mgh_conv2d_i8_pack_weights)
+    // 4: the same kernel quantized per (channel, 32-block) for the int8 conv (mgh_conv2d_i8_pack_weights);
+    // 5: quantized weight in the K-loop-dequant layout, GGUF-sized (mgh_pack_weights_dq)
     void* upload_leaf(const Tensor* t, int layout) {
         const size_t n = t->nbytes();
         const auto key = std::make_tuple((const void*)t->data, n, layout ? 100 * layout + (int)t->type : -1);
@@ -206,10 +234,14 @@ struct HipRuntime::Impl {
         } else if (layout) {
             const int wt = t->type == Type::Q8_0 ? MGH_WTYPE_Q8_0 : MGH_WTYPE_Q4_K;
             const int K = (int)t->ne[0], N = (int)(t->nelements() / t->ne[0]);
-            const size_t pb = layout == 2 ? mgh_packed_weight_bytes_f16(N, K) : mgh_packed_weight_bytes(wt, N, K);
+            const size_t pb = layout == 2   ? mgh_packed_weight_bytes_f16(N, K)
+                              : layout == 5 ? mgh_packed_weight_bytes_dq(wt, N, K)
+                                            : mgh_packed_weight_bytes(wt, N, K);
             if (!pb) throw std::runtime_error("HipRuntime: unsupported quantized weight shape for '" + t->name + "'");
             check(mgh_alloc(ctx, pb, &d));
-            check(layout == 2 ? mgh_pack_weights_f16(ctx, wt, raw, N, K, d) : mgh_pack_weights(ctx, wt, raw, N, K, d));
+            check(layout == 2   ? mgh_pack_weights_f16(ctx, wt, raw, N, K, d)
+                  : layout == 5 ? mgh_pack_weights_dq(ctx, wt, raw, N, K, d)
+                                : mgh_pack_weights(ctx, wt, raw, N, K, d));
             check(mgh_free(ctx, raw));
         }
         leaves[key] = d;
@@ -221,13 +253,40 @@ struct HipRuntime::Impl {
         return t;
     }
 
-    // fp16 weights of a fused FC group, rows concatenated in member order (cached)
+    // weights of a fused FC group, rows concatenated in member order (cached): fp16 copies, or
+    // (MGH_ALGO_DEQ_Q) the K-loop-dequant layout of the stacked blocks -- ggml blocks are
+    // row-local, so the members' block bytes back to back are the stacked matrix's
     void* fused_weight(const std::vector<Tensor*>& grp, int K, int64_t Nt) {
         std::vector<const void*> key;
         for (const Tensor* m : grp) key.push_back(m->src[0]->data);
         const auto it = fused_w.find(key);
         if (it != fused_w.end()) return it->second;
         void* d = nullptr;
+        if (algo == MGH_ALGO_DEQ_Q) {
+            const Tensor* w0 = grp[0]->src[0];
+            const int wt = w0->type == Type::Q8_0 ? MGH_WTYPE_Q8_0 : MGH_WTYPE_Q4_K;
+            size_t total = 0;
+            for (const Tensor* m : grp) {
+                if (m->src[0]->type != w0->type) throw std::runtime_error("HipRuntime: fused FC weights differ in type");
+                total += m->src[0]->nbytes();
+            }
+            void* raw = nullptr;
+            check(mgh_alloc(ctx, total, &raw));
+            size_t off = 0;
+            for (const Tensor* m : grp) {
+                const Tensor* w = m->src[0];
+                if (!w->data) throw std::runtime_error("HipRuntime: leaf '" + w->name + "' has no host data");
+                check(mgh_h2d(ctx, (char*)raw + off, w->data, w->nbytes()));
+                off += w->nbytes();
+            }
+            const size_t pb = mgh_packed_weight_bytes_dq(wt, (int)Nt, K);
+            if (!pb) throw std::runtime_error("HipRuntime: unsupported quantized weight shape for a fused FC group");
+            check(mgh_alloc(ctx, pb, &d));
+            check(mgh_pack_weights_dq(ctx, wt, raw, (int)Nt, K, d));
+            check(mgh_sync(ctx));
+            check(mgh_free(ctx, raw));
+            return fused_w[key] = d;
+        }
         check(mgh_alloc(ctx, mgh_packed_weight_bytes_f16((int)Nt, K), &d));
         int64_t off = 0;
         for (const Tensor* m : grp) {
@@ -371,8 +430,9 @@ std::vector<OpProfile> HipRuntime::profile_report() const {
 }
 
 void HipRuntime::set_quant_algo(int algo) {
-    if (algo != MGH_ALGO_INT8 && algo != MGH_ALGO_DEQ_F16)
-        throw std::runtime_error("HipRuntime: quant algo must be 1 (int8) or 2 (dequant-fp16)");
+    if (algo != MGH_ALGO_INT8 && algo != MGH_ALGO_DEQ_F16 && algo != MGH_ALGO_DEQ_Q)
+        throw std::runtime_error("HipRuntime: quant algo must be 1 (int8), 2 (dequant, fp16 weight copies) or 3 "
+                                 "(dequant on the quantized bytes)");
     p_->algo = algo;
 }
 
@@ -473,7 +533,7 @@ const void* HipRuntime::run(Graph& g, bool readback) {
         // attention (q, k, v: mg-transformer.cpp:59-70) run as one GEMM on row-concatenated
         // weights; each output is a column range of the wide result, which the attention reads
         // through its strides
-        if (I.algo == MGH_ALGO_DEQ_F16) {
+        if (I.deq()) {
             std::unordered_map<const Tensor*, std::vector<const Tensor*>> cons;   // root -> consumer nodes
             for (const Tensor* t : g.nodes) {
                 if (is_view_op(t->op)) continue;
@@ -536,7 +596,7 @@ const void* HipRuntime::run(Graph& g, bool readback) {
         // dequantize-fused path: an attention output or an FC output whose only consumers are
         // dequantize-fused FCs reading it as their activations is stored as fp16 directly (the
         // consumers would round it to fp16 on their way in; the result is identical)
-        if (I.algo == MGH_ALGO_DEQ_F16) {
+        if (I.deq()) {
             std::unordered_map<const Tensor*, std::vector<const Tensor*>> cons;
             for (const Tensor* t : g.nodes) {
                 if (is_view_op(t->op)) continue;
@@ -563,7 +623,7 @@ const void* HipRuntime::run(Graph& g, bool readback) {
         // activation whose only consumer is a Norm over its rows runs as one mgh_gemm_h16_ln call,
         // which for split-K plans (a few hundred rows) normalizes the rows in the reduce, one
         // launch fewer; the Norm node then launches nothing. Same bits as the two nodes apart.
-        if (I.algo == MGH_ALGO_DEQ_F16) {
+        if (I.deq()) {
             std::unordered_map<const Tensor*, std::vector<const Tensor*>> cons;
             for (const Tensor* t : g.nodes)
                 for (const Tensor* s : t->src)
@@ -694,7 +754,7 @@ const void* HipRuntime::run(Graph& g, bool readback) {
             o.gamma = (const float*)u.first;
             o.beta = (const float*)u.second;
         }
-        if ((I.algo == MGH_ALGO_INT8 || I.algo == MGH_ALGO_DEQ_F16) && fc_uses.count(t)) {
+        if ((I.algo == MGH_ALGO_INT8 || I.deq()) && fc_uses.count(t)) {
             o.emit = I.algo == MGH_ALGO_INT8 ? MGH_EMIT_INT8 : MGH_EMIT_DEQ_F16;
             const size_t T = (size_t)D / 32;
             o.cd.q = I.take((size_t)rows * D * 2);
@@ -740,17 +800,18 @@ const void* HipRuntime::run(Graph& g, bool readback) {
             int64_t Nt = 0;
             for (const Tensor* m : grp) Nt += m->src[0]->ne[1];
             void* wp = I.fused_weight(grp, K, Nt);
+            const int wt = t->src[0]->type == Type::Q8_0 ? MGH_WTYPE_Q8_0 : MGH_WTYPE_Q4_K;
             const float* bias = (const float*)I.fused_bias(grp, Nt);
             const auto c = I.codes.find(I.root(x));
             const bool h16 = c != I.codes.end() && grp16.count(grp_of.at(t));
             out = I.take((size_t)M * Nt * (h16 ? 2 : 4));
             if (h16)
-                I.check(mgh_gemm_h16_y16(I.ctx, wp, (int)Nt, K, c->second.q, M, bias, t->iparam[0], nullptr, out));
+                I.check(I.fc_y16(wt, wp, (int)Nt, K, c->second.q, M, bias, t->iparam[0], nullptr, out));
             else if (c != I.codes.end())
-                I.check(mgh_gemm_h16(I.ctx, wp, (int)Nt, K, c->second.q, M, bias, t->iparam[0], nullptr, (float*)out));
+                I.check(I.fc(wt, wp, (int)Nt, K, c->second.q, M, bias, t->iparam[0], nullptr, (float*)out));
             else
-                I.check(mgh_gemm_h16_f32in(I.ctx, wp, (int)Nt, K, (const float*)I.dev(x), M, bias, t->iparam[0],
-                                           nullptr, (float*)out));
+                I.check(I.fc_f32in(wt, wp, (int)Nt, K, (const float*)I.dev(x), M, bias, t->iparam[0], nullptr,
+                                   (float*)out));
             int64_t off = 0;
             for (const Tensor* m : grp) {
                 I.addr[m] = (char*)out + off * (h16 ? 2 : 4);
@@ -817,29 +878,29 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                 const float* bias = (const float*)I.dev(t->src[2]);
                 const float* resid = (const float*)I.dev(t->src[3]);
                 const int act = t->iparam[0];
-                if (quant(w) && I.algo == MGH_ALGO_DEQ_F16) {
-                    void* wp = I.upload_leaf(w, 2);
+                if (quant(w) && I.deq()) {
+                    void* wp = I.upload_leaf(w, I.algo == MGH_ALGO_DEQ_Q ? 5 : 2);
+                    const int wt = w->type == Type::Q8_0 ? MGH_WTYPE_Q8_0 : MGH_WTYPE_Q4_K;
                     const auto c = I.codes.find(I.root(x));
                     if (c != I.codes.end() && emit16.count(t)) {
                         Impl::Codes cd;
                         cd.q = I.take((size_t)M * N * 2);
-                        I.check(mgh_gemm_h16_y16(I.ctx, wp, N, K, c->second.q, M, bias, act, resid, cd.q));
+                        I.check(I.fc_y16(wt, wp, N, K, c->second.q, M, bias, act, resid, cd.q));
                         I.codes[t] = cd;
                     } else if (c != I.codes.end() && ln_pair.count(t)) {
                         const Tensor* nr = ln_pair.at(t);
                         void* yl = I.take(nr->nbytes());
                         I.addr[nr] = yl;
                         const NormOut o = norm_out(nr);
-                        I.check(mgh_gemm_h16_ln(I.ctx, wp, N, K, c->second.q, M, bias, act, resid, (float*)out,
-                                                o.gamma, o.beta, nr->fparam[0], (float*)yl, o.emit, o.cd.q,
-                                                (float*)o.cd.dx, o.cd.sx));
+                        I.check(I.fc_ln(wt, wp, N, K, c->second.q, M, bias, act, resid, (float*)out, o.gamma,
+                                        o.beta, nr->fparam[0], (float*)yl, o.emit, o.cd.q, (float*)o.cd.dx,
+                                        o.cd.sx));
                         if (o.emit) I.codes[nr] = o.cd;
                         ln_done.insert(nr);
                     } else if (c != I.codes.end())
-                        I.check(mgh_gemm_h16(I.ctx, wp, N, K, c->second.q, M, bias, act, resid, (float*)out));
+                        I.check(I.fc(wt, wp, N, K, c->second.q, M, bias, act, resid, (float*)out));
                     else
-                        I.check(mgh_gemm_h16_f32in(I.ctx, wp, N, K, (const float*)I.dev(x), M, bias, act, resid,
-                                                   (float*)out));
+                        I.check(I.fc_f32in(wt, wp, N, K, (const float*)I.dev(x), M, bias, act, resid, (float*)out));
                 } else if (quant(w)) {
                     void* wp = I.upload_leaf(w, 1);
                     const auto c = I.codes.find(I.root(x));

@@ -46,10 +46,12 @@ enum { MGH_ACT_NONE = 0, MGH_ACT_GELU = 1, MGH_ACT_SILU = 2 };
 /* GEMM algorithm for quantized weights. INT8 = per-32 int8 activation codes, exact block
  * dots (the reference's int8-dot path, mg-opencl.cpp:1381-1398); DEQ_F16 = fp16-rounded
  * activations against the dequantized weights, fp32 accumulation (the reference's
- * dequant-fused fp16-slab path, mg-opencl.cpp:1400-1423). AUTO = DEQ_F16, the reference's
- * choice on any device without cl_arm_integer_dot_product (mg-opencl.cpp:1237-1238), which
- * includes this one. */
-enum { MGH_ALGO_AUTO = 0, MGH_ALGO_INT8 = 1, MGH_ALGO_DEQ_F16 = 2 };
+ * dequant-fused fp16-slab path, mg-opencl.cpp:1400-1423), on fp16 weight copies made at
+ * upload; DEQ_Q = the same product on the Q8_0 / Q4_K bytes themselves, decoded inside the K
+ * loop as the reference does (mgh_gemm_dq), with identical results. AUTO = DEQ_F16, the
+ * reference's choice on any device without cl_arm_integer_dot_product
+ * (mg-opencl.cpp:1237-1238), which includes this one, in its faster weight form. */
+enum { MGH_ALGO_AUTO = 0, MGH_ALGO_INT8 = 1, MGH_ALGO_DEQ_F16 = 2, MGH_ALGO_DEQ_Q = 3 };
 
 /* ---- context: replaces OpenCLRuntime::OpenCLRuntime / ~OpenCLRuntime / device_name
  *      (reference include/mg-opencl.hpp:25-31, src/mg-opencl/mg-opencl.cpp:1214-1280) ---- */

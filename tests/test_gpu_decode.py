@@ -145,7 +145,7 @@ def q4_model(tmp_path_factory):
     return p
 
 
-@pytest.mark.parametrize("algo", [1, 2])
+@pytest.mark.parametrize("algo", [1, 2, 3])
 def test_generate_matches_host_loop(q4_model, algo):
     classes, seeds, steps = [207, 3], [42, 2**40 + 1], 8
     print(f"generate B=2 (q4_k, 2 layers, algo {algo}) vs host loop", flush=True)

@@ -1,6 +1,6 @@
 """GPU parity of the dequantize-fused FC path on the quantized bytes: mgh_pack_weights_dq and
-mgh_gemm_dq / _f32in / _y16 / _ln (k_gemm_h16.hip, weight forms 8 and 12: the Q8_0 / Q4_K
-bytes are read on every call and decoded to fp16 as the MFMA fragments are read; k_gemv_h16
+mgh_gemm_dq / _f32in / _y16 / _ln (k_gemm_fc.hip, weight forms 8 and 12: the Q8_0 / Q4_K
+bytes are read on every call and decoded to fp16 as the MFMA fragments are read; k_gemv_fc
 for a few activation rows).
 
 Bars:

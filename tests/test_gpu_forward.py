@@ -257,7 +257,8 @@ def test_forward_full_cfg4_properties(tmp_path, algo):
             assert dmax < 1.0
 
 
-@pytest.mark.parametrize("quant,algo", [("q8_0", 1), ("q4_k", 1), ("q8_0", 2), ("q4_k", 2)])
+@pytest.mark.parametrize("quant,algo", [("q8_0", 1), ("q4_k", 1), ("q8_0", 2), ("q4_k", 2), ("q8_0", 3),
+                                        ("q4_k", 3)])
 def test_forward_24_layers_per_sublayer_vs_oracle(tmp_path, monkeypatch, quant, algo):
     """Every piece of the 24-layer forward against the oracle applied to the GPU's own input for
     that piece: with MG_DUMP_NAMED set the runtime reads back the named nodes the reference's
@@ -295,6 +296,24 @@ def test_forward_24_layers_per_sublayer_vs_oracle(tmp_path, monkeypatch, quant, 
     el = _rel(logits.reshape(257, -1), L.logits(got["output_norm"]))
     print(f"  worst piece rel {worst:.2e}; logits from the GPU's output_norm: rel {el:.2e}", flush=True)
     assert el <= 1e-3
+
+
+@pytest.mark.parametrize("quant,B", [("q8_0", 1), ("q4_k", 1), ("q8_0", 16), ("q4_k", 4)])
+def test_forward_quantized_bytes_equals_fp16_copies(tmp_path, quant, B):
+    """The dequantize-fused forward on the quantized bytes (algo 3: every FC decodes its Q8_0 /
+    Q4_K blocks inside the K loop, including the fused q/k/v GEMM on the stacked blocks) and on
+    fp16 weight copies (algo 2) decode every weight to the same fp16 value and run the same
+    tile plans, so the logits agree bit for bit; with B = 16 the FCs take the 128-row tile
+    plans."""
+    path = str(tmp_path / "m.gguf")
+    mg_gguf.write_model(path, n_layer=4, quant=quant, seed=9)
+    tok = mg_gguf.tokens(np.random.default_rng(B), 257, B)
+    print(f"forward 4 layers {quant} B={B}: algo 3 vs algo 2", flush=True)
+    with rt.TransformerRuntime(path, algo=3) as m:
+        q = m.forward(tok)
+    with rt.TransformerRuntime(path, algo=2) as m:
+        f = m.forward(tok)
+    assert np.array_equal(q.view(np.uint32), f.view(np.uint32))
 
 
 @pytest.mark.parametrize("quant", ["q8_0", "q4_k"])

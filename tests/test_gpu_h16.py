@@ -1,5 +1,5 @@
 """GPU parity of the dequantize-fused fp16 FC path: mgh_pack_weights_f16, mgh_f32_to_f16,
-mgh_gemm_h16 / mgh_gemm_h16_f32in (k_gemm_h16.hip: the tiled kernel and, for a few activation
+mgh_gemm_h16 / mgh_gemm_h16_f32in (k_gemm_fc.hip: the tiled kernel and, for a few activation
 rows, the skinny-M kernel).
 
 Bars:
@@ -79,7 +79,7 @@ def test_f32_to_f16_rounding(ctx):
     assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
 
 
-# the first eight run the skinny-M kernel (k_gemv_h16: M <= 16, or M <= 32 with K <= 1024),
+# the first eight run the skinny-M kernel (k_gemv_fc: M <= 16, or M <= 32 with K <= 1024),
 # the rest the tiled plans; the pairs (16 | 17, 32 | 33) sit on both sides of the switch and N = 132
 # ends in a partial 16-row weight group
 SHAPES = [(1, 4, 64), (7, 132, 256), (1, 2304, 768), (16, 3072, 768), (17, 2304, 768),
