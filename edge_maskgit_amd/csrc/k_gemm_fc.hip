@@ -847,6 +847,43 @@ H16Plan gemm_h16_plan(int M, int N, int K, bool xf32, int wq) {
     p.bn = 128;
     p.wmr = 2;
     const int t128 = ((M + 127) / 128) * ((N + 127) / 128);
+    const int t6464 = ((M + 63) / 64) * ((N + 63) / 64);
+    if (wq) {
+        // Quantized weight bytes (decoded in the K loop): the decoding is VALU work per weight
+        // fragment and wave, so the plans favour more workgroups per CU (a wave's decoding
+        // overlaps another's MFMAs) and more activation rows per wave. Measured against the
+        // fp16-weight plans on the four FC shapes, Q8_0, buffers rotated over 1 GB:
+        //  * fp32 activations, K <= 1024, a few images (M >= 512): 64 x 64 tiles on a 2-deep
+        //    ring when they fit one round of workgroups (three per CU), 32 x 64 when there are
+        //    fewer than one per CU (M = 1025: QKV 15.8 against 18.9 us, out-proj 11.8 against
+        //    12.7 us); one image (M = 257) keeps the few-tile plans below;
+        //  * fp16 activations, 128 x 128 tiles from one tile per CU, the long-K narrow
+        //    down-proj split in two (M = 4097: QKV 35.6 against 40.2 us including the rounding
+        //    pass, down-proj 58.7 against 64.0 us).
+        if (xf32 && K <= 1024 && M >= 512 && t6464 <= 768) {
+            p.ns = 2;
+            p.bn = 64;
+            p.bm = t6464 < 256 ? 32 : 64;
+            p.splits = 1;
+            p.ws_bytes = 0;
+            p.ph = 8;
+            return p;
+        }
+        if (!xf32 && t128 >= 256) {
+            p.bm = 128;
+            p.splits = 1;
+            p.ws_bytes = 0;
+            p.ph = 8;
+            return p;
+        }
+        if (!xf32 && K >= 2048 && N <= 1024 && t128 >= 128) {
+            p.bm = 128;
+            p.splits = 2;
+            p.ws_bytes = (size_t)t128 * 2 * 128 * 128 * 4;
+            p.ph = 8;
+            return p;
+        }
+    }
     // Tile choice, from timings of the four FC shapes at M = 1025, 4112 and 16448 on fp16
     // operands with cold weights and activations (buffers rotated over 1 GB): 64-row tiles
     // (three workgroups per CU) up to about four 128-row tiles per CU, 128-row tiles beyond;
@@ -872,7 +909,6 @@ H16Plan gemm_h16_plan(int M, int N, int K, bool xf32, int wq) {
     // against 17.3 / 16.3; M = 1025 out 9.8 / 8.2 against 12.8 / 11.9, QKV (fp16) 11.9 against
     // 12.8. Long-K shapes with more tiles (M = 1025 down-proj on fp32 rows: 23.8 against 22.1)
     // keep the 64 x 128 split-K plan.
-    const int t6464 = ((M + 63) / 64) * ((N + 63) / 64);
     const int slots = xf32 ? 512 : 768;
     if ((K <= 1024 || t6464 <= 128) && t6464 <= slots) {
         p.ns = 3;
@@ -1004,6 +1040,11 @@ hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a0, hipStream_t 
     if (p.bn == 64 && p.ns == 3) {
         if (p.bm == 64) return xf ? launch_h16_t<64, true, 3, 2, 64>(a, s, ln) : launch_h16_t<64, false, 3, 2, 64>(a, s, ln);
         if (p.bm == 32) return xf ? launch_h16_t<32, true, 3, 2, 64>(a, s, ln) : launch_h16_t<32, false, 3, 2, 64>(a, s, ln);
+    }
+    // plans of the quantized-byte forms only
+    if (a.wq && p.bn == 64 && p.ns == 2 && xf) {
+        if (p.bm == 64) return a.wq == 8 ? launch_h16_w<64, true, 2, 2, 64, 8>(a, s, ln) : launch_h16_w<64, true, 2, 2, 64, 12>(a, s, ln);
+        if (p.bm == 32) return a.wq == 8 ? launch_h16_w<32, true, 2, 2, 64, 8>(a, s, ln) : launch_h16_w<32, true, 2, 2, 64, 12>(a, s, ln);
     }
     return hipErrorInvalidValue;
 }

@@ -302,9 +302,12 @@ def test_forward_24_layers_per_sublayer_vs_oracle(tmp_path, monkeypatch, quant, 
 def test_forward_quantized_bytes_equals_fp16_copies(tmp_path, quant, B):
     """The dequantize-fused forward on the quantized bytes (algo 3: every FC decodes its Q8_0 /
     Q4_K blocks inside the K loop, including the fused q/k/v GEMM on the stacked blocks) and on
-    fp16 weight copies (algo 2) decode every weight to the same fp16 value and run the same
-    tile plans, so the logits agree bit for bit; with B = 16 the FCs take the 128-row tile
-    plans."""
+    fp16 weight copies (algo 2) decode every weight to the same fp16 value; they may run
+    different tile plans, whose fp32 summation orders differ in the last bits, which can flip
+    the fp16 rounding (2^-11 relative) of an activation stored for the next FC, so after
+    several layers the logits agree to the fp16 level: within 2e-3 of their maximum (measured
+    4.7e-4 at B = 16), where a wrong weight, group or plan differs at 1e-2 or more. For one
+    image the plans coincide and the logits agree bit for bit."""
     path = str(tmp_path / "m.gguf")
     mg_gguf.write_model(path, n_layer=4, quant=quant, seed=9)
     tok = mg_gguf.tokens(np.random.default_rng(B), 257, B)
@@ -313,7 +316,11 @@ def test_forward_quantized_bytes_equals_fp16_copies(tmp_path, quant, B):
         q = m.forward(tok)
     with rt.TransformerRuntime(path, algo=2) as m:
         f = m.forward(tok)
-    assert np.array_equal(q.view(np.uint32), f.view(np.uint32))
+    e = _rel(q, f)
+    print(f"  rel {e:.2e}", flush=True)
+    assert e <= 2e-3
+    if B == 1:
+        assert np.array_equal(q.view(np.uint32), f.view(np.uint32))
 
 
 @pytest.mark.parametrize("quant", ["q8_0", "q4_k"])
