@@ -43,7 +43,7 @@ MGH_SYMBOLS = [
     "mgh_conv2d_packed_bytes", "mgh_conv2d_pack_weights", "mgh_conv2d_i8_weight_bytes",
     "mgh_conv2d_i8_pack_weights", "mgh_conv2d_i8",
     "mgh_packed_weight_bytes_dq", "mgh_pack_weights_dq", "mgh_gemm_dq", "mgh_gemm_dq_f32in",
-    "mgh_gemm_dq_y16", "mgh_gemm_dq_ln",
+    "mgh_gemm_dq_y16", "mgh_gemm_dq_ln", "mgh_dequant_weights_f32",
 ]
 
 _lib = None
@@ -112,6 +112,7 @@ def lib():
         L.mgh_packed_weight_bytes_dq.argtypes = [I, I, I]
         L.mgh_packed_weight_bytes_dq.restype = SZ
         L.mgh_pack_weights_dq.argtypes = [P, I, P, I, I, P]
+        L.mgh_dequant_weights_f32.argtypes = [P, I, P, I, I, P]
         L.mgh_gemm_dq.argtypes = [P, I, P, I, I, P, I, P, I, P, P]
         L.mgh_gemm_dq_f32in.argtypes = [P, I, P, I, I, P, I, P, I, P, P]
         L.mgh_gemm_dq_y16.argtypes = [P, I, P, I, I, P, I, P, I, P, P]
@@ -366,6 +367,9 @@ class Context:
     def gemm_h16_f32in(self, wp16, N, K, x, M, bias, act, resid, y):
         P = self._ptr
         self._check(lib().mgh_gemm_h16_f32in(self.h, P(wp16), N, K, P(x), M, P(bias), act, P(resid), P(y)))
+
+    def dequant_weights_f32(self, wtype, w, N, K, out):
+        self._check(lib().mgh_dequant_weights_f32(self.h, wtype, self._ptr(w), N, K, self._ptr(out)))
 
     def pack_weights_dq(self, wtype, w, N, K, wdq):
         self._check(lib().mgh_pack_weights_dq(self.h, wtype, self._ptr(w), N, K, self._ptr(wdq)))

@@ -233,17 +233,14 @@ __global__ __launch_bounds__(256) void k_pack_wdq(const uint8_t* __restrict__ w,
     }
 }
 
-// One thread per 32-value block: the block's 32 dequantized values as fp16 (4 x 16 bytes).
+// The 32 values of block t of weight row n as the reference decodes them (fp32): Q8_0
+// d * q (DEQ_Q8, mg-opencl.cpp:386-387), Q4_K (d * sc) * q - dmin * m (deq_q4k_elem, :252-262;
+// the 6-bit scale / min unpacking of get_scale_min_k4, :178-184). Bytes are read one at a
+// time: Q8_0 rows need not be aligned at all.
 template <int WTYPE>
-__global__ __launch_bounds__(256) void k_pack_w16(const uint8_t* __restrict__ w, u32x4* __restrict__ out,
-                                                  int N, int K) {
+__device__ __forceinline__ void decode_block(const uint8_t* __restrict__ w, int64_t n, int t, int T, float (&v)[32]) {
 #pragma clang fp contract(off)
-    const int T = K / 32;
-    const int64_t blk = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (blk >= (int64_t)N * T) return;
-    const int64_t n = blk / T;
-    const int t = (int)(blk - n * T);
-    float v[32];
+    const int64_t blk = n * T + t;
     if (WTYPE == 8) {
         const uint8_t* b = w + blk * 34;
         const float d = h2f((uint32_t)b[0] | ((uint32_t)b[1] << 8));
@@ -269,6 +266,19 @@ __global__ __launch_bounds__(256) void k_pack_w16(const uint8_t* __restrict__ w,
 #pragma unroll
         for (int i = 0; i < 32; i++) v[i] = s * (float)((qs[i] >> sh) & 15) - m;
     }
+}
+
+// One thread per 32-value block: the block's 32 dequantized values as fp16 (4 x 16 bytes).
+template <int WTYPE>
+__global__ __launch_bounds__(256) void k_pack_w16(const uint8_t* __restrict__ w, u32x4* __restrict__ out,
+                                                  int N, int K) {
+    const int T = K / 32;
+    const int64_t blk = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (blk >= (int64_t)N * T) return;
+    const int64_t n = blk / T;
+    const int t = (int)(blk - n * T);
+    float v[32];
+    decode_block<WTYPE>(w, n, t, T, v);
     u32x4* dst = out + blk * 4;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
@@ -277,6 +287,23 @@ __global__ __launch_bounds__(256) void k_pack_w16(const uint8_t* __restrict__ w,
         for (int e = 0; e < 4; e++) c[e] = f16_bits(v[8 * q + 2 * e]) | (f16_bits(v[8 * q + 2 * e + 1]) << 16);
         dst[q] = c;
     }
+}
+
+// One thread per 32-value block: the block's dequantized values as fp32, row-major [N][K] (any
+// N; the weight of a MulMat whose shape the tiled kernels do not take)
+template <int WTYPE>
+__global__ __launch_bounds__(256) void k_dequant_w32(const uint8_t* __restrict__ w, float* __restrict__ out,
+                                                     int N, int K) {
+    const int T = K / 32;
+    const int64_t blk = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (blk >= (int64_t)N * T) return;
+    const int64_t n = blk / T;
+    const int t = (int)(blk - n * T);
+    float v[32];
+    decode_block<WTYPE>(w, n, t, T, v);
+    float* dst = out + n * K + t * 32;
+#pragma unroll
+    for (int i = 0; i < 32; i++) dst[i] = v[i];
 }
 
 // fp32 -> fp16 (round to nearest even), 8 values per thread
@@ -682,12 +709,13 @@ __global__ __launch_bounds__(256) void k_gemm_fc_reduce_ln(GemmH16Args g, int bm
 #pragma unroll
                 for (int c = 0; c < C; c++) v[c] = k0 + kk == 0 ? pv[kk][c] : v[c] + pv[kk][c];
     }
-    // then +bias -> +resid (no activation), each rounded, as split_sum4<0>
+    // then +bias -> +resid (no activation), each rounded, as split_sum4<0>; y stored unless
+    // the caller needs only the LayerNorm's outputs (g.y null)
 #pragma unroll
     for (int c = 0; c < C; c++) {
         if (g.bias) v[c] += bb[c];
         if (g.resid) v[c] += rb[c];
-        __builtin_nontemporal_store(v[c], (f32x4*)(g.y + (size_t)row * N + 4 * (lane + 64 * c)));
+        if (g.y) __builtin_nontemporal_store(v[c], (f32x4*)(g.y + (size_t)row * N + 4 * (lane + 64 * c)));
     }
     ln_affine_row<C, EMIT>(v, lane, row, ln.gamma, ln.beta, ln.y, ln.eps, ln.codes, ln.dx, ln.s4);
 }
@@ -988,6 +1016,19 @@ hipError_t launch_pack_weights_dq(int wtype, const void* w, void* out, int N, in
     return hipGetLastError();
 }
 
+hipError_t launch_dequant_weights_f32(int wtype, const void* w, float* out, int N, int K, hipStream_t s) {
+    const int64_t blocks = (int64_t)N * (K / 32);
+    if (blocks == 0) return hipSuccess;
+    const dim3 grid((unsigned)((blocks + 255) / 256)), block(256);
+    if (wtype == 8)
+        hipLaunchKernelGGL(k_dequant_w32<8>, grid, block, 0, s, (const uint8_t*)w, out, N, K);
+    else if (wtype == 12)
+        hipLaunchKernelGGL(k_dequant_w32<12>, grid, block, 0, s, (const uint8_t*)w, out, N, K);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 hipError_t launch_f32_to_f16(const float* x, _Float16* h, int64_t n, hipStream_t s) {
     const int64_t n8 = n / 8;
     if (n8 == 0) return hipSuccess;
@@ -1031,7 +1072,7 @@ hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a0, hipStream_t 
     const bool xf = a.xf != nullptr;
     if (p.wmr != 2) return hipErrorInvalidValue;
     // the reduce takes the LayerNorm only when K is split, without activation or fp16 output
-    if (ln && (p.splits < 2 || a.act != 0 || a.y16 || !a.y || a.N % 256 || a.N > 2048)) return hipErrorInvalidValue;
+    if (ln && (p.splits < 2 || a.act != 0 || a.y16 || a.N % 256 || a.N > 2048)) return hipErrorInvalidValue;
     if (p.bn == 128 && p.ns == 2) {
         if (p.bm == 128 && !xf) return launch_h16_t<128, false, 2, 2, 128>(a, s, ln);
         if (p.bm == 64) return xf ? launch_h16_t<64, true, 2, 2, 128>(a, s, ln) : launch_h16_t<64, false, 2, 2, 128>(a, s, ln);

@@ -148,13 +148,13 @@ int run_gemm_h16(mgh_ctx* c, mgh::GemmH16Args a) {
 }
 
 int check_h16(mgh_ctx* c, const char* fn, const void* wp, int N, int K, const void* x, int M,
-              const float* bias, int act, const float* resid, const float* y) {
+              const float* bias, int act, const float* resid, const float* y, bool y_optional = false) {
     if (N <= 0 || K <= 0 || M < 0) return fail(c, MGH_ERR_ARG, std::string(fn) + ": shape must have N>0, K>0, M>=0");
     if (act < 0 || act > 2) return fail(c, MGH_ERR_ARG, "act must be 0 (none), 1 (gelu) or 2 (silu)");
     if (K % 64) return fail(c, MGH_ERR_UNSUPPORTED, std::string(fn) + ": needs K % 64 == 0");
     if (N % 4) return fail(c, MGH_ERR_UNSUPPORTED, std::string(fn) + ": needs N % 4 == 0");
     if (M == 0) return MGH_OK;
-    if (!wp || !x || !y) return fail(c, MGH_ERR_ARG, std::string(fn) + ": null pointer");
+    if (!wp || !x || (!y && !y_optional)) return fail(c, MGH_ERR_ARG, std::string(fn) + ": null pointer");
     if (!aligned16(wp) || !aligned16(x) || !aligned16(bias) || !aligned16(resid) || !aligned16(y))
         return fail(c, MGH_ERR_ARG, std::string(fn) + ": operands must be 16-byte aligned");
     return MGH_OK;
@@ -955,7 +955,10 @@ int gemm_h16_ln_any(mgh_ctx* c, const char* fn, int wq, const void* w, int N, in
                     const float* beta, float eps, float* y_ln, int emit, void* codes, float* dx, void* s4) {
     if (!c) return MGH_ERR_ARG;
     const std::string f(fn);
-    if (int r = check_h16(c, fn, w, N, K, x16, M, bias, act, resid, y)) return r;
+    // y may be null: then only the LayerNorm's outputs are written (y in the context scratch
+    // when the plan runs the FC and the LayerNorm as two launches)
+    const bool no_y = y == nullptr;
+    if (int r = check_h16(c, fn, w, N, K, x16, M, bias, act, resid, y, true)) return r;
     if (N % 256 || N > 2048) return fail(c, MGH_ERR_UNSUPPORTED, f + ": needs N % 256 == 0 and N <= 2048");
     if (emit < 0 || emit > 2) return fail(c, MGH_ERR_ARG, f + ": emit must be 0, 1 or 2");
     if (M == 0) return MGH_OK;
@@ -979,6 +982,10 @@ int gemm_h16_ln_any(mgh_ctx* c, const char* fn, int wq, const void* w, int N, in
         const mgh::LnArgs ln{gamma, beta, eps, y_ln, emit, codes, dx, s4};
         MGH_HIP(c, mgh::launch_gemm_h16(p, a, c->stream, &ln), "k_gemm_fc + k_gemm_fc_reduce_ln");
         return MGH_OK;
+    }
+    if (no_y) {
+        if (int r = ensure_scratch(c, round256((size_t)M * N * 4))) return r;
+        a.y = y = (float*)c->scratch;
     }
     if (int r = run_gemm_h16(c, a)) return r;
     MGH_HIP(c, mgh::launch_layernorm_affine(y, gamma, beta, y_ln, M, N, eps, emit, codes, dx, s4, c->stream),
@@ -1044,6 +1051,20 @@ int mgh_gemm_h16_ln(mgh_ctx* c, const void* wp16, int N, int K, const void* x16,
 int mgh_gemm_h16_f32in(mgh_ctx* c, const void* wp16, int N, int K, const float* x, int M,
                        const float* bias, int act, const float* resid, float* y) {
     return gemm_h16_f32in_any(c, "gemm_h16_f32in", 0, wp16, N, K, x, M, bias, act, resid, y);
+}
+
+int mgh_dequant_weights_f32(mgh_ctx* c, int wtype, const void* w, int N, int K, float* out) {
+    if (!c) return MGH_ERR_ARG;
+    if (wtype != MGH_WTYPE_Q8_0 && wtype != MGH_WTYPE_Q4_K)
+        return fail(c, MGH_ERR_ARG, "dequant_weights_f32: wtype must be MGH_WTYPE_Q8_0 (8) or MGH_WTYPE_Q4_K (12)");
+    if (N <= 0 || K <= 0) return fail(c, MGH_ERR_ARG, "dequant_weights_f32: needs N > 0, K > 0");
+    if (K % (wtype == MGH_WTYPE_Q8_0 ? 32 : 256))
+        return fail(c, MGH_ERR_ARG, "dequant_weights_f32: K must be a multiple of the block size (32 / 256)");
+    if (!w || !out) return fail(c, MGH_ERR_ARG, "dequant_weights_f32: null pointer");
+    if ((uintptr_t)out & 3u) return fail(c, MGH_ERR_ARG, "dequant_weights_f32: output must be 4-byte aligned");
+    if (int r = set_dev(c)) return r;
+    MGH_HIP(c, mgh::launch_dequant_weights_f32(wtype, w, out, N, K, c->stream), "k_dequant_w32");
+    return MGH_OK;
 }
 
 size_t mgh_packed_weight_bytes_dq(int wtype, int N, int K) {
@@ -1118,15 +1139,22 @@ int mgh_gemm_h16_f32in_noalloc(mgh_ctx* c, const void* wp16, int N, int K, const
     if (int r = set_dev(c)) return r;
     void* base = nullptr;
     MGH_HIP(c, mgh::noalloc_scratch(c->device, &base), "hipGetSymbolAddress(scratch)");
+    // calls on other streams of this GPU share the array: run after the previous one
+    bool capturing = false;
+    MGH_HIP(c, mgh::noalloc_order_begin(c->device, c->stream, &capturing), "noalloc ordering");
+    hipError_t e = hipSuccess;
     if (round_pass) {
-        MGH_HIP(c, mgh::launch_f32_to_f16(x, (_Float16*)base, (int64_t)M * K, c->stream), "k_f32_to_f16");
+        e = mgh::launch_f32_to_f16(x, (_Float16*)base, (int64_t)M * K, c->stream);
         a.x = (const _Float16*)base;
     } else {
         a.xf = x;
     }
     a.splits = p.splits;
     if (p.splits > 1) a.ws = (float*)((char*)base + x16_b);
-    MGH_HIP(c, mgh::launch_gemm_h16(p, a, c->stream), "k_gemm_fc");
+    if (e == hipSuccess) e = mgh::launch_gemm_h16(p, a, c->stream);
+    const hipError_t e2 = mgh::noalloc_order_end(c->device, c->stream, capturing);
+    MGH_HIP(c, e, "k_gemm_fc (no-allocation entry)");
+    MGH_HIP(c, e2, "noalloc ordering");
     return MGH_OK;
 }
 

@@ -193,6 +193,8 @@ hipError_t launch_pack_weights_f16(int wtype, const void* w, void* out, int N, i
 //   Q4_K: nibbles [G][K/64][2][4][16][4] (byte e: element e low, e + 4 high), then the raw
 //         16-byte super-block headers (d, dmin, packed 6-bit scales) [G][K/256][16][16]
 // with G = ceil(N / 16) row groups; [2][4][16] = K half, 8-wide K slice, row in the group.
+// raw Q8_0 / Q4_K blocks -> fp32 [N][K] (any N, K % 32 resp. % 256; any byte alignment)
+hipError_t launch_dequant_weights_f32(int wtype, const void* w, float* out, int N, int K, hipStream_t s);
 size_t packed_weight_bytes_dq(int wtype, int64_t N, int64_t K);
 hipError_t launch_pack_weights_dq(int wtype, const void* w, void* out, int N, int K, hipStream_t s);
 hipError_t launch_f32_to_f16(const float* x, _Float16* h, int64_t n, hipStream_t s);
@@ -270,5 +272,10 @@ hipError_t launch_upscale(const float* x, int IW, int IH, int64_t CN, int f, flo
 
 size_t noalloc_scratch_bytes();
 hipError_t noalloc_scratch(int device, void** out);
+// order a call's launches on `s` after the previous call's on this device (event wait; takes a
+// host lock), then (end) record the event after them and release the lock; *capturing: `s` is
+// under stream capture, where neither is done. end must follow every successful begin.
+hipError_t noalloc_order_begin(int device, hipStream_t s, bool* capturing);
+hipError_t noalloc_order_end(int device, hipStream_t s, bool capturing);
 
 }  // namespace mgh

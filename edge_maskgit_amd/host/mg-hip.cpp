@@ -210,7 +210,8 @@ struct HipRuntime::Impl {
     // (mgh_pack_weights); 2: quantized weight dequantized into fp16 (mgh_pack_weights_f16);
     // 3: F32 conv kernel {KW, KH, IC, OC} in the tap-major layout (mgh_conv2d_pack_weights);
     // 4: the same kernel quantized per (channel, 32-block) for the int8 conv (mgh_conv2d_i8_pack_weights);
-    // 5: quantized weight in the K-loop-dequant layout, GGUF-sized (mgh_pack_weights_dq)
+    // 5: quantized weight in the K-loop-dequant layout, GGUF-sized (mgh_pack_weights_dq);
+    // 6: quantized weight dequantized into fp32 [N][K] (mgh_dequant_weights_f32)
     void* upload_leaf(const Tensor* t, int layout) {
         const size_t n = t->nbytes();
         const auto key = std::make_tuple((const void*)t->data, n, layout ? 100 * layout + (int)t->type : -1);
@@ -236,11 +237,13 @@ struct HipRuntime::Impl {
             const int K = (int)t->ne[0], N = (int)(t->nelements() / t->ne[0]);
             const size_t pb = layout == 2   ? mgh_packed_weight_bytes_f16(N, K)
                               : layout == 5 ? mgh_packed_weight_bytes_dq(wt, N, K)
+                              : layout == 6 ? (size_t)N * K * 4
                                             : mgh_packed_weight_bytes(wt, N, K);
             if (!pb) throw std::runtime_error("HipRuntime: unsupported quantized weight shape for '" + t->name + "'");
             check(mgh_alloc(ctx, pb, &d));
             check(layout == 2   ? mgh_pack_weights_f16(ctx, wt, raw, N, K, d)
                   : layout == 5 ? mgh_pack_weights_dq(ctx, wt, raw, N, K, d)
+                  : layout == 6 ? mgh_dequant_weights_f32(ctx, wt, raw, N, K, (float*)d)
                                 : mgh_pack_weights(ctx, wt, raw, N, K, d));
             check(mgh_free(ctx, raw));
         }
@@ -460,7 +463,14 @@ const void* HipRuntime::run(Graph& g, bool readback) {
     I.addr.clear();
     I.codes.clear();
     const int n = (int)g.nodes.size();
-    auto quant = [](const Tensor* w) { return w->type == Type::Q8_0 || w->type == Type::Q4_K; };
+    // quantized weights the fused kernels take (mgh_gemm_h16 / _dq / _q_packed: Q8_0 with
+    // K % 64 == 0, N % 4 == 0; Q4_K with N % 4 == 0); other quantized shapes run the
+    // reference's F32 dequant GEMM on weights dequantized once at upload (layout 6)
+    auto quant = [](const Tensor* w) {
+        if (w->type != Type::Q8_0 && w->type != Type::Q4_K) return false;
+        const int64_t K = w->ne[0], N = w->nelements() / w->ne[0];
+        return N % 4 == 0 && (w->type == Type::Q4_K || K % 64 == 0);
+    };
 
     // ---- plan (reused for a graph that matches the last planned one) ----
     Impl::Plan& P = I.plan;
@@ -628,12 +638,22 @@ const void* HipRuntime::run(Graph& g, bool readback) {
             for (const Tensor* t : g.nodes)
                 for (const Tensor* s : t->src)
                     if (s) cons[I.root(s)].push_back(t);
+            std::unordered_map<const Tensor*, size_t> pos;
+            for (size_t i = 0; i < g.nodes.size(); i++) pos[g.nodes[i]] = i;
+            // the Norm's gamma / beta are read when the FC runs: they must be leaves or nodes
+            // computed before it (a computed gamma between the FC and the Norm would not exist yet)
+            auto ready_at = [&](const Tensor* s, const Tensor* fc) {
+                if (!s) return true;
+                const auto it = pos.find(I.root(s));
+                return it == pos.end() || it->second < pos.at(fc);
+            };
             for (const Tensor* t : g.nodes) {
                 if (t->op != Op::MulMat || !quant(t->src[0]) || grp_of.count(t) || emit16.count(t) ||
                     t == g.nodes.back() || t->iparam[0] != 0)
                     continue;
                 const auto& cs = cons[t];
                 if (cs.size() != 1 || cs[0]->op != Op::Norm || cs[0]->src[0] != t) continue;
+                if (!ready_at(cs[0]->src[1], t) || !ready_at(cs[0]->src[2], t)) continue;
                 const int64_t N = t->src[0]->ne[1];
                 if (cs[0]->ne[0] != N || N % 256 || N > 2048 || cs[0]->nelements() != t->nelements()) continue;
                 ln_pair[t] = cs[0];
@@ -837,6 +857,13 @@ const void* HipRuntime::run(Graph& g, bool readback) {
             I.addr[cfuse.at(t).out] = out;
             for (auto& ab : absorbed)
                 if (ab.second == t) I.addr[ab.first] = out;
+        } else if (t->op == Op::MulMat && ln_pair.count(t) && I.codes.count(I.root(t->src[1])) &&
+                   !(dump_named && !t->name.empty())) {
+            // an FC whose only reader is its post-norm: the pair call writes only the Norm's
+            // outputs (the FC's own rows stay in the library's scratch, or in registers when
+            // the split-K reduce normalizes them)
+            out = nullptr;
+            I.addr[t] = out;
         } else {
             out = I.take(t->nbytes());
             I.addr[t] = out;
@@ -913,6 +940,12 @@ const void* HipRuntime::run(Graph& g, bool readback) {
                                                         w->type == Type::Q8_0 ? MGH_WTYPE_Q8_0 : MGH_WTYPE_Q4_K, wp,
                                                         N, K, (const float*)I.dev(x), M, bias, act, resid,
                                                         (float*)out));
+                } else if (w->type == Type::Q8_0 || w->type == Type::Q4_K) {
+                    // a quantized shape the fused kernels do not take: the reference's F32
+                    // dequant GEMM (k_mul_mat_q8_0_t2 / q4k_t2, mg-opencl.cpp:320-411) on the
+                    // weights dequantized once at upload
+                    I.check(mgh_gemm_f32(I.ctx, (const float*)I.upload_leaf(w, 6), N, K, (const float*)I.dev(x), M,
+                                         bias, act, resid, (float*)out));
                 } else if (w->type == Type::F32) {
                     I.check(mgh_gemm_f32(I.ctx, (const float*)I.dev(w), N, K, (const float*)I.dev(x), M, bias,
                                          act, resid, (float*)out));

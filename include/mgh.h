@@ -291,8 +291,11 @@ int mgh_gemm_h16_f32in(mgh_ctx* ctx, const void* d_wp16, int N, int K, const flo
  * results, with the rounded activations and split-K partials in a fixed 64 MiB scratch array
  * the library holds on each GPU it runs on (no hipMalloc/hipFree, no context buffer growth).
  * Shapes whose scratch exceeds 64 MiB return MGH_ERR_UNSUPPORTED before anything runs. All
- * calls on one GPU share that array: calls that overlap on one GPU race. No counterpart in the
- * reference (its runtime grows scratch buffers on demand, mg-opencl.cpp:1130-1134). */
+ * calls on one GPU share that array; the library orders them on the device (each call's
+ * launches wait for the previous call's, whatever context or stream made it, through one
+ * event per GPU), except under stream capture, where a captured call must not be replayed
+ * while another call on the same GPU runs. No counterpart in the reference (its runtime grows
+ * scratch buffers on demand, mg-opencl.cpp:1130-1134). */
 int mgh_gemm_h16_f32in_noalloc(mgh_ctx* ctx, const void* d_wp16, int N, int K, const float* d_x, int M,
                                const float* d_bias, int act, const float* d_resid, float* d_y);
 /* mgh_gemm_h16 followed by mgh_layernorm_affine of its output rows, the pair a post-norm
@@ -301,7 +304,9 @@ int mgh_gemm_h16_f32in_noalloc(mgh_ctx* ctx, const void* d_wp16, int N, int K, c
  * d_y_ln, d_codes, d_dx, d_s4 as mgh_layernorm_affine(y) writes them (gamma/beta [N], N % 256
  * == 0, N <= 2048), bit for bit. When the product splits K (a few hundred activation rows)
  * and act is 0, the split-K reduce normalizes each row as it leaves, one launch instead of
- * two. No single reference counterpart: the reference runs the two nodes as two dispatches. */
+ * two. d_y may be NULL when the caller needs only the LayerNorm's outputs: the split-K reduce
+ * then skips y's store, and the two-launch form keeps y in the context scratch. No single
+ * reference counterpart: the reference runs the two nodes as two dispatches. */
 int mgh_gemm_h16_ln(mgh_ctx* ctx, const void* d_wp16, int N, int K, const void* d_x16, int M,
                     const float* d_bias, int act, const float* d_resid, float* d_y, const float* d_gamma,
                     const float* d_beta, float eps, float* d_y_ln, int emit, void* d_codes, float* d_dx,
@@ -325,6 +330,12 @@ int mgh_gemm_h16_y16(mgh_ctx* ctx, const void* d_wp16, int N, int K, const void*
  *      mgh_gemm_h16's for the same tile plan. Shapes and alignment as mgh_gemm_h16 (K % 64 == 0,
  *      Q4_K K % 256 == 0, N % 4 == 0, 16-byte aligned operands). ---- */
 size_t mgh_packed_weight_bytes_dq(int wtype, int N, int K);
+/* raw Q8_0 / Q4_K blocks (GGUF layout, any byte alignment) -> fp32 [N][K], the values the
+ * reference's dequantizing kernels compute (DEQ_Q8 mg-opencl.cpp:386-387; deq_q4k_elem
+ * :252-262): any N >= 1, K a multiple of the block size. HipRuntime runs a quantized MulMat
+ * whose shape the tiled kernels do not take (Q8_0 with K % 64 != 0, N % 4 != 0) as the
+ * reference's F32 dequant GEMM on these values (k_mul_mat_q8_0_t2, :320-411). */
+int mgh_dequant_weights_f32(mgh_ctx* ctx, int wtype, const void* d_w, int N, int K, float* d_out);
 int mgh_pack_weights_dq(mgh_ctx* ctx, int wtype, const void* d_w, int N, int K, void* d_wdq);
 int mgh_gemm_dq(mgh_ctx* ctx, int wtype, const void* d_wdq, int N, int K, const void* d_x16, int M,
                 const float* d_bias, int act, const float* d_resid, float* d_y);

@@ -41,6 +41,62 @@ int gh_graph_case(int which, int64_t a, int64_t b, int64_t c, int64_t d, float* 
     }
 }
 
+// One quantized MulMat node with its fused epilogue, y = act(w . x + bias) + resid, through
+// HipRuntime under quant algorithm `algo`: w raw GGUF blocks (wtype 8 = Q8_0, 12 = Q4_K) of
+// N rows of K, x {K, M} fp32, bias [N] (nullable), resid {N, M} (nullable); out {N, M}.
+int gh_quant_mulmat(int wtype, int64_t N, int64_t K, int64_t M, void* wq, float* x, float* bias, float* resid,
+                    int act, int algo, float* out) {
+    try {
+        mg::Context ctx((size_t)64 << 20);
+        const int64_t wne[4] = {K, N, 1, 1};
+        mg::Tensor* w = ctx.external(wtype == 8 ? mg::Type::Q8_0 : mg::Type::Q4_K, 2, wne, wq);
+        const int64_t xne[4] = {K, M, 1, 1};
+        mg::Tensor* xt = ctx.external(mg::Type::F32, 2, xne, x);
+        const int64_t bne[4] = {N, 1, 1, 1};
+        mg::Tensor* b = bias ? ctx.external(mg::Type::F32, 1, bne, bias) : nullptr;
+        const int64_t rne[4] = {N, M, 1, 1};
+        mg::Tensor* r = resid ? ctx.external(mg::Type::F32, 2, rne, resid) : nullptr;
+        mg::Tensor* y = mg::mul_mat_ex(ctx, w, xt, b, act, r);
+        mg::Graph g;
+        g.build_forward(y);
+        mg::HipRuntime rt;
+        rt.set_quant_algo(algo);
+        rt.compute(g);
+        std::memcpy(out, y->data, (size_t)(N * M) * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
+// A post-norm pair whose gamma is computed after the FC: y = norm_affine(mul_mat_ex(w, x, bias,
+// 0, resid), gamma = scale(g0, gs), beta = b0, eps) through HipRuntime under `algo` (the
+// graph order puts the scale node between the FC and the Norm). out {N, M}.
+int gh_post_norm_case(int wtype, int64_t N, int64_t K, int64_t M, void* wq, float* x, float* bias, float* resid,
+                      float* g0, float gs, float* b0, int algo, float* out) {
+    try {
+        mg::Context ctx((size_t)64 << 20);
+        const int64_t wne[4] = {K, N, 1, 1}, xne[4] = {K, M, 1, 1}, nne[4] = {N, 1, 1, 1}, rne[4] = {N, M, 1, 1};
+        mg::Tensor* w = ctx.external(wtype == 8 ? mg::Type::Q8_0 : mg::Type::Q4_K, 2, wne, wq);
+        mg::Tensor* fc = mg::mul_mat_ex(ctx, w, ctx.external(mg::Type::F32, 2, xne, x),
+                                        ctx.external(mg::Type::F32, 1, nne, bias), 0,
+                                        ctx.external(mg::Type::F32, 2, rne, resid));
+        mg::Tensor* gamma = mg::scale(ctx, ctx.external(mg::Type::F32, 1, nne, g0), gs);
+        mg::Tensor* y = mg::norm_affine(ctx, fc, gamma, ctx.external(mg::Type::F32, 1, nne, b0), 1e-5f);
+        mg::Graph g;
+        g.build_forward(y);
+        mg::HipRuntime rt;
+        rt.set_quant_algo(algo);
+        rt.compute(g);
+        std::memcpy(out, y->data, (size_t)(N * M) * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
 // Host-only checks of the graph API semantics (no device): returns 0 or the first failed check.
 //  1: build_forward starts from an empty node list (reference src/mg-tensor.cpp:241)
 //  2: a view whose size-1 dimension carries a non-packed stride is not contiguous

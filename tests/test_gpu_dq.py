@@ -199,3 +199,25 @@ def test_pack_dq_rejects_bad_shapes(ctx):
         ctx.pack_weights_dq(7, dW, 4, 256, dW)                        # not a quantized type
     ctx.free(dW)
     assert ema.packed_weight_bytes_dq(ema.WTYPE_Q4_K, 4, 128) == 0
+
+
+@pytest.mark.parametrize("wtype,N,K", [(ema.WTYPE_Q8_0, 1, 32), (ema.WTYPE_Q8_0, 99, 96), (ema.WTYPE_Q8_0, 768, 3072),
+                                       (ema.WTYPE_Q4_K, 3, 256), (ema.WTYPE_Q4_K, 99, 512)])
+def test_dequant_weights_f32_matches_oracle(ctx, wtype, N, K):
+    """mgh_dequant_weights_f32 (the weights of the F32 dequant GEMM for shapes outside the fused
+    kernels) equals the oracle's dequantization, itself pinned to the reference decoder, bit for
+    bit; the source rows start at an odd byte offset, as Q8_0 rows of K % 64 != 0 do"""
+    rng = np.random.default_rng(N + K)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    w[0, :32] = 0.0
+    wq = oracle.quantize(wtype, w)
+    buf = np.zeros(wq.nbytes + 1, np.uint8)
+    buf[1:] = wq.reshape(-1)
+    dW = ctx.upload(buf)
+    dO = ctx.alloc(N * K * 4)
+    ctx.dequant_weights_f32(wtype, dW.ptr + 1, N, K, dO)
+    got = ctx.download(dO, (N, K), np.float32)
+    ctx.free(dW)
+    ctx.free(dO)
+    want = oracle.dequant(wtype, wq, N, K)
+    assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))

@@ -256,3 +256,73 @@ def test_forward_unfused_attention_q8_0(tmp_path, no_flash_attn):
     err = float(np.abs(got - want).max() / np.abs(want).max())
     print(f"  rel err {err:.2e}")
     assert err <= 1e-3
+
+
+@pytest.mark.parametrize("wtype,N,K", [(8, 100, 96), (8, 99, 96), (8, 99, 128), (8, 30, 32), (12, 100, 256),
+                                       (12, 99, 512), (8, 96, 256), (12, 96, 256)])
+@pytest.mark.parametrize("algo", [1, 2, 3])
+def test_quant_mulmat_any_shape(wtype, N, K, algo):
+    """Every quantized MulMat the reference's dequant kernels run (mg-opencl.cpp:1400-1423: any
+    N, K a multiple of the block size) runs through HipRuntime under every quant algorithm:
+    shapes outside the fused kernels' (Q8_0 with K % 64 != 0 or N % 4 != 0, Q4_K with
+    N % 4 != 0) take the reference's F32 dequant GEMM on weights dequantized once at upload,
+    within 1e-5 of the oracle's dequantize-then-F32 product; the fused kernels' shapes (N = 96)
+    keep their bars (1e-3 of max|y| against dequantize-then-F32 on the dequant paths; the int8
+    path against the oracle's int8-dot product)."""
+    import oracle
+    print(f"quant mulmat wtype={wtype} N={N} K={K} algo={algo}", flush=True)
+    rng = np.random.default_rng(N * 7 + K + algo)
+    M = 37
+    wq = oracle.quantize(wtype, (rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+    resid = rng.standard_normal((M, N)).astype(np.float32)
+    L = _harness()
+    L.gh_quant_mulmat.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64] + \
+        [ctypes.c_void_p] * 4 + [ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    out = np.zeros((M, N), np.float32)
+    P = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    rc = L.gh_quant_mulmat(wtype, N, K, M, P(wq), P(x), P(bias), P(resid), 1, algo, P(out))
+    assert rc == 0, L.gh_last_error().decode()
+    fused = N % 4 == 0 and (wtype == 12 or K % 64 == 0)
+    if fused and algo == 1:
+        qx, dx, _ = oracle.quantize_act_q8(x)
+        ref = oracle.gemm_q_i8(wtype, wq, N, K, qx, dx, bias=bias, act=1, resid=resid)
+    else:
+        ref = oracle.gemm_q_deq_f32(wtype, wq, N, K, x, bias=bias, act=1, resid=resid)
+    err = float(np.abs(out - ref).max() / np.abs(ref).max())
+    print(f"  rel err {err:.2e}", flush=True)
+    assert err <= (1e-3 if fused else 1e-5)
+
+
+@pytest.mark.parametrize("algo", [2, 3])
+@pytest.mark.parametrize("M", [257, 1025])
+def test_post_norm_with_computed_gamma(algo, M):
+    """A post-norm pair (quantized FC + residual, then Norm-affine) whose gamma is a computed
+    node placed between the FC and the Norm in graph order: HipRuntime runs the pair unfused
+    (gamma does not exist yet when the FC runs) and matches the oracle: dequantize-then-F32, then
+    the LayerNorm in float64, within 1e-3 of max|y| (the fp16 operands of the dequant path)."""
+    import oracle
+    N, K = 768, 768
+    print(f"post-norm computed gamma M={M} algo={algo}", flush=True)
+    rng = np.random.default_rng(M + algo)
+    wq = oracle.quantize(8, (rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+    resid = rng.standard_normal((M, N)).astype(np.float32)
+    g0 = (0.5 + 0.05 * rng.standard_normal(N)).astype(np.float32)
+    b0 = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    L = _harness()
+    L.gh_post_norm_case.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64] + \
+        [ctypes.c_void_p] * 5 + [ctypes.c_float, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    out = np.zeros((M, N), np.float32)
+    P = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    rc = L.gh_post_norm_case(8, N, K, M, P(wq), P(x), P(bias), P(resid), P(g0), 2.0, P(b0), algo, P(out))
+    assert rc == 0, L.gh_last_error().decode()
+    h = oracle.gemm_q_deq_f32(8, wq, N, K, x, bias=bias, resid=resid).astype(np.float64)
+    mu = h.mean(1, keepdims=True)
+    var = ((h - mu) ** 2).mean(1, keepdims=True)
+    ref = (h - mu) / np.sqrt(var + 1e-5) * (2.0 * g0.astype(np.float64)) + b0
+    err = float(np.abs(out - ref).max() / np.abs(ref).max())
+    print(f"  rel err {err:.2e}", flush=True)
+    assert err <= 1e-3

@@ -92,8 +92,6 @@ SHAPES = [(1, 4, 64), (7, 132, 256), (1, 2304, 768), (16, 3072, 768), (17, 2304,
 @pytest.mark.parametrize("M,N,K", SHAPES)
 @pytest.mark.parametrize("act,res", [(0, False), (1, False), (0, True), (2, True)])
 def test_gemm_h16_vs_float64(ctx, M, N, K, act, res):
-    if M >= 4097 and (act, res) not in ((0, True), (1, False)):
-        pytest.skip("one epilogue at the largest shape")
     print(f"gemm_h16 M={M} N={N} K={K} act={act} resid={res}", flush=True)
     rng = np.random.default_rng(M * 7 + N * 3 + K + act)
     w16 = (rng.standard_normal((N, K)) * 0.02).astype(np.float16)
@@ -259,15 +257,21 @@ def test_gemm_h16_ln_equals_gemm_then_layernorm(ctx, M, N, K, emit, act):
     dR = ctx.upload(rng.standard_normal((M, N)).astype(np.float32)) if res else None
     T = N // 32
     outs = []
-    for fused in (False, True):
+    for mode in ("apart", "fused", "fused_no_y"):
         y, yl = ctx.alloc(M * N * 4), ctx.alloc(M * N * 4)
         c, dx, s4 = (ctx.alloc(M * N * 2), ctx.alloc(M * T * 4), ctx.alloc(M * T * 4)) if emit else (None, None, None)
-        if fused:
+        if mode == "fused":
             ctx.gemm_h16_ln(dP, N, K, dX, M, dB, act, dR, y, dG, dBe, 1e-5, yl, emit, c, dx, s4)
+        elif mode == "fused_no_y":                # only the LayerNorm's outputs wanted (y NULL)
+            ctx.fill_u32(y, 0x7FC00000, M * N)
+            ctx.gemm_h16_ln(dP, N, K, dX, M, dB, act, dR, None, dG, dBe, 1e-5, yl, emit, c, dx, s4)
         else:
             ctx.gemm_h16(dP, N, K, dX, M, dB, act, dR, y)
             ctx.layernorm_affine(y, dG, dBe, M, N, 1e-5, yl, emit, c, dx, s4)
         o = [ctx.download(y, (M, N), np.float32).view(np.uint32), ctx.download(yl, (M, N), np.float32).view(np.uint32)]
+        if mode == "fused_no_y":
+            assert (o[0] == 0x7FC00000).all()     # y untouched
+            o[0] = outs[0][0]
         if emit:
             o += [ctx.download(c, (M, N), np.float16).view(np.uint16), ctx.download(dx, (M, T), np.float32).view(np.uint32),
                   ctx.download(s4, (M, T), np.uint32)]
@@ -278,8 +282,9 @@ def test_gemm_h16_ln_equals_gemm_then_layernorm(ctx, M, N, K, emit, act):
     for t in (dP, dX, dB, dG, dBe, dR):
         if t is not None:
             ctx.free(t)
-    for a, b in zip(*outs):
-        assert np.array_equal(a, b)
+    for o in outs[1:]:
+        for a, b in zip(outs[0], o):
+            assert np.array_equal(a, b)
     assert np.isfinite(outs[1][1].view(np.float32)).all()
 
 

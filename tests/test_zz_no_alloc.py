@@ -46,6 +46,36 @@ def test_noalloc_equals_allocating_entry_point():
             assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32))
 
 
+def test_noalloc_two_streams_share_the_array_in_order():
+    """Two contexts (two streams) on one GPU call the no-allocation entry point back to back with
+    no host synchronization between them: both need the shared array (a rounding pass and
+    split-K partials), and the library's per-GPU event orders the second call after the first,
+    so each result equals the allocating entry point's bit for bit, twice in a row."""
+    rng = np.random.default_rng(5)
+    shapes = [(2500, 768, 3072, 0), (1025, 768, 3072, 0)]
+    with ema.Context(0) as c0, ema.Context(0) as c1:
+        bufs = []
+        for (M, N, K, act), c in zip(shapes, (c0, c1)):
+            x = rng.standard_normal((M, K)).astype(np.float32)
+            wq = oracle.quantize(ema.WTYPE_Q8_0, (rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+            dW, dX = c.upload(wq), c.upload(x)
+            dP = c.alloc(ema.packed_weight_bytes_f16(N, K))
+            c.pack_weights_f16(ema.WTYPE_Q8_0, dW, N, K, dP)
+            dR = c.upload(rng.standard_normal((M, N)).astype(np.float32))
+            d0, d1 = c.alloc(M * N * 4), c.alloc(M * N * 4)
+            c.gemm_h16_f32in(dP, N, K, dX, M, None, act, dR, d0)
+            c.sync()
+            bufs.append((c, M, N, K, act, dP, dX, dR, d0, d1))
+        for rep in range(2):
+            print(f"noalloc two streams, round {rep}", flush=True)
+            for c, M, N, K, act, dP, dX, dR, d0, d1 in bufs:
+                c.gemm_h16_f32in_noalloc(dP, N, K, dX, M, None, act, dR, d1)
+            for c, M, N, K, act, dP, dX, dR, d0, d1 in bufs:
+                y0 = c.download(d0, (M, N), np.float32)
+                y1 = c.download(d1, (M, N), np.float32)
+                assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32))
+
+
 def test_noalloc_rejects_shapes_beyond_the_array():
     """M = 16448, K = 3072 needs a 101 MB rounded copy of x: refused before any launch (the
     dummy buffers below are never touched)"""
