@@ -38,6 +38,16 @@ __device__ __forceinline__ f16x8 cat8(f16x4 a, f16x4 b) {
     return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
+// -1.0f as a value the compiler cannot fold: with it, fmaf((float)h, -1, p) for an fp16 h
+// is selected as v_fma_mix_f32 (h read as an fp16 half of its register, no conversion), where
+// the constant form becomes a conversion and a subtraction. A scalar move, read by VALU
+// instructions only.
+__device__ __forceinline__ float opaque_neg_one() {
+    float m;
+    asm("s_mov_b32 %0, 0xbf800000" : "=s"(m));
+    return m;
+}
+
 constexpr int KT = 64;             // keys per LDS chunk
 constexpr int VLD = KT + 8;        // V^T row stride (halves)
 
@@ -185,11 +195,20 @@ __global__ __launch_bounds__(256) void k_flash_attn_f16kv(FaArgs a) {
 // scale folded into one fma. Both products run on v_mfma_f32_16x16x32_f16 (the 16-deep
 // instruction takes as many cycles on gfx950): scores over pairs of d chunks, P . V over pairs
 // of key tiles (k = 8lg + j maps to key 16(t + j/4) + 4lg + j%4 in both operands, so the score
-// registers are the P operand as they stand).
-// at most NW waves (a workgroup takes min(NW, ~half the query tiles) waves), so the score
-// registers (4 * KT per lane) fit without spilling
-template <int KT>
-constexpr int kHeadWaves = KT <= 17 ? (KT + 1) / 2 : 8;
+// registers are the P operand as they stand). The work per tile is VALU-bound (exp, the
+// hi/lo split of P), so the VALU is kept to what the math needs: P . V is computed transposed
+// (each lane ends with consecutive features of one query: one division, 8/16-byte stores),
+// the row sums come from the MFMA on an all-ones operand, the lo part of P takes one
+// v_fma_mix_f32 per element, and LDS fragments are read ahead of their MFMAs.
+// At most NW waves (a workgroup takes min(NW, ~half the query tiles) waves), so the score
+// registers (4 * KT per lane) fit without spilling: 17 key tiles take 9 waves (3 per SIMD,
+// 168 registers) only for fp16 q/k/v at D <= 48 with a 17th, partial tile (S = 257 .. 272);
+// at D = 64, with fp32 q/k/v (the next tile's Q held as fp32) or for S <= 256 (16 query
+// tiles, two per wave) 8 (256 registers per wave, two waves per SIMD); 32 key tiles with
+// D >= 48 need more than 256, so there one wave per SIMD
+template <int DC, int KT, bool I16, bool TAIL>
+constexpr int kHeadWaves = KT <= 17 ? std::min((KT + 1) / 2, DC >= 4 || !I16 || !TAIL ? 8 : 9)
+                                    : (KT == 32 && DC >= 3 ? 4 : 8);
 
 // 4 consecutive elements of q/k/v as fp16: rounded from fp32 (RNE) or, with I16, loaded as
 // stored (the producer rounded them the same way)
@@ -210,9 +229,11 @@ __device__ __forceinline__ f16x8 load_h8(const float* p32, const _Float16* p16, 
 // TAIL: S > 16 (KT - 1), so every key tile but the last is full (no masking there).
 // A16: fp16 inputs whose rows start on 16-byte boundaries (element strides multiples of 8).
 template <int DC, int KT, bool I16, bool TAIL, bool A16>
-__global__ __launch_bounds__(64 * kHeadWaves<KT>) void k_attn_head(FaArgs a) {
+__global__ __launch_bounds__(64 * (kHeadWaves<DC, KT, I16, TAIL>)) void k_attn_head(FaArgs a) {
     constexpr int D = 16 * DC;
-    constexpr int KLD = D + 8;         // K row stride (halves)
+    // K row stride (halves): an odd number of 16-wide d chunks is padded with one chunk of
+    // zeros, the upper half of the last score MFMA's K operand, so it is read, not zeroed
+    constexpr int KLD = D + 8;
     constexpr int SP = 16 * KT;        // keys, padded
     constexpr int VT = SP + 8;         // V^T row stride (halves)
     __shared__ __attribute__((aligned(16))) _Float16 Ks[SP * KLD];
@@ -284,37 +305,71 @@ __global__ __launch_bounds__(64 * kHeadWaves<KT>) void k_attn_head(FaArgs a) {
     // scores in log2 units: exp(s*scale - max) = exp2(s*scale*log2(e) - max'), evaluated with
     // the hardware exp2 (v_exp_f32, ~1 ulp)
     const float scale2 = a.scale * 1.4426950408889634f;
+    // Output rows are written with 8-byte (fp16) or 16-byte (fp32) stores when the features are
+    // unit-stride and every row starts 16-byte aligned, element by element otherwise.
+    const bool vec = a.os[0] == 1 && ((a.os[1] | a.os[2] | a.os[3]) & 3) == 0 &&
+                     ((uintptr_t)(a.o16 ? (const void*)a.o16 : (const void*)a.o) & 15) == 0;
+    constexpr int KC = (DC + 1) / 2;   // 32-deep MFMAs per score tile
+    constexpr int NPT = (KT + 1) / 2;  // key-tile pairs of P . V (an odd last tile with zeros)
+    // LDS fragment prefetch distances (key tiles for K, key-tile pairs for V), as far as the
+    // registers allow
+    constexpr int PF = KT <= 17 ? (DC <= 3 ? 2 : 0) : (DC <= 2 ? 1 : 0);
+    constexpr int PFV = KT <= 17 && DC <= 3 ? 1 : 0;
+    // P . V is computed transposed, O^T = V^T . P^T, with row i of the chunk-c V^T fragment
+    // holding feature d = 4 DC (i / 4) + 4c + i % 4: O^T register r of chunk c in lane (l16,
+    // lg) is then feature 4 DC lg + 4c + r of query q0 + l16, so each lane ends with 4 DC
+    // consecutive features of one query and that query's softmax sum.
+    const int vrow0 = 4 * DC * (l16 >> 2) + (l16 & 3);
+    const float m1 = opaque_neg_one();
     for (; qt < nqt; qt += qstep) {
         const int q0 = 16 * qt;
+        // Q as the B operand of the score MFMAs, d chunks in pairs
+        f16x8 qb[KC];
+#pragma unroll
+        for (int i = 0; i < KC; i++)
+            qb[i] = cat8(qf[2 * i], 2 * i + 1 < DC ? qf[2 * i + 1] : f16x4{0, 0, 0, 0});
         // scores: register r of key tile t holds key 16t + 4lg + r of query q0 + l16
         f32x4 sc[KT];
         float mx = -INFINITY;
+        // pairs of 16-wide d chunks on the 32-deep MFMA (k = 8lg + j: d = 16(c + j/4) + 4lg + j%4
+        // in both operands); an odd last chunk is paired with zeros (the 16-deep MFMA takes as
+        // long, and a 16-deep MFMA accumulating right after a 32-deep one into the same
+        // registers gave wrong sums). Fragments are read PF key tiles ahead.
+        f16x8 kf[PF + 1][KC];
+        auto kfrag = [&](int t, int i) {
+            const _Float16* krow = &Ks[(16 * t + l16) * KLD + 4 * lg + 32 * i];
+            return cat8(*(const f16x4*)krow, 2 * i + 1 < DC ? *(const f16x4*)(krow + 16) : f16x4{0, 0, 0, 0});
+        };
+        auto load_k = [&](int t, f16x8 (&f)[KC]) {
+#pragma unroll
+            for (int i = 0; i < KC; i++) f[i] = kfrag(t, i);
+        };
+#pragma unroll
+        for (int t = 0; t < PF && t < KT; t++) load_k(t, kf[t]);
 #pragma unroll
         for (int t = 0; t < KT; t++) {
-            // pairs of 16-wide d chunks on the 32-deep MFMA (k = 8lg + j: d = 16(c + j/4) + 4lg +
-            // j%4 in both operands); an odd last chunk is paired with zeros (the 16-deep MFMA
-            // takes as long, and a 16-deep MFMA accumulating right after a 32-deep one into
-            // the same registers gave wrong sums)
+            if (PF && t + PF < KT) load_k(t + PF, kf[(t + PF) % (PF + 1)]);
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            const _Float16* krow = &Ks[(16 * t + l16) * KLD + 4 * lg];
 #pragma unroll
-            for (int c = 0; c < DC; c += 2) {
-                const f16x4 k1 = c + 1 < DC ? *(const f16x4*)(krow + 16 * c + 16) : f16x4{0, 0, 0, 0};
-                const f16x4 q1 = c + 1 < DC ? qf[c + 1] : f16x4{0, 0, 0, 0};
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(cat8(*(const f16x4*)(krow + 16 * c), k1),
-                                                             cat8(qf[c], q1), acc, 0, 0, 0);
-            }
-            // raw scores; keys past S are -inf (with TAIL only the last tile holds such keys)
-            if (TAIL && t < KT - 1) {
+            for (int i = 0; i < KC; i++)   // without prefetch, one fragment at a time
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(PF ? kf[t % (PF + 1)][i] : kfrag(t, i), qb[i], acc, 0, 0, 0);
+            // raw scores; keys past S are -inf (with TAIL only the last tile holds such keys;
+            // otherwise the tiles from key S on, a uniform branch)
+            if ((TAIL && t < KT - 1) || 16 * t + 16 <= S) {
                 sc[t] = acc;
             } else {
 #pragma unroll
                 for (int r = 0; r < 4; r++) sc[t][r] = 16 * t + 4 * lg + r < S ? acc[r] : -INFINITY;
             }
-            mx = fmaxf(fmaxf(mx, sc[t][0]), sc[t][1]);
-            mx = fmaxf(fmaxf(mx, sc[t][2]), sc[t][3]);
-            __builtin_amdgcn_sched_barrier(0);  // keep the K fragment loads per key tile
+            // the running max takes the previous tile, whose MFMAs have completed by now
+            if (t > 0) {
+                mx = fmaxf(fmaxf(mx, sc[t - 1][0]), sc[t - 1][1]);
+                mx = fmaxf(fmaxf(mx, sc[t - 1][2]), sc[t - 1][3]);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // the fragment reads stay PF tiles ahead
         }
+        mx = fmaxf(fmaxf(mx, sc[KT - 1][0]), sc[KT - 1][1]);
+        mx = fmaxf(fmaxf(mx, sc[KT - 1][2]), sc[KT - 1][3]);
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         // the scores are done with Q: request the next tile's while this one's P . V runs
@@ -322,71 +377,89 @@ __global__ __launch_bounds__(64 * kHeadWaves<KT>) void k_attn_head(FaArgs a) {
         // scale2 > 0 (checked at launch), so the max of the scaled scores is the scaled max;
         // p = exp2(s * scale2 - max) as one fma, and exp2(-inf) = 0 for the masked keys
         const float mxs = mx * scale2;
-        float ps = 0.f;
 #pragma unroll
         for (int t = 0; t < KT; t++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float p = __builtin_amdgcn_exp2f(fmaf(sc[t][r], scale2, -mxs));
-                sc[t][r] = p;
-                ps += p;
-            }
-        ps += __shfl_xor(ps, 16);
-        ps += __shfl_xor(ps, 32);
-        // O += P . V, P = hi + lo in fp16 (A operand: query l16, keys 16t + 4lg + j): hi is P
-        // rounded toward zero, lo the exact remainder rounded toward zero (|P - hi - lo| <=
-        // 2^-20 P)
-        f32x4 O[DC];
+            for (int r = 0; r < 4; r++) sc[t][r] = __builtin_amdgcn_exp2f(fmaf(sc[t][r], scale2, -mxs));
+        // O^T += V^T . P^T, P = hi + lo in fp16 (B operand: query l16, keys 16t + 4lg + j): hi
+        // is P rounded toward zero, lo the exact remainder P - hi rounded toward zero
+        // (|P - hi - lo| <= 2^-20 P, or 2^-24 where lo is an fp16 subnormal). The row sums
+        // come from the same MFMAs on an all-ones V^T chunk (S1 = 1 . P^T: every register of
+        // lane (l16, lg) holds the sum of query l16), so they add exactly the hi + lo that
+        // the numerators use.
+        f32x4 O[DC], S1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < DC; c++) O[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-        auto split = [&](int t, f16x4& ph, f16x4& pl) {
-            const auto h01 = __builtin_amdgcn_cvt_pkrtz(sc[t][0], sc[t][1]);
-            const auto h23 = __builtin_amdgcn_cvt_pkrtz(sc[t][2], sc[t][3]);
-            const auto l01 = __builtin_amdgcn_cvt_pkrtz(sc[t][0] - (float)h01[0], sc[t][1] - (float)h01[1]);
-            const auto l23 = __builtin_amdgcn_cvt_pkrtz(sc[t][2] - (float)h23[0], sc[t][3] - (float)h23[1]);
-            ph = __builtin_bit_cast(f16x4, u32x2{__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)});
-            pl = __builtin_bit_cast(f16x4, u32x2{__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)});
+        const f16x4 z4 = {0, 0, 0, 0};
+        const f16x8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+        // hi and lo operands of key tiles t, t + 1 (t + 1 = KT: zeros); p - hi is exact in fp32
+        // and taken as one v_fma_mix_f32 (m1 = -1) per element
+        auto split = [&](int t, f16x8& ph, f16x8& pl) {
+            const f32x4 zf = {0.f, 0.f, 0.f, 0.f};
+            const f32x4 a = sc[t], b = t + 1 < KT ? sc[t + 1] : zf;
+            const auto h0 = __builtin_amdgcn_cvt_pkrtz(a[0], a[1]), h1 = __builtin_amdgcn_cvt_pkrtz(a[2], a[3]);
+            const auto h2 = __builtin_amdgcn_cvt_pkrtz(b[0], b[1]), h3 = __builtin_amdgcn_cvt_pkrtz(b[2], b[3]);
+            const auto l0 = __builtin_amdgcn_cvt_pkrtz(fmaf((float)h0[0], m1, a[0]), fmaf((float)h0[1], m1, a[1]));
+            const auto l1 = __builtin_amdgcn_cvt_pkrtz(fmaf((float)h1[0], m1, a[2]), fmaf((float)h1[1], m1, a[3]));
+            const auto l2 = __builtin_amdgcn_cvt_pkrtz(fmaf((float)h2[0], m1, b[0]), fmaf((float)h2[1], m1, b[1]));
+            const auto l3 = __builtin_amdgcn_cvt_pkrtz(fmaf((float)h3[0], m1, b[2]), fmaf((float)h3[1], m1, b[3]));
+            auto u = [](auto v) { return __builtin_bit_cast(uint32_t, v); };
+            ph = __builtin_bit_cast(f16x8, u32x4{u(h0), u(h1), u(h2), u(h3)});
+            pl = __builtin_bit_cast(f16x8, u32x4{u(l0), u(l1), u(l2), u(l3)});
         };
         // pairs of key tiles on the 32-deep MFMA (k = 8lg + j: key 16(t + j/4) + 4lg + j%4 in
-        // both operands), an odd last tile on the 16-deep one
+        // both operands); an odd last tile is paired with zeros. V^T fragments are read PF
+        // pairs ahead.
+        f16x8 vf[PFV + 1][DC];
+        auto vfrag = [&](int p, int c) {
+            const _Float16* vrow = &Vt[(vrow0 + 4 * c) * VT + 32 * p + 4 * lg];
+            return cat8(*(const f16x4*)vrow, 2 * p + 1 < KT ? *(const f16x4*)(vrow + 16) : z4);
+        };
+        auto load_v = [&](int p, f16x8 (&f)[DC]) {
 #pragma unroll
-        for (int t = 0; t + 1 < KT; t += 2) {
-            f16x4 ph0, pl0, ph1, pl1;
-            split(t, ph0, pl0);
-            split(t + 1, ph1, pl1);
-            const f16x8 ph = cat8(ph0, ph1), pl = cat8(pl0, pl1);
+            for (int c = 0; c < DC; c++) f[c] = vfrag(p, c);
+        };
 #pragma unroll
-            for (int c = 0; c < DC; c++) {
-                const _Float16* vrow = &Vt[(16 * c + l16) * VT + 16 * t + 4 * lg];
-                const f16x8 vf = cat8(*(const f16x4*)vrow, *(const f16x4*)(vrow + 16));
-                O[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vf, O[c], 0, 0, 0);
-                O[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vf, O[c], 0, 0, 0);
-            }
-            __builtin_amdgcn_sched_barrier(0);  // keep the V fragment loads per key tile pair (registers)
-        }
-        if (KT % 2) {                          // the odd last tile, paired with zeros
-            f16x4 ph, pl;
-            split(KT - 1, ph, pl);
-            const f16x4 z = {0, 0, 0, 0};
+        for (int p = 0; p < PFV && p < NPT; p++) load_v(p, vf[p]);
+#pragma unroll
+        for (int p = 0; p < NPT; p++) {
+            if (PFV && p + PFV < NPT) load_v(p + PFV, vf[(p + PFV) % (PFV + 1)]);
+            f16x8 ph, pl;
+            split(2 * p, ph, pl);
 #pragma unroll
             for (int c = 0; c < DC; c++) {
-                const f16x8 vf = cat8(*(const f16x4*)&Vt[(16 * c + l16) * VT + 16 * (KT - 1) + 4 * lg], z);
-                O[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cat8(ph, z), vf, O[c], 0, 0, 0);
-                O[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cat8(pl, z), vf, O[c], 0, 0, 0);
+                const f16x8 v = PFV ? vf[p % (PFV + 1)][c] : vfrag(p, c);   // without prefetch, one chunk at a time
+                O[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v, ph, O[c], 0, 0, 0);
+                O[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v, pl, O[c], 0, 0, 0);
             }
+            S1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, ph, S1, 0, 0, 0);
+            S1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pl, S1, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);  // the fragment reads stay PFV pairs ahead
         }
-        // O register r: query q0 + 4lg + r, d = 16c + l16; its row sum sits in lane 4lg + r
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float inv = 1.f / __shfl(ps, 4 * lg + r);
-            const int qi = q0 + 4 * lg + r;
-            if (qi >= S) continue;
+        // features 4 DC lg .. 4 DC lg + 4 DC - 1 of query q0 + l16, divided by its row sum
+        const float inv = 1.f / S1[0];
+        const int qi = q0 + l16;
+        if (qi < S) {
             const int64_t ro = (int64_t)b * a.os[3] + (int64_t)h * a.os[2] + (int64_t)qi * a.os[1];
+            const int d0 = 4 * DC * lg;
+            if (vec) {
 #pragma unroll
-            for (int c = 0; c < DC; c++) {
-                const int64_t e = ro + (int64_t)(16 * c + l16) * a.os[0];
-                if (a.o16) a.o16[e] = (_Float16)(O[c][r] * inv);
-                else a.o[e] = O[c][r] * inv;
+                for (int c = 0; c < DC; c++) {
+                    const f32x4 v = O[c] * inv;
+                    if (a.o16)
+                        *(f16x4*)(a.o16 + ro + d0 + 4 * c) = f16x4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+                    else
+                        *(f32x4*)(a.o + ro + d0 + 4 * c) = v;
+                }
+            } else {
+#pragma unroll
+                for (int c = 0; c < DC; c++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int64_t e = ro + (int64_t)(d0 + 4 * c + r) * a.os[0];
+                        if (a.o16) a.o16[e] = (_Float16)(O[c][r] * inv);
+                        else a.o[e] = O[c][r] * inv;
+                    }
             }
         }
     }
@@ -408,11 +481,13 @@ void launch_head_t(const FaArgs& a, hipStream_t s) {
     // against 8.5 us (3 workgroups of 6 waves), two images 7.6 against 8.7; 3, 5, 6 or 9 waves
     // 8.4-9.8 us at one image.
     int qs = (int)std::max<int64_t>(1, std::min<int64_t>(256 / std::max<int64_t>(heads, 1), (nqt + 5) / 6));
-    int nw = std::min(kHeadWaves<KT>, std::max(1, qs > 1 ? (nqt + qs - 1) / qs : (nqt + 1) / 2));
-    if (qs > 1 && kHeadWaves<KT> >= 4 && heads * ((nqt + 3) / 4) <= 256) nw = 4;
+    const bool tail = a.S > 16 * (KT - 1);
+    const int maxw = a.q16 ? (tail ? kHeadWaves<DC, KT, true, true> : kHeadWaves<DC, KT, true, false>)
+                           : (tail ? kHeadWaves<DC, KT, false, true> : kHeadWaves<DC, KT, false, false>);
+    int nw = std::min(maxw, std::max(1, qs > 1 ? (nqt + qs - 1) / qs : (nqt + 1) / 2));
+    if (qs > 1 && maxw >= 4 && heads * ((nqt + 3) / 4) <= 256) nw = 4;
     if (qs > 1) qs = (nqt + nw - 1) / nw;
     const dim3 grid((unsigned)a.H, (unsigned)a.B, (unsigned)qs), block((unsigned)(64 * nw));
-    const bool tail = a.S > 16 * (KT - 1);
     // fp16 rows 16-byte aligned (the pointers are, head_ok): one load per 8 elements
     const bool a16 = a.st[1] % 8 == 0 && a.st[2] % 8 == 0 && a.st[3] % 8 == 0;
     if (a.q16 && a16) {
