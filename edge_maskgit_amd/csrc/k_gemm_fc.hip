@@ -630,12 +630,24 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_fc
 template <int ACT>
 __device__ __forceinline__ f32x4 split_sum4(const f32x4* part, size_t q_stride, int splits, const float* bias,
                                             int n, const float* resid, size_t o) {
-    f32x4 v = __builtin_nontemporal_load(part);
-    for (int k = 1; k < splits; k++) v += __builtin_nontemporal_load(part + (size_t)k * q_stride);
-    if (bias) v += *(const f32x4*)(bias + n);
+    // the first KB partials, the bias and the residual are all requested before any is summed
+    // (one memory round trip, not one per split); the sum keeps split order
+    constexpr int KB = 4;
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    f32x4 p[KB];
+#pragma unroll
+    for (int k = 0; k < KB; k++) p[k] = k < splits ? __builtin_nontemporal_load(part + (size_t)k * q_stride) : z;
+    const f32x4 bv = bias ? *(const f32x4*)(bias + n) : z;
+    const f32x4 rv = resid ? *(const f32x4*)(resid + o) : z;
+    f32x4 v = p[0];
+#pragma unroll
+    for (int k = 1; k < KB; k++)
+        if (k < splits) v += p[k];
+    for (int k = KB; k < splits; k++) v += __builtin_nontemporal_load(part + (size_t)k * q_stride);
+    if (bias) v += bv;
 #pragma unroll
     for (int e = 0; e < 4; e++) v[e] = act_h<ACT>(v[e]);
-    if (resid) v += *(const f32x4*)(resid + o);
+    if (resid) v += rv;
     return v;
 }
 

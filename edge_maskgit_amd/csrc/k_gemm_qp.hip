@@ -445,13 +445,25 @@ __global__ __launch_bounds__(256) void k_gemm_qp_reduce(GemmArgs g) {
     const int m = m0 + r, n = n0 + c;
     if (m >= M || n >= N) return;
     const f32x4* part = (const f32x4*)(g.ws + (size_t)lt * splits * BM * BN) + q;
-    f32x4 v = __builtin_nontemporal_load(part);
-    for (int k = 1; k < splits; k++) v += __builtin_nontemporal_load(part + (size_t)k * Q);
-    if (g.bias) v += *(const f32x4*)(g.bias + n);
+    const size_t o = (size_t)m * N + n;
+    // the first KB partials, the bias and the residual are requested before any is summed (one
+    // memory round trip, not one per split); the sum keeps split order
+    constexpr int KB = 4;
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    f32x4 p[KB];
+#pragma unroll
+    for (int k = 0; k < KB; k++) p[k] = k < splits ? __builtin_nontemporal_load(part + (size_t)k * Q) : z;
+    const f32x4 bv = g.bias ? *(const f32x4*)(g.bias + n) : z;
+    const f32x4 rv = g.resid ? *(const f32x4*)(g.resid + o) : z;
+    f32x4 v = p[0];
+#pragma unroll
+    for (int k = 1; k < KB; k++)
+        if (k < splits) v += p[k];
+    for (int k = KB; k < splits; k++) v += __builtin_nontemporal_load(part + (size_t)k * Q);
+    if (g.bias) v += bv;
 #pragma unroll
     for (int e = 0; e < 4; e++) v[e] = act_x<ACT>(v[e]);
-    const size_t o = (size_t)m * N + n;
-    if (g.resid) v += *(const f32x4*)(g.resid + o);
+    if (g.resid) v += rv;
     __builtin_nontemporal_store(v, (f32x4*)(g.y + o));
 }
 
