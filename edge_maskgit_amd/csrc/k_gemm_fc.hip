@@ -893,14 +893,15 @@ H16Plan gemm_h16_plan(int M, int N, int K, bool xf32, int wq) {
         // fragment and wave, so the plans favour more workgroups per CU (a wave's decoding
         // overlaps another's MFMAs) and more activation rows per wave. Measured against the
         // fp16-weight plans on the four FC shapes, Q8_0, buffers rotated over 1 GB:
-        //  * fp32 activations, K <= 1024, a few images (M >= 512): 64 x 64 tiles on a 2-deep
-        //    ring when they fit one round of workgroups (three per CU), 32 x 64 when there are
-        //    fewer than one per CU (M = 1025: QKV 15.8 against 18.9 us, out-proj 11.8 against
-        //    12.7 us); one image (M = 257) keeps the few-tile plans below;
+        //  * fp32 activations, K <= 1024, M > 128: 64 x 64 tiles on a 2-deep ring when they fit
+        //    one round of workgroups (three per CU), 32 x 64 when there are fewer than one per
+        //    CU (M = 1025: QKV 15.8 against 18.9 us, out-proj 11.8 against 12.7 us; M = 257, all
+        //    32 x 64: QKV 10.6 against 11.2 us, out-proj 10.6 against 10.9 us, the 3072-wide
+        //    up-proj 11.5 against 12.3 us on the few-tile plan's 3-deep 64 x 64 ring);
         //  * fp16 activations, 128 x 128 tiles from one tile per CU, the long-K narrow
         //    down-proj split in two (M = 4097: QKV 35.6 against 40.2 us including the rounding
         //    pass, down-proj 58.7 against 64.0 us).
-        if (xf32 && K <= 1024 && M >= 512 && t6464 <= 768) {
+        if (xf32 && K <= 1024 && M > 128 && t6464 <= 768) {
             p.ns = 2;
             p.bn = 64;
             p.bm = t6464 < 256 ? 32 : 64;
