@@ -44,6 +44,8 @@
 //    (deterministic) and applies the epilogue.
 #include <algorithm>
 
+#include <atomic>
+
 #include "mgh_common.h"
 #include "mgh_kernels.h"
 #include "k_ln_row.h"
@@ -1079,28 +1081,72 @@ static hipError_t launch_h16_t(const GemmH16Args& a, hipStream_t s, const LnArgs
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a0, hipStream_t s, const LnArgs* ln) {
-    GemmH16Args a = a0;
-    a.ph = p.ph;
+// The plan's kernel
+static hipError_t dispatch_h16(const H16Plan& p, const GemmH16Args& a, hipStream_t s, const LnArgs* ln) {
     const bool xf = a.xf != nullptr;
-    if (p.wmr != 2) return hipErrorInvalidValue;
-    // the reduce takes the LayerNorm only when K is split, without activation or fp16 output
-    if (ln && (p.splits < 2 || a.act != 0 || a.y16 || a.N % 256 || a.N > 2048)) return hipErrorInvalidValue;
     if (p.bn == 128 && p.ns == 2) {
         if (p.bm == 128 && !xf) return launch_h16_t<128, false, 2, 2, 128>(a, s, ln);
-        if (p.bm == 64) return xf ? launch_h16_t<64, true, 2, 2, 128>(a, s, ln) : launch_h16_t<64, false, 2, 2, 128>(a, s, ln);
+        if (p.bm == 64)
+            return xf ? launch_h16_t<64, true, 2, 2, 128>(a, s, ln) : launch_h16_t<64, false, 2, 2, 128>(a, s, ln);
     }
     if (p.bn == 128 && p.ns == 3 && p.bm == 64 && !xf) return launch_h16_t<64, false, 3, 2, 128>(a, s, ln);
     if (p.bn == 64 && p.ns == 3) {
-        if (p.bm == 64) return xf ? launch_h16_t<64, true, 3, 2, 64>(a, s, ln) : launch_h16_t<64, false, 3, 2, 64>(a, s, ln);
-        if (p.bm == 32) return xf ? launch_h16_t<32, true, 3, 2, 64>(a, s, ln) : launch_h16_t<32, false, 3, 2, 64>(a, s, ln);
+        if (p.bm == 64)
+            return xf ? launch_h16_t<64, true, 3, 2, 64>(a, s, ln) : launch_h16_t<64, false, 3, 2, 64>(a, s, ln);
+        if (p.bm == 32)
+            return xf ? launch_h16_t<32, true, 3, 2, 64>(a, s, ln) : launch_h16_t<32, false, 3, 2, 64>(a, s, ln);
     }
     // plans of the quantized-byte forms only
     if (a.wq && p.bn == 64 && p.ns == 2 && xf) {
-        if (p.bm == 64) return a.wq == 8 ? launch_h16_w<64, true, 2, 2, 64, 8>(a, s, ln) : launch_h16_w<64, true, 2, 2, 64, 12>(a, s, ln);
-        if (p.bm == 32) return a.wq == 8 ? launch_h16_w<32, true, 2, 2, 64, 8>(a, s, ln) : launch_h16_w<32, true, 2, 2, 64, 12>(a, s, ln);
+        if (p.bm == 64)
+            return a.wq == 8 ? launch_h16_w<64, true, 2, 2, 64, 8>(a, s, ln) : launch_h16_w<64, true, 2, 2, 64, 12>(a, s, ln);
+        if (p.bm == 32)
+            return a.wq == 8 ? launch_h16_w<32, true, 2, 2, 64, 8>(a, s, ln) : launch_h16_w<32, true, 2, 2, 64, 12>(a, s, ln);
     }
     return hipErrorInvalidValue;
+}
+
+// CUs of the current device (asked once per device)
+static int device_cus() {
+    static std::atomic<int> n[64];
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) return 0;
+    int v = n[d].load(std::memory_order_relaxed);
+    if (v <= 0 && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, d) == hipSuccess) n[d].store(v);
+    return v > 0 ? v : 0;
+}
+
+hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a0, hipStream_t s, const LnArgs* ln) {
+    GemmH16Args a = a0;
+    a.ph = p.ph;
+    if (p.wmr != 2) return hipErrorInvalidValue;
+    // the reduce takes the LayerNorm only when K is split, without activation or fp16 output
+    if (ln && (p.splits < 2 || a.act != 0 || a.y16 || a.N % 256 || a.N > 2048)) return hipErrorInvalidValue;
+    // A last, partial row of tiles that raises the most tiles any CU runs (ceil(tiles / CUs))
+    // goes to the skinny-M kernel instead, after the tiled kernel has taken the whole tile
+    // rows: a launch takes about as long as its most loaded CU. At M = 4097 the up-proj's 33rd row of 128-row tiles
+    // (24 tiles past 768 = three per CU) costs ~9 us on the Q8_0 bytes (M = 4096: 43.1 us,
+    // 4097: 52.5 us, 4224: 51.7 us) and ~6.5 us on fp16 copies, the skinny kernel ~4.5 us at
+    // K <= 1024. Rows past the split are summed in the skinny kernel's fp32 order.
+    if (!ln && p.splits <= 1 && a.K <= 1024) {
+        const int mfull = a.M / p.bm * p.bm, rem = a.M - mfull, cus = device_cus();
+        const int tn = (a.N + p.bn - 1) / p.bn, full = (mfull / p.bm) * tn, total = full + tn;
+        if (mfull > 0 && rem > 0 && use_gemv_h16(rem, a.K) && cus > 0 &&
+            (total + cus - 1) / cus > (full + cus - 1) / cus) {
+            GemmH16Args m = a, t = a0;
+            m.M = mfull;
+            t.M = rem;
+            const size_t xo = (size_t)mfull * a.K, yo = (size_t)mfull * a.N;
+            if (t.x) t.x += xo;
+            if (t.xf) t.xf += xo;
+            if (t.resid) t.resid += yo;
+            if (t.y) t.y += yo;
+            if (t.y16) t.y16 += yo;
+            const hipError_t e = dispatch_h16(p, m, s, nullptr);
+            return e != hipSuccess ? e : launch_gemv_h16(t, s);
+        }
+    }
+    return dispatch_h16(p, a, s, ln);
 }
 
 }  // namespace mgh
