@@ -87,7 +87,10 @@ def test_dq_layout_size(wtype, N, K):
 # partial 16-row group
 SHAPES = [(1, 2304, 768), (7, 132, 256), (16, 768, 3072), (32, 768, 768), (33, 100, 768),
           (65, 128, 768), (257, 3072, 768), (257, 768, 3072), (1025, 2304, 768), (1025, 768, 768),
-          (1025, 3072, 768), (1025, 768, 3072), (4097, 2304, 768), (4112, 768, 3072)]
+          (1025, 3072, 768), (1025, 768, 3072), (4097, 2304, 768), (4112, 768, 3072),
+          # the up-proj at M = 4097 / 4112: the last, partial row of 128-row tiles runs on the
+          # skinny-M kernel after the tiled kernel (GELU without residual, residual without act)
+          (4097, 3072, 768), (4112, 3072, 768)]
 
 
 @pytest.mark.parametrize("wtype", [ema.WTYPE_Q8_0, ema.WTYPE_Q4_K])
