@@ -242,7 +242,14 @@ __global__ __launch_bounds__(64 * (kHeadWaves<DC, KT, I16, TAIL>)) void k_attn_h
     const int S = a.S;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
     const int l16 = lane & 15, lg = lane >> 4;
-    const int h = blockIdx.x, b = blockIdx.y;
+    // XCD-aware placement: workgroup i runs on XCD i % 8, so the logical (query split, head,
+    // image) order is remapped into contiguous runs per XCD — each XCD takes whole images, whose
+    // q/k/v rows (all heads interleaved in one row) its L2 then fetches once
+    const int QS = gridDim.z;
+    const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const int lid = xcd_remap(lin, gridDim.x * gridDim.y * QS);
+    const int zq = lid % QS, hb = lid / QS;
+    const int h = hb % gridDim.x, b = hb / gridDim.x;
     const int64_t base = (int64_t)b * a.st[3] + (int64_t)h * a.st[2];
 
     // The staging is latency-bound (one workgroup per CU at typical shapes), so each round
@@ -257,7 +264,7 @@ __global__ __launch_bounds__(64 * (kHeadWaves<DC, KT, I16, TAIL>)) void k_attn_h
 
     const int nqt = (S + 15) / 16;
     const int qstep = nw * gridDim.z;
-    int qt = blockIdx.z * nw + wave;   // workgroup z takes query tiles z*nw + wave, + qstep, ...
+    int qt = zq * nw + wave;           // query split z takes query tiles z*nw + wave, + qstep, ...
     // Q as the B operand: lane = query 16t + l16, k = d = 16c + 4lg + j
     f16x4 qf[DC];
     auto load_q = [&](int t) {
