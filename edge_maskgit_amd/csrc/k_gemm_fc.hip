@@ -22,12 +22,16 @@
 //  * y tile BN (128 or 64) weight rows x BM (128, 64 or 32) activation rows per 256-thread
 //    workgroup (2 x 2 waves, each BN/2 x BM/2 outputs as v_mfma_f32_16x16x32_f16 tiles); K
 //    stage 64. gemm_h16_plan picks the tile, the ring depth and the K split per shape.
-//  * Operands move with global_load_lds (16 bytes per lane; 4 for the Q8_0 scales and the Q4_K
-//    headers) straight into a 2- or 3-deep LDS ring: one instruction moves whole 128-byte row
-//    segments (fp16 weights, activations: XOR-swizzled so the MFMA fragment reads are
-//    bank-conflict free) or whole 16-row groups of quantized weights (already in fragment
-//    order). The stage hand-over is an explicit vmcnt/lgkmcnt wait and s_barrier
-//    (stage_sync), which keeps the prefetched stages in flight.
+//  * Operands move with buffer loads into LDS (16 bytes per lane; 4 for the Q8_0 scales and
+//    the Q4_K headers) straight into a 2- or 3-deep LDS ring: one instruction moves whole
+//    128-byte row segments (fp16 weights, activations: XOR-swizzled so the MFMA fragment reads
+//    are bank-conflict free) or whole 16-row groups of quantized weights (already in fragment
+//    order). Resource and stage offset are scalar, the lane offset loop-invariant, and the
+//    ring slot of each unrolled stage a constant: the K loop's vector instructions are the
+//    MFMAs, the decoding and the fp32 -> fp16 rounding, nothing for addresses (every vector
+//    instruction per stage and wave adds to the kernel time: the decoding leaves the VALU
+//    busier than the matrix pipe). The stage hand-over is an explicit vmcnt/lgkmcnt wait and
+//    s_barrier (stage_sync), which keeps the prefetched stages in flight.
 //  * Software pipeline: the fragments of the next K half are read from LDS (and decoded) while
 //    the current half's MFMAs issue; the stage boundary (vmcnt wait, barrier, next DMA, first
 //    fragment reads of the new stage) sits between two halves of the second K half's MFMAs, so
@@ -105,11 +109,21 @@ struct HLds {
     u32x4 x[NS][BM * kCpr<XF32>];
 };
 
-__device__ __forceinline__ void dma16(const void* g, void* lds) {
-    __builtin_amdgcn_global_load_lds(g, (lds_void*)lds, 16, 0, 0);
+// Raw buffer resource over [base, base + bytes) (extent capped at 4 GB): loads past the extent
+// return zeros instead of faulting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint64_t bytes) {
+    const int n = bytes >= 0xFFFFFFFFull ? -1 : (int)(uint32_t)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
 }
-__device__ __forceinline__ void dma4(const void* g, void* lds) {
-    __builtin_amdgcn_global_load_lds(g, (lds_void*)lds, 4, 0, 0);
+// DMA of 16 (4) bytes per lane from resource offset voff + soff into LDS at lds + 16 (4) * lane.
+// The resource and soff live in SGPRs and voff is loop-invariant, so a DMA in the K loop costs
+// no vector instruction (a global_load_lds takes a 64-bit per-lane address, one 64-bit add per
+// DMA and stage).
+__device__ __forceinline__ void bdma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void* lds) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, (int)voff, (int)soff, 0, 0);
+}
+__device__ __forceinline__ void bdma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void* lds) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 4, (int)voff, (int)soff, 0, 0);
 }
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 template <int N>
@@ -366,87 +380,97 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_fc
     int m0, n0;
     tile_origin(lt, tiles_m, tiles_n, BM, BN, g.ph, m0, n0);
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wn = wave & 1, wm = wave >> 1;
+    // the wave index is uniform: held in an SGPR, everything derived from it (LDS DMA
+    // destinations, group offsets) is scalar work
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = (tid >> 6) & 1, wm = tid >> 7;
     const int l16 = lane & 15, lq = lane >> 4;
 
-    // DMA instruction c of an operand moves rows (64/CPR)*c + lane/CPR, slot lane % CPR, which
-    // holds that row's chunk slot ^ swz(row)
-    const uint8_t* srcw[CW];
-    const uint8_t* srcx[CX];
-    const uint8_t* srca[CA > 0 ? CA : 1];
+    // Operand DMA: per-tile buffer resources, a loop-invariant per-lane offset per DMA
+    // instruction and a per-stage scalar offset. DMA instruction c of a row-major operand moves
+    // rows (64/CPR)*c + lane/CPR, slot lane % CPR, which holds that row's chunk slot ^ swz(row);
+    // rows past the operand's end re-read its last row (their outputs are discarded).
     const int S = K / 64;
-    // dequant layout: this wave's groups of the tile (past the last group: the last one, whose
-    // values only reach discarded rows)
-    const int G = (N + 15) / 16;
+    // dequant layout: the tile's first 16-row group g0 and this wave's groups of the tile (past
+    // the last group: the last one, whose values only reach discarded rows)
+    const int G = (N + 15) / 16, g0 = n0 / 16;
+    uint32_t offw[CW], offx[CX], offa[CA > 0 ? CA : 1];
+    __amdgpu_buffer_rsrc_t rw, ra, rx;
     if (WQ == 0) {
+        rw = make_rsrc((const uint8_t*)g.w + (size_t)n0 * K * 2, (uint64_t)(N - n0) * K * 2);
+        ra = rw;
 #pragma unroll
         for (int q = 0; q < CW; q++) {
             const int r = (64 / CPW) * (wave + NW * q) + lane / CPW;
             const int n = min(n0 + r, N - 1);
-            srcw[q] = (const uint8_t*)g.w + (size_t)n * K * 2 + ((lane % CPW) ^ swz<CPW>(r)) * 16;
+            offw[q] = (uint32_t)(n - n0) * K * 2 + ((lane % CPW) ^ swz<CPW>(r)) * 16;
         }
     } else if (WQ == 8) {
+        // codes: 1 KB per group and stage; then the scale rows, 64 bytes per group and stage
+        const uint64_t wb = (uint64_t)G * S * 1024;
+        rw = make_rsrc((const uint8_t*)g.w + (size_t)g0 * S * 1024, wb - (uint64_t)g0 * S * 1024);
+        ra = make_rsrc((const uint8_t*)g.w + wb + (size_t)g0 * S * 64, (uint64_t)(G - g0) * S * 64);
 #pragma unroll
-        for (int q = 0; q < CW; q++) {
-            const int gi = min(n0 / 16 + wave * GPW + q, G - 1);
-            srcw[q] = (const uint8_t*)g.w + (size_t)gi * S * 1024 + lane * 16;
-        }
+        for (int q = 0; q < CW; q++)
+            offw[q] = (uint32_t)(min(g0 + wave * GPW + q, G - 1) - g0) * S * 1024 + lane * 16;
         // lanes 16 * GPW.. repeat the wave's last scale row into the padding
-        const int gi = min(n0 / 16 + wave * GPW + min(lane / 16, GPW - 1), G - 1);
-        srca[0] = (const uint8_t*)g.w + (size_t)G * S * 1024 + (size_t)gi * S * 64 + (lane % 16) * 4;
+        offa[0] = (uint32_t)(min(g0 + wave * GPW + min(lane / 16, GPW - 1), G - 1) - g0) * S * 64 + (lane % 16) * 4;
     } else {
+        // nibbles: 512 bytes per group and stage; then the headers, 256 bytes per group and
+        // super-block
+        const uint64_t wb = (uint64_t)G * S * 512;
+        rw = make_rsrc((const uint8_t*)g.w + (size_t)g0 * S * 512, wb - (uint64_t)g0 * S * 512);
+        ra = make_rsrc((const uint8_t*)g.w + wb + (size_t)g0 * (K / 256) * 256, (uint64_t)(G - g0) * (K / 256) * 256);
         if (GPW >= 2) {
 #pragma unroll
-            for (int q = 0; q < CW; q++) {
-                const int gi = min(n0 / 16 + wave * GPW + 2 * q + lane / 32, G - 1);
-                srcw[q] = (const uint8_t*)g.w + (size_t)gi * S * 512 + (lane % 32) * 16;
-            }
+            for (int q = 0; q < CW; q++)
+                offw[q] = (uint32_t)(min(g0 + wave * GPW + 2 * q + lane / 32, G - 1) - g0) * S * 512 + (lane % 32) * 16;
         } else {
-            const int gi = min(n0 / 16 + wave, G - 1);
+            const uint32_t gw = (uint32_t)(min(g0 + wave, G - 1) - g0) * S * 512;
 #pragma unroll
-            for (int q = 0; q < CW; q++) srcw[q] = (const uint8_t*)g.w + (size_t)gi * S * 512 + q * 256 + lane * 4;
+            for (int q = 0; q < CW; q++) offw[q] = gw + q * 256 + lane * 4;
         }
 #pragma unroll
-        for (int q = 0; q < CA; q++) {
-            const int ga = min(n0 / 16 + wave * GPW + q, G - 1);
-            srca[q] = (const uint8_t*)g.w + (size_t)G * S * 512 + (size_t)ga * (K / 256) * 256 + lane * 4;
-        }
+        for (int q = 0; q < CA; q++)
+            offa[q] = (uint32_t)(min(g0 + wave * GPW + q, G - 1) - g0) * (K / 256) * 256 + lane * 4;
     }
+    {
+        constexpr int XB = XF32 ? 4 : 2;        // bytes per activation value
+        const uint8_t* xb = XF32 ? (const uint8_t*)g.xf : (const uint8_t*)g.x;
+        rx = make_rsrc(xb + (size_t)m0 * K * XB, (uint64_t)(M - m0) * K * XB);
 #pragma unroll
-    for (int q = 0; q < CX; q++) {
-        const int r = (64 / CPX) * (wave + NW * q) + lane / CPX;
-        const int m = min(m0 + r, M - 1);
-        const uint8_t* base = XF32 ? (const uint8_t*)g.xf + (size_t)m * K * 4 : (const uint8_t*)g.x + (size_t)m * K * 2;
-        srcx[q] = base + ((lane % CPX) ^ swz<CPX>(r)) * 16;
+        for (int q = 0; q < CX; q++) {
+            const int r = (64 / CPX) * (wave + NW * q) + lane / CPX;
+            const int m = min(m0 + r, M - 1);
+            offx[q] = (uint32_t)(m - m0) * K * XB + ((lane % CPX) ^ swz<CPX>(r)) * 16;
+        }
     }
     const int s_beg = (int)((int64_t)ks * S / splits), s_end = (int)((int64_t)(ks + 1) * S / splits);
     const int SL = s_end - s_beg;
     const int s0 = ((m0 / BM) + 4 * (n0 / BN)) % SL;          // K rotation
     auto kst = [&](int s) { int v = s + s0; return s_beg + (v >= SL ? v - SL : v); };
     auto dma_stage = [&](int st, int s) {
-        const int ks_ = kst(s);
-        const size_t ofs = (size_t)ks_ * 16;
+        const uint32_t k_ = (uint32_t)kst(s);
         if (WQ == 0) {
 #pragma unroll
-            for (int d = 0; d < CW; d++) dma16(srcw[d] + ofs * CPW, &L.w[st][(wave + NW * d) * 64]);
+            for (int d = 0; d < CW; d++) bdma16(rw, offw[d], k_ * 128, &L.w[st][(wave + NW * d) * 64]);
         } else if (WQ == 8) {
 #pragma unroll
-            for (int d = 0; d < CW; d++) dma16(srcw[d] + (size_t)ks_ * 1024, &L.w[st][(wave * GPW + d) * 64]);
-            dma4(srca[0] + (size_t)ks_ * 64, &L.aux[st][wave * 16]);
+            for (int d = 0; d < CW; d++) bdma16(rw, offw[d], k_ * 1024, &L.w[st][(wave * GPW + d) * 64]);
+            bdma4(ra, offa[0], k_ * 64, &L.aux[st][wave * 16]);
         } else {
             if (GPW >= 2) {
 #pragma unroll
-                for (int d = 0; d < CW; d++) dma16(srcw[d] + (size_t)ks_ * 512, &L.w[st][(wave * GPW + 2 * d) * 32]);
+                for (int d = 0; d < CW; d++) bdma16(rw, offw[d], k_ * 512, &L.w[st][(wave * GPW + 2 * d) * 32]);
             } else {
 #pragma unroll
-                for (int d = 0; d < CW; d++) dma4(srcw[d] + (size_t)ks_ * 512, &L.w[st][wave * 32 + d * 16]);
+                for (int d = 0; d < CW; d++) bdma4(rw, offw[d], k_ * 512, &L.w[st][wave * 32 + d * 16]);
             }
 #pragma unroll
-            for (int d = 0; d < CA; d++) dma4(srca[d] + (size_t)(ks_ >> 2) * 256, &L.aux[st][(wave * GPW + d) * 16]);
+            for (int d = 0; d < CA; d++) bdma4(ra, offa[d], (k_ >> 2) * 256, &L.aux[st][(wave * GPW + d) * 16]);
         }
 #pragma unroll
-        for (int d = 0; d < CX; d++) dma16(srcx[d] + ofs * CPX, &L.x[st][(wave + NW * d) * 64]);
+        for (int d = 0; d < CX; d++) bdma16(rx, offx[d], k_ * (XF32 ? 256 : 128), &L.x[st][(wave + NW * d) * 64]);
     };
     // fragment of 16 rows from r0 (r0 % 16 == 0), K half kb: lane (l16, lq) takes 8 values
     auto frag = [&](const u32x4* B, int r0, int kb) {
@@ -547,12 +571,37 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_fc
         mfma_all(ca, cb, MID, I * J);
     };
 
-    int st = 0;
-    for (int s = 0; s < SL; s++) {
-        const int stn = st + 1 == NS ? 0 : st + 1;
-        half_inner(a[0], b[0], a[1], b[1], st, kst(s));
-        half_boundary(a[1], b[1], a[0], b[0], s, st, stn);
-        st = stn;
+    // Stage s uses ring slot s % NS. The loop runs NS stages per iteration with the slots as
+    // constants, so every LDS fragment read is a loop-invariant lane address plus an immediate
+    // offset (with the slot a loop variable, each read costs one or two address instructions).
+    // 128 x 128 tiles on quantized bytes keep the slot a variable: unrolled, their fragments,
+    // accumulators and decoding no longer fit the registers of three workgroups per CU. (The
+    // stage body is written out at each call site: called through a lambda capturing the
+    // fragment arrays, the 128 x 128 kernels kept ~80 more registers live and spilled.)
+    if constexpr (I * J <= 8 || WQ == 0) {
+        int s = 0;
+        for (; s + NS <= SL; s += NS) {
+#pragma unroll
+            for (int u = 0; u < NS; u++) {
+                half_inner(a[0], b[0], a[1], b[1], u, kst(s + u));
+                half_boundary(a[1], b[1], a[0], b[0], s + u, u, u + 1 == NS ? 0 : u + 1);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < NS - 1; u++) {
+            if (s + u < SL) {
+                half_inner(a[0], b[0], a[1], b[1], u, kst(s + u));
+                half_boundary(a[1], b[1], a[0], b[0], s + u, u, u + 1);
+            }
+        }
+    } else {
+        int st = 0;
+        for (int s = 0; s < SL; s++) {
+            const int stn = st + 1 == NS ? 0 : st + 1;
+            half_inner(a[0], b[0], a[1], b[1], st, kst(s));
+            half_boundary(a[1], b[1], a[0], b[0], s, st, stn);
+            st = stn;
+        }
     }
     wait_vm0();
 
