@@ -993,6 +993,16 @@ int gemm_h16_ln_any(mgh_ctx* c, const char* fn, int wq, const void* w, int N, in
     return MGH_OK;
 }
 
+// fp32 activations are rounded to fp16 either inside the GEMM's K loop (the 64-row fp32-operand
+// plans) or by a separate pass feeding the fp16-operand plans (128-row tiles): every weight-row
+// tile repeats the in-loop rounding, the pass is paid once per call. Measured on the four FC
+// shapes at M = 2056 .. 16448 (Q8_0 bytes and fp16 copies): the pass wins from about 4096 x
+// 3072 outputs (M = 4097 up-proj: 42.6 against 46.0 us on Q8_0 bytes) and from M = 8192 on
+// (QKV 53.7 against 62.3 us), rounding in the loop below that (M = 4097 Q8_0: QKV 32.3 against
+// 34.0, out-proj 19.2 against 25.2, down-proj 49.1 against 56.9 us; M = 2056: the four FCs
+// 95 against 112 us).
+bool round_act_pass(int M, int N) { return M >= 8192 || (M >= 2048 && (int64_t)M * N >= (int64_t)4096 * 3072); }
+
 int gemm_h16_f32in_any(mgh_ctx* c, const char* fn, int wq, const void* w, int N, int K, const float* x, int M,
                        const float* bias, int act, const float* resid, float* y) {
     if (!c) return MGH_ERR_ARG;
@@ -1003,14 +1013,10 @@ int gemm_h16_f32in_any(mgh_ctx* c, const char* fn, int wq, const void* w, int N,
     a.w = w; a.wq = wq;
     a.bias = bias; a.resid = resid; a.y = y;
     a.M = M; a.N = N; a.K = K; a.act = act;
-    if (M < 2048) {
-        // few activation rows: round them while the GEMM reads them (one launch; the 64-row
-        // fp32 stage costs less than the separate rounding pass)
-        a.xf = x;
+    if (!round_act_pass(M, N)) {
+        a.xf = x;                               // rounded while the GEMM reads them
     } else {
-        // many rows: a rounding pass, then the fp16-operand kernel and its tile plans (128-row
-        // and 3-deep tiles exist for fp16 operands only); per four-FC step at M = 4097 this
-        // measured equal to rounding inside the GEMM (377.7 against 376.4 TOPS)
+        // a rounding pass, then the fp16-operand kernel and its tile plans
         if (int r = ensure_scratch(c, round256((size_t)M * K * 2))) return r;
         MGH_HIP(c, mgh::launch_f32_to_f16(x, (_Float16*)c->scratch, (int64_t)M * K, c->stream), "k_f32_to_f16");
         a.x = (const _Float16*)c->scratch;
@@ -1116,8 +1122,8 @@ int mgh_gemm_h16_f32in_noalloc(mgh_ctx* c, const void* wp16, int N, int K, const
     if (!c) return MGH_ERR_ARG;
     if (int r = check_h16(c, "gemm_h16_f32in_noalloc", wp16, N, K, x, M, bias, act, resid, y)) return r;
     if (M == 0) return MGH_OK;
-    // the same launches as mgh_gemm_h16_f32in, with the rounded activations (M >= 2048) and the
-    // split-K partials placed in the fixed scratch array instead of context buffers
+    // the same launches as mgh_gemm_h16_f32in, with the rounded activations (round_act_pass)
+    // and the split-K partials placed in the fixed scratch array instead of context buffers
     mgh::GemmH16Args a{};
     a.w = wp16;
     a.bias = bias; a.resid = resid; a.y = y;
@@ -1128,7 +1134,7 @@ int mgh_gemm_h16_f32in_noalloc(mgh_ctx* c, const void* wp16, int N, int K, const
         MGH_HIP(c, mgh::launch_gemv_h16(a, c->stream), "k_gemv_fc");
         return MGH_OK;
     }
-    const bool round_pass = M >= 2048;
+    const bool round_pass = round_act_pass(M, N);
     const size_t x16_b = round_pass ? round256((size_t)M * K * 2) : 0;
     const mgh::H16Plan p = mgh::gemm_h16_plan(M, N, K, !round_pass, 0);
     const size_t need = x16_b + (p.splits > 1 ? round256(p.ws_bytes) : 0);
