@@ -172,23 +172,14 @@ __device__ __forceinline__ f16x8 deq_q8(u32x2 c, uint32_t dbits) {
 }
 
 // Q4_K fragment: eight 4-bit values (byte e of c: element e in the low nibble, element e + 4
-// in the high one) of sub-block j of a super-block with header h (fp16 d | fp16 dmin, then
-// the 12 bytes of packed 6-bit scales / mins) -> (d*sc) * q - dmin*m rounded to fp16. d*sc and
-// (d*sc)*q are exact in fp32, so the fma rounds once, as the multiply-then-subtract of
-// k_pack_w16; then one rounding to fp16.
-__device__ __forceinline__ f16x8 deq_q4(uint32_t c, u32x4 h, int j) {
-    // j is the same for the whole wave: the masks select the j < 4 form (6 low bits of byte j
-    // of scales[0..3] / [4..7]) or the j >= 4 form (4 bits of byte j - 4 of scales[8..11] plus
-    // the top 2 bits of byte j - 4 of scales[0..3] / [4..7]) without a branch
-    const int sh = 8 * (j & 3);
-    const bool first = j < 4;
-    const uint32_t m1 = first ? 63u : 0u, m2 = first ? 0u : 15u, m3 = first ? 0u : 0xC0u;
-    const uint32_t by = h.y >> sh, bz = h.z >> sh, bw = h.w >> sh;
-    const uint32_t sc = (by & m1) | (bw & m2) | ((by & m3) >> 2);
-    const uint32_t mn = (bz & m1) | ((bw >> 4) & m2) | ((bz & m3) >> 2);
-    const float s = h2f(h.x & 0xFFFFu) * (float)sc;
-    const float m = h2f(h.x >> 16) * (float)mn;
-    const uint32_t lo = c & 0x0F0F0F0Fu, hn = (c >> 4) & 0x0F0F0F0Fu;
+// in the high one) of a sub-block with scale s = d * sc and offset m = dmin * mn -> s * q - m
+// rounded to fp16. s and s * q are exact in fp32, so the fma rounds once, as the
+// multiply-then-subtract of k_pack_w16; then one rounding to fp16.
+__device__ __forceinline__ f16x8 deq_q4v(uint32_t c, float s, float m) {
+    uint32_t lo = c & 0x0F0F0F0Fu, hn = (c >> 4) & 0x0F0F0F0Fu;
+    // (the empty asm keeps the masks apart from the byte conversions below: folded into them,
+    // every byte became a 4-bit extract plus a convert instead of one v_cvt_f32_ubyteN)
+    asm volatile("" : "+v"(lo), "+v"(hn));
     f32x4 a, b;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
@@ -196,6 +187,32 @@ __device__ __forceinline__ f16x8 deq_q4(uint32_t c, u32x4 h, int j) {
         b[e] = __builtin_fmaf(s, (float)((hn >> (8 * e)) & 0xFFu), -m);
     }
     return cvt8_f16(a, b);
+}
+
+// (d * sc, dmin * mn) of the sub-blocks j0 = 2 (t % 4) and j0 + 1 of the super-block with header
+// h (fp16 d | fp16 dmin, then the 12 bytes of packed 6-bit scales / mins) that 64-value K stage
+// t covers (get_scale_min_k4: j < 4 takes the 6 low bits of scales[j] / scales[j + 4]; j >= 4
+// the low / high nibble of scales[j + 4] plus the top 2 bits of scales[j - 4] / scales[j]).
+// The two sub-blocks lie on the same side of 4, so one set of masks (uniform) decodes both,
+// four bytes at a time.
+__device__ __forceinline__ void q4_scales(u32x4 h, int t, float& s0, float& m0, float& s1, float& m1) {
+    const bool first = (t & 2) == 0;
+    const int sh = 16 * (t & 1);                // byte of sub-block j0 in its dword
+    const uint32_t lo6 = first ? 0x3F3F3F3Fu : 0u, lo4 = first ? 0u : 0x0F0F0F0Fu, hi2 = first ? 0u : 0x30303030u;
+    const uint32_t sc = (h.y & lo6) | (h.w & lo4) | ((h.y >> 2) & hi2);
+    const uint32_t mn = (h.z & lo6) | ((h.w >> 4) & lo4) | ((h.z >> 2) & hi2);
+    const float d = h2f(h.x & 0xFFFFu), dm = h2f(h.x >> 16);
+    s0 = d * (float)((sc >> sh) & 0xFFu);
+    s1 = d * (float)((sc >> (sh + 8)) & 0xFFu);
+    m0 = dm * (float)((mn >> sh) & 0xFFu);
+    m1 = dm * (float)((mn >> (sh + 8)) & 0xFFu);
+}
+
+// One sub-block j of a Q4_K super-block (the skinny-M kernel's form)
+__device__ __forceinline__ f16x8 deq_q4(uint32_t c, u32x4 h, int j) {
+    float s0, m0, s1, m1;
+    q4_scales(h, j >> 1, s0, m0, s1, m1);
+    return (j & 1) ? deq_q4v(c, s1, m1) : deq_q4v(c, s0, m0);
 }
 
 // K-loop-dequant layout (packed_weight_bytes_dq): one thread per 32-value block (row n, block t
@@ -366,7 +383,7 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_fc
     constexpr int NR = (WQ ? 2 : 1) * I + (XF32 ? 2 : 1) * J;  // LDS reads per K half
     // dequantizing forms: MFMAs that carry the LDS reads (two each), VALU per later MFMA
     constexpr int NRD = (NR + 1) / 2 < I * J ? (NR + 1) / 2 : I * J - 1;
-    constexpr int VK = (WQ == 8 ? 14 : 34) * I + (XF32 ? 5 : 0) * J;   // decoding VALU per K half
+    constexpr int VK = (WQ == 8 ? 14 : 24) * I + (XF32 ? 5 : 0) * J;   // decoding VALU per K half
     constexpr int VPM = (VK + (I * J - NRD) - 1) / (I * J - NRD);
     constexpr int NI = NR < I * J ? NR : I * J;  // MFMA : LDS-read pairs in the interleave
     static_assert(NS >= 2 && (NS - 1) * (CW + CX + CA) < 64, "ring depth");
@@ -476,9 +493,11 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_fc
     auto frag = [&](const u32x4* B, int r0, int kb) {
         return __builtin_bit_cast(f16x8, B[(r0 + l16) * CPW + ((4 * kb + lq) ^ swz<CPW>(l16))]);
     };
-    // weight fragment of rows r0..r0+15 of the tile (r0 % 16 == 0), K half kb of ring stage st
+    float q4s[WQ == 12 ? I : 1], q4m[WQ == 12 ? I : 1];   // Q4_K: second-half sub-block scales
+    // weight fragment of subtile i (rows r0 = WN*wn + 16i ..) of the tile, K half kb of ring stage st
     // (global K stage ksg): fp16 as stored, or dequantized from the group's codes / nibbles
-    auto wfrag = [&](int st, int r0, int kb, int ksg) -> f16x8 {
+    auto wfrag = [&](int st, int i, int kb, int ksg) -> f16x8 {
+        const int r0 = WN * wn + 16 * i;
         if constexpr (WQ == 0) {
             return frag(L.w[st], r0, kb);
         } else if constexpr (WQ == 8) {
@@ -487,9 +506,16 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_fc
             const uint32_t d = ((const uint16_t*)&L.aux[st][(gi / GPW) * 16 + (gi % GPW) * 4])[kb * 16 + l16];
             return deq_q8(c, d);
         } else {
+            // the stage's two sub-block scales come from its header at the first half's read
+            // and serve the second half's
             const int gi = r0 >> 4;
             const uint32_t c = ((const uint32_t*)&L.w[st][gi * 32])[kb * 64 + lane];
-            return deq_q4(c, L.aux[st][gi * 16 + l16], (2 * ksg + kb) & 7);
+            if (kb == 0) {
+                float s0, m0;
+                q4_scales(L.aux[st][gi * 16 + l16], ksg, s0, m0, q4s[i], q4m[i]);
+                return deq_q4v(c, s0, m0);
+            }
+            return deq_q4v(c, q4s[i], q4m[i]);
         }
     };
     // activation fragment: fp16 rows as stored, or fp32 rows rounded to fp16 on the way in
@@ -517,7 +543,7 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_fc
     for (int k = 0; k < NS; k++) dma_stage(k, min(k, SL - 1));
     stage_sync<(NS - 1) * NDMA>();              // stage 0 has landed (mine, then everyone's)
 #pragma unroll
-    for (int i = 0; i < I; i++) a[0][i] = wfrag(0, WN * wn + 16 * i, 0, kst(0));
+    for (int i = 0; i < I; i++) a[0][i] = wfrag(0, i, 0, kst(0));
 #pragma unroll
     for (int j = 0; j < J; j++) b[0][j] = xfrag(L.x[0], RW * wm + 16 * j, 0);
 
@@ -532,7 +558,7 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_fc
     auto half_inner = [&](const f16x8 (&ca)[I], const f16x8 (&cb)[J], f16x8 (&na)[I], f16x8 (&nb)[J], int st,
                           int ksg) {
 #pragma unroll
-        for (int i = 0; i < I; i++) na[i] = wfrag(st, WN * wn + 16 * i, 1, ksg);
+        for (int i = 0; i < I; i++) na[i] = wfrag(st, i, 1, ksg);
 #pragma unroll
         for (int j = 0; j < J; j++) nb[j] = xfrag(L.x[st], RW * wm + 16 * j, 1);
         mfma_all(ca, cb, 0, I * J);
@@ -565,7 +591,7 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_fc
         // (a 2-deep ring waits for everything, so it skips the re-loads past the end)
         if (NS > 2 ? s + 1 < SL : s + NS < SL) dma_stage(st, min(s + NS, SL - 1));
 #pragma unroll
-        for (int i = 0; i < I; i++) na[i] = wfrag(stn, WN * wn + 16 * i, 0, kst(s + 1 < SL ? s + 1 : s));
+        for (int i = 0; i < I; i++) na[i] = wfrag(stn, i, 0, kst(s + 1 < SL ? s + 1 : s));
 #pragma unroll
         for (int j = 0; j < J; j++) nb[j] = xfrag(L.x[stn], RW * wm + 16 * j, 0);
         mfma_all(ca, cb, MID, I * J);
