@@ -1011,8 +1011,12 @@ H16Plan gemm_h16_plan(int M, int N, int K, bool xf32, int wq) {
     // activations, 64-row tiles: their stage is already as large as a 128-row fp16 stage.
     // 3072-wide outputs (the MLP up-proj) take 128-row tiles from about 1.5 tiles per CU
     // (M = 4112: 43.6 against 46.2 us; M = 2056: 23.8 against 27.2 us; at M = 1025 the 64-row
-    // tiles win, 15.2 against 17.2 us)
-    const bool wide128 = t128 >= 1024 || (N <= 1024 && t128 >= 192) || (N >= 3072 && t128 >= 384);
+    // tiles win, 15.2 against 17.2 us). Narrow outputs with short K (the out-proj) keep 64-row
+    // tiles below 256 128-row tiles (M = 4112 out-proj on fp16 activations: 14.9 against
+    // 16.4 us on fp16 copies, 17.5 against 19.0 on Q8_0 bytes; at M = 8193 the 128-row tiles
+    // win, 24.4 against 27.0 us)
+    const bool wide128 = t128 >= 1024 || (N <= 1024 && t128 >= 192 && (K >= 2048 || t128 >= 256)) ||
+                         (N >= 3072 && t128 >= 384);
     p.bm = wide128 && !xf32 ? 128 : 64;
     const int tiles = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
     const int S = K / 64;
