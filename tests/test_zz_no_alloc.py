@@ -35,9 +35,9 @@ def _case(ctx, rng, M, N, K, act, resid):
 def test_noalloc_equals_allocating_entry_point():
     rng = np.random.default_rng(77)
     with ema.Context(0) as ctx:
-        # rounding pass into the array (M >= 2048), then a smaller split-K call, then a tiny one,
-        # then a skinny-M call
-        for M, N, K, act, resid in ((2500, 768, 3072, 0, True), (1025, 768, 3072, 0, True),
+        # a rounding pass into the array (4200 x 3072 outputs take the separate pass), then a
+        # split-K call with fp32 rows (partials in the array), then a tiny one, then a skinny-M call
+        for M, N, K, act, resid in ((4200, 3072, 768, ema.ACT_GELU, True), (1025, 768, 3072, 0, True),
                                     (37, 96, 512, ema.ACT_GELU, False),
                                     (12, 768, 768, ema.ACT_GELU, True)):
             print(f"noalloc M={M} N={N} K={K}", flush=True)
@@ -52,7 +52,7 @@ def test_noalloc_two_streams_share_the_array_in_order():
     split-K partials), and the library's per-GPU event orders the second call after the first,
     so each result equals the allocating entry point's bit for bit, twice in a row."""
     rng = np.random.default_rng(5)
-    shapes = [(2500, 768, 3072, 0), (1025, 768, 3072, 0)]
+    shapes = [(4200, 3072, 768, 0), (1025, 768, 3072, 0)]
     with ema.Context(0) as c0, ema.Context(0) as c1:
         bufs = []
         for (M, N, K, act), c in zip(shapes, (c0, c1)):
