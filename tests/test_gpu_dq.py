@@ -126,6 +126,46 @@ def test_gemm_dq_f32in(ctx, wtype, M, N, K):
         assert err <= 1e-3
 
 
+# K loops whose stage count is not a multiple of the ring depth: the unrolled ring's last,
+# partial iteration (2-deep ring on fp32 rows: 5 stages; 3-deep few-tile ring: 5 stages and a
+# split of 14; 2-deep split-K ring: 7 stages per split; the fp16-operand 128 x 128 kernel of the
+# fp16 copies: 21 stages)
+ODD_STAGES = [(ema.WTYPE_Q8_0, 300, 256, 320, False), (ema.WTYPE_Q8_0, 100, 256, 320, False),
+              (ema.WTYPE_Q4_K, 200, 256, 1792, False), (ema.WTYPE_Q4_K, 1025, 768, 1792, False),
+              (ema.WTYPE_Q8_0, 4112, 3072, 1344, True)]
+
+
+@pytest.mark.parametrize("wtype,M,N,K,x16in", ODD_STAGES)
+def test_gemm_odd_stage_counts(ctx, wtype, M, N, K, x16in):
+    print(f"odd stage count wtype={wtype} M={M} N={N} K={K} fp16 operand={x16in}", flush=True)
+    rng = np.random.default_rng(M + N + K + wtype)
+    _, dP16, dQ, _ = _weights(ctx, wtype, N, K, M * 7 + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x16 = x.astype(np.float16)
+    bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+    resid = rng.standard_normal((M, N)).astype(np.float32)
+    dX = ctx.upload(x16 if x16in else x)
+    dB, dR = ctx.upload(bias), ctx.upload(resid)
+    dY = ctx.alloc(M * N * 4)
+    ref = _ref64(ctx, dP16, N, K, x16, bias, 1, resid)
+    for form in ("dq", "h16"):
+        if x16in:
+            if form == "dq":
+                ctx.gemm_dq(wtype, dQ, N, K, dX, M, dB, 1, dR, dY)
+            else:
+                ctx.gemm_h16(dP16, N, K, dX, M, dB, 1, dR, dY)
+        elif form == "dq":
+            ctx.gemm_dq_f32in(wtype, dQ, N, K, dX, M, dB, 1, dR, dY)
+        else:
+            ctx.gemm_h16_f32in(dP16, N, K, dX, M, dB, 1, dR, dY)
+        y = ctx.download(dY, (M, N), np.float32)
+        err = _rel(y, ref)
+        print(f"  {form}: rel err vs float64 of the fp16 operands {err:.2e}")
+        assert err <= 1e-5, form
+    for t in (dP16, dQ, dX, dB, dR, dY):
+        ctx.free(t)
+
+
 @pytest.mark.parametrize("wtype", [ema.WTYPE_Q8_0, ema.WTYPE_Q4_K])
 @pytest.mark.parametrize("M,N,K", [(12, 768, 768), (257, 2304, 768), (1025, 3072, 768), (4112, 768, 3072)])
 def test_gemm_dq_fp16_operand_and_y16(ctx, wtype, M, N, K):
