@@ -90,7 +90,10 @@ SHAPES = [(1, 2304, 768), (7, 132, 256), (16, 768, 3072), (32, 768, 768), (33, 1
           (1025, 3072, 768), (1025, 768, 3072), (4097, 2304, 768), (4112, 768, 3072),
           # the up-proj at M = 4097 / 4112: the last, partial row of 128-row tiles runs on the
           # skinny-M kernel after the tiled kernel (GELU without residual, residual without act)
-          (4097, 3072, 768), (4112, 3072, 768)]
+          (4097, 3072, 768), (4112, 3072, 768),
+          # a partial last 16-row weight group under the tiled plans (N = 1000: 62 full groups
+          # and 8 rows; the buffer resources end at the packed bytes)
+          (1025, 1000, 768), (4097, 1000, 768)]
 
 
 @pytest.mark.parametrize("wtype", [ema.WTYPE_Q8_0, ema.WTYPE_Q4_K])
