@@ -634,11 +634,12 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_fc
     // bias and activation on the accumulators (lane column n0 + WN*wn + 16i + 4lq + e), where
     // every value is independent of the others, before the transpose
     if (!PART) {
+        // columns past N (and a null bias: an empty range) read zeros in the range check
+        const __amdgpu_buffer_rsrc_t rb = make_rsrc(g.bias, g.bias ? (uint64_t)N * 4 : 0);
 #pragma unroll
         for (int i = 0; i < I; i++) {
             const int nb = n0 + WN * wn + 16 * i + 4 * lq;
-            f32x4 bi = {0.f, 0.f, 0.f, 0.f};
-            if (g.bias && nb < N) bi = *(const f32x4*)(g.bias + nb);
+            const f32x4 bi = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, nb * 4, 0, 0));
 #pragma unroll
             for (int j = 0; j < J; j++) {
                 acc[i][j] += bi;
@@ -660,16 +661,34 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_fc
     const int n = n0 + c;
     float* part = PART ? g.ws + ((size_t)lt * splits + ks) * (size_t)BM * BN : nullptr;
     constexpr int NP = HR / (NTH / TR);         // output rows per thread and pass
+    // Residual loads and output stores are buffer accesses from the tile origin, over a range
+    // that ends with the tile's last row inside M: rows past M fall outside it, and a column
+    // past N takes an offset beyond any range (N <= 2^21 keeps every offset below 2^31), so the
+    // hardware range check drops those stores and zero-fills those loads — no per-row branch
+    // or 64-bit address arithmetic in the store loop.
+    const size_t org = (size_t)m0 * N + n0;
+    const uint32_t span = (uint32_t)min(BM, M - m0) * (uint32_t)N - (uint32_t)n0;   // elements
+    // this thread's byte offset in its first row of the tile, fp32 / fp16 elements (a row
+    // offset (HR h + (NTH / TR) p) N elements is added per store)
+    const uint32_t el0 = (uint32_t)(tid / TR) * N + c;
+    const uint32_t ob4 = n < N ? el0 * 4 : 0x80000000u, ob2 = n < N ? el0 * 2 : 0x80000000u;
+    const bool rs = !PART && g.resid, o16 = g.y16 != nullptr, o32 = !PART && !o16 && g.y;
+    const __amdgpu_buffer_rsrc_t rres = make_rsrc(rs ? g.resid + org : nullptr, rs ? (uint64_t)span * 4 : 0);
+    const __amdgpu_buffer_rsrc_t rout =
+        o16 ? make_rsrc(g.y16 + org, (uint64_t)span * 2) : make_rsrc(o32 ? g.y + org : nullptr, o32 ? (uint64_t)span * 4 : 0);
 #pragma unroll
     for (int h = 0; h < WMR * HPW; h++) {
         // the pass's residual loads go out before the transpose, all at once (one HBM
         // round trip per pass, overlapped with the LDS work)
+        // without a residual -0.0, which leaves every value as it is when added
         f32x4 rv[NP];
 #pragma unroll
         for (int p = 0; p < NP; p++) {
-            const int m = m0 + HR * h + (NTH / TR) * p + tid / TR;
-            rv[p] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (!PART && g.resid && m < M && n < N) rv[p] = *(const f32x4*)(g.resid + (size_t)m * N + n);
+            rv[p] = f32x4{-0.f, -0.f, -0.f, -0.f};
+            if (rs) {
+                const uint32_t ro = ob4 + (uint32_t)(HR * h + (NTH / TR) * p) * N * 4;
+                rv[p] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rres, (int)ro, 0, 0));
+            }
         }
         __syncthreads();                        // ring / previous rows no longer read
         if (wm == h / HPW) {
@@ -688,16 +707,13 @@ __global__ __launch_bounds__(128 * WMR, (kH16MinBlocks<WMR, BN>)) void k_gemm_fc
                 __builtin_nontemporal_store(v, (f32x4*)(part + (size_t)(HR * h + r) * BN + c));
                 continue;
             }
-            const int m = m0 + HR * h + r;
-            if (m >= M || n >= N) continue;
-            f32x4 o = v;
-            const size_t idx = (size_t)m * N + n;
-            if (g.resid) o += rv[p];
+            const f32x4 o = v + rv[p];
+            const uint32_t rb = (uint32_t)(HR * h + (NTH / TR) * p) * N;  // row offset, elements
+            // aux 2: non-temporal (the output is not re-read by this launch)
             if (g.y16)
-                __builtin_nontemporal_store(cvt4_f16(o),
-                                            (f16x4*)(g.y16 + idx));
+                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, cvt4_f16(o)), rout, (int)(ob2 + rb * 2), 0, 2);
             else
-                __builtin_nontemporal_store(o, (f32x4*)(g.y + idx));
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), rout, (int)(ob4 + rb * 4), 0, 2);
         }
     }
 }
@@ -1199,6 +1215,7 @@ hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a0, hipStream_t 
     GemmH16Args a = a0;
     a.ph = p.ph;
     if (p.wmr != 2) return hipErrorInvalidValue;
+    if (a.N > kFcMaxN) return hipErrorInvalidValue;     // the epilogue's 32-bit tile offsets
     // the reduce takes the LayerNorm only when K is split, without activation or fp16 output
     if (ln && (p.splits < 2 || a.act != 0 || a.y16 || a.N % 256 || a.N > 2048)) return hipErrorInvalidValue;
     // A last, partial row of tiles that raises the most tiles any CU runs (ceil(tiles / CUs))

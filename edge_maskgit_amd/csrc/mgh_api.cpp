@@ -153,6 +153,7 @@ int check_h16(mgh_ctx* c, const char* fn, const void* wp, int N, int K, const vo
     if (act < 0 || act > 2) return fail(c, MGH_ERR_ARG, "act must be 0 (none), 1 (gelu) or 2 (silu)");
     if (K % 64) return fail(c, MGH_ERR_UNSUPPORTED, std::string(fn) + ": needs K % 64 == 0");
     if (N % 4) return fail(c, MGH_ERR_UNSUPPORTED, std::string(fn) + ": needs N % 4 == 0");
+    if (N > mgh::kFcMaxN) return fail(c, MGH_ERR_UNSUPPORTED, std::string(fn) + ": needs N <= 2097152");
     if (M == 0) return MGH_OK;
     if (!wp || !x || (!y && !y_optional)) return fail(c, MGH_ERR_ARG, std::string(fn) + ": null pointer");
     if (!aligned16(wp) || !aligned16(x) || !aligned16(bias) || !aligned16(resid) || !aligned16(y))

@@ -199,7 +199,9 @@ size_t packed_weight_bytes_dq(int wtype, int64_t N, int64_t K);
 hipError_t launch_pack_weights_dq(int wtype, const void* w, void* out, int N, int K, hipStream_t s);
 hipError_t launch_f32_to_f16(const float* x, _Float16* h, int64_t n, hipStream_t s);
 // ln: the split-K reduce also writes the LayerNorm-affine of y's rows (the plan must split K;
-// act 0, fp32 y, N % 256 == 0, N <= 2048)
+// act 0, fp32 y, N % 256 == 0, N <= 2048). N <= kFcMaxN: the tiled epilogue addresses a tile's
+// outputs with 32-bit offsets from its origin.
+constexpr int kFcMaxN = 1 << 21;
 hipError_t launch_gemm_h16(const H16Plan& p, const GemmH16Args& a, hipStream_t s, const LnArgs* ln = nullptr);
 // skinny-M form of the same product (1 <= M <= kGemvMaxRows; no workspace), and the rule that
 // picks it over the tiled plan
