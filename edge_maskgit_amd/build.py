@@ -32,11 +32,15 @@ HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC",
 KERNEL_SOURCES = ["k_quant_act.hip", "k_gemm_i8.hip",
                   "k_pack_w.hip", "k_gemm_qp.hip", "k_layernorm.hip", "k_flash_attn.hip",
                   "k_gemm_f32.hip", "k_glue.hip", "k_ops.hip", "k_vqgan.hip", "k_conv_i8.hip", "noalloc.hip", "k_decode.hip", "k_gemm_fc.hip", "mgh_api.cpp"]
-# Per-source extra flags. The int8 GEMMs keep MFMA results in VGPRs so the per-block
-# scale arithmetic reads them without v_accvgpr_read copies.
-EXTRA_FLAGS = {"k_gemm_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-               "k_gemm_qp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-               "k_conv_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Per-source extra flags. Every MFMA kernel keeps its MFMA results in VGPRs: the int8 GEMMs'
+# per-block scale arithmetic then reads them without v_accvgpr_read copies, and in the
+# unrolled K loops of the FC GEMM and the attention's tile loops the accumulators no longer
+# rotate through the AGPRs at each loop back edge (4-28 v_accvgpr moves per iteration in the
+# FC kernels with 64-row weight tiles, up to ~200 per attention kernel), with the same
+# occupancy and fewer registers.
+_VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+EXTRA_FLAGS = {src: _VGPR_FORM for src in ("k_gemm_i8.hip", "k_gemm_qp.hip", "k_conv_i8.hip", "k_gemm_fc.hip",
+                                           "k_flash_attn.hip", "k_gemm_f32.hip", "k_vqgan.hip")}
 # C++ host runtime (graph API mirror, GGUF loader, transformer builder, HipRuntime, mgr C ABI):
 # plain host code over the libmgh C ABI, compiled with g++ into lib/libmg_hip.so.
 HOST_SOURCES = ["mg-tensor.cpp", "mg-model.cpp", "mg-transformer.cpp", "mg-vqgan.cpp", "mg-hip.cpp", "mgr_api.cpp"]
