@@ -464,12 +464,12 @@ const void* HipRuntime::run(Graph& g, bool readback) {
     I.codes.clear();
     const int n = (int)g.nodes.size();
     // quantized weights the fused kernels take (mgh_gemm_h16 / _dq / _q_packed: Q8_0 with
-    // K % 64 == 0, N % 4 == 0; Q4_K with N % 4 == 0); other quantized shapes run the
+    // K % 64 == 0, N % 4 == 0; Q4_K with N % 4 == 0; N <= 2^21); other quantized shapes run the
     // reference's F32 dequant GEMM on weights dequantized once at upload (layout 6)
     auto quant = [](const Tensor* w) {
         if (w->type != Type::Q8_0 && w->type != Type::Q4_K) return false;
         const int64_t K = w->ne[0], N = w->nelements() / w->ne[0];
-        return N % 4 == 0 && (w->type == Type::Q4_K || K % 64 == 0);
+        return N % 4 == 0 && N <= (int64_t)1 << 21 && (w->type == Type::Q4_K || K % 64 == 0);
     };
 
     // ---- plan (reused for a graph that matches the last planned one) ----

@@ -277,7 +277,7 @@ int mgh_upscale(mgh_ctx* ctx, const float* d_x, int W, int H, int C, int N, int 
  *      scratch). A few activation rows (M <= 16, or M <= 32 with K <= 1024: decode- and
  *      GEMV-shaped calls) take a skinny-M kernel that streams each weight row once and sums
  *      K slices across waves, the rest the tiled kernel; the same product and rounding.
- *      K % 64 == 0, N % 4 == 0, 16-byte aligned operands. ---- */
+ *      K % 64 == 0, N % 4 == 0, N <= 2097152, 16-byte aligned operands. ---- */
 size_t mgh_packed_weight_bytes_f16(int N, int K);
 int mgh_pack_weights_f16(mgh_ctx* ctx, int wtype, const void* d_w, int N, int K, void* d_wp16);
 /* x -> fp16 (round to nearest even); n % 8 == 0 */
@@ -328,7 +328,7 @@ int mgh_gemm_h16_y16(mgh_ctx* ctx, const void* d_wp16, int N, int K, const void*
  *      kernels decode each weight to d*q, resp. (d*sc)*q - dmin*m rounded once to fp16 -- the
  *      value mgh_pack_weights_f16 stores -- as the MFMA fragments are read, so results equal
  *      mgh_gemm_h16's for the same tile plan. Shapes and alignment as mgh_gemm_h16 (K % 64 == 0,
- *      Q4_K K % 256 == 0, N % 4 == 0, 16-byte aligned operands). ---- */
+ *      Q4_K K % 256 == 0, N % 4 == 0, N <= 2097152, 16-byte aligned operands). ---- */
 size_t mgh_packed_weight_bytes_dq(int wtype, int N, int K);
 /* raw Q8_0 / Q4_K blocks (GGUF layout, any byte alignment) -> fp32 [N][K], the values the
  * reference's dequantizing kernels compute (DEQ_Q8 mg-opencl.cpp:386-387; deq_q4k_elem

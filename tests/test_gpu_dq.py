@@ -247,6 +247,18 @@ def test_pack_dq_rejects_bad_shapes(ctx):
     assert ema.packed_weight_bytes_dq(ema.WTYPE_Q4_K, 4, 128) == 0
 
 
+def test_gemm_rejects_n_past_the_epilogue_offsets(ctx):
+    # the tiled epilogue addresses a tile's outputs with 32-bit offsets from its origin: N is
+    # refused past 2^21 (before any pointer is touched, so a small buffer stands in)
+    d = ctx.alloc(4096)
+    for fn in (ctx.gemm_dq, ctx.gemm_dq_f32in):
+        with pytest.raises(ema.MghError, match="N <= 2097152"):
+            fn(ema.WTYPE_Q8_0, d, (1 << 21) + 4, 64, d, 1, None, 0, None, d)
+    with pytest.raises(ema.MghError, match="N <= 2097152"):
+        ctx.gemm_h16(d, (1 << 21) + 4, 64, d, 1, None, 0, None, d)
+    ctx.free(d)
+
+
 @pytest.mark.parametrize("wtype,N,K", [(ema.WTYPE_Q8_0, 1, 32), (ema.WTYPE_Q8_0, 99, 96), (ema.WTYPE_Q8_0, 768, 3072),
                                        (ema.WTYPE_Q4_K, 3, 256), (ema.WTYPE_Q4_K, 99, 512)])
 def test_dequant_weights_f32_matches_oracle(ctx, wtype, N, K):
