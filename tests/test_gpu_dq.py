@@ -237,6 +237,42 @@ def test_gemm_dq_ln_equals_fp16_copy(ctx, wtype, M, N, K):
             assert np.array_equal(a, b)
 
 
+# Partial tiles in both directions with a residual: the epilogue's buffer ranges end with the
+# tile's last row inside M, and columns past N take an offset beyond any range, so these outputs
+# (and their residual reads) rely on the hardware range check; fp32 rows (64-row tiles, the
+# skinny-M kernel for a ragged last row) and fp16 rows (128-row tiles), fp32 and fp16 output.
+@pytest.mark.parametrize("wtype", [ema.WTYPE_Q8_0, ema.WTYPE_Q4_K])
+@pytest.mark.parametrize("M,N,K", [(65, 100, 768), (1025, 1000, 768), (4097, 1000, 768), (300, 1000, 256)])
+def test_gemm_dq_ragged_tiles_with_residual(ctx, wtype, M, N, K):
+    print(f"gemm_dq ragged wtype={wtype} M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M * 7 + N + K + wtype)
+    _, dP16, dQ, _ = _weights(ctx, wtype, N, K, M + 2 * N + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x16 = x.astype(np.float16)
+    bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+    resid = rng.standard_normal((M, N)).astype(np.float32)
+    dX, dX16, dB, dR = ctx.upload(x), ctx.upload(x16), ctx.upload(bias), ctx.upload(resid)
+    # the outputs carry a guard past M x N that no store may touch
+    guard = 4096
+    dY = ctx.upload(np.full(M * N + guard, 7.0, np.float32))
+    dY16 = ctx.upload(np.full(M * N + guard, 7.0, np.float16))
+    for act in (0, 1):
+        ref = _ref64(ctx, dP16, N, K, x16, bias, act, resid)
+        for form, call in (("fp32 rows", lambda: ctx.gemm_dq_f32in(wtype, dQ, N, K, dX, M, dB, act, dR, dY)),
+                           ("fp16 rows", lambda: ctx.gemm_dq(wtype, dQ, N, K, dX16, M, dB, act, dR, dY))):
+            call()
+            y = ctx.download(dY, (M * N + guard,), np.float32)
+            assert _rel(y[:M * N].reshape(M, N), ref) <= 1e-5, f"{form} act {act}"
+            assert np.all(y[M * N:] == 7.0), f"{form} act {act}: store past the output"
+        ctx.gemm_dq_y16(wtype, dQ, N, K, dX16, M, dB, act, dR, dY16)
+        y16 = ctx.download(dY16, (M * N + guard,), np.float16)
+        a = y16[:M * N].reshape(M, N).astype(np.float64)
+        assert np.all(np.abs(a - ref) <= 2.0 ** -10 * np.abs(ref) + 1e-5 * np.abs(ref).max()), f"y16 act {act}"
+        assert np.all(y16[M * N:] == 7.0), f"y16 act {act}: store past the output"
+    for t in (dP16, dQ, dX, dX16, dB, dR, dY, dY16):
+        ctx.free(t)
+
+
 def test_pack_dq_rejects_bad_shapes(ctx):
     dW = ctx.alloc(1024)
     with pytest.raises(ema.MghError):
