@@ -49,6 +49,8 @@
 #include <algorithm>
 
 #include <atomic>
+#include <cstdio>
+#include <cstdlib>
 
 #include "mgh_common.h"
 #include "mgh_kernels.h"
@@ -974,7 +976,49 @@ hipError_t launch_gemv_h16(const GemmH16Args& a, hipStream_t s) {
     return xf ? launch_gemv_t<true, 2>(a, s) : launch_gemv_t<false, 2>(a, s);
 }
 
+static H16Plan gemm_h16_plan_rules(int M, int N, int K, bool xf32, int wq);
+
+namespace {
+// Tile-plan override for measurements, so that the plan comparisons quoted above can be rerun
+// with the committed library: MGH_FC_PLAN="bm,bn,ns,splits" (or "bm,bn,ns,splits,K,N" for the
+// launches of one K x N shape) replaces the plan of every tiled FC launch. The kernel set holds
+// the plans the rules pick and a few more; a plan outside it makes the launch fail with
+// hipErrorInvalidValue. Read once per process.
+struct PlanOverride {
+    bool on = false;
+    int bm = 0, bn = 0, ns = 0, splits = 1, k = 0, n = 0;
+};
+const PlanOverride& plan_override() {
+    static const PlanOverride o = [] {
+        PlanOverride r;
+        const char* e = std::getenv("MGH_FC_PLAN");
+        int v[6] = {0, 0, 0, 1, 0, 0};
+        if (e && std::sscanf(e, "%d,%d,%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3], &v[4], &v[5]) >= 4 && v[0] > 0 &&
+            v[1] > 0 && v[2] >= 2 && v[3] >= 1) {
+            r.on = true;
+            r.bm = v[0], r.bn = v[1], r.ns = v[2], r.splits = v[3], r.k = v[4], r.n = v[5];
+        }
+        return r;
+    }();
+    return o;
+}
+}  // namespace
+
 H16Plan gemm_h16_plan(int M, int N, int K, bool xf32, int wq) {
+    H16Plan p = gemm_h16_plan_rules(M, N, K, xf32, wq);
+    const PlanOverride& o = plan_override();
+    if (o.on && (!o.k || o.k == K) && (!o.n || o.n == N)) {
+        p.bm = o.bm;
+        p.bn = o.bn;
+        p.ns = o.ns;
+        p.splits = o.splits;
+        const int tiles = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
+        p.ws_bytes = p.splits > 1 ? (size_t)tiles * p.splits * p.bm * p.bn * 4 : 0;
+    }
+    return p;
+}
+
+static H16Plan gemm_h16_plan_rules(int M, int N, int K, bool xf32, int wq) {
     H16Plan p{};
     p.ns = 2;
     p.bn = 128;

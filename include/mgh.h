@@ -277,7 +277,10 @@ int mgh_upscale(mgh_ctx* ctx, const float* d_x, int W, int H, int C, int N, int 
  *      scratch). A few activation rows (M <= 16, or M <= 32 with K <= 1024: decode- and
  *      GEMV-shaped calls) take a skinny-M kernel that streams each weight row once and sums
  *      K slices across waves, the rest the tiled kernel; the same product and rounding.
- *      K % 64 == 0, N % 4 == 0, N <= 2097152, 16-byte aligned operands. ---- */
+ *      K % 64 == 0, N % 4 == 0, N <= 2097152, 16-byte aligned operands.
+ *      For measurements, the environment variable MGH_FC_PLAN="bm,bn,ns,splits[,K,N]" (read
+ *      once per process) replaces the tile plan of the tiled launches; a plan outside the
+ *      compiled kernel set makes the call fail. ---- */
 size_t mgh_packed_weight_bytes_f16(int N, int K);
 int mgh_pack_weights_f16(mgh_ctx* ctx, int wtype, const void* d_w, int N, int K, void* d_wp16);
 /* x -> fp16 (round to nearest even); n % 8 == 0 */

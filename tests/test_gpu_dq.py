@@ -273,6 +273,51 @@ def test_gemm_dq_ragged_tiles_with_residual(ctx, wtype, M, N, K):
         ctx.free(t)
 
 
+_PLAN_CHILD = r"""
+import os, sys
+import numpy as np
+sys.path.insert(0, os.getcwd())
+import edge_maskgit_amd as ema
+from tests.test_gpu_dq import _weights, _ref64, _rel
+M, N, K = 1025, 2304, 768
+ctx = ema.Context(0)
+rng = np.random.default_rng(5)
+_, dP16, dQ, _ = _weights(ctx, ema.WTYPE_Q8_0, N, K, 11)
+x = rng.standard_normal((M, K)).astype(np.float32)
+bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+dX, dB, dY = ctx.upload(x), ctx.upload(bias), ctx.alloc(M * N * 4)
+try:
+    ctx.gemm_dq_f32in(ema.WTYPE_Q8_0, dQ, N, K, dX, M, dB, 0, None, dY)
+except ema.MghError as e:
+    print("REFUSED", e)
+    sys.exit(0)
+y = ctx.download(dY, (M, N), np.float32)
+print("ERR", _rel(y, _ref64(ctx, dP16, N, K, x.astype(np.float16), bias, 0, None)))
+"""
+
+
+@pytest.mark.parametrize("plan,ok", [("64,128,2,4", True), ("64,64,3,1,768,2304", True), ("48,128,2,1", False)])
+def test_plan_override(plan, ok):
+    """MGH_FC_PLAN replaces the tile plan of the tiled FC launches (read once per process, so in a
+    child process): a plan the kernel set holds gives the same product (the float64 bar), one it
+    does not hold is refused."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, MGH_FC_PLAN=plan)
+    print(f"MGH_FC_PLAN={plan}", flush=True)
+    r = subprocess.run([sys.executable, "-c", _PLAN_CHILD], cwd=root, env=env, capture_output=True, text=True,
+                       timeout=300)
+    print(r.stdout[-400:], r.stderr[-400:])
+    assert r.returncode == 0
+    if ok:
+        err = float(r.stdout.split("ERR")[-1])
+        assert err <= 1e-5
+    else:
+        assert "REFUSED" in r.stdout
+
+
 def test_pack_dq_rejects_bad_shapes(ctx):
     dW = ctx.alloc(1024)
     with pytest.raises(ema.MghError):
