@@ -74,3 +74,19 @@ def test_runtime_errors_without_device(tmp_path):
     bad.write_bytes(b"NOTAGGUF" * 8)
     with pytest.raises(ema.MghError):
         runtime.gguf_info(str(bad))
+
+
+def test_every_mfma_kernel_builds_with_vgpr_results():
+    """Every kernel source that issues MFMAs is compiled with -amdgpu-mfma-vgpr-form (results in
+    VGPRs; without it the unrolled loops rotate their accumulators through the AGPRs), and the
+    packed-fp32 feature is off for all of them."""
+    import glob
+    from edge_maskgit_amd import build
+    srcs = sorted(glob.glob(os.path.join(build.CSRC, "*.hip")))
+    mfma = [os.path.basename(s) for s in srcs if "__builtin_amdgcn_mfma" in open(s).read()]
+    assert mfma
+    for name in mfma:
+        assert name in build.KERNEL_SOURCES, name
+        assert "-amdgpu-mfma-vgpr-form" in build.EXTRA_FLAGS.get(name, []), name
+    flags = " ".join(build.HIP_FLAGS)
+    assert "-target-feature -Xclang -packed-fp32-ops" in flags
